@@ -1,0 +1,161 @@
+/*
+ * swl.h — C ABI of libswl.so, the MI355X (gfx950) implementation of SwarmLoRA's
+ * per-layer gather -> base-GEMM -> scatter rounds, the LoRA delta, the paged-KV
+ * decode attention, and the slot-pool / command-ring runtime around them.
+ *
+ * Conventions
+ *   - Every entry point returns an int status (SWL_OK == 0).  On failure the
+ *     thread-local message behind swl_last_error() holds the text; the Python
+ *     shims raise RuntimeError(text), which is what the reference's pybind
+ *     modules do with the std::runtime_error they throw.
+ *   - Tensors are plain device pointers to row-major bf16 (or int32/int64)
+ *     arrays; sizes are int64 element counts.  `stream` is a hipStream_t passed
+ *     as void* (NULL = the null stream).  No torch types cross this boundary.
+ *   - Kernels are stream-ordered and never synchronise the host unless the
+ *     comment says so.
+ *
+ * Reference citations are relative to SHUs-Lab/SwarmLoRA's tree.
+ */
+#ifndef SWL_H
+#define SWL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ status */
+enum {
+  SWL_OK = 0,
+  SWL_ERR_INVALID = 1,   /* bad argument / shape / range                      */
+  SWL_ERR_HIP = 2,       /* a HIP runtime call failed ("CUDA error: ..." text)  */
+  SWL_ERR_STATE = 3,     /* not initialised / wrong order of calls             */
+  SWL_ERR_FULL = 4,      /* ring buffer full                                   */
+  SWL_ERR_QUIT = 5,      /* quit flag observed                                 */
+  SWL_ERR_NOT_FOUND = 6, /* slot not open / no free slot                       */
+  SWL_ERR_UNSUPPORTED = 7
+};
+
+/* Constants shared with the reference's ABI (src/cpp_extensions/common/ipc_types.h:16-25). */
+#define SWL_MAX_SLOTS 128
+#define SWL_OP_O_PROJ 3
+#define SWL_OP_DOWN_PROJ 6
+#define SWL_OP_QKV_FUSED 9
+#define SWL_OP_GATE_UP_FUSED 10
+#define SWL_OP_EMBED 11
+#define SWL_OP_LM_HEAD 12
+#define SWL_OP_SET_SAMPLING 13
+#define SWL_IPC_HANDLE_BYTES 64
+#define SWL_MAX_LORA_BLOCKS 4
+
+/* Thread-local text of the last failure on the calling thread. */
+const char* swl_last_error(void);
+/* ABI version of this library (bumped on any signature/layout change). */
+int swl_abi_version(void);
+/* Number of HIP devices visible (0 on a host without a GPU); never faults. */
+int swl_device_count(void);
+
+/* ============================================================ kernels ====
+ * Stateless, stream-ordered device entry points.  These are the compute path
+ * the runtime entry points below and the Python worker classes call.
+ */
+
+/* Slot gather: packed[off_i + j, :] = slot_in[i][j, :] for j < rows[i], where
+ * off = exclusive prefix sum of rows in the given (ring-arrival) order.
+ * Replaces torch::cat of from_blob slot views, ext_aggregator.cpp:545-551.
+ * slot_in / rows are HOST arrays of n (<= 128) entries; d in elements. */
+int swl_gather_bf16(const void* const* slot_in, const int64_t* rows, int n,
+                    int64_t d, void* packed, void* stream);
+
+/* Slot scatter (+ optional delta add): slot_out[i][j, :] = y[off_i + j, :]
+ * (+ delta[off_i + j, :], added in fp32 and rounded once to bf16).
+ * Replaces the per-slot narrow().copy_() of ext_aggregator.cpp:564-570 and the
+ * worker's `q + q_delta` adds of src/worker/worker_sync.py:276-284.
+ * delta may be NULL.  Host arrays as for swl_gather_bf16. */
+int swl_scatter_add_bf16(const void* y, const void* delta, void* const* slot_out,
+                         const int64_t* rows, int n, int64_t d_out, void* stream);
+
+/* Base projection y[m, n] = x[m, k] . w[n, k]^T (+ bias[n]); bf16 in/out,
+ * fp32 accumulation, one rounding.  m <= 64 runs the skinny MFMA streaming
+ * kernel, larger m the LDS-tiled MFMA kernel.  Replaces
+ * torch::matmul_out(out, x, W.t()) (+ out.add_(bias)), ext_aggregator.cpp:562,
+ * :576-580, :598, :612-616 and the N==1 fast path :506-522.  bias may be NULL.
+ * Requires k % 32 == 0. */
+int swl_gemm_bf16(const void* x, const void* w, const void* bias, void* y,
+                  int64_t m, int64_t n, int64_t k, void* stream);
+
+/* One adapter's weights for one (fused) projection, as the segmented LoRA
+ * kernels read them.  `a` stacks the lora_A matrices of the column blocks:
+ * bf16 [nblk * rank, k] (PEFT lora_A.weight layout [r, in] per block, block j
+ * at rows j*rank..).  b[j] is block j's lora_B.weight, bf16 [blk_cols[j], rank].
+ * delta = scale * (x . a_j^T) . b_j^T, i.e. PEFT's lora_B(lora_A(x)) * scaling
+ * (src/worker/worker_sync.py:305, :375) and FusedLoRA's
+ * (x @ cat(A_i^T * s)) @ blockdiag(B_i^T) (src/worker/model_builder.py:232-262). */
+typedef struct swl_lora_entry {
+  const void* a;
+  const void* b[SWL_MAX_LORA_BLOCKS];
+  int32_t rank;
+  float scale;
+} swl_lora_entry;
+
+/* The fused round: gather -> base GEMM -> (+ per-segment LoRA delta) ->
+ * (+ bias) -> scatter, for n_seg (<= 128) slots in arrival order.
+ *   seg_in[i]  : device [rows[i], k] bf16 (slot input buffer)
+ *   seg_out[i] : device [rows[i], n] bf16 (slot output buffer)
+ *   seg_lora   : HOST [n_seg] index into lora_table (-1 = no adapter); NULL =
+ *                no LoRA at all (the reference's aggregator-only behaviour)
+ *   lora_table : DEVICE array of swl_lora_entry
+ *   nblk / blk_cols : column blocks of the fused output (QKV: 3 blocks
+ *                {q, k, v}; Gate+Up: 2; O / Down: 1); sum(blk_cols) == n.
+ * Equivalent to execute_batched_gemm_slots (ext_aggregator.cpp:470-626)
+ * followed by the worker-side delta add (worker_sync.py:270-389) without the
+ * bf16 rounding of the delta.  Scratch memory is owned by the library. */
+int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
+                   void* const* seg_out, const void* w, const void* bias,
+                   int64_t n, int64_t k, const int32_t* seg_lora,
+                   const swl_lora_entry* lora_table, int nblk,
+                   const int64_t* blk_cols, void* stream);
+
+/* Row-major matrix product with an explicit layout, used by the worker-side
+ * LoRA modules: y[m, n] = alpha * x[m, k] . B where B is b[k, n] (trans_b = 0,
+ * ldb = row stride of b) or b[n, k]^T (trans_b = 1).  fp32 accumulation,
+ * bf16 output rounded once (the rounding torch's bf16 matmul performs).
+ * Replaces the bf16 nn.Linear / `@` products of model_builder.py:261 and
+ * worker_sync.py:305, :375. */
+int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb,
+                    int trans_b, void* y, int64_t ldy, int64_t m, int64_t n,
+                    int64_t k, float alpha, void* stream);
+
+/* Paged-KV attention for one q_len group, replacing
+ * WorkerBatchedOps.batch_flash_attention (worker_sync.py:169-205):
+ *   1. NeoX RoPE in place on q [nseq, q_len, hq, d] and k [nseq, q_len, hkv, d]
+ *      at positions[nseq * q_len] using cos_sin [max_pos, d] (cos | sin halves,
+ *      the cache of paged_attention.py:131-142), when rope != 0;
+ *   2. append k and v into the pages k_cache / v_cache
+ *      [num_blocks, block_size, hkv, d] at cache_seqlens[s] + i through
+ *      block_table [nseq, max_blocks] (int32);
+ *   3. causal GQA attention of each query over cache_seqlens[s] + i + 1 keys,
+ *      scale softmax_scale, written to out [nseq, q_len, hq * d].
+ * d must be 128; hq % hkv == 0; q_len <= 1024. */
+int swl_paged_attention_bf16(void* q, void* k, const void* v, int nseq, int q_len,
+                             int hq, int hkv, int d, void* k_cache, void* v_cache,
+                             int64_t num_blocks, int block_size,
+                             const int32_t* block_table, int64_t max_blocks,
+                             const int32_t* cache_seqlens, const int64_t* positions,
+                             const void* cos_sin, int64_t max_pos, int rope,
+                             float softmax_scale, void* out, void* stream);
+
+/* Zero whole KV pages: cache[block_ids[i], ...] = 0 for i < nblocks, for each
+ * of the ncache caches in `caches` (HOST array of device pointers; block_ids
+ * is a device int64 array, each id < the cache's block count).
+ * Replaces index_fill_(0, blocks, 0) per layer, paged_attention.py:77-89. */
+int swl_zero_blocks_bf16(void* const* caches, int ncache, const int64_t* block_ids,
+                         int64_t nblocks, int64_t block_elems, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWL_H */

@@ -1,0 +1,1239 @@
+// HIP kernels for gfx950 (MI355X) and their stream-ordered C-ABI launchers.
+//
+// Kernels
+//   gather_rows_kernel      slot rows -> packed batch (128-bit copies)
+//   scatter_rows_kernel     packed rows (+ delta) -> slot rows
+//   skinny_kernel<...>      M <= 64 "decode" projection: W streamed from HBM
+//                           straight into MFMA A-fragments, activations read
+//                           through per-token row pointers (the gather is
+//                           fused), split-K across the waves of a workgroup
+//                           with an LDS reduction, and an epilogue that adds
+//                           bias + the LoRA expand and stores each token's row
+//                           into its slot buffer (the scatter is fused).
+//                           The same template in SHRINK mode computes the LoRA
+//                           shrink u = x . A^T for groups of tokens sharing an
+//                           adapter (each adapter's A is read once per round).
+//   tiled_kernel            M > 64 "prefill" projection: 128x128x64 LDS-staged
+//                           MFMA tiles, fp32 accumulation, same epilogue.
+//   matmul_generic_kernel   small row-major products with arbitrary strides
+//                           (worker-side LoRA modules).
+//   rope_append_kernel / attention_kernel   paged-KV decode attention.
+//
+// MFMA used: v_mfma_f32_16x16x32_bf16.  Operand layout (wave64): lane l feeds
+// row (l % 16) of A and column (l % 16) of B with the 8 consecutive k values of
+// k-group (l / 16); the 16x16 fp32 result lands in lane l as rows
+// 4*(l/16)+j, j=0..3, of column (l % 16).  The k-group -> k assignment is the
+// same for A and B, so any consistent assignment of memory k to (group, j)
+// computes the same dot products.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "swl_common.h"
+#include "swl.h"
+
+namespace {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kMaxSeg = SWL_MAX_SLOTS;
+constexpr int kSkinnyMaxTok = 64;
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
+__device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }  // v_cvt_pk_bf16_f32, RNE
+
+__device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
+  bf16x8 b = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = (float)b[i];
+}
+
+// ---------------------------------------------------------------- gather ---
+struct SegPtrs {
+  int32_t n;
+  int32_t vec;                  // 1 = 16-byte path usable
+  int64_t off[kMaxSeg + 1];     // exclusive prefix sum of rows
+  const void* ptr[kMaxSeg];     // per-segment base pointer
+};
+
+__device__ __forceinline__ int find_seg(const int64_t* off, int n, int64_t row) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= row) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// One workgroup per packed row; segment lookup is uniform per workgroup.
+__global__ __launch_bounds__(256) void gather_rows_kernel(SegPtrs sp, int64_t d, bf16* __restrict__ packed) {
+  const int64_t row = blockIdx.x;
+  const int s = find_seg(sp.off, sp.n, row);
+  const bf16* src = reinterpret_cast<const bf16*>(sp.ptr[s]) + (row - sp.off[s]) * d;
+  bf16* dst = packed + row * d;
+  if (sp.vec) {
+    const int64_t nv = d >> 3;
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x)
+      reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(src)[i];
+  } else {
+    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src);
+    uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
+    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) d16[i] = s16[i];
+  }
+}
+
+__global__ __launch_bounds__(256) void scatter_rows_kernel(SegPtrs sp, int64_t d, const bf16* __restrict__ y,
+                                                           const bf16* __restrict__ delta) {
+  const int64_t row = blockIdx.x;
+  const int s = find_seg(sp.off, sp.n, row);
+  bf16* dst = reinterpret_cast<bf16*>(const_cast<void*>(sp.ptr[s])) + (row - sp.off[s]) * d;
+  const bf16* src = y + row * d;
+  const bf16* dl = delta ? delta + row * d : nullptr;
+  if (sp.vec) {
+    const int64_t nv = d >> 3;
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+      u32x4 v = reinterpret_cast<const u32x4*>(src)[i];
+      if (dl) {
+        float a[8], b[8];
+        unpack8(v, a);
+        unpack8(reinterpret_cast<const u32x4*>(dl)[i], b);
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = f2bf(a[j] + b[j]);
+        v = __builtin_bit_cast(u32x4, o);
+      }
+      reinterpret_cast<u32x4*>(dst)[i] = v;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
+      float v = bf2f(src[i]);
+      if (dl) v += bf2f(dl[i]);
+      dst[i] = dl ? f2bf(v) : src[i];
+    }
+  }
+}
+
+// ------------------------------------------------------- LoRA epilogue ----
+// Column blocks of a fused projection output and the LoRA state a round
+// carries into the base kernel's epilogue.
+struct LoraEpi {
+  const swl_lora_entry* table;  // device
+  const float* u;               // [usplit][u_rows][u_ld] fp32 shrink partials
+  int32_t usplit, u_ld;
+  int64_t u_split_stride;       // u_rows * u_ld
+  int32_t nblk;
+  int64_t blk_start[SWL_MAX_LORA_BLOCKS + 1];
+};
+
+__device__ __forceinline__ int find_blk(const LoraEpi L, int64_t n) {
+  int b = 0;
+#pragma unroll
+  for (int i = 1; i < SWL_MAX_LORA_BLOCKS; ++i)
+    if (i < L.nblk && n >= L.blk_start[i]) b = i;
+  return b;
+}
+
+__device__ __forceinline__ int64_t blk_start_of(const LoraEpi L, int b) {
+  int64_t v = 0;
+#pragma unroll
+  for (int i = 0; i <= SWL_MAX_LORA_BLOCKS; ++i)
+    if (i == b) v = L.blk_start[i];
+  return v;
+}
+
+// delta for 4 consecutive output columns (all inside block `blk`, first one at
+// in-block row `nin`) of the token whose shrink row is `urow`:
+// scale * sum_q u[q] * B[nin + j][q].
+__device__ __forceinline__ void lora_delta4(const LoraEpi L, const swl_lora_entry* ep, int urow, int blk,
+                                            int64_t nin, float (&d)[4]) {
+  const int r = ep->rank;
+  const float scale = ep->scale;
+  const bf16* b0 = reinterpret_cast<const bf16*>(ep->b[blk]) + nin * r;
+  const float* up = L.u + (int64_t)urow * L.u_ld + blk * r;
+  d[0] = d[1] = d[2] = d[3] = 0.f;
+  if ((r & 7) == 0) {
+    for (int q = 0; q < r; q += 8) {
+      float uq[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) uq[i] = 0.f;
+      for (int s = 0; s < L.usplit; ++s) {
+        const f32x4* p = reinterpret_cast<const f32x4*>(up + s * L.u_split_stride + q);
+        f32x4 a = p[0], c = p[1];
+        uq[0] += a[0]; uq[1] += a[1]; uq[2] += a[2]; uq[3] += a[3];
+        uq[4] += c[0]; uq[5] += c[1]; uq[6] += c[2]; uq[7] += c[3];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float bv[8];
+        unpack8(ld16(b0 + (int64_t)j * r + q), bv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d[j] += uq[i] * bv[i];
+      }
+    }
+  } else {
+    for (int q = 0; q < r; ++q) {
+      float uq = 0.f;
+      for (int s = 0; s < L.usplit; ++s) uq += up[s * L.u_split_stride + q];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[j] += uq * bf2f(b0[(int64_t)j * r + q]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) d[j] *= scale;
+}
+
+__device__ __forceinline__ float lora_delta1(const LoraEpi L, const swl_lora_entry* ep, int urow, int64_t n) {
+  const int blk = find_blk(L, n);
+  const int r = ep->rank;
+  const bf16* b0 = reinterpret_cast<const bf16*>(ep->b[blk]) + (n - blk_start_of(L, blk)) * r;
+  const float* up = L.u + (int64_t)urow * L.u_ld + blk * r;
+  float d = 0.f;
+  for (int q = 0; q < r; ++q) {
+    float uq = 0.f;
+    for (int s = 0; s < L.usplit; ++s) uq += up[s * L.u_split_stride + q];
+    d += uq * bf2f(b0[q]);
+  }
+  return d * ep->scale;
+}
+
+// Finalise 4 consecutive columns n..n+3 of one token and store them (bf16).
+// lora_idx < 0: no adapter for this token.
+__device__ __forceinline__ void epilogue_store4(float (&v)[4], int64_t n, int64_t N, const bf16* bias,
+                                                const LoraEpi L, int lora_idx, int urow, bf16* yrow) {
+  if (bias) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (n + j < N) v[j] += bf2f(bias[n + j]);
+  }
+  if (lora_idx >= 0) {
+    const swl_lora_entry* ep = L.table + lora_idx;
+    const int blk = find_blk(L, n);
+    const int64_t bs = blk_start_of(L, blk), be = blk_start_of(L, blk + 1);
+    if (n + 3 < N && n + 3 < be) {
+      float d[4];
+      lora_delta4(L, ep, urow, blk, n - bs, d);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += d[j];
+    } else {
+      for (int j = 0; j < 4; ++j)
+        if (n + j < N) v[j] += lora_delta1(L, ep, urow, n + j);
+    }
+  }
+  if (n + 3 < N && ((reinterpret_cast<uintptr_t>(yrow + n) & 7) == 0)) {
+    bf16 o0 = f2bf(v[0]), o1 = f2bf(v[1]), o2 = f2bf(v[2]), o3 = f2bf(v[3]);
+    u32x2 pk;
+    pk[0] = (uint32_t)__builtin_bit_cast(uint16_t, o0) | ((uint32_t)__builtin_bit_cast(uint16_t, o1) << 16);
+    pk[1] = (uint32_t)__builtin_bit_cast(uint16_t, o2) | ((uint32_t)__builtin_bit_cast(uint16_t, o3) << 16);
+    *reinterpret_cast<u32x2*>(yrow + n) = pk;
+  } else {
+    for (int j = 0; j < 4; ++j)
+      if (n + j < N) yrow[n + j] = f2bf(v[j]);
+  }
+}
+
+// ------------------------------------------------------ skinny (M<=64) ----
+struct SkinnyBaseArgs {
+  const bf16* w;          // [N, K]
+  const bf16* bias;       // [N] or null
+  int64_t N, K;
+  int32_t ntok;
+  int32_t has_lora;
+  const bf16* x[kSkinnyMaxTok];   // token input rows (length K)
+  bf16* y[kSkinnyMaxTok];         // token output rows (length N)
+  int32_t lora[kSkinnyMaxTok];    // lora table index per token (-1 none)
+  int32_t urow[kSkinnyMaxTok];    // row of the token in the shrink output
+  LoraEpi L;
+};
+
+struct SkinnyShrinkArgs {
+  const swl_lora_entry* table;
+  float* u;                       // [ksplit][u_rows][u_ld]
+  int64_t K;
+  int32_t u_ld;
+  int64_t u_split_stride;
+  int32_t ngroups;
+  int32_t ksplit;
+  int32_t g_entry[kSkinnyMaxTok];       // lora table index of the group
+  int32_t g_arows[kSkinnyMaxTok];       // rows of the group's stacked A (nblk * rank)
+  int32_t g_tile0[kSkinnyMaxTok + 1];   // prefix sum of 16-row tiles of A per group
+  int32_t g_tok0[kSkinnyMaxTok + 1];    // prefix sum into tok[]
+  int32_t tok[kSkinnyMaxTok];           // u row of each grouped token
+  const bf16* x[kSkinnyMaxTok];         // input row of each grouped token
+};
+
+template <int TT, int U>
+__device__ __forceinline__ void load_batch(u32x4 (&w)[U], u32x4 (&x)[U][TT], const bf16* wp, const bf16* const (&xp)[TT],
+                                           int s) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    w[u] = ld16(wp + 32 * (s + u));
+#pragma unroll
+    for (int t = 0; t < TT; ++t) x[u][t] = ld16(xp[t] + 32 * (s + u));
+  }
+}
+
+template <int TT, int U>
+__device__ __forceinline__ void mma_batch(f32x4 (&acc)[TT], const u32x4 (&w)[U], const u32x4 (&x)[U][TT]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[u], x[u][t], acc[t]);
+}
+
+// Streams `nsteps` k-steps of 32 from wp (one W row per lane) against TT token
+// tiles, double-buffered in registers so one batch is in flight while the
+// previous one feeds the MFMAs.
+template <int TT>
+__device__ __forceinline__ void kloop(f32x4 (&acc)[TT], const bf16* wp, const bf16* const (&xp)[TT], int nsteps) {
+  constexpr int U = (TT <= 2) ? 4 : 2;
+  const int nb = nsteps / U;
+  u32x4 wA[U], xA[U][TT], wB[U], xB[U][TT];
+  if (nb > 0) load_batch<TT, U>(wA, xA, wp, xp, 0);
+  int b = 0;
+  for (; b + 2 <= nb; b += 2) {
+    load_batch<TT, U>(wB, xB, wp, xp, (b + 1) * U);
+    mma_batch<TT, U>(acc, wA, xA);
+    if (b + 2 < nb) load_batch<TT, U>(wA, xA, wp, xp, (b + 2) * U);
+    mma_batch<TT, U>(acc, wB, xB);
+  }
+  if (b < nb) mma_batch<TT, U>(acc, wA, xA);
+  for (int s = nb * U; s < nsteps; ++s) {
+    u32x4 w1 = ld16(wp + 32 * s);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w1, ld16(xp[t] + 32 * s), acc[t]);
+  }
+}
+
+// Base projection for <= 64 tokens.  Workgroup = KW waves over one 16-row tile
+// of W; wave w covers the w-th slice of K.  Grid = ceil(N / 16).
+template <int TT, int KW>
+__global__ __launch_bounds__(KW * 64) void skinny_base_kernel(SkinnyBaseArgs a) {
+  __shared__ f32x4 red[KW][TT][64];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t row0 = (int64_t)blockIdx.x * 16;
+  const int64_t wrow = (row0 + (lane & 15) < a.N) ? row0 + (lane & 15) : a.N - 1;
+  const int nsteps_all = (int)(a.K >> 5);
+  const int s0 = (nsteps_all * wv) / KW, s1 = (nsteps_all * (wv + 1)) / KW;
+  const int koff = s0 * 32 + 8 * (lane >> 4);
+
+  const bf16* wp = a.w + wrow * a.K + koff;
+  const bf16* xp[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    int tok = 16 * t + (lane & 15);
+    tok = tok < a.ntok ? tok : 0;
+    xp[t] = a.x[tok] + koff;
+  }
+  f32x4 acc[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  kloop<TT>(acc, wp, xp, s1 - s0);
+
+#pragma unroll
+  for (int t = 0; t < TT; ++t) red[wv][t][lane] = acc[t];
+  __syncthreads();
+  for (int t = wv; t < TT; t += KW) {
+    f32x4 s = red[0][t][lane];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) s += red[w][t][lane];
+    const int tok = 16 * t + (lane & 15);
+    if (tok >= a.ntok) continue;
+    const int64_t n = row0 + 4 * (lane >> 4);
+    if (n >= a.N) continue;
+    float v[4] = {s[0], s[1], s[2], s[3]};
+    epilogue_store4(v, n, a.N, a.bias, a.L, a.has_lora ? a.lora[tok] : -1, a.urow[tok], a.y[tok]);
+  }
+}
+
+// LoRA shrink u[token, q] = x[token] . A[q]^T for groups of tokens that share
+// an adapter.  Grid = (total A tiles, ksplit); workgroup = KW waves that split
+// the k-split's range.  Output is one fp32 partial per k-split (the base
+// epilogue sums them), so no atomics and no clearing are needed.
+template <int TT, int KW>
+__global__ __launch_bounds__(KW * 64) void skinny_shrink_kernel(SkinnyShrinkArgs a) {
+  __shared__ f32x4 red[KW][TT][64];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int tile = blockIdx.x;
+  const int ks = blockIdx.y;
+  int g = 0;
+  while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
+  const bf16* amat = reinterpret_cast<const bf16*>(a.table[a.g_entry[g]].a);
+  const int rt = tile - a.g_tile0[g];
+  const int t0 = a.g_tok0[g], tcount = a.g_tok0[g + 1] - t0;
+
+  const int64_t klen = a.K / a.ksplit;
+  const int64_t kbeg = klen * ks;
+  const int nsteps_all = (int)(klen >> 5);
+  const int s0 = (nsteps_all * wv) / KW, s1 = (nsteps_all * (wv + 1)) / KW;
+  const int64_t koff = kbeg + s0 * 32 + 8 * (lane >> 4);
+
+  // rows past the stacked A (last tile of a rank that is not a multiple of
+  // 16) re-read the last row; their u columns are never consumed.
+  const int arow = min(rt * 16 + (lane & 15), a.g_arows[g] - 1);
+  const bf16* wp = amat + (int64_t)arow * a.K + koff;
+  const bf16* xp[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    int i = 16 * t + (lane & 15);
+    i = i < tcount ? i : 0;
+    xp[t] = a.x[t0 + i] + koff;
+  }
+  f32x4 acc[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  kloop<TT>(acc, wp, xp, s1 - s0);
+
+#pragma unroll
+  for (int t = 0; t < TT; ++t) red[wv][t][lane] = acc[t];
+  __syncthreads();
+  for (int t = wv; t < TT; t += KW) {
+    f32x4 s = red[0][t][lane];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) s += red[w][t][lane];
+    const int i = 16 * t + (lane & 15);
+    if (i >= tcount) continue;
+    const int q = rt * 16 + 4 * (lane >> 4);
+    float* dst = a.u + ks * a.u_split_stride + (int64_t)a.tok[t0 + i] * a.u_ld + q;
+    *reinterpret_cast<f32x4*>(dst) = s;
+  }
+}
+
+// ------------------------------------------------------- tiled (M>64) -----
+// y[m, n] = sum_k x[m, k] w[n, k] for a packed x [M, K]; rows of y go to the
+// segment (slot) the packed row belongs to.  128x128 output tile per
+// workgroup (4 waves in 2x2, 64x64 each = 4x4 MFMA tiles), BK = 64 staged in
+// LDS with a register prefetch of the next stage.
+constexpr int TM = 128, TN = 128, TK = 64, TPAD = 8;
+
+struct TiledArgs {
+  const bf16* x;          // packed [M, K]
+  const bf16* w;          // [N, K]
+  const bf16* bias;
+  int64_t M, N, K;
+  int32_t has_lora;
+  // output: either dense y (ldy) or per-segment rows
+  bf16* y;                // dense output if non-null
+  int64_t ldy;
+  SegPtrs out;            // per-segment output base pointers (row stride N)
+  int32_t seg_lora[kMaxSeg];
+  LoraEpi L;              // u rows are packed rows
+};
+
+__global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2][TM][TK + TPAD];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2][TN][TK + TPAD];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * TM;
+  const int64_t n0 = (int64_t)blockIdx.x * TN;
+
+  // global -> LDS mapping: 8 threads per row (8 x 16 B = 128 B = TK bf16),
+  // 32 rows per pass, 4 passes per 128-row tile.
+  const int lr = tid >> 3, lc = (tid & 7) * 8;
+  const bf16* xg[4];
+  const bf16* wg[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int64_t mr = (m0 + lr + 32 * p < a.M) ? m0 + lr + 32 * p : a.M - 1;
+    const int64_t nr = (n0 + lr + 32 * p < a.N) ? n0 + lr + 32 * p : a.N - 1;
+    xg[p] = a.x + mr * a.K + lc;
+    wg[p] = a.w + nr * a.K + lc;
+  }
+  u32x4 ra[4], rb[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) { ra[p] = ld16(xg[p]); rb[p] = ld16(wg[p]); }
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)(a.K / TK);
+  int buf = 0;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    *reinterpret_cast<u32x4*>(&As[0][lr + 32 * p][lc]) = ra[p];
+    *reinterpret_cast<u32x4*>(&Bs[0][lr + 32 * p][lc]) = rb[p];
+  }
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        ra[p] = ld16(xg[p] + (int64_t)(kt + 1) * TK);
+        rb[p] = ld16(wg[p] + (int64_t)(kt + 1) * TK);
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < TK / 32; ++ks) {
+      u32x4 fa[4], fb[4];
+      const int kc = ks * 32 + 8 * (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        fa[i] = *reinterpret_cast<const u32x4*>(&As[buf][wm * 64 + i * 16 + (lane & 15)][kc]);
+        fb[i] = *reinterpret_cast<const u32x4*>(&Bs[buf][wn * 64 + i * 16 + (lane & 15)][kc]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) {
+      const int nb = buf ^ 1;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        *reinterpret_cast<u32x4*>(&As[nb][lr + 32 * p][lc]) = ra[p];
+        *reinterpret_cast<u32x4*>(&Bs[nb][lr + 32 * p][lc]) = rb[p];
+      }
+      __syncthreads();
+      buf = nb;
+    }
+  }
+
+  // Epilogue.  acc[i][j] lane l holds rows (tokens) m0+wm*64+i*16+4*(l/16)+r,
+  // column n0+wn*64+j*16+(l%16).  Transpose through LDS so each lane owns 4
+  // consecutive columns of one token (8-byte stores, shared epilogue).
+  __syncthreads();
+  float* ct = reinterpret_cast<float*>(&As[0][0][0]);  // reuse: 64x(64+4) floats per wave pass
+  // Each wave handles its own 64x64 sub-tile in 4 passes of 16 tokens.
+  constexpr int CLD = 64 + 4;
+  float* cw = ct + wv * 16 * CLD;  // 16 tokens x 64 columns per wave per pass
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) cw[(4 * (lane >> 4) + r) * CLD + j * 16 + (lane & 15)] = acc[i][j][r];
+    __syncthreads();
+    // lane -> (token = lane / 4 ... ) 16 tokens x 16 column-quads = 256 items, 4 per lane
+    for (int it = 0; it < 4; ++it) {
+      const int item = lane + 64 * it;
+      const int tk = item >> 4;          // 0..15
+      const int cq = (item & 15) * 4;    // 0..60
+      const int64_t m = m0 + wm * 64 + i * 16 + tk;
+      const int64_t n = n0 + wn * 64 + cq;
+      if (m >= a.M || n >= a.N) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = cw[tk * CLD + cq + r];
+      bf16* yrow;
+      int lidx = -1;
+      if (a.y) {
+        yrow = a.y + m * a.ldy;
+      } else {
+        const int s = find_seg(a.out.off, a.out.n, m);
+        yrow = reinterpret_cast<bf16*>(const_cast<void*>(a.out.ptr[s])) + (m - a.out.off[s]) * a.N;
+        lidx = a.has_lora ? a.seg_lora[s] : -1;
+      }
+      epilogue_store4(v, n, a.N, a.bias, a.L, lidx, (int)m, yrow);
+    }
+    __syncthreads();
+  }
+}
+
+// ----------------------------------------------- generic small matmul -----
+// y[m, n] = alpha * sum_k x[m, k] * B(k, n), B(k, n) = b[k*ldb + n] (nn) or
+// b[n*ldb + k] (nt).  Workgroup: 64 columns x 4 k-partitions, LDS reduce.
+__global__ __launch_bounds__(256) void matmul_generic_kernel(const bf16* __restrict__ x, int64_t ldx,
+                                                             const bf16* __restrict__ b, int64_t ldb, int trans_b,
+                                                             bf16* __restrict__ y, int64_t ldy, int64_t N, int64_t K,
+                                                             float alpha) {
+  __shared__ float part[4][64];
+  const int c = threadIdx.x & 63, p = threadIdx.x >> 6;
+  const int64_t m = blockIdx.y;
+  const int64_t n = (int64_t)blockIdx.x * 64 + c;
+  float s = 0.f;
+  if (n < N) {
+    const bf16* xr = x + m * ldx;
+    if (!trans_b) {
+      for (int64_t k = p; k < K; k += 4) s += bf2f(xr[k]) * bf2f(b[k * ldb + n]);
+    } else {
+      const bf16* br = b + n * ldb;
+      for (int64_t k = p; k < K; k += 4) s += bf2f(xr[k]) * bf2f(br[k]);
+    }
+  }
+  part[p][c] = s;
+  __syncthreads();
+  if (p == 0 && n < N) {
+    float t = part[0][c] + part[1][c] + part[2][c] + part[3][c];
+    y[m * ldy + n] = f2bf(alpha * t);
+  }
+}
+
+// ------------------------------------------------------ paged attention ---
+struct AttnArgs {
+  bf16* q;               // [nseq, L, hq, 128]
+  bf16* k;               // [nseq, L, hkv, 128]
+  const bf16* v;         // [nseq, L, hkv, 128]
+  bf16* kc;              // [num_blocks, bs, hkv, 128]
+  bf16* vc;
+  const int32_t* bt;     // [nseq, max_blocks]
+  const int32_t* seqlens;
+  const int64_t* pos;    // [nseq * L]
+  const bf16* cs;        // [max_pos, 128]
+  bf16* out;             // [nseq, L, hq*128]
+  int64_t num_blocks, max_blocks, max_pos;
+  int32_t nseq, L, hq, hkv, bs, rope;
+  float scale;
+};
+
+// NeoX rotation of q and k at their positions, then k/v appended to the pages.
+// One workgroup per (sequence, new token); 64 threads per head-pair loop.
+__global__ __launch_bounds__(256) void rope_append_kernel(AttnArgs a) {
+  const int tokid = blockIdx.x;  // s * L + i
+  const int s = tokid / a.L, i = tokid % a.L;
+  const int64_t pos = a.rope ? a.pos[tokid] : 0;
+  const bool do_rope = a.rope && pos >= 0 && pos < a.max_pos;
+  const bf16* cs = a.cs + (do_rope ? pos : 0) * 128;
+  const int nh = a.hq + a.hkv;
+  for (int it = threadIdx.x; it < nh * 64; it += blockDim.x) {
+    const int h = it >> 6, d = it & 63;
+    bf16* base = (h < a.hq) ? a.q + ((int64_t)tokid * a.hq + h) * 128
+                            : a.k + ((int64_t)tokid * a.hkv + (h - a.hq)) * 128;
+    if (do_rope) {
+      const float c = bf2f(cs[d]), sn = bf2f(cs[64 + d]);
+      const float x1 = bf2f(base[d]), x2 = bf2f(base[d + 64]);
+      base[d] = f2bf(x1 * c - x2 * sn);
+      base[d + 64] = f2bf(x2 * c + x1 * sn);
+    }
+  }
+  __syncthreads();
+  const int64_t p = (int64_t)a.seqlens[s] + i;
+  const int64_t blk_i = p / a.bs;
+  if (p < 0 || blk_i >= a.max_blocks) return;
+  const int32_t blk = a.bt[(int64_t)s * a.max_blocks + blk_i];
+  if (blk < 0 || blk >= a.num_blocks) return;
+  const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * a.hkv * 128;
+  const int64_t src = (int64_t)tokid * a.hkv * 128;
+  for (int e = threadIdx.x; e < a.hkv * 16; e += blockDim.x) {
+    reinterpret_cast<u32x4*>(a.kc + dst)[e] = reinterpret_cast<const u32x4*>(a.k + src)[e];
+    reinterpret_cast<u32x4*>(a.vc + dst)[e] = reinterpret_cast<const u32x4*>(a.v + src)[e];
+  }
+}
+
+// Attention of one query token over its causal context for one kv head and
+// its G = hq / hkv query heads.  Workgroup = 4 waves; each 16-lane quarter of
+// a wave owns one key at a time (lane holds 8 of the 128 dims), so a wave
+// consumes 4 keys per step and the workgroup 16 keys (one page) per step.
+// Online softmax per quarter; quarters are merged through LDS at the end.
+template <int G>
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+  const int h = blockIdx.x;       // kv head
+  const int i = blockIdx.y;       // query index within the group
+  const int s = blockIdx.z;       // sequence
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int quarter = tid >> 4;   // 0..15 across the workgroup
+  const int dl = (lane & 15) * 8; // this lane's 8 dims
+  const int64_t ctx = (int64_t)a.seqlens[s] + i + 1;
+
+  float qv[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const bf16* qp = a.q + (((int64_t)s * a.L + i) * a.hq + h * G + g) * 128 + dl;
+    unpack8(ld16(qp), qv[g]);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) qv[g][d] *= a.scale;
+  }
+  float mx[G], sm[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mx[g] = -INFINITY;
+    sm[g] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.f;
+  }
+  const int32_t* bt = a.bt + (int64_t)s * a.max_blocks;
+  const int64_t rowstride = (int64_t)a.hkv * 128;
+  for (int64_t key = quarter; key < ctx; key += 16) {
+    const int64_t bi = key / a.bs;
+    int32_t blk = (bi < a.max_blocks) ? bt[bi] : -1;
+    if (blk < 0 || blk >= a.num_blocks) continue;
+    const int64_t off = ((int64_t)blk * a.bs + key % a.bs) * rowstride + h * 128 + dl;
+    float kv[8], vv[8];
+    unpack8(ld16(a.kc + off), kv);
+    unpack8(ld16(a.vc + off), vv);
+    float sc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float t = 0.f;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) t += qv[g][d] * kv[d];
+      sc[g] = t;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) sc[g] += __shfl_xor(sc[g], o, 16);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float nm = fmaxf(mx[g], sc[g]);
+      const float corr = __expf(mx[g] - nm);
+      const float p = __expf(sc[g] - nm);
+      sm[g] = sm[g] * corr + p;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[g][d] = acc[g][d] * corr + p * vv[d];
+      mx[g] = nm;
+    }
+  }
+  // merge the 16 quarters
+  __shared__ float smx[16][G], ssm[16][G];
+  __shared__ float sacc[16][G][128];
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) { smx[quarter][g] = mx[g]; ssm[quarter][g] = sm[g]; }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) sacc[quarter][g][dl + d] = acc[g][d];
+  __syncthreads();
+  for (int it = tid; it < G * 128; it += 256) {
+    const int g = it >> 7, d = it & 127;
+    float m = -INFINITY;
+    for (int qq = 0; qq < 16; ++qq) m = fmaxf(m, smx[qq][g]);
+    float l = 0.f, o = 0.f;
+    if (m != -INFINITY) {
+      for (int qq = 0; qq < 16; ++qq) {
+        const float c = (smx[qq][g] == -INFINITY) ? 0.f : __expf(smx[qq][g] - m);
+        l += ssm[qq][g] * c;
+        o += sacc[qq][g][d] * c;
+      }
+    }
+    const float r = (l > 0.f) ? o / l : 0.f;
+    a.out[(((int64_t)s * a.L + i) * a.hq + h * G + g) * 128 + d] = f2bf(r);
+  }
+}
+
+__global__ void zero_blocks_kernel(bf16* cache, const int64_t* ids, int64_t nblocks, int64_t block_elems) {
+  const int64_t b = blockIdx.x;
+  if (b >= nblocks) return;
+  u32x4* p = reinterpret_cast<u32x4*>(cache + ids[b] * block_elems);
+  const int64_t nv = block_elems >> 3;
+  for (int64_t e = threadIdx.x; e < nv; e += blockDim.x) p[e] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// --------------------------------------------------- library scratch ------
+// One growable device scratch area per device, used for the LoRA shrink
+// partials and the packed activations of the prefill path.  Growth calls
+// hipMalloc and is refused while the stream is being captured.
+struct Scratch {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_scratch_mu;
+std::vector<Scratch> g_scratch;
+
+int scratch_get(size_t need, hipStream_t stream, void** out) {
+  int dev = 0;
+  SWL_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if ((int)g_scratch.size() <= dev) g_scratch.resize(dev + 1);
+  Scratch& s = g_scratch[dev];
+  if (s.bytes < need) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (stream) SWL_HIP(hipStreamIsCapturing(stream, &cs));
+    SWL_CHECK(cs == hipStreamCaptureStatusNone, SWL_ERR_STATE,
+              "scratch must grow outside graph capture (run the call once before capturing)");
+    if (s.ptr) {
+      SWL_HIP(hipDeviceSynchronize());
+      SWL_HIP(hipFree(s.ptr));
+      s.ptr = nullptr;
+      s.bytes = 0;
+    }
+    size_t nb = std::max(need, (size_t)1 << 20);
+    nb = (nb + 4095) & ~(size_t)4095;
+    SWL_HIP(hipMalloc(&s.ptr, nb));
+    s.bytes = nb;
+  }
+  *out = s.ptr;
+  return SWL_OK;
+}
+
+// -------------------------------------------------------------- launchers
+int fill_segptrs(SegPtrs& sp, const void* const* ptrs, const int64_t* rows, int n, int64_t d, int64_t* total) {
+  SWL_CHECK(n >= 1 && n <= kMaxSeg, SWL_ERR_INVALID, "segment count must be in [1, 128]");
+  SWL_CHECK(d > 0, SWL_ERR_INVALID, "row length must be positive");
+  sp.n = n;
+  sp.off[0] = 0;
+  bool vec = (d % 8) == 0;
+  for (int i = 0; i < n; ++i) {
+    SWL_CHECK(rows[i] >= 0, SWL_ERR_INVALID, "segment rows must be >= 0");
+    SWL_CHECK(rows[i] == 0 || ptrs[i] != nullptr, SWL_ERR_INVALID, "null segment pointer");
+    sp.off[i + 1] = sp.off[i] + rows[i];
+    sp.ptr[i] = ptrs[i];
+    if ((reinterpret_cast<uintptr_t>(ptrs[i]) & 15) != 0) vec = false;
+  }
+  sp.vec = vec ? 1 : 0;
+  *total = sp.off[n];
+  return SWL_OK;
+}
+
+template <int TT>
+int launch_skinny_base_tt(const SkinnyBaseArgs& a, int kw, hipStream_t st) {
+  const dim3 grid((unsigned)((a.N + 15) / 16));
+  switch (kw) {
+    case 4: hipLaunchKernelGGL((skinny_base_kernel<TT, 4>), grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((skinny_base_kernel<TT, 8>), grid, dim3(512), 0, st, a); break;
+    default: hipLaunchKernelGGL((skinny_base_kernel<TT, 16>), grid, dim3(1024), 0, st, a); break;
+  }
+  SWL_LAUNCH_CHECK("skinny_base_kernel launch");
+  return SWL_OK;
+}
+
+int launch_skinny_base(const SkinnyBaseArgs& a, hipStream_t st) {
+  const int tt = (a.ntok + 15) / 16;
+  // Waves per workgroup: enough workgroups to cover the chip, and each wave
+  // keeps >= 8 k-steps so its loads stay pipelined.
+  const int64_t tiles = (a.N + 15) / 16;
+  const int64_t ksteps = a.K / 32;
+  int kw = 8;
+  if (tiles < 512 && ksteps >= 16 * 16) kw = 16;
+  if (ksteps < 8 * 8) kw = 4;
+  switch (tt) {
+    case 1: return launch_skinny_base_tt<1>(a, kw, st);
+    case 2: return launch_skinny_base_tt<2>(a, kw, st);
+    case 3: return launch_skinny_base_tt<3>(a, kw, st);
+    default: return launch_skinny_base_tt<4>(a, kw, st);
+  }
+}
+
+template <int TT>
+int launch_skinny_shrink_tt(const SkinnyShrinkArgs& a, int tiles, hipStream_t st) {
+  const dim3 grid((unsigned)tiles, (unsigned)a.ksplit);
+  hipLaunchKernelGGL((skinny_shrink_kernel<TT, 8>), grid, dim3(512), 0, st, a);
+  SWL_LAUNCH_CHECK("skinny_shrink_kernel launch");
+  return SWL_OK;
+}
+
+int launch_skinny_shrink(const SkinnyShrinkArgs& a, int tiles, int max_group_tok, hipStream_t st) {
+  const int tt = (max_group_tok + 15) / 16;
+  switch (tt) {
+    case 1: return launch_skinny_shrink_tt<1>(a, tiles, st);
+    case 2: return launch_skinny_shrink_tt<2>(a, tiles, st);
+    case 3: return launch_skinny_shrink_tt<3>(a, tiles, st);
+    default: return launch_skinny_shrink_tt<4>(a, tiles, st);
+  }
+}
+
+}  // namespace
+
+// ================================================================ C ABI ===
+namespace swl {
+thread_local std::string t_err;
+void set_error(const std::string& msg) { t_err = msg; }
+const std::string& last_error() { return t_err; }
+int fail(int code, const std::string& msg) {
+  t_err = msg;
+  return code;
+}
+int hip_fail(hipError_t e, const char* where) {
+  t_err = std::string("CUDA error: ") + hipGetErrorString(e) + " (" + where + ")";
+  return SWL_ERR_HIP;
+}
+
+// Round planning shared with the aggregator runtime: builds and launches the
+// shrink + base kernels for n_seg segments given host-side lora metadata.
+int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
+                 const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
+                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st);
+}  // namespace swl
+
+extern "C" {
+
+const char* swl_last_error(void) { return swl::last_error().c_str(); }
+int swl_abi_version(void) { return 1; }
+int swl_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int swl_gather_bf16(const void* const* slot_in, const int64_t* rows, int n, int64_t d, void* packed, void* stream) {
+  SWL_CHECK(slot_in && rows && packed, SWL_ERR_INVALID, "swl_gather_bf16: null argument");
+  SegPtrs sp;
+  int64_t total = 0;
+  int rc = fill_segptrs(sp, slot_in, rows, n, d, &total);
+  if (rc) return rc;
+  if ((reinterpret_cast<uintptr_t>(packed) & 15) != 0) sp.vec = 0;
+  if (total == 0) return SWL_OK;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, sp, d,
+                     reinterpret_cast<bf16*>(packed));
+  SWL_LAUNCH_CHECK("gather_rows_kernel launch");
+  return SWL_OK;
+}
+
+int swl_scatter_add_bf16(const void* y, const void* delta, void* const* slot_out, const int64_t* rows, int n,
+                         int64_t d_out, void* stream) {
+  SWL_CHECK(y && slot_out && rows, SWL_ERR_INVALID, "swl_scatter_add_bf16: null argument");
+  SegPtrs sp;
+  int64_t total = 0;
+  int rc = fill_segptrs(sp, reinterpret_cast<const void* const*>(slot_out), rows, n, d_out, &total);
+  if (rc) return rc;
+  if ((reinterpret_cast<uintptr_t>(y) & 15) != 0) sp.vec = 0;
+  if (delta && (reinterpret_cast<uintptr_t>(delta) & 15) != 0) sp.vec = 0;
+  if (total == 0) return SWL_OK;
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, sp, d_out,
+                     reinterpret_cast<const bf16*>(y), reinterpret_cast<const bf16*>(delta));
+  SWL_LAUNCH_CHECK("scatter_rows_kernel launch");
+  return SWL_OK;
+}
+
+int swl_gemm_bf16(const void* x, const void* w, const void* bias, void* y, int64_t m, int64_t n, int64_t k,
+                  void* stream) {
+  SWL_CHECK(x && w && y, SWL_ERR_INVALID, "swl_gemm_bf16: null argument");
+  SWL_CHECK(m >= 0 && n > 0 && k > 0, SWL_ERR_INVALID, "swl_gemm_bf16: bad shape");
+  SWL_CHECK(k % 32 == 0, SWL_ERR_INVALID, "swl_gemm_bf16: k must be a multiple of 32");
+  SWL_CHECK((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
+            SWL_ERR_INVALID, "swl_gemm_bf16: x and w must be 16-byte aligned");
+  if (m == 0) return SWL_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (m <= kSkinnyMaxTok) {
+    SkinnyBaseArgs a{};
+    a.w = reinterpret_cast<const bf16*>(w);
+    a.bias = reinterpret_cast<const bf16*>(bias);
+    a.N = n;
+    a.K = k;
+    a.ntok = (int)m;
+    a.has_lora = 0;
+    for (int i = 0; i < m; ++i) {
+      a.x[i] = reinterpret_cast<const bf16*>(x) + (int64_t)i * k;
+      a.y[i] = reinterpret_cast<bf16*>(y) + (int64_t)i * n;
+      a.lora[i] = -1;
+      a.urow[i] = 0;
+    }
+    return launch_skinny_base(a, st);
+  }
+  SWL_CHECK(k % TK == 0, SWL_ERR_INVALID, "swl_gemm_bf16: k must be a multiple of 64 for m > 64");
+  TiledArgs a{};
+  a.x = reinterpret_cast<const bf16*>(x);
+  a.w = reinterpret_cast<const bf16*>(w);
+  a.bias = reinterpret_cast<const bf16*>(bias);
+  a.M = m;
+  a.N = n;
+  a.K = k;
+  a.y = reinterpret_cast<bf16*>(y);
+  a.ldy = n;
+  a.has_lora = 0;
+  const dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM));
+  hipLaunchKernelGGL(tiled_kernel, grid, dim3(256), 0, st, a);
+  SWL_LAUNCH_CHECK("tiled_kernel launch");
+  return SWL_OK;
+}
+
+int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
+                   const void* bias, int64_t n, int64_t k, const int32_t* seg_lora, const swl_lora_entry* lora_table,
+                   int nblk, const int64_t* blk_cols, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  std::vector<swl_lora_entry> host_entries;
+  if (seg_lora) {
+    SWL_CHECK(lora_table != nullptr, SWL_ERR_INVALID, "swl_round_bf16: seg_lora given without lora_table");
+    SWL_CHECK(n_seg >= 1 && n_seg <= kMaxSeg, SWL_ERR_INVALID, "segment count must be in [1, 128]");
+    int maxi = -1;
+    for (int i = 0; i < n_seg; ++i) maxi = std::max(maxi, (int)seg_lora[i]);
+    if (maxi >= 0) {
+      host_entries.resize(maxi + 1);
+      SWL_HIP(hipMemcpy(host_entries.data(), lora_table, sizeof(swl_lora_entry) * (maxi + 1),
+                        hipMemcpyDeviceToHost));
+    }
+  }
+  return swl::round_launch(n_seg, rows, seg_in, seg_out, w, bias, n, k, seg_lora, lora_table,
+                           host_entries.empty() ? nullptr : host_entries.data(), nblk, blk_cols, st);
+}
+
+int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int trans_b, void* y, int64_t ldy,
+                    int64_t m, int64_t n, int64_t k, float alpha, void* stream) {
+  SWL_CHECK(x && b && y, SWL_ERR_INVALID, "swl_matmul_bf16: null argument");
+  SWL_CHECK(m >= 0 && n > 0 && k > 0, SWL_ERR_INVALID, "swl_matmul_bf16: bad shape");
+  SWL_CHECK(m <= 65535, SWL_ERR_INVALID, "swl_matmul_bf16: m too large");
+  if (m == 0) return SWL_OK;
+  hipLaunchKernelGGL(matmul_generic_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)m), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const bf16*>(x), ldx, reinterpret_cast<const bf16*>(b),
+                     ldb, trans_b, reinterpret_cast<bf16*>(y), ldy, n, k, alpha);
+  SWL_LAUNCH_CHECK("matmul_generic_kernel launch");
+  return SWL_OK;
+}
+
+int swl_paged_attention_bf16(void* q, void* k, const void* v, int nseq, int q_len, int hq, int hkv, int d,
+                             void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+                             const int32_t* block_table, int64_t max_blocks, const int32_t* cache_seqlens,
+                             const int64_t* positions, const void* cos_sin, int64_t max_pos, int rope,
+                             float softmax_scale, void* out, void* stream) {
+  SWL_CHECK(q && k && v && k_cache && v_cache && block_table && cache_seqlens && out, SWL_ERR_INVALID,
+            "swl_paged_attention_bf16: null argument");
+  SWL_CHECK(d == 128, SWL_ERR_INVALID, "swl_paged_attention_bf16: head_dim must be 128");
+  SWL_CHECK(hq > 0 && hkv > 0 && hq % hkv == 0, SWL_ERR_INVALID, "swl_paged_attention_bf16: bad head counts");
+  const int G = hq / hkv;
+  SWL_CHECK(G == 1 || G == 2 || G == 4 || G == 8, SWL_ERR_INVALID,
+            "swl_paged_attention_bf16: hq / hkv must be 1, 2, 4 or 8");
+  SWL_CHECK(nseq >= 0 && q_len >= 1 && q_len <= 1024, SWL_ERR_INVALID, "swl_paged_attention_bf16: bad q_len");
+  SWL_CHECK(block_size > 0 && num_blocks > 0 && max_blocks > 0, SWL_ERR_INVALID,
+            "swl_paged_attention_bf16: bad page geometry");
+  SWL_CHECK(!rope || (cos_sin && positions && max_pos > 0), SWL_ERR_INVALID,
+            "swl_paged_attention_bf16: rope needs positions and cos_sin");
+  if (nseq == 0) return SWL_OK;
+  AttnArgs a{};
+  a.q = reinterpret_cast<bf16*>(q);
+  a.k = reinterpret_cast<bf16*>(k);
+  a.v = reinterpret_cast<const bf16*>(v);
+  a.kc = reinterpret_cast<bf16*>(k_cache);
+  a.vc = reinterpret_cast<bf16*>(v_cache);
+  a.bt = block_table;
+  a.seqlens = cache_seqlens;
+  a.pos = positions;
+  a.cs = reinterpret_cast<const bf16*>(cos_sin);
+  a.out = reinterpret_cast<bf16*>(out);
+  a.num_blocks = num_blocks;
+  a.max_blocks = max_blocks;
+  a.max_pos = max_pos;
+  a.nseq = nseq;
+  a.L = q_len;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.bs = block_size;
+  a.rope = rope;
+  a.scale = softmax_scale;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(nseq * q_len)), dim3(256), 0, st, a);
+  SWL_LAUNCH_CHECK("rope_append_kernel launch");
+  const dim3 grid((unsigned)hkv, (unsigned)q_len, (unsigned)nseq);
+  switch (G) {
+    case 1: hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(256), 0, st, a); break;
+  }
+  SWL_LAUNCH_CHECK("attention_kernel launch");
+  return SWL_OK;
+}
+
+int swl_zero_blocks_bf16(void* const* caches, int ncache, const int64_t* block_ids, int64_t nblocks,
+                         int64_t block_elems, void* stream) {
+  SWL_CHECK(caches && block_ids, SWL_ERR_INVALID, "swl_zero_blocks_bf16: null argument");
+  SWL_CHECK(block_elems % 8 == 0, SWL_ERR_INVALID, "swl_zero_blocks_bf16: block size must be a multiple of 8");
+  if (nblocks == 0) return SWL_OK;
+  for (int c = 0; c < ncache; ++c) {
+    hipLaunchKernelGGL(zero_blocks_kernel, dim3((unsigned)nblocks), dim3(256), 0, (hipStream_t)stream,
+                       reinterpret_cast<bf16*>(caches[c]), block_ids, nblocks, block_elems);
+    SWL_LAUNCH_CHECK("zero_blocks_kernel launch");
+  }
+  return SWL_OK;
+}
+
+}  // extern "C"
+
+// ======================================================== round planner ===
+namespace swl {
+
+int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
+                 const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
+                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st) {
+  SWL_CHECK(rows && seg_in && seg_out && w, SWL_ERR_INVALID, "round: null argument");
+  SWL_CHECK(n_seg >= 1 && n_seg <= kMaxSeg, SWL_ERR_INVALID, "round: segment count must be in [1, 128]");
+  SWL_CHECK(N > 0 && K > 0 && K % 32 == 0, SWL_ERR_INVALID, "round: K must be a positive multiple of 32");
+  SWL_CHECK((reinterpret_cast<uintptr_t>(w) & 15) == 0, SWL_ERR_INVALID, "round: weight must be 16-byte aligned");
+  int64_t T = 0;
+  for (int i = 0; i < n_seg; ++i) {
+    SWL_CHECK(rows[i] >= 0, SWL_ERR_INVALID, "round: negative row count");
+    SWL_CHECK(rows[i] == 0 || (seg_in[i] && seg_out[i]), SWL_ERR_INVALID, "round: null slot buffer");
+    SWL_CHECK((reinterpret_cast<uintptr_t>(seg_in[i]) & 15) == 0, SWL_ERR_INVALID,
+              "round: slot input must be 16-byte aligned");
+    T += rows[i];
+  }
+  if (T == 0) return SWL_OK;
+
+  // LoRA planning.
+  bool has_lora = false;
+  LoraEpi L{};
+  if (seg_lora) {
+    SWL_CHECK(nblk >= 1 && nblk <= SWL_MAX_LORA_BLOCKS, SWL_ERR_INVALID, "round: nblk must be in [1, 4]");
+    SWL_CHECK(blk_cols != nullptr, SWL_ERR_INVALID, "round: blk_cols required with LoRA");
+    L.nblk = nblk;
+    L.blk_start[0] = 0;
+    for (int b = 0; b < nblk; ++b) {
+      SWL_CHECK(blk_cols[b] > 0, SWL_ERR_INVALID, "round: column blocks must be positive");
+      L.blk_start[b + 1] = L.blk_start[b] + blk_cols[b];
+    }
+    for (int b = nblk + 1; b <= SWL_MAX_LORA_BLOCKS; ++b) L.blk_start[b] = L.blk_start[nblk];
+    SWL_CHECK(L.blk_start[nblk] == N, SWL_ERR_INVALID, "round: column blocks must sum to N");
+    for (int i = 0; i < n_seg; ++i)
+      if (seg_lora[i] >= 0 && rows[i] > 0) has_lora = true;
+    L.table = lora_table;
+  }
+
+  int max_r = 0;
+  if (has_lora) {
+    SWL_CHECK(host_entries != nullptr, SWL_ERR_INVALID, "round: missing adapter metadata");
+    for (int i = 0; i < n_seg; ++i) {
+      if (seg_lora[i] < 0 || rows[i] == 0) continue;
+      const swl_lora_entry& e = host_entries[seg_lora[i]];
+      SWL_CHECK(e.a != nullptr && e.rank > 0 && e.rank <= 256, SWL_ERR_INVALID, "round: bad adapter entry");
+      for (int b = 0; b < nblk; ++b) SWL_CHECK(e.b[b] != nullptr, SWL_ERR_INVALID, "round: adapter missing lora_B");
+      max_r = std::max(max_r, (int)e.rank);
+    }
+  }
+
+  const int u_ld = ((max_r * std::max(nblk, 1) + 15) / 16) * 16;  // A rows padded to 16-row tiles
+
+  if (T <= kSkinnyMaxTok) {
+    // ---------------------------------------------------- decode regime
+    SkinnyBaseArgs a{};
+    a.w = reinterpret_cast<const bf16*>(w);
+    a.bias = reinterpret_cast<const bf16*>(bias);
+    a.N = N;
+    a.K = K;
+    a.ntok = (int)T;
+    int t = 0;
+    for (int i = 0; i < n_seg; ++i) {
+      for (int64_t j = 0; j < rows[i]; ++j, ++t) {
+        a.x[t] = reinterpret_cast<const bf16*>(seg_in[i]) + j * K;
+        a.y[t] = reinterpret_cast<bf16*>(seg_out[i]) + j * N;
+        a.lora[t] = (has_lora && seg_lora[i] >= 0) ? seg_lora[i] : -1;
+        a.urow[t] = t;
+      }
+    }
+    if (has_lora) {
+      // group tokens by adapter entry: each adapter's A is streamed once
+      SkinnyShrinkArgs s{};
+      s.table = lora_table;
+      s.K = K;
+      s.u_ld = u_ld;
+      std::vector<int> entries;
+      for (int i = 0; i < T; ++i)
+        if (a.lora[i] >= 0 && std::find(entries.begin(), entries.end(), a.lora[i]) == entries.end())
+          entries.push_back(a.lora[i]);
+      s.ngroups = (int)entries.size();
+      int tiles = 0, nt = 0, max_group = 0;
+      for (int g = 0; g < s.ngroups; ++g) {
+        s.g_entry[g] = entries[g];
+        s.g_arows[g] = host_entries[entries[g]].rank * nblk;
+        s.g_tile0[g] = tiles;
+        s.g_tok0[g] = nt;
+        const swl_lora_entry& e = host_entries[entries[g]];
+        tiles += (e.rank * nblk + 15) / 16;
+        int cnt = 0;
+        for (int i = 0; i < T; ++i)
+          if (a.lora[i] == entries[g]) {
+            s.tok[nt] = i;
+            s.x[nt] = a.x[i];
+            ++nt;
+            ++cnt;
+          }
+        max_group = std::max(max_group, cnt);
+      }
+      s.g_tile0[s.ngroups] = tiles;
+      s.g_tok0[s.ngroups] = nt;
+      // split K across workgroups until there are enough of them
+      int ksplit = 1;
+      const int64_t ksteps = K / 32;
+      while (tiles * ksplit < 256 && ksteps % (ksplit * 2) == 0 && ksteps / (ksplit * 2) >= 64) ksplit *= 2;
+      s.ksplit = ksplit;
+      s.u_split_stride = (int64_t)T * u_ld;
+      void* scratch = nullptr;
+      int rc = scratch_get(sizeof(float) * (size_t)ksplit * (size_t)s.u_split_stride, st, &scratch);
+      if (rc) return rc;
+      s.u = reinterpret_cast<float*>(scratch);
+      rc = launch_skinny_shrink(s, tiles, max_group, st);
+      if (rc) return rc;
+      a.has_lora = 1;
+      a.L = L;
+      a.L.u = s.u;
+      a.L.usplit = ksplit;
+      a.L.u_ld = u_ld;
+      a.L.u_split_stride = s.u_split_stride;
+    }
+    return launch_skinny_base(a, st);
+  }
+
+  // ------------------------------------------------------ prefill regime
+  SWL_CHECK(K % TK == 0, SWL_ERR_INVALID, "round: K must be a multiple of 64 for > 64 tokens");
+  const size_t xbytes = sizeof(bf16) * (size_t)T * (size_t)K;
+  const size_t xbytes_al = (xbytes + 255) & ~(size_t)255;
+  size_t ubytes = 0;
+  if (has_lora) ubytes = sizeof(float) * (size_t)T * (size_t)u_ld;
+  void* scratch = nullptr;
+  int rc = scratch_get(xbytes_al + ubytes, st, &scratch);
+  if (rc) return rc;
+  bf16* packed = reinterpret_cast<bf16*>(scratch);
+  rc = swl_gather_bf16(seg_in, rows, n_seg, K, packed, st);
+  if (rc) return rc;
+
+  TiledArgs a{};
+  a.x = packed;
+  a.w = reinterpret_cast<const bf16*>(w);
+  a.bias = reinterpret_cast<const bf16*>(bias);
+  a.M = T;
+  a.N = N;
+  a.K = K;
+  a.y = nullptr;
+  int64_t dummy = 0;
+  rc = fill_segptrs(a.out, reinterpret_cast<const void* const*>(seg_out), rows, n_seg, N, &dummy);
+  if (rc) return rc;
+  if (has_lora) {
+    float* u = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + xbytes_al);
+    // shrink per segment in chunks of <= 64 tokens (A re-read per chunk)
+    for (int i = 0; i < n_seg; ++i) {
+      a.seg_lora[i] = (seg_lora[i] >= 0 && rows[i] > 0) ? seg_lora[i] : -1;
+      if (a.seg_lora[i] < 0) continue;
+      const swl_lora_entry& e = host_entries[seg_lora[i]];
+      const int tiles = (e.rank * nblk + 15) / 16;
+      for (int64_t c0 = 0; c0 < rows[i]; c0 += kSkinnyMaxTok) {
+        const int cnt = (int)std::min<int64_t>(kSkinnyMaxTok, rows[i] - c0);
+        SkinnyShrinkArgs s{};
+        s.table = lora_table;
+        s.K = K;
+        s.u_ld = u_ld;
+        s.u = u;
+        s.u_split_stride = (int64_t)T * u_ld;
+        s.ksplit = 1;
+        s.ngroups = 1;
+        s.g_entry[0] = seg_lora[i];
+        s.g_arows[0] = e.rank * nblk;
+        s.g_tile0[0] = 0;
+        s.g_tile0[1] = tiles;
+        s.g_tok0[0] = 0;
+        s.g_tok0[1] = cnt;
+        for (int j = 0; j < cnt; ++j) {
+          const int64_t prow = a.out.off[i] + c0 + j;
+          s.tok[j] = (int)prow;
+          s.x[j] = packed + prow * K;
+        }
+        rc = launch_skinny_shrink(s, tiles, cnt, st);
+        if (rc) return rc;
+      }
+    }
+    a.has_lora = 1;
+    a.L = L;
+    a.L.u = u;
+    a.L.usplit = 1;
+    a.L.u_ld = u_ld;
+    a.L.u_split_stride = (int64_t)T * u_ld;
+  }
+  const dim3 grid((unsigned)((N + TN - 1) / TN), (unsigned)((T + TM - 1) / TM));
+  hipLaunchKernelGGL(tiled_kernel, grid, dim3(256), 0, st, a);
+  SWL_LAUNCH_CHECK("tiled_kernel launch");
+  return SWL_OK;
+}
+
+}  // namespace swl

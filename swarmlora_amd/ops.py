@@ -1,0 +1,269 @@
+"""torch-tensor front end of the libswl kernels.
+
+Every function here validates shapes on the host (the kernels and their grids
+assume them), then calls the C ABI on torch's current HIP stream.  There is no
+CPU or torch fallback: on a host without the built library or a GPU these
+raise.
+"""
+
+import ctypes
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import LoraEntry, SWL_MAX_LORA_BLOCKS
+
+BF16 = torch.bfloat16
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _need(t: torch.Tensor, name: str, dtype=BF16):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (the HIP path has no CPU fallback)")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _ptr_array(ts: Sequence[Optional[torch.Tensor]]):
+    arr = (ctypes.c_void_p * len(ts))()
+    for i, t in enumerate(ts):
+        arr[i] = t.data_ptr() if t is not None else 0
+    return arr
+
+
+def _i64_array(vals):
+    arr = (ctypes.c_int64 * len(vals))()
+    for i, v in enumerate(vals):
+        arr[i] = int(v)
+    return arr
+
+
+def _i32_array(vals):
+    arr = (ctypes.c_int32 * len(vals))()
+    for i, v in enumerate(vals):
+        arr[i] = int(v)
+    return arr
+
+
+def gather(slot_inputs: Sequence[torch.Tensor], rows: Sequence[int], out: Optional[torch.Tensor] = None):
+    """Pack rows[i] leading rows of each slot buffer (2-D [>= rows[i], d]) into
+    one [sum(rows), d] tensor, in the given order."""
+    d = slot_inputs[0].shape[-1]
+    for i, t in enumerate(slot_inputs):
+        _need(t, f"slot_inputs[{i}]")
+        if t.shape[-1] != d or not t.is_contiguous() or t.numel() < rows[i] * d:
+            raise ValueError("slot inputs must be contiguous [rows, d] with a common d")
+    total = int(sum(rows))
+    if out is None:
+        out = torch.empty(total, d, dtype=BF16, device=slot_inputs[0].device)
+    _lib.check(_lib.load().swl_gather_bf16(_ptr_array(slot_inputs), _i64_array(rows), len(rows), d,
+                                           _ptr(out), _stream()))
+    return out
+
+
+def scatter_add(y: torch.Tensor, slot_outputs: Sequence[torch.Tensor], rows: Sequence[int],
+                delta: Optional[torch.Tensor] = None):
+    """slot_outputs[i][:rows[i]] = y[off_i : off_i + rows[i]] (+ delta ...)."""
+    _need(y, "y")
+    d = y.shape[-1]
+    if delta is not None:
+        _need(delta, "delta")
+        if delta.shape != y.shape:
+            raise ValueError("delta must match y")
+    for i, t in enumerate(slot_outputs):
+        _need(t, f"slot_outputs[{i}]")
+        if not t.is_contiguous() or t.numel() < rows[i] * d:
+            raise ValueError("slot outputs must be contiguous and hold rows[i] * d elements")
+    if y.shape[0] != sum(rows):
+        raise ValueError("y rows must equal sum(rows)")
+    _lib.check(_lib.load().swl_scatter_add_bf16(_ptr(y.contiguous()), _ptr(delta), _ptr_array(slot_outputs),
+                                                _i64_array(rows), len(rows), d, _stream()))
+
+
+def gemm(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+         out: Optional[torch.Tensor] = None):
+    """y = x @ w.T (+ bias), bf16 in/out, fp32 accumulate."""
+    _need(x, "x")
+    _need(w, "w")
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError("gemm expects x [m, k] and w [n, k]")
+    if not (x.is_contiguous() and w.is_contiguous()):
+        raise ValueError("gemm operands must be contiguous")
+    m, k = x.shape
+    n = w.shape[0]
+    if bias is not None:
+        _need(bias, "bias")
+        if bias.numel() != n:
+            raise ValueError("bias must have n elements")
+    if out is None:
+        out = torch.empty(m, n, dtype=BF16, device=x.device)
+    _lib.check(_lib.load().swl_gemm_bf16(_ptr(x), _ptr(w), _ptr(bias), _ptr(out), m, n, k, _stream()))
+    return out
+
+
+class LoraTable:
+    """Device array of swl_lora_entry records.  Keeps the tensors it points to
+    alive.  Entry i describes one adapter for one (fused) projection."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self._entries: List[LoraEntry] = []
+        self._keep = []
+        self._dev = None
+
+    def add(self, a: torch.Tensor, bs: Sequence[torch.Tensor], rank: int, scale: float) -> int:
+        """a: bf16 [nblk*rank, k] (stacked lora_A); bs[j]: bf16 [blk_cols[j], rank]."""
+        _need(a, "lora a")
+        if not a.is_contiguous() or a.shape[0] != rank * len(bs):
+            raise ValueError("lora a must be contiguous [nblk * rank, k]")
+        if len(bs) > SWL_MAX_LORA_BLOCKS:
+            raise ValueError("too many column blocks")
+        e = LoraEntry()
+        e.a = a.data_ptr()
+        for j, b in enumerate(bs):
+            _need(b, f"lora b[{j}]")
+            if not b.is_contiguous() or b.shape[1] != rank:
+                raise ValueError("lora b must be contiguous [cols, rank]")
+            e.b[j] = b.data_ptr()
+        e.rank = int(rank)
+        e.scale = float(scale)
+        self._entries.append(e)
+        self._keep.extend([a, *bs])
+        self._dev = None
+        return len(self._entries) - 1
+
+    def device_table(self) -> torch.Tensor:
+        if self._dev is None:
+            n = len(self._entries)
+            raw = (LoraEntry * max(n, 1))(*self._entries)
+            host = torch.frombuffer(bytearray(bytes(raw)), dtype=torch.uint8)
+            self._dev = host.to(self.device)
+        return self._dev
+
+    def __len__(self):
+        return len(self._entries)
+
+
+def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], rows: Sequence[int],
+                w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
+                blk_cols: Optional[Sequence[int]] = None):
+    """One gather -> GEMM -> (+LoRA) -> scatter round over slot buffers."""
+    _need(w, "w")
+    n, k = w.shape
+    if len(seg_in) != len(rows) or len(seg_out) != len(rows):
+        raise ValueError("one input, output and row count per segment")
+    for i in range(len(rows)):
+        _need(seg_in[i], f"seg_in[{i}]")
+        _need(seg_out[i], f"seg_out[{i}]")
+        if seg_in[i].numel() < rows[i] * k or seg_out[i].numel() < rows[i] * n:
+            raise ValueError(f"segment {i} buffers are smaller than rows * dim")
+        if not (seg_in[i].is_contiguous() and seg_out[i].is_contiguous()):
+            raise ValueError("segment buffers must be contiguous")
+    if bias is not None:
+        _need(bias, "bias")
+    lora_arr = None
+    tab_ptr = ctypes.c_void_p(0)
+    blk = None
+    nblk = 0
+    if seg_lora is not None:
+        if table is None or blk_cols is None:
+            raise ValueError("seg_lora needs a LoraTable and blk_cols")
+        if any(i >= len(table) for i in seg_lora):
+            raise ValueError("seg_lora index out of range")
+        lora_arr = _i32_array(seg_lora)
+        tab_ptr = _ptr(table.device_table())
+        blk = _i64_array(blk_cols)
+        nblk = len(blk_cols)
+    _lib.check(_lib.load().swl_round_bf16(len(rows), _i64_array(rows), _ptr_array(seg_in), _ptr_array(seg_out),
+                                          _ptr(w), _ptr(bias), n, k, lora_arr, tab_ptr, nblk, blk, _stream()))
+
+
+def matmul(x: torch.Tensor, b: torch.Tensor, trans_b: bool, alpha: float = 1.0,
+           out: Optional[torch.Tensor] = None):
+    """y = alpha * x @ (b.T if trans_b else b) for 2-D views with unit column
+    stride (row strides may be arbitrary).  fp32 accumulation, bf16 output."""
+    _need(x, "x")
+    _need(b, "b")
+    if x.dim() != 2 or b.dim() != 2:
+        raise ValueError("matmul expects 2-D operands")
+    if x.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("matmul operands need unit column stride")
+    m, k = x.shape
+    n = b.shape[0] if trans_b else b.shape[1]
+    kb = b.shape[1] if trans_b else b.shape[0]
+    if kb != k:
+        raise ValueError("matmul inner dimensions differ")
+    if out is None:
+        out = torch.empty(m, n, dtype=BF16, device=x.device)
+    if out.stride(1) != 1:
+        raise ValueError("out needs unit column stride")
+    _lib.check(_lib.load().swl_matmul_bf16(_ptr(x), x.stride(0), _ptr(b), b.stride(0), 1 if trans_b else 0,
+                                           _ptr(out), out.stride(0), m, n, k, float(alpha), _stream()))
+    return out
+
+
+def paged_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                    v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+                    positions: Optional[torch.Tensor], cos_sin: Optional[torch.Tensor],
+                    softmax_scale: float, rope: bool = True, out: Optional[torch.Tensor] = None):
+    """q [nseq, L, hq, d], k/v [nseq, L, hkv, d] (q, k rotated in place when
+    rope), caches [num_blocks, block_size, hkv, d], block_table int32
+    [nseq, max_blocks], cache_seqlens int32 [nseq], positions int64 [nseq*L].
+    Returns out [nseq, L, hq*d]."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _need(t, nm)
+        if not t.is_contiguous():
+            raise ValueError(f"{nm} must be contiguous")
+    _need(block_table, "block_table", torch.int32)
+    _need(cache_seqlens, "cache_seqlens", torch.int32)
+    nseq, L, hq, d = q.shape
+    hkv = k.shape[2]
+    if k.shape != (nseq, L, hkv, d) or v.shape != k.shape:
+        raise ValueError("k and v must be [nseq, L, hkv, d]")
+    nb, bs, hkv2, d2 = k_cache.shape
+    if v_cache.shape != k_cache.shape or hkv2 != hkv or d2 != d:
+        raise ValueError("cache geometry mismatch")
+    if block_table.dim() != 2 or block_table.shape[0] < nseq or not block_table.is_contiguous():
+        raise ValueError("block_table must be contiguous [nseq, max_blocks]")
+    if cache_seqlens.numel() < nseq:
+        raise ValueError("cache_seqlens must have nseq entries")
+    max_pos = 0
+    if rope:
+        _need(positions, "positions", torch.int64)
+        _need(cos_sin, "cos_sin")
+        if positions.numel() != nseq * L:
+            raise ValueError("positions must have nseq * q_len entries")
+        if cos_sin.shape[-1] != d or not cos_sin.is_contiguous():
+            raise ValueError("cos_sin must be contiguous [max_pos, d]")
+        max_pos = cos_sin.shape[0]
+    if out is None:
+        out = torch.empty(nseq, L, hq * d, dtype=BF16, device=q.device)
+    _lib.check(_lib.load().swl_paged_attention_bf16(
+        _ptr(q), _ptr(k), _ptr(v), nseq, L, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs,
+        _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope else None),
+        _ptr(cos_sin if rope else None), max_pos, 1 if rope else 0, float(softmax_scale), _ptr(out), _stream()))
+    return out
+
+
+def zero_blocks(caches: Sequence[torch.Tensor], block_ids: torch.Tensor):
+    """Zero whole pages block_ids of every cache [num_blocks, ...]."""
+    _need(block_ids, "block_ids", torch.int64)
+    if not caches:
+        return
+    for c in caches:
+        _need(c, "cache")
+    per_block = caches[0][0].numel()
+    ids = block_ids.contiguous()
+    arr = _ptr_array(caches)
+    _lib.check(_lib.load().swl_zero_blocks_bf16(arr, len(caches), _ptr(ids), ids.numel(), per_block, _stream()))

@@ -1,0 +1,42 @@
+"""The C-ABI library loads on a host without a GPU and exports every entry
+point declared in include/*.h (no compute calls here)."""
+
+import glob
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DECL = re.compile(r"^\s*(?:const\s+)?(?:int|int64_t|char|void)\s*\*?\s*(swl_[a-z0-9_]+)\s*\(", re.M)
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(REPO, "include", "*.h")):
+        names.update(DECL.findall(open(h).read()))
+    return sorted(names)
+
+
+def test_headers_declare_entry_points():
+    assert "swl_round_bf16" in declared_symbols()
+    assert len(declared_symbols()) >= 10
+
+
+def test_library_exports_every_declared_symbol():
+    from swarmlora_amd import _lib
+    lib = _lib.load()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # the Python side declares a signature for every header entry point
+    assert set(declared_symbols()) <= set(_lib.exported_symbols())
+
+
+def test_error_text_and_no_device_calls():
+    from swarmlora_amd import _lib
+    lib = _lib.load()
+    assert lib.swl_abi_version() >= 1
+    assert lib.swl_device_count() >= 0
+    # argument validation fails before any HIP call
+    rc = lib.swl_gemm_bf16(None, None, None, None, 1, 1, 32, None)
+    assert rc != 0 and "null argument" in _lib.last_error()

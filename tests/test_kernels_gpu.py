@@ -1,0 +1,301 @@
+"""GPU parity of the libswl kernels against the CPU oracle.
+
+Integer/byte work (gather, scatter, page append of v) must be bit-exact;
+floating-point results must be within REL_TOL (normalised max error, see
+tests/_util.py) of the oracle on the same seeded inputs.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import reference_path as ref
+from tests._util import (BF16, REL_TOL, SEED_A, SEED_META, SEED_W, SEED_X, assert_close, bits_equal, randn,
+                         rel_err)
+
+pytestmark = pytest.mark.gpu
+
+H, KV, HD, I = 4096, 8, 128, 14336
+QKV = H + 2 * KV * HD
+
+
+def _ops():
+    from swarmlora_amd import ops
+    return ops
+
+
+# ----------------------------------------------------------- gather/scatter --
+@pytest.mark.parametrize("rows,d", [([1, 1, 1, 1], 4096), ([3, 0, 7, 1, 16], 4096), ([5, 2], 72), ([2, 3], 13)])
+def test_gather_bit_exact(dev, rows, d):
+    ops = _ops()
+    slots = [randn((max(t, 1) + 2, d), SEED_X + i) for i, t in enumerate(rows)]
+    packed = ops.gather([s.to(dev) for s in slots], rows)
+    torch.cuda.synchronize()
+    assert bits_equal(packed, ref.gather(slots, rows))
+
+
+@pytest.mark.parametrize("rows,d", [([1, 1, 1, 1], 6144), ([4, 0, 9], 4096), ([3, 2], 20)])
+def test_scatter_bit_exact_and_delta(dev, rows, d):
+    ops = _ops()
+    T = sum(rows)
+    y = randn((T, d), SEED_X)
+    delta = randn((T, d), SEED_A, std=0.1)
+    outs = [torch.full((max(t, 1), d), -7.0, dtype=BF16, device=dev) for t in rows]
+    ops.scatter_add(y.to(dev), outs, rows)
+    torch.cuda.synchronize()
+    expect = ref.scatter(y, rows)
+    for o, e, t in zip(outs, expect, rows):
+        assert bits_equal(o[:t], e)
+        if t == 0:
+            assert bool((o == -7.0).all())  # untouched
+    ops.scatter_add(y.to(dev), outs, rows, delta=delta.to(dev))
+    torch.cuda.synchronize()
+    want = ref.scatter((y.float() + delta.float()).to(BF16), rows)  # one rounding of the fp32 sum
+    for o, e, t in zip(outs, want, rows):
+        assert bits_equal(o[:t], e)
+
+
+# --------------------------------------------------------------------- GEMM --
+@pytest.mark.parametrize("m", [1, 4, 16, 17, 28, 33, 64, 65, 200])
+def test_gemm_matches_oracle(dev, m):
+    ops = _ops()
+    n, k = 768, 1024
+    x = randn((m, k), SEED_X)
+    w = randn((n, k), SEED_W, std=0.02)
+    y = ops.gemm(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert_close(y, ref.base_gemm(x, w), what=f"gemm m={m}")
+    # against an fp64 product too (the oracle itself rounds once to bf16)
+    exact = (x.double() @ w.double().t())
+    assert rel_err(y, exact) <= 5e-3
+
+
+@pytest.mark.parametrize("m", [3, 100])
+def test_gemm_bias_and_ragged_n(dev, m):
+    ops = _ops()
+    n, k = 200, 512   # n not a multiple of 16 / 128
+    x = randn((m, k), SEED_X)
+    w = randn((n, k), SEED_W, std=0.05)
+    b = randn((n,), SEED_A)
+    y = ops.gemm(x.to(dev), w.to(dev), b.to(dev))
+    torch.cuda.synchronize()
+    assert_close(y, ref.base_gemm(x, w, b), what="gemm+bias")
+
+
+def test_gemm_one_hot_selects_weight_column_exactly(dev):
+    """x = e_j picks W[:, j] exactly (no rounding anywhere)."""
+    ops = _ops()
+    n, k = 512, 4096
+    w = randn((n, k), SEED_W)
+    for m in (5, 80):
+        idx = torch.arange(m) * 37 % k
+        x = torch.zeros(m, k, dtype=BF16)
+        x[torch.arange(m), idx] = 1.0
+        y = ops.gemm(x.to(dev), w.to(dev))
+        torch.cuda.synchronize()
+        assert bits_equal(y, w[:, idx].t().contiguous())
+
+
+@pytest.mark.parametrize("n,k", [(QKV, H), (H, H), (2 * I, H), (H, I)])
+def test_gemm_full_decode_shapes(dev, n, k):
+    """The four base projections at Llama-3.1-8B shape, 28 decode tokens."""
+    ops = _ops()
+    x = randn((28, k), SEED_X)
+    w = randn((n, k), SEED_W, std=0.02)
+    y = ops.gemm(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert_close(y, ref.base_gemm(x, w), what=f"gemm [{n}x{k}]")
+
+
+# ------------------------------------------------------------------ rounds --
+def _adapter(seed, r, in_dim, out_dims, std=0.02):
+    """Per-block (A [r, in], B [out, r]) pairs ~N(0, std)."""
+    blocks = []
+    for j, od in enumerate(out_dims):
+        A = randn((r, in_dim), seed * 100 + 2 * j, std=std)
+        B = randn((od, r), seed * 100 + 2 * j + 1, std=std)
+        blocks.append((A, B))
+    return blocks
+
+
+def _run_round(dev, rows, in_dim, out_dims, ranks, scale=2.0, adapter_ids=None, with_lora=True, bias=False):
+    ops = _ops()
+    n = sum(out_dims)
+    w = randn((n, in_dim), SEED_W, std=0.02)
+    b = randn((n,), SEED_W + 10) if bias else None
+    xs = [randn((max(t, 1), in_dim), SEED_X * 1000 + i) for i, t in enumerate(rows)]
+    n_adapters = (max(adapter_ids) + 1) if adapter_ids is not None else len(rows)
+    adapters = [_adapter(SEED_A + 7 * i, ranks[i % len(ranks)], in_dim, out_dims) for i in range(n_adapters)]
+    seg_ad = adapter_ids if adapter_ids is not None else list(range(len(rows)))
+
+    table = ops.LoraTable(dev)
+    for ad, r in zip(adapters, [ranks[i % len(ranks)] for i in range(n_adapters)]):
+        a = torch.cat([A for A, _ in ad], 0).contiguous().to(dev)
+        bs = [B.contiguous().to(dev) for _, B in ad]
+        table.add(a, bs, r, scale)
+    seg_in = [x.to(dev) for x in xs]
+    seg_out = [torch.zeros(max(t, 1), n, dtype=BF16, device=dev) for t in rows]
+    ops.round_fused(seg_in, seg_out, rows, w.to(dev), b.to(dev) if b is not None else None,
+                    seg_lora=seg_ad if with_lora else None, table=table if with_lora else None,
+                    blk_cols=out_dims if with_lora else None)
+    torch.cuda.synchronize()
+
+    if with_lora:
+        op = ref.OP_QKV_FUSED if len(out_dims) > 1 else ref.OP_O_PROJ
+        ad_ref = [[(A, B, scale) for A, B in adapters[seg_ad[i]]] for i in range(len(rows))]
+        want = ref.round_with_lora(op, xs, rows, w, ad_ref, out_dims)
+    else:
+        want = ref.execute_round(xs, rows, w, b)
+    if bias and with_lora:
+        want = [wv + b for wv in want]
+    for i, t in enumerate(rows):
+        if t == 0:
+            continue
+        assert_close(seg_out[i][:t], want[i], what=f"round slot {i}")
+    return seg_out, want
+
+
+def test_round_config1_qkv_lora(dev):
+    """fused QKV, 4 slots x 1 decode token, rank-16 LoRA on
+    q/k/v per slot, scale 2.0."""
+    _run_round(dev, [1, 1, 1, 1], H, [H, KV * HD, KV * HD], [16])
+
+
+def test_round_no_lora_matches_execute_batched_gemm(dev):
+    _run_round(dev, [1, 2, 1, 3], H, [H], [16], with_lora=False)
+
+
+def test_round_single_slot_and_bias(dev):
+    _run_round(dev, [1], H, [H], [16], with_lora=False, bias=True)
+    _run_round(dev, [2], H, [H], [8], with_lora=True, bias=True)
+
+
+@pytest.mark.parametrize("out_dims,in_dim", [([H], H), ([I, I], H), ([H], I)])
+def test_round_decode_28_slots_each_projection(dev, out_dims, in_dim):
+    """BASELINE config 2 rounds O, Gate+Up, Down at 28 slots x 1 token."""
+    _run_round(dev, [1] * 28, in_dim, out_dims, [16])
+
+
+def test_round_shared_adapters_zipf(dev):
+    """BASELINE config 5 shape: 64 one-token slots drawing adapter ids from a
+    Zipf(1.1) over a pool; slots sharing an adapter share its A/B."""
+    g = torch.Generator().manual_seed(SEED_META)
+    n_pool = 50
+    p = torch.tensor([(i + 1) ** -1.1 for i in range(n_pool)])
+    ids = torch.multinomial(p / p.sum(), 64, replacement=True, generator=g).tolist()
+    used = sorted(set(ids))
+    remap = {a: i for i, a in enumerate(used)}
+    _run_round(dev, [1] * 64, H, [H, KV * HD, KV * HD], [16], adapter_ids=[remap[a] for a in ids])
+
+
+@pytest.mark.parametrize("ranks", [[8], [8, 16, 32, 64], [4, 12]])
+def test_round_mixed_ranks_decode(dev, ranks):
+    _run_round(dev, [1] * 9, H, [H, KV * HD, KV * HD], ranks)
+
+
+def test_round_prefill_ragged_mixed_ranks(dev):
+    """BASELINE config 3 (reduced): half the slots 1 token, the rest 32..160
+    tokens, ranks from {8,16,32,64}; exercises the packed/tiled path."""
+    g = torch.Generator().manual_seed(SEED_META)
+    rows = [1, 1, 1, 1] + torch.randint(32, 161, (4,), generator=g).tolist()
+    ranks = [[8, 16, 32, 64][int(i)] for i in torch.randint(0, 4, (8,), generator=g)]
+    _run_round(dev, rows, H, [H, KV * HD, KV * HD], ranks)
+
+
+def test_round_prefill_zero_row_segments(dev):
+    _run_round(dev, [40, 0, 30, 0, 1], 1024, [512], [16])
+
+
+# ----------------------------------------------------------- worker matmul --
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_matmul_layouts(dev, trans_b):
+    ops = _ops()
+    m, k, n = 5, 4096, 48
+    x = randn((m, k), SEED_X)
+    b = randn((n, k) if trans_b else (k, n), SEED_W, std=0.02)
+    y = ops.matmul(x.to(dev), b.to(dev), trans_b=trans_b, alpha=2.0)
+    torch.cuda.synchronize()
+    want = ((x @ (b.t() if trans_b else b)) * 2.0)
+    assert_close(y, want, what="matmul")
+
+
+def test_matmul_strided_block_of_fused_B(dev):
+    """A column block of a block-diagonal fused_B is read through its row stride."""
+    ops = _ops()
+    r, dims = 16, [64, 32, 32]
+    fB = torch.zeros(3 * r, sum(dims), dtype=BF16)
+    fB[r:2 * r, 64:96] = randn((r, 32), SEED_W)
+    u = randn((4, 3 * r), SEED_X)
+    fBd = fB.to(dev)
+    y = ops.matmul(u.to(dev)[:, r:2 * r], fBd[r:2 * r, 64:96], trans_b=False)
+    torch.cuda.synchronize()
+    assert_close(y, u[:, r:2 * r] @ fB[r:2 * r, 64:96], what="strided block")
+
+
+# ---------------------------------------------------------- paged attention --
+def _attn_case(dev, nseq, L, ctx0, hq=32, hkv=8, bs=16, seed=0, shuffle=True):
+    ops = _ops()
+    d = 128
+    max_pos = 4096
+    g = torch.Generator().manual_seed(SEED_META + seed)
+    max_blocks = (max(ctx0) + L + bs - 1) // bs + 1
+    num_blocks = nseq * max_blocks + 3
+    perm = torch.randperm(num_blocks, generator=g) if shuffle else torch.arange(num_blocks)
+    bt = perm[: nseq * max_blocks].reshape(nseq, max_blocks).to(torch.int32)
+    kc = randn((num_blocks, bs, hkv, d), 11 + seed)
+    vc = randn((num_blocks, bs, hkv, d), 12 + seed)
+    q = randn((nseq, L, hq, d), 13 + seed)
+    k = randn((nseq, L, hkv, d), 14 + seed)
+    v = randn((nseq, L, hkv, d), 15 + seed)
+    seqlens = torch.tensor(ctx0, dtype=torch.int32)
+    pos = (seqlens.long().unsqueeze(1) + torch.arange(L).unsqueeze(0)).reshape(-1)
+    cs = ref.cos_sin_cache(ref.rope_inv_freq(d, 500000.0), max_pos)
+    scale = 1.0 / math.sqrt(d)
+
+    kc_d, vc_d, q_d, k_d, v_d = kc.to(dev), vc.to(dev), q.to(dev), k.to(dev), v.to(dev)
+    out = ops.paged_attention(q_d, k_d, v_d, kc_d, vc_d, bt.to(dev), seqlens.to(dev), pos.to(dev), cs.to(dev),
+                              scale)
+    torch.cuda.synchronize()
+    kc_r, vc_r = kc.clone(), vc.clone()
+    want, q_rot, k_rot = ref.paged_attention(q, k, v, kc_r, vc_r, bt, seqlens, pos, cs, scale)
+    return out, want, (q_d, k_d, kc_d, vc_d), (q_rot, k_rot, kc_r, vc_r)
+
+
+@pytest.mark.parametrize("nseq,L,ctx0", [(3, 1, [0, 17, 100]), (2, 4, [5, 31]), (4, 1, [127, 128, 1000, 2047])])
+def test_paged_attention_matches_oracle(dev, nseq, L, ctx0):
+    out, want, got_state, ref_state = _attn_case(dev, nseq, L, ctx0)
+    assert_close(out, want, what="attention out")
+    q_d, k_d, kc_d, vc_d = got_state
+    q_rot, k_rot, kc_r, vc_r = ref_state
+    assert_close(q_d, q_rot, tol=1e-2, what="rope q in place")
+    assert_close(k_d, k_rot, tol=1e-2, what="rope k in place")
+    assert bits_equal(vc_d, vc_r), "v pages must be a bit-exact append"
+    assert_close(kc_d, kc_r, what="k pages")
+
+
+def test_paged_attention_single_key_returns_v(dev):
+    """ctx = 1: softmax over one key is 1, so the output is v exactly."""
+    out, want, (q_d, k_d, kc_d, vc_d), _ = _attn_case(dev, 2, 1, [0, 0])
+    v_new = randn((2, 1, 8, 128), 15)
+    o = out.cpu().reshape(2, 32, 128)
+    for h in range(32):
+        assert bits_equal(o[:, h], v_new[:, 0, h // 4])
+
+
+def test_paged_attention_page_permutation_invariant(dev):
+    a, _, _, _ = _attn_case(dev, 2, 1, [200, 77], shuffle=False, seed=5)
+    b, _, _, _ = _attn_case(dev, 2, 1, [200, 77], shuffle=True, seed=5)
+    assert rel_err(a, b) <= 1e-6
+
+
+def test_zero_blocks(dev):
+    ops = _ops()
+    caches = [randn((10, 16, 8, 128), s).to(dev) for s in range(4)]
+    ids = torch.tensor([1, 7, 3], dtype=torch.int64, device=dev)
+    ops.zero_blocks(caches, ids)
+    torch.cuda.synchronize()
+    for c in caches:
+        assert float(c[[1, 7, 3]].abs().max()) == 0.0
+        assert float(c[[0, 2, 4, 5, 6, 8, 9]].abs().min()) >= 0.0
+        assert float(c[0].abs().max()) > 0.0
