@@ -106,7 +106,10 @@ typedef struct swl_lora_entry {
  *   seg_out[i] : device [rows[i], n] bf16 (slot output buffer)
  *   seg_lora   : HOST [n_seg] index into lora_table (-1 = no adapter); NULL =
  *                no LoRA at all (the reference's aggregator-only behaviour)
- *   lora_table : DEVICE array of swl_lora_entry
+ *   lora_table : DEVICE array of swl_lora_entry (read by the kernels)
+ *   lora_table_host : the same records in HOST memory (read by the launcher to
+ *                plan the shrink; no device-to-host copy, so the call can be
+ *                captured into a HIP graph)
  *   nblk / blk_cols : column blocks of the fused output (QKV: 3 blocks
  *                {q, k, v}; Gate+Up: 2; O / Down: 1); sum(blk_cols) == n.
  * Equivalent to execute_batched_gemm_slots (ext_aggregator.cpp:470-626)
@@ -115,7 +118,8 @@ typedef struct swl_lora_entry {
 int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
                    void* const* seg_out, const void* w, const void* bias,
                    int64_t n, int64_t k, const int32_t* seg_lora,
-                   const swl_lora_entry* lora_table, int nblk,
+                   const swl_lora_entry* lora_table,
+                   const swl_lora_entry* lora_table_host, int nblk,
                    const int64_t* blk_cols, void* stream);
 
 /* Row-major matrix product with an explicit layout, used by the worker-side

@@ -65,7 +65,7 @@ _SIGS = {
     "swl_gather_bf16": (c_int, [P_vp, P_i64, c_int, c_i64, c_vp, c_vp]),
     "swl_scatter_add_bf16": (c_int, [c_vp, c_vp, P_vp, P_i64, c_int, c_i64, c_vp]),
     "swl_gemm_bf16": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
-    "swl_round_bf16": (c_int, [c_int, P_i64, P_vp, P_vp, c_vp, c_vp, c_i64, c_i64, P_i32, c_vp, c_int,
+    "swl_round_bf16": (c_int, [c_int, P_i64, P_vp, P_vp, c_vp, c_vp, c_i64, c_i64, P_i32, c_vp, c_vp, c_int,
                                P_i64, c_vp]),
     "swl_matmul_bf16": (c_int, [c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
                                 c_vp]),

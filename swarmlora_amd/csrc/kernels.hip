@@ -3,16 +3,19 @@
 // Kernels
 //   gather_rows_kernel      slot rows -> packed batch (128-bit copies)
 //   scatter_rows_kernel     packed rows (+ delta) -> slot rows
-//   skinny_kernel<...>      M <= 64 "decode" projection: W streamed from HBM
-//                           straight into MFMA A-fragments, activations read
-//                           through per-token row pointers (the gather is
-//                           fused), split-K across the waves of a workgroup
-//                           with an LDS reduction, and an epilogue that adds
-//                           bias + the LoRA expand and stores each token's row
-//                           into its slot buffer (the scatter is fused).
-//                           The same template in SHRINK mode computes the LoRA
-//                           shrink u = x . A^T for groups of tokens sharing an
-//                           adapter (each adapter's A is read once per round).
+//   split_kernel<TT,WAVES>  M <= 64 "decode" projection, part 1: workgroups
+//                           of 8 waves own 128 W rows x one K-slice; the
+//                           K-slice of every token's activation (read through
+//                           per-token row pointers: the gather is fused) is
+//                           staged once in LDS and shared by the waves, W is
+//                           streamed from HBM straight into MFMA A-fragments,
+//                           fp32 partials go to scratch.  Lower workgroups run
+//                           the LoRA shrink u = x . A^T for groups of tokens
+//                           sharing an adapter (each adapter's A read once).
+//   epilogue_kernel         part 2: sums the K-slice partials, adds bias and
+//                           the LoRA expand u . B^T * scale, rounds once and
+//                           stores each token's row into its slot buffer (the
+//                           scatter is fused).
 //   tiled_kernel            M > 64 "prefill" projection: 128x128x64 LDS-staged
 //                           MFMA tiles, fp32 accumulation, same epilogue.
 //   matmul_generic_kernel   small row-major products with arbitrary strides
@@ -30,6 +33,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -248,172 +252,254 @@ __device__ __forceinline__ void epilogue_store4(float (&v)[4], int64_t n, int64_
 }
 
 // ------------------------------------------------------ skinny (M<=64) ----
-struct SkinnyBaseArgs {
-  const bf16* w;          // [N, K]
-  const bf16* bias;       // [N] or null
+// Decode-shaped projections (<= 64 tokens) run as two kernels:
+//   split_kernel     workgroup = 8 waves over 128 rows of W and one K-slice.
+//                    The K-slice of every token's activation row is staged once
+//                    in LDS and shared by the 8 waves (activation fetch is
+//                    tokens/128 of the weight bytes); each wave streams its 16
+//                    W rows from HBM into MFMA A-fragments and writes fp32
+//                    partial sums for its K-slice.  Workgroups below
+//                    n_shrink_wg instead run LoRA-shrink items, one per wave.
+//   epilogue_kernel  sums the K-slice partials, adds bias and the LoRA expand,
+//                    rounds once to bf16 and stores each token's row into its
+//                    slot buffer (the scatter).
+constexpr int kKDepth = 8;            // k-steps of W in flight per wave
+constexpr int kLdsBudget = 64 * 1024;  // activation slice bytes per workgroup (default dynamic LDS limit)
+
+struct SplitArgs {
+  // base projection -> part[ks][tok][N]
+  const bf16* w;
   int64_t N, K;
   int32_t ntok;
+  int32_t n_rg, n_ks, n_base_wg;
+  int32_t total_steps, ks_steps;      // k-steps of 32 in K; max per K-slice
+  float* part;
+  const bf16* x[kSkinnyMaxTok];
+  // LoRA shrink items -> u[uks][urow][u_ld]
+  int32_t n_items, n_shrink_wg, u_ks, u_ld;
+  int64_t u_split_stride;
+  float* u;
+  const swl_lora_entry* table;
+  int32_t ngroups;
+  int32_t g_entry[kSkinnyMaxTok];
+  int32_t g_arows[kSkinnyMaxTok];
+  int32_t g_tile0[kSkinnyMaxTok + 1];
+  int32_t g_tok0[kSkinnyMaxTok + 1];
+  int32_t g_tok[kSkinnyMaxTok];
+  const bf16* g_x[kSkinnyMaxTok];
+};
+
+struct EpiArgs {
+  const float* part;
+  int32_t n_ks, ntok;
+  int64_t N;
+  const bf16* bias;
   int32_t has_lora;
-  const bf16* x[kSkinnyMaxTok];   // token input rows (length K)
-  bf16* y[kSkinnyMaxTok];         // token output rows (length N)
-  int32_t lora[kSkinnyMaxTok];    // lora table index per token (-1 none)
-  int32_t urow[kSkinnyMaxTok];    // row of the token in the shrink output
+  bf16* y[kSkinnyMaxTok];
+  int32_t lora[kSkinnyMaxTok];
+  int32_t urow[kSkinnyMaxTok];
   LoraEpi L;
 };
 
-struct SkinnyShrinkArgs {
-  const swl_lora_entry* table;
-  float* u;                       // [ksplit][u_rows][u_ld]
-  int64_t K;
-  int32_t u_ld;
-  int64_t u_split_stride;
-  int32_t ngroups;
-  int32_t ksplit;
-  int32_t g_entry[kSkinnyMaxTok];       // lora table index of the group
-  int32_t g_arows[kSkinnyMaxTok];       // rows of the group's stacked A (nblk * rank)
-  int32_t g_tile0[kSkinnyMaxTok + 1];   // prefix sum of 16-row tiles of A per group
-  int32_t g_tok0[kSkinnyMaxTok + 1];    // prefix sum into tok[]
-  int32_t tok[kSkinnyMaxTok];           // u row of each grouped token
-  const bf16* x[kSkinnyMaxTok];         // input row of each grouped token
-};
+__device__ __forceinline__ u32x4 lds16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-template <int TT, int U>
-__device__ __forceinline__ void load_batch(u32x4 (&w)[U], u32x4 (&x)[U][TT], const bf16* wp, const bf16* const (&xp)[TT],
-                                           int s) {
+// W (one row per lane, k-group per lane quarter) streamed through a D-deep
+// register pipeline; B-fragments of TT token tiles read from LDS.  The caller
+// has already issued the first D W-fragments into w[] (so their latency
+// overlaps the activation staging).  The steady-state body is branch-free so
+// s_waitcnt counts are exact.
+template <int TT, int D>
+__device__ __forceinline__ void kloop_lds(f32x4 (&acc)[TT], u32x4 (&w)[D], const bf16* wp, const bf16* xl,
+                                          int tstride, int nsteps) {
+  const int niter = nsteps / D;
+  if (niter > 0) {
+    for (int it = 0; it + 1 < niter; ++it) {
+      const int base = it * D, nxt = base + D;
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    w[u] = ld16(wp + 32 * (s + u));
+      for (int d = 0; d < D; ++d) {
 #pragma unroll
-    for (int t = 0; t < TT; ++t) x[u][t] = ld16(xp[t] + 32 * (s + u));
+        for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + t * tstride + 32 * (base + d)), acc[t]);
+        w[d] = ld16(wp + 32 * (nxt + d));
+      }
+    }
+    const int base = (niter - 1) * D;
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + t * tstride + 32 * (base + d)), acc[t]);
+  }
+  for (int s = niter * D; s < nsteps; ++s) {
+    const u32x4 w1 = ld16(wp + 32 * s);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w1, lds16(xl + t * tstride + 32 * s), acc[t]);
   }
 }
 
-template <int TT, int U>
-__device__ __forceinline__ void mma_batch(f32x4 (&acc)[TT], const u32x4 (&w)[U], const u32x4 (&x)[U][TT]) {
+// Same pipeline with B-fragments loaded from global memory (LoRA shrink: a
+// handful of tokens per adapter, so the activation traffic is small).
+template <int TT, int D>
+__device__ __forceinline__ void kloop_global(f32x4 (&acc)[TT], const bf16* wp, const bf16* const (&xp)[TT],
+                                             int nsteps) {
+  const int niter = nsteps / D;
+  if (niter > 0) {
+    u32x4 w[D], x[D][TT];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
+    for (int d = 0; d < D; ++d) {
+      w[d] = ld16(wp + 32 * d);
 #pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[u], x[u][t], acc[t]);
-}
-
-// Streams `nsteps` k-steps of 32 from wp (one W row per lane) against TT token
-// tiles, double-buffered in registers so one batch is in flight while the
-// previous one feeds the MFMAs.
-template <int TT>
-__device__ __forceinline__ void kloop(f32x4 (&acc)[TT], const bf16* wp, const bf16* const (&xp)[TT], int nsteps) {
-  constexpr int U = (TT <= 2) ? 4 : 2;
-  const int nb = nsteps / U;
-  u32x4 wA[U], xA[U][TT], wB[U], xB[U][TT];
-  if (nb > 0) load_batch<TT, U>(wA, xA, wp, xp, 0);
-  int b = 0;
-  for (; b + 2 <= nb; b += 2) {
-    load_batch<TT, U>(wB, xB, wp, xp, (b + 1) * U);
-    mma_batch<TT, U>(acc, wA, xA);
-    if (b + 2 < nb) load_batch<TT, U>(wA, xA, wp, xp, (b + 2) * U);
-    mma_batch<TT, U>(acc, wB, xB);
+      for (int t = 0; t < TT; ++t) x[d][t] = ld16(xp[t] + 32 * d);
+    }
+    for (int it = 0; it + 1 < niter; ++it) {
+      const int nxt = (it + 1) * D;
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], x[d][t], acc[t]);
+        w[d] = ld16(wp + 32 * (nxt + d));
+#pragma unroll
+        for (int t = 0; t < TT; ++t) x[d][t] = ld16(xp[t] + 32 * (nxt + d));
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], x[d][t], acc[t]);
   }
-  if (b < nb) mma_batch<TT, U>(acc, wA, xA);
-  for (int s = nb * U; s < nsteps; ++s) {
-    u32x4 w1 = ld16(wp + 32 * s);
+  for (int s = niter * D; s < nsteps; ++s) {
+    const u32x4 w1 = ld16(wp + 32 * s);
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = mfma16(w1, ld16(xp[t] + 32 * s), acc[t]);
   }
 }
 
-// Base projection for <= 64 tokens.  Workgroup = KW waves over one 16-row tile
-// of W; wave w covers the w-th slice of K.  Grid = ceil(N / 16).
-template <int TT, int KW>
-__global__ __launch_bounds__(KW * 64) void skinny_base_kernel(SkinnyBaseArgs a) {
-  __shared__ f32x4 red[KW][TT][64];
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int64_t row0 = (int64_t)blockIdx.x * 16;
-  const int64_t wrow = (row0 + (lane & 15) < a.N) ? row0 + (lane & 15) : a.N - 1;
-  const int nsteps_all = (int)(a.K >> 5);
-  const int s0 = (nsteps_all * wv) / KW, s1 = (nsteps_all * (wv + 1)) / KW;
-  const int koff = s0 * 32 + 8 * (lane >> 4);
-
-  const bf16* wp = a.w + wrow * a.K + koff;
+template <int TT>
+__device__ __forceinline__ void shrink_item(const SplitArgs& a, int item, int lane) {
+  const int tile = item / a.u_ks;
+  const int uks = item - tile * a.u_ks;
+  int g = 0;
+  while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
+  const int rt = tile - a.g_tile0[g];
+  const bf16* amat = reinterpret_cast<const bf16*>(a.table[a.g_entry[g]].a);
+  const int arow = min(rt * 16 + (lane & 15), a.g_arows[g] - 1);
+  const int st0 = (int)((int64_t)a.total_steps * uks / a.u_ks);
+  const int st1 = (int)((int64_t)a.total_steps * (uks + 1) / a.u_ks);
+  const int64_t koff = (int64_t)st0 * 32 + 8 * (lane >> 4);
+  const bf16* wp = amat + (int64_t)arow * a.K + koff;
+  const int t0 = a.g_tok0[g], cnt = a.g_tok0[g + 1] - t0;
   const bf16* xp[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) {
-    int tok = 16 * t + (lane & 15);
-    tok = tok < a.ntok ? tok : 0;
-    xp[t] = a.x[tok] + koff;
+    const int i = min(16 * t + (lane & 15), cnt - 1);
+    xp[t] = a.g_x[t0 + i] + koff;
   }
   f32x4 acc[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  kloop<TT>(acc, wp, xp, s1 - s0);
-
+  kloop_global<TT, (TT >= 4 ? 2 : 4)>(acc, wp, xp, st1 - st0);
+  const int q = rt * 16 + 4 * (lane >> 4);
 #pragma unroll
-  for (int t = 0; t < TT; ++t) red[wv][t][lane] = acc[t];
-  __syncthreads();
-  for (int t = wv; t < TT; t += KW) {
-    f32x4 s = red[0][t][lane];
-#pragma unroll
-    for (int w = 1; w < KW; ++w) s += red[w][t][lane];
-    const int tok = 16 * t + (lane & 15);
-    if (tok >= a.ntok) continue;
-    const int64_t n = row0 + 4 * (lane >> 4);
-    if (n >= a.N) continue;
-    float v[4] = {s[0], s[1], s[2], s[3]};
-    epilogue_store4(v, n, a.N, a.bias, a.L, a.has_lora ? a.lora[tok] : -1, a.urow[tok], a.y[tok]);
+  for (int t = 0; t < TT; ++t) {
+    const int i = 16 * t + (lane & 15);
+    if (i < cnt) {
+      float* dst = a.u + uks * a.u_split_stride + (int64_t)a.g_tok[t0 + i] * a.u_ld + q;
+      *reinterpret_cast<f32x4*>(dst) = acc[t];
+    }
   }
 }
 
-// LoRA shrink u[token, q] = x[token] . A[q]^T for groups of tokens that share
-// an adapter.  Grid = (total A tiles, ksplit); workgroup = KW waves that split
-// the k-split's range.  Output is one fp32 partial per k-split (the base
-// epilogue sums them), so no atomics and no clearing are needed.
-template <int TT, int KW>
-__global__ __launch_bounds__(KW * 64) void skinny_shrink_kernel(SkinnyShrinkArgs a) {
-  __shared__ f32x4 red[KW][TT][64];
+template <int TT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 16 / WAVES) void split_kernel(SplitArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16 xs[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int tile = blockIdx.x;
-  const int ks = blockIdx.y;
-  int g = 0;
-  while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
-  const bf16* amat = reinterpret_cast<const bf16*>(a.table[a.g_entry[g]].a);
-  const int rt = tile - a.g_tile0[g];
-  const int t0 = a.g_tok0[g], tcount = a.g_tok0[g + 1] - t0;
-
-  const int64_t klen = a.K / a.ksplit;
-  const int64_t kbeg = klen * ks;
-  const int nsteps_all = (int)(klen >> 5);
-  const int s0 = (nsteps_all * wv) / KW, s1 = (nsteps_all * (wv + 1)) / KW;
-  const int64_t koff = kbeg + s0 * 32 + 8 * (lane >> 4);
-
-  // rows past the stacked A (last tile of a rank that is not a multiple of
-  // 16) re-read the last row; their u columns are never consumed.
-  const int arow = min(rt * 16 + (lane & 15), a.g_arows[g] - 1);
-  const bf16* wp = amat + (int64_t)arow * a.K + koff;
-  const bf16* xp[TT];
-#pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    int i = 16 * t + (lane & 15);
-    i = i < tcount ? i : 0;
-    xp[t] = a.x[t0 + i] + koff;
+  if ((int)blockIdx.x < a.n_shrink_wg) {
+    // LoRA shrink: independent wave items, no workgroup barrier on this path
+    const int item = blockIdx.x * WAVES + wv;
+    if (item >= a.n_items) return;
+    int cnt_max = 0;
+    {
+      const int tile = item / a.u_ks;
+      int g = 0;
+      while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
+      cnt_max = a.g_tok0[g + 1] - a.g_tok0[g];
+    }
+    if (cnt_max <= 16) shrink_item<1>(a, item, lane);
+    else if (cnt_max <= 32) shrink_item<2>(a, item, lane);
+    else shrink_item<4>(a, item, lane);
+    return;
   }
+  const int b = blockIdx.x - a.n_shrink_wg;
+  const int rg = b % a.n_rg, ks = b / a.n_rg;
+  const int st0 = (int)((int64_t)a.total_steps * ks / a.n_ks);
+  const int st1 = (int)((int64_t)a.total_steps * (ks + 1) / a.n_ks);
+  const int nst = st1 - st0;
+  const int64_t kbeg = (int64_t)st0 * 32;
+  const int ld = a.ks_steps * 32 + 8;  // LDS row stride (elements), +16 B against bank conflicts
+
+  const int64_t r0 = (int64_t)rg * (16 * WAVES) + wv * 16;
+  const int64_t wrow = (r0 + (lane & 15) < a.N) ? r0 + (lane & 15) : a.N - 1;
+  const bf16* wp = a.w + wrow * a.K + kbeg + 8 * (lane >> 4);
+  // first W fragments go out before the activation staging
+  u32x4 w[kKDepth];
+  if (nst >= kKDepth) {
+#pragma unroll
+    for (int d = 0; d < kKDepth; ++d) w[d] = ld16(wp + 32 * d);
+  }
+
+  // stage x[:, kbeg : kbeg + 32*nst] for TT*16 token rows (zeros past ntok)
+  const int cpr = nst * 4;  // 16-byte chunks per row
+  for (int c = threadIdx.x; c < TT * 16 * cpr; c += WAVES * 64) {
+    const int r = c / cpr, cc = c - r * cpr;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (r < a.ntok) v = ld16(a.x[r] + kbeg + cc * 8);
+    *reinterpret_cast<u32x4*>(xs + r * ld + cc * 8) = v;
+  }
+  __syncthreads();
+
+  const bf16* xl = xs + (lane & 15) * ld + 8 * (lane >> 4);
   f32x4 acc[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  kloop<TT>(acc, wp, xp, s1 - s0);
+  kloop_lds<TT, kKDepth>(acc, w, wp, xl, 16 * ld, nst);
 
+  const int64_t n0 = r0 + 4 * (lane >> 4);
+  if (n0 < a.N) {
+    const bool vec = (n0 + 3 < a.N) && ((a.N & 3) == 0);
 #pragma unroll
-  for (int t = 0; t < TT; ++t) red[wv][t][lane] = acc[t];
-  __syncthreads();
-  for (int t = wv; t < TT; t += KW) {
-    f32x4 s = red[0][t][lane];
-#pragma unroll
-    for (int w = 1; w < KW; ++w) s += red[w][t][lane];
-    const int i = 16 * t + (lane & 15);
-    if (i >= tcount) continue;
-    const int q = rt * 16 + 4 * (lane >> 4);
-    float* dst = a.u + ks * a.u_split_stride + (int64_t)a.tok[t0 + i] * a.u_ld + q;
-    *reinterpret_cast<f32x4*>(dst) = s;
+    for (int t = 0; t < TT; ++t) {
+      const int tok = 16 * t + (lane & 15);
+      if (tok >= a.ntok) continue;
+      float* dst = a.part + ((int64_t)ks * a.ntok + tok) * a.N + n0;
+      if (vec) {
+        *reinterpret_cast<f32x4*>(dst) = acc[t];
+      } else {
+        for (int j = 0; j < 4; ++j)
+          if (n0 + j < a.N) dst[j] = acc[t][j];
+      }
+    }
   }
+}
+
+__global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
+  const int64_t quads = (a.N + 3) >> 2;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int tok = (int)(idx / quads);
+  if (tok >= a.ntok) return;
+  const int64_t n = (idx - (int64_t)tok * quads) * 4;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  const int64_t kstride = (int64_t)a.ntok * a.N;
+  const float* p = a.part + (int64_t)tok * a.N + n;
+  if (n + 3 < a.N && (a.N & 3) == 0) {
+    for (int ks = 0; ks < a.n_ks; ++ks) {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(p + ks * kstride);
+      v[0] += q[0]; v[1] += q[1]; v[2] += q[2]; v[3] += q[3];
+    }
+  } else {
+    for (int ks = 0; ks < a.n_ks; ++ks)
+      for (int j = 0; j < 4; ++j)
+        if (n + j < a.N) v[j] += p[ks * kstride + j];
+  }
+  epilogue_store4(v, n, a.N, a.bias, a.L, a.has_lora ? a.lora[tok] : -1, a.urow[tok], a.y[tok]);
 }
 
 // ------------------------------------------------------- tiled (M>64) -----
@@ -790,51 +876,208 @@ int fill_segptrs(SegPtrs& sp, const void* const* ptrs, const int64_t* rows, int 
   return SWL_OK;
 }
 
-template <int TT>
-int launch_skinny_base_tt(const SkinnyBaseArgs& a, int kw, hipStream_t st) {
-  const dim3 grid((unsigned)((a.N + 15) / 16));
-  switch (kw) {
-    case 4: hipLaunchKernelGGL((skinny_base_kernel<TT, 4>), grid, dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((skinny_base_kernel<TT, 8>), grid, dim3(512), 0, st, a); break;
-    default: hipLaunchKernelGGL((skinny_base_kernel<TT, 16>), grid, dim3(1024), 0, st, a); break;
+// Launch-shape tuning of the decode path.  Defaults are the measured best on
+// MI355X; SWL_SKINNY_WAVES (4 or 8) and SWL_SKINNY_TARGET_WG override them for
+// sweeps.
+struct Tuning {
+  int waves = 8;
+  int target_wg = 256;
+};
+const Tuning& tuning() {
+  static Tuning t = [] {
+    Tuning v;
+    if (const char* e = getenv("SWL_SKINNY_WAVES")) v.waves = (atoi(e) == 4) ? 4 : 8;
+    if (const char* e = getenv("SWL_SKINNY_TARGET_WG")) v.target_wg = std::max(1, atoi(e));
+    return v;
+  }();
+  return t;
+}
+
+// Adapter groups for the LoRA shrink: tokens that share a lora table entry.
+struct ShrinkPlan {
+  int ngroups = 0, tiles = 0, max_cnt = 0;
+  int32_t g_entry[kSkinnyMaxTok];
+  int32_t g_arows[kSkinnyMaxTok];
+  int32_t g_tile0[kSkinnyMaxTok + 1];
+  int32_t g_tok0[kSkinnyMaxTok + 1];
+  int32_t g_tok[kSkinnyMaxTok];
+  const bf16* g_x[kSkinnyMaxTok];
+};
+
+// tok_lora[i] >= 0: token i uses entry tok_lora[i]; u row of token i is
+// urow0 + i.  Tokens are grouped per entry so each adapter's A is read once.
+int plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const bf16* const* xrows, int urow0,
+                const swl_lora_entry* host_entries, int nblk) {
+  p.ngroups = 0;
+  p.tiles = 0;
+  p.max_cnt = 0;
+  int nt = 0;
+  for (int i = 0; i < ntok; ++i) {
+    const int e = tok_lora[i];
+    if (e < 0) continue;
+    bool seen = false;
+    for (int g = 0; g < p.ngroups; ++g) seen |= (p.g_entry[g] == e);
+    if (seen) continue;
+    const int g = p.ngroups++;
+    p.g_entry[g] = e;
+    p.g_arows[g] = host_entries[e].rank * nblk;
+    p.g_tile0[g] = p.tiles;
+    p.g_tok0[g] = nt;
+    p.tiles += (p.g_arows[g] + 15) / 16;
+    int cnt = 0;
+    for (int j = i; j < ntok; ++j)
+      if (tok_lora[j] == e) {
+        p.g_tok[nt] = urow0 + j;
+        p.g_x[nt] = xrows[j];
+        ++nt;
+        ++cnt;
+      }
+    p.max_cnt = std::max(p.max_cnt, cnt);
   }
-  SWL_LAUNCH_CHECK("skinny_base_kernel launch");
+  p.g_tile0[p.ngroups] = p.tiles;
+  p.g_tok0[p.ngroups] = nt;
   return SWL_OK;
 }
 
-int launch_skinny_base(const SkinnyBaseArgs& a, hipStream_t st) {
-  const int tt = (a.ntok + 15) / 16;
-  // Waves per workgroup: enough workgroups to cover the chip, and each wave
-  // keeps >= 8 k-steps so its loads stay pipelined.
-  const int64_t tiles = (a.N + 15) / 16;
-  const int64_t ksteps = a.K / 32;
-  int kw = 8;
-  if (tiles < 512 && ksteps >= 16 * 16) kw = 16;
-  if (ksteps < 8 * 8) kw = 4;
-  switch (tt) {
-    case 1: return launch_skinny_base_tt<1>(a, kw, st);
-    case 2: return launch_skinny_base_tt<2>(a, kw, st);
-    case 3: return launch_skinny_base_tt<3>(a, kw, st);
-    default: return launch_skinny_base_tt<4>(a, kw, st);
+void copy_shrink(SplitArgs& a, const ShrinkPlan& p) {
+  a.ngroups = p.ngroups;
+  for (int g = 0; g < p.ngroups; ++g) {
+    a.g_entry[g] = p.g_entry[g];
+    a.g_arows[g] = p.g_arows[g];
+    a.g_tile0[g] = p.g_tile0[g];
+    a.g_tok0[g] = p.g_tok0[g];
+  }
+  a.g_tile0[p.ngroups] = p.g_tile0[p.ngroups];
+  a.g_tok0[p.ngroups] = p.g_tok0[p.ngroups];
+  for (int i = 0; i < p.g_tok0[p.ngroups]; ++i) {
+    a.g_tok[i] = p.g_tok[i];
+    a.g_x[i] = p.g_x[i];
   }
 }
 
-template <int TT>
-int launch_skinny_shrink_tt(const SkinnyShrinkArgs& a, int tiles, hipStream_t st) {
-  const dim3 grid((unsigned)tiles, (unsigned)a.ksplit);
-  hipLaunchKernelGGL((skinny_shrink_kernel<TT, 8>), grid, dim3(512), 0, st, a);
-  SWL_LAUNCH_CHECK("skinny_shrink_kernel launch");
+// K-slices per LoRA-shrink item: ~16 k-steps of A per wave.
+int shrink_ksplit(int64_t total_steps) { return (int)std::max<int64_t>(1, total_steps / 16); }
+
+// Decode-shaped projection of ntok (<= 64) token rows: y[i] = x[i] . W^T
+// (+ bias) (+ LoRA delta of entry tok_lora[i]).  xrows[i] / yrows[i] are the
+// token's input / output rows (slot buffers).
+int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok, const bf16* const* xrows,
+                  bf16* const* yrows, const int32_t* tok_lora, const swl_lora_entry* table,
+                  const swl_lora_entry* host_entries, const LoraEpi* Lblk, int nblk, hipStream_t st) {
+  const int TT = (ntok + 15) / 16;
+  const int64_t total_steps = K / 32;
+  SplitArgs a{};
+  a.w = w;
+  a.N = N;
+  a.K = K;
+  a.ntok = ntok;
+  a.total_steps = (int)total_steps;
+  const Tuning& tu = tuning();
+  const int waves = tu.waves;
+  a.n_rg = (int)((N + 16 * waves - 1) / (16 * waves));
+  const int64_t max_steps_lds = ((int64_t)kLdsBudget / (TT * 16 * 2) - 8) / 32;
+  int64_t n_ks = std::max<int64_t>((tu.target_wg + a.n_rg - 1) / a.n_rg,
+                                   (total_steps + max_steps_lds - 1) / max_steps_lds);
+  n_ks = std::min<int64_t>(n_ks, total_steps);
+  a.n_ks = (int)n_ks;
+  a.ks_steps = (int)((total_steps + n_ks - 1) / n_ks);
+  a.n_base_wg = a.n_rg * a.n_ks;
+  for (int i = 0; i < ntok; ++i) a.x[i] = xrows[i];
+
+  bool has_lora = false;
+  if (tok_lora)
+    for (int i = 0; i < ntok; ++i) has_lora |= tok_lora[i] >= 0;
+  int max_r = 0;
+  ShrinkPlan sp;
+  if (has_lora) {
+    plan_shrink(sp, ntok, tok_lora, xrows, 0, host_entries, nblk);
+    for (int g = 0; g < sp.ngroups; ++g) max_r = std::max(max_r, host_entries[sp.g_entry[g]].rank);
+    a.u_ks = shrink_ksplit(total_steps);
+    a.n_items = sp.tiles * a.u_ks;
+    a.n_shrink_wg = (a.n_items + waves - 1) / waves;
+    a.u_ld = ((max_r * nblk + 15) / 16) * 16;
+    a.u_split_stride = (int64_t)ntok * a.u_ld;
+    a.table = table;
+    copy_shrink(a, sp);
+  }
+  const size_t part_bytes = sizeof(float) * (size_t)a.n_ks * ntok * N;
+  const size_t part_al = (part_bytes + 255) & ~(size_t)255;
+  const size_t u_bytes = has_lora ? sizeof(float) * (size_t)a.u_ks * a.u_split_stride : 0;
+  void* scratch = nullptr;
+  int rc = scratch_get(part_al + u_bytes, st, &scratch);
+  if (rc) return rc;
+  a.part = reinterpret_cast<float*>(scratch);
+  a.u = has_lora ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + part_al) : nullptr;
+
+  const size_t lds = sizeof(bf16) * (size_t)TT * 16 * ((size_t)a.ks_steps * 32 + 8);
+  const dim3 grid((unsigned)(a.n_shrink_wg + a.n_base_wg));
+  const dim3 block((unsigned)(waves * 64));
+  if (waves == 4) {
+    switch (TT) {
+      case 1: hipLaunchKernelGGL((split_kernel<1, 4>), grid, block, lds, st, a); break;
+      case 2: hipLaunchKernelGGL((split_kernel<2, 4>), grid, block, lds, st, a); break;
+      case 3: hipLaunchKernelGGL((split_kernel<3, 4>), grid, block, lds, st, a); break;
+      default: hipLaunchKernelGGL((split_kernel<4, 4>), grid, block, lds, st, a); break;
+    }
+  } else {
+    switch (TT) {
+      case 1: hipLaunchKernelGGL((split_kernel<1, 8>), grid, block, lds, st, a); break;
+      case 2: hipLaunchKernelGGL((split_kernel<2, 8>), grid, block, lds, st, a); break;
+      case 3: hipLaunchKernelGGL((split_kernel<3, 8>), grid, block, lds, st, a); break;
+      default: hipLaunchKernelGGL((split_kernel<4, 8>), grid, block, lds, st, a); break;
+    }
+  }
+  SWL_LAUNCH_CHECK("split_kernel launch");
+
+  EpiArgs e{};
+  e.part = a.part;
+  e.n_ks = a.n_ks;
+  e.ntok = ntok;
+  e.N = N;
+  e.bias = bias;
+  e.has_lora = has_lora ? 1 : 0;
+  for (int i = 0; i < ntok; ++i) {
+    e.y[i] = yrows[i];
+    e.lora[i] = (has_lora && tok_lora[i] >= 0) ? tok_lora[i] : -1;
+    e.urow[i] = i;
+  }
+  if (has_lora) {
+    e.L = *Lblk;
+    e.L.table = table;
+    e.L.u = a.u;
+    e.L.usplit = a.u_ks;
+    e.L.u_ld = a.u_ld;
+    e.L.u_split_stride = a.u_split_stride;
+  }
+  const int64_t quads = (N + 3) / 4;
+  const unsigned eg = (unsigned)(((int64_t)ntok * quads + 255) / 256);
+  hipLaunchKernelGGL(epilogue_kernel, dim3(eg), dim3(256), 0, st, e);
+  SWL_LAUNCH_CHECK("epilogue_kernel launch");
   return SWL_OK;
 }
 
-int launch_skinny_shrink(const SkinnyShrinkArgs& a, int tiles, int max_group_tok, hipStream_t st) {
-  const int tt = (max_group_tok + 15) / 16;
-  switch (tt) {
-    case 1: return launch_skinny_shrink_tt<1>(a, tiles, st);
-    case 2: return launch_skinny_shrink_tt<2>(a, tiles, st);
-    case 3: return launch_skinny_shrink_tt<3>(a, tiles, st);
-    default: return launch_skinny_shrink_tt<4>(a, tiles, st);
-  }
+// LoRA shrink alone for up to 64 tokens of the packed prefill batch
+// (u rows are packed rows); used by the tiled path.
+int launch_shrink_only(int64_t K, int ntok, const bf16* const* xrows, const int32_t* tok_lora, int urow0,
+                       const swl_lora_entry* table, const swl_lora_entry* host_entries, int nblk, float* u,
+                       int u_ld, int64_t u_split_stride, int u_ks, hipStream_t st) {
+  ShrinkPlan sp;
+  plan_shrink(sp, ntok, tok_lora, xrows, urow0, host_entries, nblk);
+  if (sp.ngroups == 0) return SWL_OK;
+  SplitArgs a{};
+  a.K = K;
+  a.total_steps = (int)(K / 32);
+  a.u_ks = u_ks;
+  a.n_items = sp.tiles * u_ks;
+  a.n_shrink_wg = (a.n_items + 7) / 8;
+  a.u_ld = u_ld;
+  a.u_split_stride = u_split_stride;
+  a.u = u;
+  a.table = table;
+  copy_shrink(a, sp);
+  hipLaunchKernelGGL((split_kernel<1, 8>), dim3((unsigned)a.n_shrink_wg), dim3(8 * 64), 0, st, a);
+  SWL_LAUNCH_CHECK("split_kernel (shrink) launch");
+  return SWL_OK;
 }
 
 }  // namespace
@@ -910,20 +1153,14 @@ int swl_gemm_bf16(const void* x, const void* w, const void* bias, void* y, int64
   if (m == 0) return SWL_OK;
   hipStream_t st = (hipStream_t)stream;
   if (m <= kSkinnyMaxTok) {
-    SkinnyBaseArgs a{};
-    a.w = reinterpret_cast<const bf16*>(w);
-    a.bias = reinterpret_cast<const bf16*>(bias);
-    a.N = n;
-    a.K = k;
-    a.ntok = (int)m;
-    a.has_lora = 0;
+    const bf16* xr[kSkinnyMaxTok];
+    bf16* yr[kSkinnyMaxTok];
     for (int i = 0; i < m; ++i) {
-      a.x[i] = reinterpret_cast<const bf16*>(x) + (int64_t)i * k;
-      a.y[i] = reinterpret_cast<bf16*>(y) + (int64_t)i * n;
-      a.lora[i] = -1;
-      a.urow[i] = 0;
+      xr[i] = reinterpret_cast<const bf16*>(x) + (int64_t)i * k;
+      yr[i] = reinterpret_cast<bf16*>(y) + (int64_t)i * n;
     }
-    return launch_skinny_base(a, st);
+    return launch_skinny(reinterpret_cast<const bf16*>(w), reinterpret_cast<const bf16*>(bias), n, k, (int)m, xr, yr,
+                         nullptr, nullptr, nullptr, nullptr, 1, st);
   }
   SWL_CHECK(k % TK == 0, SWL_ERR_INVALID, "swl_gemm_bf16: k must be a multiple of 64 for m > 64");
   TiledArgs a{};
@@ -944,22 +1181,13 @@ int swl_gemm_bf16(const void* x, const void* w, const void* bias, void* y, int64
 
 int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
                    const void* bias, int64_t n, int64_t k, const int32_t* seg_lora, const swl_lora_entry* lora_table,
-                   int nblk, const int64_t* blk_cols, void* stream) {
-  hipStream_t st = (hipStream_t)stream;
-  std::vector<swl_lora_entry> host_entries;
+                   const swl_lora_entry* lora_table_host, int nblk, const int64_t* blk_cols, void* stream) {
   if (seg_lora) {
-    SWL_CHECK(lora_table != nullptr, SWL_ERR_INVALID, "swl_round_bf16: seg_lora given without lora_table");
-    SWL_CHECK(n_seg >= 1 && n_seg <= kMaxSeg, SWL_ERR_INVALID, "segment count must be in [1, 128]");
-    int maxi = -1;
-    for (int i = 0; i < n_seg; ++i) maxi = std::max(maxi, (int)seg_lora[i]);
-    if (maxi >= 0) {
-      host_entries.resize(maxi + 1);
-      SWL_HIP(hipMemcpy(host_entries.data(), lora_table, sizeof(swl_lora_entry) * (maxi + 1),
-                        hipMemcpyDeviceToHost));
-    }
+    SWL_CHECK(lora_table != nullptr && lora_table_host != nullptr, SWL_ERR_INVALID,
+              "swl_round_bf16: seg_lora needs lora_table and lora_table_host");
   }
-  return swl::round_launch(n_seg, rows, seg_in, seg_out, w, bias, n, k, seg_lora, lora_table,
-                           host_entries.empty() ? nullptr : host_entries.data(), nblk, blk_cols, st);
+  return swl::round_launch(n_seg, rows, seg_in, seg_out, w, bias, n, k, seg_lora, lora_table, lora_table_host, nblk,
+                           blk_cols, (hipStream_t)stream);
 }
 
 int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int trans_b, void* y, int64_t ldy,
@@ -1098,72 +1326,19 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
 
   if (T <= kSkinnyMaxTok) {
     // ---------------------------------------------------- decode regime
-    SkinnyBaseArgs a{};
-    a.w = reinterpret_cast<const bf16*>(w);
-    a.bias = reinterpret_cast<const bf16*>(bias);
-    a.N = N;
-    a.K = K;
-    a.ntok = (int)T;
+    const bf16* xr[kSkinnyMaxTok];
+    bf16* yr[kSkinnyMaxTok];
+    int32_t tl[kSkinnyMaxTok];
     int t = 0;
     for (int i = 0; i < n_seg; ++i) {
       for (int64_t j = 0; j < rows[i]; ++j, ++t) {
-        a.x[t] = reinterpret_cast<const bf16*>(seg_in[i]) + j * K;
-        a.y[t] = reinterpret_cast<bf16*>(seg_out[i]) + j * N;
-        a.lora[t] = (has_lora && seg_lora[i] >= 0) ? seg_lora[i] : -1;
-        a.urow[t] = t;
+        xr[t] = reinterpret_cast<const bf16*>(seg_in[i]) + j * K;
+        yr[t] = reinterpret_cast<bf16*>(seg_out[i]) + j * N;
+        tl[t] = (has_lora && seg_lora[i] >= 0) ? seg_lora[i] : -1;
       }
     }
-    if (has_lora) {
-      // group tokens by adapter entry: each adapter's A is streamed once
-      SkinnyShrinkArgs s{};
-      s.table = lora_table;
-      s.K = K;
-      s.u_ld = u_ld;
-      std::vector<int> entries;
-      for (int i = 0; i < T; ++i)
-        if (a.lora[i] >= 0 && std::find(entries.begin(), entries.end(), a.lora[i]) == entries.end())
-          entries.push_back(a.lora[i]);
-      s.ngroups = (int)entries.size();
-      int tiles = 0, nt = 0, max_group = 0;
-      for (int g = 0; g < s.ngroups; ++g) {
-        s.g_entry[g] = entries[g];
-        s.g_arows[g] = host_entries[entries[g]].rank * nblk;
-        s.g_tile0[g] = tiles;
-        s.g_tok0[g] = nt;
-        const swl_lora_entry& e = host_entries[entries[g]];
-        tiles += (e.rank * nblk + 15) / 16;
-        int cnt = 0;
-        for (int i = 0; i < T; ++i)
-          if (a.lora[i] == entries[g]) {
-            s.tok[nt] = i;
-            s.x[nt] = a.x[i];
-            ++nt;
-            ++cnt;
-          }
-        max_group = std::max(max_group, cnt);
-      }
-      s.g_tile0[s.ngroups] = tiles;
-      s.g_tok0[s.ngroups] = nt;
-      // split K across workgroups until there are enough of them
-      int ksplit = 1;
-      const int64_t ksteps = K / 32;
-      while (tiles * ksplit < 256 && ksteps % (ksplit * 2) == 0 && ksteps / (ksplit * 2) >= 64) ksplit *= 2;
-      s.ksplit = ksplit;
-      s.u_split_stride = (int64_t)T * u_ld;
-      void* scratch = nullptr;
-      int rc = scratch_get(sizeof(float) * (size_t)ksplit * (size_t)s.u_split_stride, st, &scratch);
-      if (rc) return rc;
-      s.u = reinterpret_cast<float*>(scratch);
-      rc = launch_skinny_shrink(s, tiles, max_group, st);
-      if (rc) return rc;
-      a.has_lora = 1;
-      a.L = L;
-      a.L.u = s.u;
-      a.L.usplit = ksplit;
-      a.L.u_ld = u_ld;
-      a.L.u_split_stride = s.u_split_stride;
-    }
-    return launch_skinny_base(a, st);
+    return launch_skinny(reinterpret_cast<const bf16*>(w), reinterpret_cast<const bf16*>(bias), N, K, (int)T, xr, yr,
+                         has_lora ? tl : nullptr, lora_table, host_entries, &L, nblk, st);
   }
 
   // ------------------------------------------------------ prefill regime
@@ -1192,34 +1367,21 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   if (rc) return rc;
   if (has_lora) {
     float* u = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + xbytes_al);
-    // shrink per segment in chunks of <= 64 tokens (A re-read per chunk)
+    // shrink per segment in chunks of <= 64 packed rows (A re-read per chunk)
     for (int i = 0; i < n_seg; ++i) {
       a.seg_lora[i] = (seg_lora[i] >= 0 && rows[i] > 0) ? seg_lora[i] : -1;
       if (a.seg_lora[i] < 0) continue;
-      const swl_lora_entry& e = host_entries[seg_lora[i]];
-      const int tiles = (e.rank * nblk + 15) / 16;
       for (int64_t c0 = 0; c0 < rows[i]; c0 += kSkinnyMaxTok) {
         const int cnt = (int)std::min<int64_t>(kSkinnyMaxTok, rows[i] - c0);
-        SkinnyShrinkArgs s{};
-        s.table = lora_table;
-        s.K = K;
-        s.u_ld = u_ld;
-        s.u = u;
-        s.u_split_stride = (int64_t)T * u_ld;
-        s.ksplit = 1;
-        s.ngroups = 1;
-        s.g_entry[0] = seg_lora[i];
-        s.g_arows[0] = e.rank * nblk;
-        s.g_tile0[0] = 0;
-        s.g_tile0[1] = tiles;
-        s.g_tok0[0] = 0;
-        s.g_tok0[1] = cnt;
+        const bf16* xr[kSkinnyMaxTok];
+        int32_t tl[kSkinnyMaxTok];
+        const int64_t prow0 = a.out.off[i] + c0;
         for (int j = 0; j < cnt; ++j) {
-          const int64_t prow = a.out.off[i] + c0 + j;
-          s.tok[j] = (int)prow;
-          s.x[j] = packed + prow * K;
+          xr[j] = packed + (prow0 + j) * K;
+          tl[j] = seg_lora[i];
         }
-        rc = launch_skinny_shrink(s, tiles, cnt, st);
+        rc = launch_shrink_only(K, cnt, xr, tl, (int)prow0, lora_table, host_entries, nblk, u, u_ld,
+                                (int64_t)T * u_ld, 1, st);
         if (rc) return rc;
       }
     }

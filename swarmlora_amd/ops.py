@@ -142,13 +142,21 @@ class LoraTable:
         self._dev = None
         return len(self._entries) - 1
 
-    def device_table(self) -> torch.Tensor:
+    def _sync(self):
         if self._dev is None:
             n = len(self._entries)
-            raw = (LoraEntry * max(n, 1))(*self._entries)
-            host = torch.frombuffer(bytearray(bytes(raw)), dtype=torch.uint8)
+            self._host = (LoraEntry * max(n, 1))(*self._entries)
+            host = torch.frombuffer(bytearray(bytes(self._host)), dtype=torch.uint8)
             self._dev = host.to(self.device)
+
+    def device_table(self) -> torch.Tensor:
+        self._sync()
         return self._dev
+
+    def host_table(self):
+        """ctypes array of the same records (host memory)."""
+        self._sync()
+        return self._host
 
     def __len__(self):
         return len(self._entries)
@@ -174,6 +182,7 @@ def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor],
         _need(bias, "bias")
     lora_arr = None
     tab_ptr = ctypes.c_void_p(0)
+    host_tab = ctypes.c_void_p(0)
     blk = None
     nblk = 0
     if seg_lora is not None:
@@ -183,10 +192,12 @@ def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor],
             raise ValueError("seg_lora index out of range")
         lora_arr = _i32_array(seg_lora)
         tab_ptr = _ptr(table.device_table())
+        host_tab = ctypes.cast(table.host_table(), ctypes.c_void_p)
         blk = _i64_array(blk_cols)
         nblk = len(blk_cols)
     _lib.check(_lib.load().swl_round_bf16(len(rows), _i64_array(rows), _ptr_array(seg_in), _ptr_array(seg_out),
-                                          _ptr(w), _ptr(bias), n, k, lora_arr, tab_ptr, nblk, blk, _stream()))
+                                          _ptr(w), _ptr(bias), n, k, lora_arr, tab_ptr, host_tab, nblk, blk,
+                                          _stream()))
 
 
 def matmul(x: torch.Tensor, b: torch.Tensor, trans_b: bool, alpha: float = 1.0,
