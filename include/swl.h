@@ -133,17 +133,22 @@ int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb,
                     int64_t k, float alpha, void* stream);
 
 /* Paged-KV attention for one q_len group, replacing
- * WorkerBatchedOps.batch_flash_attention (worker_sync.py:169-205):
- *   1. NeoX RoPE in place on q [nseq, q_len, hq, d] and k [nseq, q_len, hkv, d]
- *      at positions[nseq * q_len] using cos_sin [max_pos, d] (cos | sin halves,
- *      the cache of paged_attention.py:131-142), when rope != 0;
+ * WorkerBatchedOps.batch_flash_attention (worker_sync.py:169-205).  Token t
+ * (t = seq * q_len + i) has its query heads at q + t*q_stride ([hq, d]), its
+ * new key heads at k + t*k_stride and value heads at v + t*v_stride ([hkv, d]);
+ * strides are in elements, so q/k/v can be read in place from the fused QKV
+ * output rows ([q | k | v], stride hq*d + 2*hkv*d).
+ *   1. NeoX RoPE in place on the q and k heads at positions[nseq * q_len]
+ *      using cos_sin [max_pos, d] (cos | sin halves, the cache of
+ *      paged_attention.py:131-142), when rope != 0;
  *   2. append k and v into the pages k_cache / v_cache
  *      [num_blocks, block_size, hkv, d] at cache_seqlens[s] + i through
  *      block_table [nseq, max_blocks] (int32);
  *   3. causal GQA attention of each query over cache_seqlens[s] + i + 1 keys,
  *      scale softmax_scale, written to out [nseq, q_len, hq * d].
  * d must be 128; hq % hkv == 0; q_len <= 1024. */
-int swl_paged_attention_bf16(void* q, void* k, const void* v, int nseq, int q_len,
+int swl_paged_attention_bf16(void* q, void* k, const void* v, int64_t q_stride,
+                             int64_t k_stride, int64_t v_stride, int nseq, int q_len,
                              int hq, int hkv, int d, void* k_cache, void* v_cache,
                              int64_t num_blocks, int block_size,
                              const int32_t* block_table, int64_t max_blocks,
@@ -157,6 +162,24 @@ int swl_paged_attention_bf16(void* q, void* k, const void* v, int nseq, int q_le
  * Replaces index_fill_(0, blocks, 0) per layer, paged_attention.py:77-89. */
 int swl_zero_blocks_bf16(void* const* caches, int ncache, const int64_t* block_ids,
                          int64_t nblocks, int64_t block_elems, void* stream);
+
+/* Embedding lookup for n segments of int64 token ids: out[i][j, :] =
+ * table[clamp(ids[i][j], 0, vocab - 1), :].  ids / rows / out are HOST arrays
+ * of device pointers / counts.  Replaces torch::embedding of clamped ids,
+ * ext_aggregator.cpp:660-705. */
+int swl_embed_bf16(const void* const* ids, const int64_t* rows, int n, const void* table, int64_t vocab,
+                   int64_t hidden, void* const* out, void* stream);
+
+/* Next token per logits row (logits bf16 [n, vocab], n <= 128): argmax (first
+ * index of the maximum) when do_sample[i] == 0, otherwise temperature, top-k,
+ * top-p and a multinomial draw from a counter-based generator seeded by
+ * (seed, row).  out_tok[i] is a device int64 (the slot output buffer).
+ * Replaces the sampling block of ext_aggregator.cpp:756-795 / :818-874.
+ * Sampled tokens follow the same distribution as the reference, not its
+ * random stream. */
+int swl_sample_bf16(const void* logits, int64_t n, int64_t vocab, void* const* out_tok, const int32_t* do_sample,
+                    const float* temperature, const int32_t* top_k, const float* top_p, uint64_t seed,
+                    void* stream);
 
 #ifdef __cplusplus
 }

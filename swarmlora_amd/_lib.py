@@ -69,9 +69,12 @@ _SIGS = {
                                P_i64, c_vp]),
     "swl_matmul_bf16": (c_int, [c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
                                 c_vp]),
-    "swl_paged_attention_bf16": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp,
-                                         c_i64, c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_f32,
-                                         c_vp, c_vp]),
+    "swl_paged_attention_bf16": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_int, c_int,
+                                         c_vp, c_vp, c_i64, c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int,
+                                         c_f32, c_vp, c_vp]),
+    "swl_embed_bf16": (c_int, [P_vp, P_i64, c_int, c_vp, c_i64, c_i64, P_vp, c_vp]),
+    "swl_sample_bf16": (c_int, [c_vp, c_i64, c_i64, P_vp, P_i32, ctypes.POINTER(c_f32), P_i32,
+                                ctypes.POINTER(c_f32), c_u64, c_vp]),
     "swl_zero_blocks_bf16": (c_int, [P_vp, c_int, c_vp, c_i64, c_i64, c_vp]),
 }
 

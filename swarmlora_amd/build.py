@@ -21,6 +21,7 @@ BUILD_DIR = os.path.join(REPO_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libswl.so")
 
 ARCH = os.environ.get("SWL_OFFLOAD_ARCH", "gfx950")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 SOURCES = [
     "kernels.hip",
@@ -49,9 +50,10 @@ def _compile(src):
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
     cmd = [hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
-        # host-only translation units: compile as HIP host code (no device objects)
-        cmd = [hipcc(), "-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}",
-               "-D__HIP_PLATFORM_AMD__", "-c", os.path.join(CSRC, src), "-o", obj]
+        # host-only translation units (runtime, no kernels): plain g++ against
+        # the HIP runtime headers
+        cmd = [shutil.which("g++") or "g++", "-O3", "-std=c++17", "-fPIC", "-Wall", f"-I{INCLUDE}", f"-I{CSRC}",
+               f"-I{ROCM}/include", "-D__HIP_PLATFORM_AMD__", "-c", os.path.join(CSRC, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "packed-fp32-ops' is not a recognized feature"
     err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)

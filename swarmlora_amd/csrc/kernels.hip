@@ -669,9 +669,10 @@ __global__ __launch_bounds__(256) void matmul_generic_kernel(const bf16* __restr
 
 // ------------------------------------------------------ paged attention ---
 struct AttnArgs {
-  bf16* q;               // [nseq, L, hq, 128]
-  bf16* k;               // [nseq, L, hkv, 128]
-  const bf16* v;         // [nseq, L, hkv, 128]
+  bf16* q;               // token t at q + t*qs: [hq, 128]
+  bf16* k;               // token t at k + t*ks: [hkv, 128]
+  const bf16* v;         // token t at v + t*vs: [hkv, 128]
+  int64_t qs, ks, vs;    // token row strides (elements)
   bf16* kc;              // [num_blocks, bs, hkv, 128]
   bf16* vc;
   const int32_t* bt;     // [nseq, max_blocks]
@@ -695,8 +696,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(AttnArgs a) {
   const int nh = a.hq + a.hkv;
   for (int it = threadIdx.x; it < nh * 64; it += blockDim.x) {
     const int h = it >> 6, d = it & 63;
-    bf16* base = (h < a.hq) ? a.q + ((int64_t)tokid * a.hq + h) * 128
-                            : a.k + ((int64_t)tokid * a.hkv + (h - a.hq)) * 128;
+    bf16* base = (h < a.hq) ? a.q + (int64_t)tokid * a.qs + h * 128
+                            : a.k + (int64_t)tokid * a.ks + (h - a.hq) * 128;
     if (do_rope) {
       const float c = bf2f(cs[d]), sn = bf2f(cs[64 + d]);
       const float x1 = bf2f(base[d]), x2 = bf2f(base[d + 64]);
@@ -711,10 +712,11 @@ __global__ __launch_bounds__(256) void rope_append_kernel(AttnArgs a) {
   const int32_t blk = a.bt[(int64_t)s * a.max_blocks + blk_i];
   if (blk < 0 || blk >= a.num_blocks) return;
   const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * a.hkv * 128;
-  const int64_t src = (int64_t)tokid * a.hkv * 128;
+  const bf16* ksrc = a.k + (int64_t)tokid * a.ks;
+  const bf16* vsrc = a.v + (int64_t)tokid * a.vs;
   for (int e = threadIdx.x; e < a.hkv * 16; e += blockDim.x) {
-    reinterpret_cast<u32x4*>(a.kc + dst)[e] = reinterpret_cast<const u32x4*>(a.k + src)[e];
-    reinterpret_cast<u32x4*>(a.vc + dst)[e] = reinterpret_cast<const u32x4*>(a.v + src)[e];
+    reinterpret_cast<u32x4*>(a.kc + dst)[e] = reinterpret_cast<const u32x4*>(ksrc)[e];
+    reinterpret_cast<u32x4*>(a.vc + dst)[e] = reinterpret_cast<const u32x4*>(vsrc)[e];
   }
 }
 
@@ -736,7 +738,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const bf16* qp = a.q + (((int64_t)s * a.L + i) * a.hq + h * G + g) * 128 + dl;
+    const bf16* qp = a.q + ((int64_t)s * a.L + i) * a.qs + (h * G + g) * 128 + dl;
     unpack8(ld16(qp), qv[g]);
 #pragma unroll
     for (int d = 0; d < 8; ++d) qv[g][d] *= a.scale;
@@ -818,6 +820,181 @@ __global__ void zero_blocks_kernel(bf16* cache, const int64_t* ids, int64_t nblo
   u32x4* p = reinterpret_cast<u32x4*>(cache + ids[b] * block_elems);
   const int64_t nv = block_elems >> 3;
   for (int64_t e = threadIdx.x; e < nv; e += blockDim.x) p[e] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// ------------------------------------------------------ embed / LM head ---
+struct EmbedArgs {
+  int32_t n;
+  int64_t off[kMaxSeg + 1];
+  const int64_t* ids[kMaxSeg];
+  bf16* out[kMaxSeg];
+  const bf16* table;
+  int64_t vocab, hidden;
+};
+
+// One workgroup per token: out row = table[clamp(id, 0, vocab - 1)]
+// (torch::embedding of clamped ids, ext_aggregator.cpp:660-705).
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+  const int64_t row = blockIdx.x;
+  const int s = find_seg(a.off, a.n, row);
+  const int64_t j = row - a.off[s];
+  int64_t id = a.ids[s][j];
+  id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);
+  const u32x4* src = reinterpret_cast<const u32x4*>(a.table + id * a.hidden);
+  u32x4* dst = reinterpret_cast<u32x4*>(a.out[s] + j * a.hidden);
+  for (int64_t i = threadIdx.x; i < (a.hidden >> 3); i += blockDim.x) dst[i] = src[i];
+}
+
+struct SampleArgs {
+  const bf16* logits;       // [n, vocab]
+  int64_t vocab;
+  int64_t* out_tok[kMaxSeg];
+  int32_t do_sample[kMaxSeg];
+  float temperature[kMaxSeg];
+  int32_t top_k[kMaxSeg];
+  float top_p[kMaxSeg];
+  uint64_t seed;
+};
+
+// order-preserving map of a float to uint32 (larger float -> larger key)
+__device__ __forceinline__ uint32_t fkey(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T* sh) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane == 0) sh[wv] = v;
+  __syncthreads();
+  T r = sh[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = op(r, sh[i]);
+  return r;
+}
+
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+  x ^= x >> 33;
+  x *= 0xff51afd7ed558ccdull;
+  x ^= x >> 33;
+  x *= 0xc4ceb9fe1a85ec53ull;
+  x ^= x >> 33;
+  return x;
+}
+
+// One workgroup (1024 threads) per row.  Greedy: first index of the largest
+// logit (argmax).  Sampling (ext_aggregator.cpp:756-795): logits/temperature,
+// keep the top-k values (ties at the k-th value kept), keep the sorted
+// prefix whose cumulative probability does not exceed top_p (the most likely
+// token always kept), softmax over the kept set and draw one token with a
+// counter-based generator seeded per (call, row).
+__global__ __launch_bounds__(1024) void sample_kernel(SampleArgs a) {
+  __shared__ float shf[16];
+  __shared__ uint32_t shu[16];
+  __shared__ unsigned long long shl[16];
+  const int row = blockIdx.x;
+  const bf16* lg = a.logits + (int64_t)row * a.vocab;
+  const int64_t V = a.vocab;
+  // argmax with first-index tie break: key = (fkey(v) << 32) | ~index
+  unsigned long long best = 0;
+  for (int64_t i = threadIdx.x; i < V; i += blockDim.x) {
+    const unsigned long long k = ((unsigned long long)fkey(bf2f(lg[i])) << 32) | (uint32_t)(~(uint32_t)i);
+    best = k > best ? k : best;
+  }
+  best = block_reduce<unsigned long long>(best, [](unsigned long long x, unsigned long long y) { return x > y ? x : y; }, shl);
+  const int64_t amax = (int64_t)(~(uint32_t)(best & 0xffffffffull));
+  if (!a.do_sample[row]) {
+    if (threadIdx.x == 0) a.out_tok[row][0] = amax;
+    return;
+  }
+  const float invt = 1.0f / a.temperature[row];
+  const float vmax = bf2f(lg[amax]) * invt;
+  // top-k threshold key: largest key t with count(key >= t) >= k
+  uint32_t tk = 0;
+  const int K = a.top_k[row];
+  if (K > 0 && K < V) {
+    uint32_t lo = 0, hi = 0xffffffffu;
+    while (lo < hi) {
+      const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+      uint32_t c = 0;
+      for (int64_t i = threadIdx.x; i < V; i += blockDim.x) c += fkey(bf2f(lg[i]) * invt) >= mid;
+      c = block_reduce<uint32_t>(c, [](uint32_t x, uint32_t y) { return x + y; }, shu);
+      if (c >= (uint32_t)K) lo = mid; else hi = mid - 1;
+    }
+    tk = lo;
+  }
+  // softmax mass over the top-k set
+  float z = 0.f;
+  for (int64_t i = threadIdx.x; i < V; i += blockDim.x) {
+    const float v = bf2f(lg[i]) * invt;
+    if (fkey(v) >= tk) z += __expf(v - vmax);
+  }
+  z = block_reduce<float>(z, [](float x, float y) { return x + y; }, shf);
+  // top-p threshold: smallest key t with mass(key >= t) <= top_p * z
+  uint32_t tp = tk;
+  const float P = a.top_p[row];
+  if (P < 1.0f) {
+    uint32_t lo = tk, hi = 0xffffffffu;
+    while (lo < hi) {
+      const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo) >> 1);
+      float m = 0.f;
+      for (int64_t i = threadIdx.x; i < V; i += blockDim.x) {
+        const float v = bf2f(lg[i]) * invt;
+        if (fkey(v) >= mid) m += __expf(v - vmax);
+      }
+      m = block_reduce<float>(m, [](float x, float y) { return x + y; }, shf);
+      if (m <= P * z) hi = mid; else lo = mid + 1;
+    }
+    tp = lo;
+  }
+  const uint32_t thr = tp > tk ? tp : tk;
+  float zk = 0.f;
+  for (int64_t i = threadIdx.x; i < V; i += blockDim.x) {
+    const float v = bf2f(lg[i]) * invt;
+    if (fkey(v) >= thr || i == amax) zk += __expf(v - vmax);
+  }
+  zk = block_reduce<float>(zk, [](float x, float y) { return x + y; }, shf);
+  const uint64_t r = mix64(a.seed * 0x9e3779b97f4a7c15ull + (uint64_t)row + 1);
+  const float target = (float)((r >> 40) * (1.0 / 16777216.0)) * zk;
+  // inverse CDF in index order: chunk of blockDim elements at a time
+  __shared__ float run;
+  __shared__ int64_t pick;
+  if (threadIdx.x == 0) { run = 0.f; pick = amax; }
+  __syncthreads();
+  for (int64_t base = 0; base < V; base += blockDim.x) {
+    const int64_t i = base + threadIdx.x;
+    float p = 0.f;
+    if (i < V) {
+      const float v = bf2f(lg[i]) * invt;
+      if (fkey(v) >= thr || i == amax) p = __expf(v - vmax);
+    }
+    // inclusive scan of p across the workgroup
+    float incl = p;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float t = __shfl_up(incl, o, 64);
+      if ((threadIdx.x & 63) >= o) incl += t;
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 63) shf[threadIdx.x >> 6] = incl;
+    __syncthreads();
+    float wpre = 0.f;
+    for (int w = 0; w < (int)(threadIdx.x >> 6); ++w) wpre += shf[w];
+    const float before = run + wpre + incl - p;
+    const float after = before + p;
+    const bool hit = p > 0.f && before <= target && target < after;
+    __syncthreads();
+    if (hit) pick = i;
+    float tot = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += shf[w];
+    __syncthreads();
+    if (threadIdx.x == 0) run += tot;
+    __syncthreads();
+    if (run > target) break;
+  }
+  if (threadIdx.x == 0) a.out_tok[row][0] = pick;
 }
 
 // --------------------------------------------------- library scratch ------
@@ -1203,8 +1380,9 @@ int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int 
   return SWL_OK;
 }
 
-int swl_paged_attention_bf16(void* q, void* k, const void* v, int nseq, int q_len, int hq, int hkv, int d,
-                             void* k_cache, void* v_cache, int64_t num_blocks, int block_size,
+int swl_paged_attention_bf16(void* q, void* k, const void* v, int64_t q_stride, int64_t k_stride, int64_t v_stride,
+                             int nseq, int q_len, int hq, int hkv, int d, void* k_cache, void* v_cache,
+                             int64_t num_blocks, int block_size,
                              const int32_t* block_table, int64_t max_blocks, const int32_t* cache_seqlens,
                              const int64_t* positions, const void* cos_sin, int64_t max_pos, int rope,
                              float softmax_scale, void* out, void* stream) {
@@ -1220,8 +1398,17 @@ int swl_paged_attention_bf16(void* q, void* k, const void* v, int nseq, int q_le
             "swl_paged_attention_bf16: bad page geometry");
   SWL_CHECK(!rope || (cos_sin && positions && max_pos > 0), SWL_ERR_INVALID,
             "swl_paged_attention_bf16: rope needs positions and cos_sin");
+  SWL_CHECK(q_stride >= hq * d && k_stride >= hkv * d && v_stride >= hkv * d, SWL_ERR_INVALID,
+            "swl_paged_attention_bf16: token strides smaller than a token row");
+  SWL_CHECK(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) ==
+                    0 &&
+                ((q_stride | k_stride | v_stride) & 7) == 0,
+            SWL_ERR_INVALID, "swl_paged_attention_bf16: q/k/v rows must be 16-byte aligned");
   if (nseq == 0) return SWL_OK;
   AttnArgs a{};
+  a.qs = q_stride;
+  a.ks = k_stride;
+  a.vs = v_stride;
   a.q = reinterpret_cast<bf16*>(q);
   a.k = reinterpret_cast<bf16*>(k);
   a.v = reinterpret_cast<const bf16*>(v);
@@ -1399,3 +1586,87 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
 }
 
 }  // namespace swl
+
+namespace swl {
+
+int embed_launch(int n, const int64_t* rows, const void* const* ids, void* const* out, const void* table,
+                 int64_t vocab, int64_t hidden, hipStream_t st) {
+  SWL_CHECK(n >= 1 && n <= kMaxSeg, SWL_ERR_INVALID, "embed: segment count must be in [1, 128]");
+  SWL_CHECK(hidden % 8 == 0, SWL_ERR_INVALID, "embed: hidden size must be a multiple of 8");
+  EmbedArgs a{};
+  a.n = n;
+  a.off[0] = 0;
+  for (int i = 0; i < n; ++i) {
+    a.off[i + 1] = a.off[i] + rows[i];
+    a.ids[i] = reinterpret_cast<const int64_t*>(ids[i]);
+    a.out[i] = reinterpret_cast<bf16*>(out[i]);
+  }
+  a.table = reinterpret_cast<const bf16*>(table);
+  a.vocab = vocab;
+  a.hidden = hidden;
+  if (a.off[n] == 0) return SWL_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)a.off[n]), dim3(256), 0, st, a);
+  SWL_LAUNCH_CHECK("embed_kernel launch");
+  return SWL_OK;
+}
+
+int lm_head_launch(int n, const void* const* last_rows, const void* lm_head, int64_t vocab, int64_t hidden,
+                   void* packed, void* logits, int64_t* next_tok, void* const* out_tok, const int32_t* do_sample,
+                   const float* temperature, const int32_t* top_k, const float* top_p, uint64_t seed,
+                   hipStream_t st) {
+  SWL_CHECK(n >= 1 && n <= kMaxSeg, SWL_ERR_INVALID, "lm_head: slot count must be in [1, 128]");
+  (void)next_tok;
+  int64_t ones[kMaxSeg];
+  for (int i = 0; i < n; ++i) ones[i] = 1;
+  int rc = swl_gather_bf16(last_rows, ones, n, hidden, packed, st);
+  if (rc) return rc;
+  rc = swl_gemm_bf16(packed, lm_head, nullptr, logits, n, vocab, hidden, st);
+  if (rc) return rc;
+  SampleArgs a{};
+  a.logits = reinterpret_cast<const bf16*>(logits);
+  a.vocab = vocab;
+  a.seed = seed;
+  for (int i = 0; i < n; ++i) {
+    a.out_tok[i] = reinterpret_cast<int64_t*>(out_tok[i]);
+    a.do_sample[i] = do_sample[i];
+    a.temperature[i] = temperature[i];
+    a.top_k[i] = top_k[i];
+    a.top_p[i] = top_p[i];
+  }
+  hipLaunchKernelGGL(sample_kernel, dim3((unsigned)n), dim3(1024), 0, st, a);
+  SWL_LAUNCH_CHECK("sample_kernel launch");
+  return SWL_OK;
+}
+
+}  // namespace swl
+
+extern "C" int swl_sample_bf16(const void* logits, int64_t n, int64_t vocab, void* const* out_tok,
+                               const int32_t* do_sample, const float* temperature, const int32_t* top_k,
+                               const float* top_p, uint64_t seed, void* stream) {
+  SWL_CHECK(logits && out_tok && do_sample && temperature && top_k && top_p, SWL_ERR_INVALID,
+            "swl_sample_bf16: null argument");
+  SWL_CHECK(n >= 1 && n <= kMaxSeg && vocab > 0 && vocab < ((int64_t)1 << 31), SWL_ERR_INVALID,
+            "swl_sample_bf16: bad shape");
+  SampleArgs a{};
+  a.logits = reinterpret_cast<const bf16*>(logits);
+  a.vocab = vocab;
+  a.seed = seed;
+  for (int i = 0; i < n; ++i) {
+    SWL_CHECK(out_tok[i] != nullptr, SWL_ERR_INVALID, "swl_sample_bf16: null output");
+    SWL_CHECK(temperature[i] > 0.f, SWL_ERR_INVALID, "swl_sample_bf16: temperature must be > 0");
+    a.out_tok[i] = reinterpret_cast<int64_t*>(out_tok[i]);
+    a.do_sample[i] = do_sample[i];
+    a.temperature[i] = temperature[i];
+    a.top_k[i] = top_k[i];
+    a.top_p[i] = top_p[i];
+  }
+  hipLaunchKernelGGL(sample_kernel, dim3((unsigned)n), dim3(1024), 0, (hipStream_t)stream, a);
+  SWL_LAUNCH_CHECK("sample_kernel launch");
+  return SWL_OK;
+}
+
+extern "C" int swl_embed_bf16(const void* const* ids, const int64_t* rows, int n, const void* table, int64_t vocab,
+                              int64_t hidden, void* const* out, void* stream) {
+  SWL_CHECK(ids && rows && table && out, SWL_ERR_INVALID, "swl_embed_bf16: null argument");
+  return swl::embed_launch(n, rows, ids, out, table, vocab, hidden, (hipStream_t)stream);
+}

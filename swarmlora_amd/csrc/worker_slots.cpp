@@ -1,0 +1,253 @@
+// Worker-side slot manager: maps the aggregator's slot buffers through HIP IPC
+// handles and moves activations in and results out.  Semantics follow
+// src/cpp_extensions/ext_unified_barrier.cpp.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "swl_common.h"
+#include "swl_runtime.h"
+
+namespace {
+
+constexpr int kMaxSlotsPerWorker = 8;
+
+struct SlotCtx {
+  int slot_id = -1;
+  bool open = false;
+  void* in = nullptr;
+  void* out = nullptr;
+  size_t in_size = 0, out_size = 0;
+  int64_t bx = 0, tx = 0, dx = 0;
+};
+
+struct Manager {
+  int worker_id = -1;
+  int worker_device = 0;
+  int aggregator_device = 0;
+  int hidden = 0, inter = 0, qkv = 0;
+  SlotCtx slots[kMaxSlotsPerWorker];
+  int nopen = 0;
+  bool initialized = false;
+} g_w;
+
+SlotCtx* find_slot(int slot_id) {
+  for (auto& s : g_w.slots)
+    if (s.open && s.slot_id == slot_id) return &s;
+  return nullptr;
+}
+
+int need_slot(const char* fn, int slot_id, SlotCtx** out) {
+  if (!g_w.initialized) return swl::fail(SWL_ERR_STATE, std::string(fn) + ": worker slot manager not initialized");
+  *out = find_slot(slot_id);
+  if (!*out) return swl::fail(SWL_ERR_NOT_FOUND, std::string(fn) + ": slot " + std::to_string(slot_id) + " not found");
+  return SWL_OK;
+}
+
+int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream_t st) {
+  if (bytes > c->in_size)
+    return swl::fail(SWL_ERR_INVALID, std::string(fn) + ": input tensor (" + std::to_string(bytes) +
+                                          " bytes) exceeds slot buffer size (" + std::to_string(c->in_size) +
+                                          " bytes)");
+  SWL_HIP(hipMemcpyAsync(c->in, src, bytes, hipMemcpyDeviceToDevice, st));
+  // the aggregator reads the buffer from another process once this worker
+  // signals ready: the copy must be complete, not just ordered
+  SWL_HIP(hipStreamSynchronize(st));
+  return SWL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int swl_w_init(int worker_id, int worker_device, int aggregator_device, int hidden_dim, int intermediate_dim,
+               int qkv_dim) {
+  SWL_HIP(hipSetDevice(worker_device));
+  g_w.worker_id = worker_id;
+  g_w.worker_device = worker_device;
+  g_w.aggregator_device = aggregator_device;
+  g_w.hidden = hidden_dim;
+  g_w.inter = intermediate_dim;
+  g_w.qkv = qkv_dim;
+  for (auto& s : g_w.slots) s = SlotCtx();
+  g_w.nopen = 0;
+  g_w.initialized = true;
+  std::printf("[Worker-%d] Slot manager initialized (worker_device=%d, aggregator_device=%d)\n", worker_id,
+              worker_device, aggregator_device);
+  std::fflush(stdout);
+  return SWL_OK;
+}
+
+int swl_w_open_slot(int slot_id, const uint8_t* input_handle, size_t input_handle_len, const uint8_t* output_handle,
+                    size_t output_handle_len, size_t input_buffer_size, size_t output_buffer_size) {
+  SWL_CHECK(g_w.initialized, SWL_ERR_STATE, "open_slot: worker slot manager not initialized");
+  SWL_CHECK(g_w.nopen < kMaxSlotsPerWorker, SWL_ERR_FULL, "open_slot: max slots per worker exceeded");
+  SWL_CHECK(input_handle_len == sizeof(hipIpcMemHandle_t) && output_handle_len == sizeof(hipIpcMemHandle_t),
+            SWL_ERR_INVALID,
+            "open_slot: invalid IPC handle size (got " + std::to_string(input_handle_len) + "/" +
+                std::to_string(output_handle_len) + ", expected " + std::to_string(sizeof(hipIpcMemHandle_t)) + ")");
+  SWL_CHECK(find_slot(slot_id) == nullptr, SWL_ERR_INVALID,
+            "open_slot: slot " + std::to_string(slot_id) + " is already open");
+  SWL_HIP(hipSetDevice(g_w.worker_device));
+  SlotCtx* c = nullptr;
+  for (auto& s : g_w.slots)
+    if (!s.open) {
+      c = &s;
+      break;
+    }
+  SWL_CHECK(c != nullptr, SWL_ERR_FULL, "open_slot: no free slot context");
+  hipIpcMemHandle_t hin, hout;
+  std::memcpy(&hin, input_handle, sizeof(hin));
+  std::memcpy(&hout, output_handle, sizeof(hout));
+  void* pin = nullptr;
+  void* pout = nullptr;
+  hipError_t e = hipIpcOpenMemHandle(&pin, hin, hipIpcMemLazyEnablePeerAccess);
+  if (e != hipSuccess)
+    return swl::fail(SWL_ERR_HIP, std::string("open_slot: input IPC open failed: ") + hipGetErrorString(e));
+  e = hipIpcOpenMemHandle(&pout, hout, hipIpcMemLazyEnablePeerAccess);
+  if (e != hipSuccess) {
+    (void)hipIpcCloseMemHandle(pin);
+    return swl::fail(SWL_ERR_HIP, std::string("open_slot: output IPC open failed: ") + hipGetErrorString(e));
+  }
+  *c = SlotCtx();
+  c->slot_id = slot_id;
+  c->open = true;
+  c->in = pin;
+  c->out = pout;
+  c->in_size = input_buffer_size;
+  c->out_size = output_buffer_size;
+  ++g_w.nopen;
+  std::printf("[Worker-%d] Opened slot %d (input=%zu bytes, output=%zu bytes)\n", g_w.worker_id, slot_id,
+              input_buffer_size, output_buffer_size);
+  std::fflush(stdout);
+  return SWL_OK;
+}
+
+int swl_w_close_slot(int slot_id) {
+  SlotCtx* c;
+  int rc = need_slot("close_slot", slot_id, &c);
+  if (rc) return rc;
+  // every stream of this process may still touch the mapping
+  SWL_HIP(hipDeviceSynchronize());
+  if (c->in) {
+    const hipError_t e = hipIpcCloseMemHandle(c->in);
+    if (e != hipSuccess)
+      std::fprintf(stderr, "[Worker-%d] Warning: hipIpcCloseMemHandle(input) for slot %d: %s\n", g_w.worker_id,
+                   slot_id, hipGetErrorString(e));
+  }
+  if (c->out) {
+    const hipError_t e = hipIpcCloseMemHandle(c->out);
+    if (e != hipSuccess)
+      std::fprintf(stderr, "[Worker-%d] Warning: hipIpcCloseMemHandle(output) for slot %d: %s\n", g_w.worker_id,
+                   slot_id, hipGetErrorString(e));
+  }
+  *c = SlotCtx();
+  --g_w.nopen;
+  std::printf("[Worker-%d] Closed slot %d\n", g_w.worker_id, slot_id);
+  std::fflush(stdout);
+  return SWL_OK;
+}
+
+int swl_w_prepare_input(int slot_id, const void* src, int64_t bx, int64_t tx, int64_t dx, size_t elem_size,
+                        void* stream) {
+  SlotCtx* c;
+  int rc = need_slot("prepare_input_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(src && bx > 0 && tx > 0 && dx > 0 && elem_size > 0, SWL_ERR_INVALID, "Input must be 3D [B, T, D]");
+  rc = copy_in("prepare_input_slot", c, src, (size_t)bx * tx * dx * elem_size, (hipStream_t)stream);
+  if (rc) return rc;
+  c->bx = bx;
+  c->tx = tx;
+  c->dx = dx;
+  return SWL_OK;
+}
+
+int swl_w_slot_shape(int slot_id, int64_t* bx, int64_t* tx, int64_t* dx) {
+  SlotCtx* c;
+  int rc = need_slot("slot_shape", slot_id, &c);
+  if (rc) return rc;
+  *bx = c->bx;
+  *tx = c->tx;
+  *dx = c->dx;
+  return SWL_OK;
+}
+
+int swl_w_slot_sizes(int slot_id, size_t* input_buffer_size, size_t* output_buffer_size) {
+  SlotCtx* c;
+  int rc = need_slot("slot_sizes", slot_id, &c);
+  if (rc) return rc;
+  *input_buffer_size = c->in_size;
+  *output_buffer_size = c->out_size;
+  return SWL_OK;
+}
+
+int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream) {
+  SlotCtx* c;
+  int rc = need_slot("get_outputs_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(dst != nullptr, SWL_ERR_INVALID, "get_outputs_slot: null destination");
+  SWL_CHECK(bytes <= c->out_size, SWL_ERR_INVALID,
+            "get_outputs_slot: output (" + std::to_string(bytes) + " bytes) exceeds slot output buffer (" +
+                std::to_string(c->out_size) + " bytes)");
+  // stream-ordered; consumers of dst on the same stream see the copy
+  SWL_HIP(hipMemcpyAsync(dst, c->out, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  return SWL_OK;
+}
+
+int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx, void* stream) {
+  SlotCtx* c;
+  int rc = need_slot("prepare_token_ids_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(src && bx > 0 && tx > 0, SWL_ERR_INVALID, "token_ids must be 2D [B, T]");
+  rc = copy_in("prepare_token_ids_slot", c, src, (size_t)bx * tx * sizeof(int64_t), (hipStream_t)stream);
+  if (rc) return rc;
+  c->bx = bx;
+  c->tx = tx;
+  c->dx = g_w.hidden;
+  return SWL_OK;
+}
+
+int swl_w_prepare_hidden_lm(int slot_id, const void* src, int64_t bx, int64_t tx, int64_t dx, size_t elem_size,
+                            void* stream) {
+  SlotCtx* c;
+  int rc = need_slot("prepare_hidden_for_lm_head_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(src && bx > 0 && tx > 0 && dx > 0, SWL_ERR_INVALID, "hidden_states must be 3D [B, T, D]");
+  rc = copy_in("prepare_hidden_for_lm_head_slot", c, src, (size_t)bx * tx * dx * elem_size, (hipStream_t)stream);
+  if (rc) return rc;
+  c->bx = bx;
+  c->tx = tx;
+  c->dx = dx;
+  return SWL_OK;
+}
+
+int swl_w_get_next_token(int slot_id, int64_t* token, void* stream) {
+  SlotCtx* c;
+  int rc = need_slot("get_next_token_slot", slot_id, &c);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  SWL_HIP(hipStreamSynchronize(st));
+  SWL_HIP(hipMemcpyAsync(token, c->out, sizeof(int64_t), hipMemcpyDeviceToHost, st));
+  SWL_HIP(hipStreamSynchronize(st));
+  return SWL_OK;
+}
+
+int swl_w_cleanup(void) {
+  if (!g_w.initialized) return SWL_OK;
+  (void)hipSetDevice(g_w.worker_device);
+  (void)hipDeviceSynchronize();
+  for (auto& s : g_w.slots) {
+    if (!s.open) continue;
+    if (s.in) (void)hipIpcCloseMemHandle(s.in);
+    if (s.out) (void)hipIpcCloseMemHandle(s.out);
+    s = SlotCtx();
+  }
+  g_w.nopen = 0;
+  g_w.initialized = false;
+  return SWL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+"""Worker-side slot manager: maps aggregator slot buffers via HIP IPC handles.
+
+Drop-in for the reference's ``ext_unified_barrier`` pybind module
+(src/cpp_extensions/ext_unified_barrier.cpp:562-630): same function names,
+arguments, return values and error texts; errors raise RuntimeError.  Copies
+run on torch's current stream of the worker device; ``get_outputs_slot`` and
+``get_embeddings_slot`` return fresh worker-owned tensors (callers mutate
+them in place), never views of the slot buffer.
+"""
+
+import ctypes
+from typing import List, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import c_i64, c_int, c_vp
+
+OP_O_PROJ = 3
+OP_DOWN_PROJ = 6
+OP_QKV_FUSED = 9
+OP_GATE_UP_FUSED = 10
+OP_EMBED = 11
+OP_LM_HEAD = 12
+OP_SET_SAMPLING = 13
+
+_P_i64 = ctypes.POINTER(c_i64)
+_P_size = ctypes.POINTER(ctypes.c_size_t)
+
+_lib.register_signatures({
+    "swl_w_init": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "swl_w_open_slot": (c_int, [c_int, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t,
+                                ctypes.c_size_t, ctypes.c_size_t]),
+    "swl_w_close_slot": (c_int, [c_int]),
+    "swl_w_prepare_input": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, ctypes.c_size_t, c_vp]),
+    "swl_w_slot_shape": (c_int, [c_int, _P_i64, _P_i64, _P_i64]),
+    "swl_w_slot_sizes": (c_int, [c_int, _P_size, _P_size]),
+    "swl_w_copy_output": (c_int, [c_int, c_vp, ctypes.c_size_t, c_vp]),
+    "swl_w_prepare_token_ids": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp]),
+    "swl_w_prepare_hidden_lm": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, ctypes.c_size_t, c_vp]),
+    "swl_w_get_next_token": (c_int, [c_int, _P_i64, c_vp]),
+    "swl_w_cleanup": (c_int, []),
+})
+
+_state = {"device": 0, "hidden_dim": 0}
+
+
+def _L():
+    return _lib.load()
+
+
+def _stream():
+    return c_vp(torch.cuda.current_stream(_state["device"]).cuda_stream)
+
+
+def _shape(slot_id):
+    bx, tx, dx = c_i64(0), c_i64(0), c_i64(0)
+    _lib.check(_L().swl_w_slot_shape(int(slot_id), ctypes.byref(bx), ctypes.byref(tx), ctypes.byref(dx)))
+    return bx.value, tx.value, dx.value
+
+
+def init_worker_slot_manager(worker_id, worker_device, aggregator_device, hidden_dim, intermediate_dim, qkv_dim):
+    _state.update(device=int(worker_device), hidden_dim=int(hidden_dim))
+    _lib.check(_L().swl_w_init(int(worker_id), int(worker_device), int(aggregator_device), int(hidden_dim),
+                               int(intermediate_dim), int(qkv_dim)))
+
+
+def open_slot(slot_id, input_handle, output_handle, input_buffer_size, output_buffer_size):
+    hin, hout = bytes(input_handle), bytes(output_handle)
+    _lib.check(_L().swl_w_open_slot(int(slot_id), hin, len(hin), hout, len(hout), int(input_buffer_size),
+                                    int(output_buffer_size)))
+
+
+def close_slot(slot_id):
+    _lib.check(_L().swl_w_close_slot(int(slot_id)))
+
+
+def _device_tensor(t, name):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor")
+    return t.contiguous()
+
+
+def prepare_input_slot(slot_id, op_type, input):
+    if not isinstance(input, torch.Tensor) or input.dim() != 3:
+        raise RuntimeError("Input must be 3D [B, T, D]")
+    x = _device_tensor(input, "input")
+    b, t, d = x.shape
+    _lib.check(_L().swl_w_prepare_input(int(slot_id), x.data_ptr(), b, t, d, x.element_size(), _stream()))
+
+
+def get_outputs_slot(slot_id, out_dims: Sequence[int], input_template) -> List[torch.Tensor]:
+    bx, tx, _ = _shape(slot_id)
+    dims = [int(d) for d in out_dims]
+    total = sum(dims)
+    out = torch.empty(bx, tx, total, dtype=input_template.dtype, device=input_template.device)
+    _lib.check(_L().swl_w_copy_output(int(slot_id), out.data_ptr(), out.numel() * out.element_size(), _stream()))
+    if len(dims) > 1:
+        return list(out.split(dims, dim=-1))
+    return [out]
+
+
+def prepare_token_ids_slot(slot_id, token_ids):
+    if not isinstance(token_ids, torch.Tensor) or token_ids.dim() != 2:
+        raise RuntimeError("token_ids must be 2D [B, T]")
+    ids = _device_tensor(token_ids, "token_ids").to(torch.int64)
+    b, t = ids.shape
+    _lib.check(_L().swl_w_prepare_token_ids(int(slot_id), ids.data_ptr(), b, t, _stream()))
+
+
+def get_embeddings_slot(slot_id, dtype):
+    bx, tx, _ = _shape(slot_id)
+    out = torch.empty(bx, tx, _state["hidden_dim"], dtype=dtype, device=torch.device("cuda", _state["device"]))
+    _lib.check(_L().swl_w_copy_output(int(slot_id), out.data_ptr(), out.numel() * out.element_size(), _stream()))
+    return out
+
+
+def prepare_hidden_for_lm_head_slot(slot_id, hidden_states):
+    if not isinstance(hidden_states, torch.Tensor) or hidden_states.dim() != 3:
+        raise RuntimeError("hidden_states must be 3D [B, T, D]")
+    h = _device_tensor(hidden_states, "hidden_states")
+    b, t, d = h.shape
+    _lib.check(_L().swl_w_prepare_hidden_lm(int(slot_id), h.data_ptr(), b, t, d, h.element_size(), _stream()))
+
+
+def get_next_token_slot(slot_id):
+    tok = c_i64(0)
+    _lib.check(_L().swl_w_get_next_token(int(slot_id), ctypes.byref(tok), _stream()))
+    return tok.value
+
+
+def cleanup_worker_slots():
+    _lib.check(_L().swl_w_cleanup())

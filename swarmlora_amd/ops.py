@@ -224,23 +224,41 @@ def matmul(x: torch.Tensor, b: torch.Tensor, trans_b: bool, alpha: float = 1.0,
     return out
 
 
+def _token_rows(t: torch.Tensor, name: str, heads: int, d: int):
+    """t is [nseq, L, heads, d] whose heads/dims are contiguous per token and
+    whose tokens (nseq*L of them) are evenly strided: returns the stride."""
+    if t.dim() != 4 or t.shape[2] != heads or t.shape[3] != d:
+        raise ValueError(f"{name} must be [nseq, q_len, {heads}, {d}]")
+    if t.stride(3) != 1 or t.stride(2) != d:
+        raise ValueError(f"{name} heads must be contiguous within a token")
+    nseq, L = t.shape[0], t.shape[1]
+    if L > 1 and nseq > 1 and t.stride(0) != L * t.stride(1):
+        raise ValueError(f"{name} tokens must be evenly strided")
+    return t.stride(1) if L > 1 else t.stride(0)
+
+
 def paged_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
                     v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
                     positions: Optional[torch.Tensor], cos_sin: Optional[torch.Tensor],
                     softmax_scale: float, rope: bool = True, out: Optional[torch.Tensor] = None):
-    """q [nseq, L, hq, d], k/v [nseq, L, hkv, d] (q, k rotated in place when
-    rope), caches [num_blocks, block_size, hkv, d], block_table int32
-    [nseq, max_blocks], cache_seqlens int32 [nseq], positions int64 [nseq*L].
+    """q [nseq, L, hq, d], k/v [nseq, L, hkv, d] (views into the fused QKV
+    output are fine: tokens may be strided), caches [num_blocks, block_size,
+    hkv, d], block_table int32 [nseq, max_blocks], cache_seqlens int32 [nseq],
+    positions int64 [nseq*L].  q and k are rotated in place when rope.
     Returns out [nseq, L, hq*d]."""
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         _need(t, nm)
+    for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
         if not t.is_contiguous():
             raise ValueError(f"{nm} must be contiguous")
     _need(block_table, "block_table", torch.int32)
     _need(cache_seqlens, "cache_seqlens", torch.int32)
     nseq, L, hq, d = q.shape
     hkv = k.shape[2]
-    if k.shape != (nseq, L, hkv, d) or v.shape != k.shape:
+    qs = _token_rows(q, "q", hq, d)
+    ks = _token_rows(k, "k", hkv, d)
+    vs = _token_rows(v, "v", hkv, d)
+    if k.shape[:2] != (nseq, L) or v.shape[:2] != (nseq, L):
         raise ValueError("k and v must be [nseq, L, hkv, d]")
     nb, bs, hkv2, d2 = k_cache.shape
     if v_cache.shape != k_cache.shape or hkv2 != hkv or d2 != d:
@@ -261,10 +279,38 @@ def paged_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: 
     if out is None:
         out = torch.empty(nseq, L, hq * d, dtype=BF16, device=q.device)
     _lib.check(_lib.load().swl_paged_attention_bf16(
-        _ptr(q), _ptr(k), _ptr(v), nseq, L, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs,
+        _ptr(q), _ptr(k), _ptr(v), qs, ks, vs, nseq, L, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs,
         _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope else None),
         _ptr(cos_sin if rope else None), max_pos, 1 if rope else 0, float(softmax_scale), _ptr(out), _stream()))
     return out
+
+
+def embed(ids: Sequence[torch.Tensor], table: torch.Tensor, outs: Sequence[torch.Tensor]):
+    """outs[i][j] = table[clamp(ids[i][j])] for int64 id tensors."""
+    _need(table, "table")
+    vocab, hidden = table.shape
+    for i, t in enumerate(ids):
+        _need(t, f"ids[{i}]", torch.int64)
+        _need(outs[i], f"outs[{i}]")
+        if outs[i].numel() < t.numel() * hidden:
+            raise ValueError("embedding output too small")
+    _lib.check(_lib.load().swl_embed_bf16(_ptr_array(ids), _i64_array([t.numel() for t in ids]), len(ids),
+                                          _ptr(table), vocab, hidden, _ptr_array(outs), _stream()))
+
+
+def sample(logits: torch.Tensor, out_tok: Sequence[torch.Tensor], do_sample: Sequence[bool],
+           temperature: Sequence[float], top_k: Sequence[int], top_p: Sequence[float], seed: int = 0):
+    """Next token of each logits row into out_tok[i][0] (int64 device tensors)."""
+    _need(logits, "logits")
+    n, vocab = logits.shape
+    if not logits.is_contiguous():
+        raise ValueError("logits must be contiguous")
+    for i, t in enumerate(out_tok):
+        _need(t, f"out_tok[{i}]", torch.int64)
+    f32 = lambda xs: (ctypes.c_float * n)(*[float(x) for x in xs])  # noqa: E731
+    _lib.check(_lib.load().swl_sample_bf16(_ptr(logits), n, vocab, _ptr_array(out_tok),
+                                           _i32_array([1 if d else 0 for d in do_sample]), f32(temperature),
+                                           _i32_array(top_k), f32(top_p), int(seed), _stream()))
 
 
 def zero_blocks(caches: Sequence[torch.Tensor], block_ids: torch.Tensor):

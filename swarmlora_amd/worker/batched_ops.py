@@ -1,0 +1,207 @@
+"""Worker-side round helpers: attention over the paged KV cache and the
+submit / signal / wait / read pattern of every aggregator round.
+
+Mirrors src/worker/worker_sync.py: WorkerBatchedOps.batch_flash_attention
+(:169-205) and BatchedAggregatorOps (:211-421), same method names and
+arguments.  Attention is the libswl paged-attention kernel (RoPE, page
+append and causal GQA attention in two launches) instead of vLLM's
+rotary_embedding + flash_attn_with_kvcache.
+
+One addition: with ``pooled_adapter`` set, the worker's adapter lives in the
+aggregator's pool (ext_aggregator.register_adapter); commands carry
+``x_key = pooled_adapter + 1`` and the aggregator adds the LoRA delta during
+the scatter, so the worker skips its own delta products.
+"""
+
+import time
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+import torch
+
+from .. import ext_ipc_queue as extq
+from .. import ext_unified_barrier as ub
+from .. import ops
+from .model_builder import OP_DOWN_PROJ, OP_EMBED, OP_GATE_UP_FUSED, OP_LM_HEAD, OP_O_PROJ, OP_QKV_FUSED
+from .model_builder import SyncRemoteLoRALinear
+
+
+@dataclass
+class SlotState:
+    """Per-request state of an active slot (worker_sync.py:100-118)."""
+    slot_id: int
+    input_ids: torch.Tensor
+    generated_tokens: List[int] = field(default_factory=list)
+    hidden: Optional[torch.Tensor] = None
+    residual: Optional[torch.Tensor] = None
+    mlp_residual: Optional[torch.Tensor] = None
+    prefill_chunks: Optional[list] = None
+    first_token_time: Optional[float] = None
+
+
+class WorkerBatchedOps:
+    @staticmethod
+    def batch_flash_attention(slot_ids: list, qkv_results: dict, paged_kv, cos_sin_cache: torch.Tensor,
+                              layer_idx: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                              attn_meta: dict = None) -> Dict[int, torch.Tensor]:
+        """RoPE at attn_meta['positions'], append k/v at cache_seqlens, causal
+        GQA attention over the pages; returns {slot: [1, q_len, hidden]}.
+        q/k/v may be views of the fused QKV output (read in place)."""
+        q_len = attn_meta["bufs_q"].shape[1]
+        n = len(slot_ids)
+
+        def gather(j, heads):
+            parts = [qkv_results[s][j].reshape(1, q_len, heads, head_dim) for s in slot_ids]
+            return parts[0] if n == 1 else torch.cat(parts, 0)
+
+        q = gather(0, num_heads)
+        k = gather(1, num_kv_heads)
+        v = gather(2, num_kv_heads)
+        out = ops.paged_attention(q, k, v, paged_kv.key_caches[layer_idx], paged_kv.value_caches[layer_idx],
+                                  attn_meta["block_tables"], attn_meta["cache_seqlens"], attn_meta["positions"],
+                                  cos_sin_cache, 1.0 / (head_dim ** 0.5))
+        return {sid: out[i:i + 1] for i, sid in enumerate(slot_ids)}
+
+
+class BatchedAggregatorOps:
+    """submit -> signal_ready -> (local LoRA delta) -> wait epoch -> read."""
+
+    def __init__(self, slot_manager, worker_id: int, dtype_code: int, pooled_adapter: Optional[int] = None):
+        self.slot_manager = slot_manager
+        self.worker_id = worker_id
+        self.dtype_code = dtype_code
+        self.dtype = torch.bfloat16 if dtype_code == 15 else torch.float16
+        self.hidden_dim = slot_manager.base_client.hidden_dim
+        self.pooled_adapter = pooled_adapter
+        self._x_key = 0 if pooled_adapter is None else int(pooled_adapter) + 1
+
+    def barrier_sync(self, epoch: int):
+        extq.wait_for_epoch(epoch)
+
+    def _get_outputs_all(self, slots, dims):
+        slot_id, state = next(iter(slots.items()))
+        return {slot_id: ub.get_outputs_slot(slot_id, dims, state.hidden)}
+
+    def _submit(self, op, layer_idx, slot_id, x):
+        b, t, d = x.shape
+        ub.prepare_input_slot(slot_id, op, x)
+        extq.submit_slot_command(op, layer_idx, slot_id, self.worker_id, b, t, d, self._x_key, 0, 0, 0, 0)
+        extq.slot_signal_ready(slot_id)
+
+    # ---------------------------------------------------------------- embed
+    def embed_submit_all(self, slots) -> int:
+        epoch = extq.get_barrier_done_epoch()
+        slot_id, state = next(iter(slots.items()))
+        ub.prepare_token_ids_slot(slot_id, state.input_ids)
+        b, t = state.input_ids.shape
+        extq.submit_slot_command(OP_EMBED, 0, slot_id, self.worker_id, b, t, self.hidden_dim, 0, 0, 0, 0, 0)
+        extq.slot_signal_ready(slot_id)
+        return epoch
+
+    def embed_get_all(self, slots):
+        slot_id, state = next(iter(slots.items()))
+        state.hidden = ub.get_embeddings_slot(slot_id, self.dtype)
+
+    # ------------------------------------------------------------------ QKV
+    def qkv_submit_all(self, slots, layer_idx: int, fused_qkv_modules: List):
+        epoch = extq.get_barrier_done_epoch()
+        slot_id, state = next(iter(slots.items()))
+        self._submit(OP_QKV_FUSED, layer_idx, slot_id, state.hidden)
+        fq = fused_qkv_modules[layer_idx]
+        if self.pooled_adapter is None and fq.fused_lora is not None and fq.fused_lora.has_lora:
+            deltas = {slot_id: fq.fused_lora(state.hidden)}
+        else:
+            deltas = {slot_id: (None, None, None)}
+        return epoch, deltas
+
+    def qkv_get_all(self, slots, layer_idx: int, deltas, dims: List[int]):
+        raw = self._get_outputs_all(slots, dims)
+        res = {}
+        for sid in slots:
+            q, k, v = raw[sid]
+            dq, dk, dv = deltas.get(sid, (None, None, None))
+            res[sid] = (q + dq if dq is not None else q, k + dk if dk is not None else k,
+                        v + dv if dv is not None else v)
+        return res
+
+    # -------------------------------------------------------------------- O
+    def o_proj_submit_all(self, slots, layer_idx: int, attn_outputs, o_proj_modules: List):
+        epoch = extq.get_barrier_done_epoch()
+        slot_id, state = next(iter(slots.items()))
+        x = attn_outputs[slot_id]
+        self._submit(OP_O_PROJ, layer_idx, slot_id, x)
+        o = o_proj_modules[layer_idx]
+        use = self.pooled_adapter is None and isinstance(o, SyncRemoteLoRALinear)
+        return epoch, {slot_id: o.delta(x) if use else None}
+
+    def o_proj_get_all(self, slots, layer_idx: int, deltas, out_dim: int):
+        raw = self._get_outputs_all(slots, [out_dim])
+        for sid, state in slots.items():
+            r = raw[sid][0]
+            d = deltas.get(sid)
+            if d is not None:
+                r = r + d
+            state.hidden = state.residual + r
+
+    # -------------------------------------------------------------- Gate+Up
+    def gate_up_submit_all(self, slots, layer_idx: int, fused_gate_up_modules: List):
+        epoch = extq.get_barrier_done_epoch()
+        slot_id, state = next(iter(slots.items()))
+        self._submit(OP_GATE_UP_FUSED, layer_idx, slot_id, state.hidden)
+        fg = fused_gate_up_modules[layer_idx]
+        if self.pooled_adapter is None and fg.fused_lora is not None and fg.fused_lora.has_lora:
+            deltas = {slot_id: fg.fused_lora(state.hidden)}
+        else:
+            deltas = {slot_id: (None, None)}
+        return epoch, deltas
+
+    def gate_up_get_all(self, slots, layer_idx: int, deltas, dims: List[int]):
+        raw = self._get_outputs_all(slots, dims)
+        res = {}
+        for sid in slots:
+            g, u = raw[sid]
+            dg, du = deltas.get(sid, (None, None))
+            res[sid] = (g + dg if dg is not None else g, u + du if du is not None else u)
+        return res
+
+    # ----------------------------------------------------------------- Down
+    def down_proj_submit_all(self, slots, layer_idx: int, mlp_intermediates, down_proj_modules: List):
+        epoch = extq.get_barrier_done_epoch()
+        slot_id, state = next(iter(slots.items()))
+        x = mlp_intermediates[slot_id]
+        self._submit(OP_DOWN_PROJ, layer_idx, slot_id, x)
+        dp = down_proj_modules[layer_idx]
+        use = self.pooled_adapter is None and isinstance(dp, SyncRemoteLoRALinear)
+        return epoch, {slot_id: dp.delta(x) if use else None}
+
+    def down_proj_get_all(self, slots, layer_idx: int, deltas, out_dim: int):
+        raw = self._get_outputs_all(slots, [out_dim])
+        for sid, state in slots.items():
+            r = raw[sid][0]
+            d = deltas.get(sid)
+            if d is not None:
+                r = r + d
+            state.hidden = state.mlp_residual + r
+
+    # -------------------------------------------------------------- LM head
+    def lm_head_submit_all(self, slots) -> int:
+        epoch = extq.get_barrier_done_epoch()
+        slot_id, state = next(iter(slots.items()))
+        ub.prepare_hidden_for_lm_head_slot(slot_id, state.hidden)
+        b, t, d = state.hidden.shape
+        extq.submit_slot_command(OP_LM_HEAD, 0, slot_id, self.worker_id, b, t, d, 0, 0, 0, 0, 0)
+        extq.slot_signal_ready(slot_id)
+        return epoch
+
+    def lm_head_get_all(self, slots):
+        for slot_id, state in slots.items():
+            tok = ub.get_next_token_slot(slot_id)
+            if state.prefill_chunks:
+                state.input_ids = state.prefill_chunks.pop(0)
+                if not state.prefill_chunks:
+                    state.prefill_chunks = None
+            else:
+                if state.first_token_time is None:
+                    state.first_token_time = time.perf_counter()
+                state.generated_tokens.append(tok)
+                state.input_ids = torch.tensor([[tok]], device=state.input_ids.device)

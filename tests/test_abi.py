@@ -25,6 +25,7 @@ def test_headers_declare_entry_points():
 
 def test_library_exports_every_declared_symbol():
     from swarmlora_amd import _lib
+    from swarmlora_amd import ext_aggregator, ext_ipc_queue, ext_unified_barrier  # noqa: F401
     lib = _lib.load()
     missing = [n for n in declared_symbols() if not hasattr(lib, n)]
     assert not missing, f"declared but not exported: {missing}"
