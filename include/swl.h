@@ -181,6 +181,34 @@ int swl_sample_bf16(const void* logits, int64_t n, int64_t vocab, void* const* o
                     const float* temperature, const int32_t* top_k, const float* top_p, uint64_t seed,
                     void* stream);
 
+/* ----------------------------------------------- worker-side row ops ----
+ * Token-row variants of the worker's per-layer elementwise work, so the
+ * batched decode step reads and writes slot buffers directly (at most 64
+ * rows; row arrays are HOST arrays of device pointers). */
+
+/* Residual stream h [ntok, d] (contiguous): when add_rows is given,
+ * h[t] = bf16(h[t] + add_rows[t]) (the worker's `residual + result`,
+ * worker_sync.py:314-319, :383-389); then out_rows[t] = LlamaRMSNorm(h[t]) with
+ * fp32 statistics, the normalised row rounded to bf16 and multiplied by the
+ * bf16 weight (worker_sync.py:1344-1350). */
+int swl_rmsnorm_rows_bf16(void* h, int64_t ntok, int64_t d, const void* const* add_rows, const void* weight,
+                          float eps, void* const* out_rows, void* stream);
+
+/* out_rows[t][j] = bf16(bf16(silu(g)) * u) with g = in_rows[t][j] and
+ * u = in_rows[t][inter + j] (the fused Gate+Up output row): F.silu(gate) * up,
+ * worker_sync.py:158, :1397. */
+int swl_silu_mul_rows_bf16(const void* const* in_rows, void* const* out_rows, int64_t ntok, int64_t inter,
+                           void* stream);
+
+/* swl_paged_attention_bf16 with per-token rows: token t = seq * q_len + i
+ * reads its fused [q | k | v] row at qkv_rows[t] (RoPE applied in place) and
+ * writes its [hq * d] output row at out_rows[t]. */
+int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len, int hq,
+                                  int hkv, int d, void* k_cache, void* v_cache, int64_t num_blocks,
+                                  int block_size, const int32_t* block_table, int64_t max_blocks,
+                                  const int32_t* cache_seqlens, const int64_t* positions, const void* cos_sin,
+                                  int64_t max_pos, int rope, float softmax_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

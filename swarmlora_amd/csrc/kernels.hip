@@ -683,7 +683,25 @@ struct AttnArgs {
   int64_t num_blocks, max_blocks, max_pos;
   int32_t nseq, L, hq, hkv, bs, rope;
   float scale;
+  // row mode (rowmode != 0): token t reads its fused [q | k | v] row at
+  // qkv_row[t] and writes its output row at out_row[t]
+  int32_t rowmode;
+  bf16* qkv_row[kSkinnyMaxTok];
+  bf16* out_row[kSkinnyMaxTok];
 };
+
+__device__ __forceinline__ bf16* tok_q(const AttnArgs& a, int64_t t) {
+  return a.rowmode ? a.qkv_row[t] : a.q + t * a.qs;
+}
+__device__ __forceinline__ bf16* tok_k(const AttnArgs& a, int64_t t) {
+  return a.rowmode ? a.qkv_row[t] + a.hq * 128 : a.k + t * a.ks;
+}
+__device__ __forceinline__ const bf16* tok_v(const AttnArgs& a, int64_t t) {
+  return a.rowmode ? a.qkv_row[t] + (a.hq + a.hkv) * 128 : a.v + t * a.vs;
+}
+__device__ __forceinline__ bf16* tok_out(const AttnArgs& a, int64_t t) {
+  return a.rowmode ? a.out_row[t] : a.out + t * (int64_t)a.hq * 128;
+}
 
 // NeoX rotation of q and k at their positions, then k/v appended to the pages.
 // One workgroup per (sequence, new token); 64 threads per head-pair loop.
@@ -696,8 +714,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(AttnArgs a) {
   const int nh = a.hq + a.hkv;
   for (int it = threadIdx.x; it < nh * 64; it += blockDim.x) {
     const int h = it >> 6, d = it & 63;
-    bf16* base = (h < a.hq) ? a.q + (int64_t)tokid * a.qs + h * 128
-                            : a.k + (int64_t)tokid * a.ks + (h - a.hq) * 128;
+    bf16* base = (h < a.hq) ? tok_q(a, tokid) + h * 128 : tok_k(a, tokid) + (h - a.hq) * 128;
     if (do_rope) {
       const float c = bf2f(cs[d]), sn = bf2f(cs[64 + d]);
       const float x1 = bf2f(base[d]), x2 = bf2f(base[d + 64]);
@@ -712,8 +729,8 @@ __global__ __launch_bounds__(256) void rope_append_kernel(AttnArgs a) {
   const int32_t blk = a.bt[(int64_t)s * a.max_blocks + blk_i];
   if (blk < 0 || blk >= a.num_blocks) return;
   const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * a.hkv * 128;
-  const bf16* ksrc = a.k + (int64_t)tokid * a.ks;
-  const bf16* vsrc = a.v + (int64_t)tokid * a.vs;
+  const bf16* ksrc = tok_k(a, tokid);
+  const bf16* vsrc = tok_v(a, tokid);
   for (int e = threadIdx.x; e < a.hkv * 16; e += blockDim.x) {
     reinterpret_cast<u32x4*>(a.kc + dst)[e] = reinterpret_cast<const u32x4*>(ksrc)[e];
     reinterpret_cast<u32x4*>(a.vc + dst)[e] = reinterpret_cast<const u32x4*>(vsrc)[e];
@@ -738,7 +755,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const bf16* qp = a.q + ((int64_t)s * a.L + i) * a.qs + (h * G + g) * 128 + dl;
+    const bf16* qp = tok_q(a, (int64_t)s * a.L + i) + (h * G + g) * 128 + dl;
     unpack8(ld16(qp), qv[g]);
 #pragma unroll
     for (int d = 0; d < 8; ++d) qv[g][d] *= a.scale;
@@ -810,7 +827,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
       }
     }
     const float r = (l > 0.f) ? o / l : 0.f;
-    a.out[(((int64_t)s * a.L + i) * a.hq + h * G + g) * 128 + d] = f2bf(r);
+    tok_out(a, (int64_t)s * a.L + i)[(h * G + g) * 128 + d] = f2bf(r);
   }
 }
 
@@ -820,6 +837,84 @@ __global__ void zero_blocks_kernel(bf16* cache, const int64_t* ids, int64_t nblo
   u32x4* p = reinterpret_cast<u32x4*>(cache + ids[b] * block_elems);
   const int64_t nv = block_elems >> 3;
   for (int64_t e = threadIdx.x; e < nv; e += blockDim.x) p[e] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// ------------------------------------------------- worker elementwise ---
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T* sh) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane == 0) sh[wv] = v;
+  __syncthreads();
+  T r = sh[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = op(r, sh[i]);
+  return r;
+}
+
+struct RowPtrs {
+  int32_t ntok;
+  const bf16* in[kSkinnyMaxTok];
+  bf16* out[kSkinnyMaxTok];
+};
+
+// h[t] = bf16(h[t] + in[t]) when has_add; out[t] = bf16(bf16(h * rsqrt(mean(h^2)
+// + eps)) * w): LlamaRMSNorm on the residual stream (worker_sync.py:1344-1350,
+// :314-319, :383-389).  One workgroup per token.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(bf16* __restrict__ h, int64_t d, RowPtrs r,
+                                                           const bf16* __restrict__ w, float eps, int has_add) {
+  __shared__ float sh[4];
+  const int t = blockIdx.x;
+  bf16* hr = h + (int64_t)t * d;
+  const int64_t nv = d >> 3;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+    float x[8];
+    unpack8(ld16(hr + 8 * i), x);
+    if (has_add) {
+      float y[8];
+      unpack8(ld16(r.in[t] + 8 * i), y);
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        o[j] = f2bf(x[j] + y[j]);
+        x[j] = bf2f(o[j]);
+      }
+      *reinterpret_cast<u32x4*>(hr + 8 * i) = __builtin_bit_cast(u32x4, o);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+  }
+  ss = block_reduce<float>(ss, [](float x, float y) { return x + y; }, sh);
+  const float rs = rsqrtf(ss / (float)d + eps);
+  for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+    float x[8], g[8];
+    unpack8(ld16(hr + 8 * i), x);
+    unpack8(ld16(w + 8 * i), g);
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(f2bf(x[j] * rs)) * g[j]);
+    *reinterpret_cast<u32x4*>(r.out[t] + 8 * i) = __builtin_bit_cast(u32x4, o);
+  }
+}
+
+// out[t][j] = bf16(bf16(silu(g)) * u), g = in[t][j], u = in[t][inter + j]
+// (F.silu(gate) * up in bf16, worker_sync.py:158, :1397).
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(RowPtrs r, int64_t inter) {
+  const int t = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (inter >> 3)) return;
+  float g[8], u[8];
+  unpack8(ld16(r.in[t] + 8 * i), g);
+  unpack8(ld16(r.in[t] + inter + 8 * i), u);
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sg = bf2f(f2bf(g[j] / (1.0f + __expf(-g[j]))));
+    o[j] = f2bf(sg * u[j]);
+  }
+  *reinterpret_cast<u32x4*>(r.out[t] + 8 * i) = __builtin_bit_cast(u32x4, o);
 }
 
 // ------------------------------------------------------ embed / LM head ---
@@ -860,19 +955,6 @@ struct SampleArgs {
 __device__ __forceinline__ uint32_t fkey(float f) {
   const uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-template <typename T, typename Op>
-__device__ __forceinline__ T block_reduce(T v, Op op, T* sh) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
-  __syncthreads();
-  if (lane == 0) sh[wv] = v;
-  __syncthreads();
-  T r = sh[0];
-  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = op(r, sh[i]);
-  return r;
 }
 
 __device__ __forceinline__ uint64_t mix64(uint64_t x) {
@@ -1257,6 +1339,20 @@ int launch_shrink_only(int64_t K, int ntok, const bf16* const* xrows, const int3
   return SWL_OK;
 }
 
+int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
+  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L)), dim3(256), 0, st, a);
+  SWL_LAUNCH_CHECK("rope_append_kernel launch");
+  const dim3 grid((unsigned)a.hkv, (unsigned)a.L, (unsigned)a.nseq);
+  switch (G) {
+    case 1: hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(256), 0, st, a); break;
+  }
+  SWL_LAUNCH_CHECK("attention_kernel launch");
+  return SWL_OK;
+}
+
 }  // namespace
 
 // ================================================================ C ABI ===
@@ -1429,18 +1525,7 @@ int swl_paged_attention_bf16(void* q, void* k, const void* v, int64_t q_stride, 
   a.bs = block_size;
   a.rope = rope;
   a.scale = softmax_scale;
-  hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(nseq * q_len)), dim3(256), 0, st, a);
-  SWL_LAUNCH_CHECK("rope_append_kernel launch");
-  const dim3 grid((unsigned)hkv, (unsigned)q_len, (unsigned)nseq);
-  switch (G) {
-    case 1: hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(attention_kernel<2>, grid, dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(256), 0, st, a); break;
-  }
-  SWL_LAUNCH_CHECK("attention_kernel launch");
-  return SWL_OK;
+  return launch_attention(a, G, (hipStream_t)stream);
 }
 
 int swl_zero_blocks_bf16(void* const* caches, int ncache, const int64_t* block_ids, int64_t nblocks,
@@ -1669,4 +1754,90 @@ extern "C" int swl_embed_bf16(const void* const* ids, const int64_t* rows, int n
                               int64_t hidden, void* const* out, void* stream) {
   SWL_CHECK(ids && rows && table && out, SWL_ERR_INVALID, "swl_embed_bf16: null argument");
   return swl::embed_launch(n, rows, ids, out, table, vocab, hidden, (hipStream_t)stream);
+}
+
+// ============================================= worker-side row entry points
+extern "C" int swl_rmsnorm_rows_bf16(void* h, int64_t ntok, int64_t d, const void* const* add_rows,
+                                     const void* weight, float eps, void* const* out_rows, void* stream) {
+  SWL_CHECK(h && weight && out_rows, SWL_ERR_INVALID, "swl_rmsnorm_rows_bf16: null argument");
+  SWL_CHECK(ntok >= 0 && ntok <= kSkinnyMaxTok, SWL_ERR_INVALID, "swl_rmsnorm_rows_bf16: at most 64 rows");
+  SWL_CHECK(d > 0 && d % 8 == 0, SWL_ERR_INVALID, "swl_rmsnorm_rows_bf16: d must be a multiple of 8");
+  if (ntok == 0) return SWL_OK;
+  RowPtrs r{};
+  r.ntok = (int)ntok;
+  for (int i = 0; i < ntok; ++i) {
+    SWL_CHECK(out_rows[i] && (!add_rows || add_rows[i]), SWL_ERR_INVALID, "swl_rmsnorm_rows_bf16: null row");
+    r.out[i] = reinterpret_cast<bf16*>(out_rows[i]);
+    r.in[i] = add_rows ? reinterpret_cast<const bf16*>(add_rows[i]) : nullptr;
+  }
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)ntok), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<bf16*>(h), d, r, reinterpret_cast<const bf16*>(weight), eps, add_rows ? 1 : 0);
+  SWL_LAUNCH_CHECK("rmsnorm_rows_kernel launch");
+  return SWL_OK;
+}
+
+extern "C" int swl_silu_mul_rows_bf16(const void* const* in_rows, void* const* out_rows, int64_t ntok,
+                                      int64_t inter, void* stream) {
+  SWL_CHECK(in_rows && out_rows, SWL_ERR_INVALID, "swl_silu_mul_rows_bf16: null argument");
+  SWL_CHECK(ntok >= 0 && ntok <= kSkinnyMaxTok, SWL_ERR_INVALID, "swl_silu_mul_rows_bf16: at most 64 rows");
+  SWL_CHECK(inter > 0 && inter % 8 == 0, SWL_ERR_INVALID, "swl_silu_mul_rows_bf16: inter must be a multiple of 8");
+  if (ntok == 0) return SWL_OK;
+  RowPtrs r{};
+  r.ntok = (int)ntok;
+  for (int i = 0; i < ntok; ++i) {
+    SWL_CHECK(in_rows[i] && out_rows[i], SWL_ERR_INVALID, "swl_silu_mul_rows_bf16: null row");
+    r.in[i] = reinterpret_cast<const bf16*>(in_rows[i]);
+    r.out[i] = reinterpret_cast<bf16*>(out_rows[i]);
+  }
+  const dim3 grid((unsigned)(((inter >> 3) + 255) / 256), (unsigned)ntok);
+  hipLaunchKernelGGL(silu_mul_rows_kernel, grid, dim3(256), 0, (hipStream_t)stream, r, inter);
+  SWL_LAUNCH_CHECK("silu_mul_rows_kernel launch");
+  return SWL_OK;
+}
+
+extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len,
+                                             int hq, int hkv, int d, void* k_cache, void* v_cache,
+                                             int64_t num_blocks, int block_size, const int32_t* block_table,
+                                             int64_t max_blocks, const int32_t* cache_seqlens,
+                                             const int64_t* positions, const void* cos_sin, int64_t max_pos,
+                                             int rope, float softmax_scale, void* stream) {
+  SWL_CHECK(qkv_rows && out_rows && k_cache && v_cache && block_table && cache_seqlens, SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: null argument");
+  SWL_CHECK(d == 128 && hq > 0 && hkv > 0 && hq % hkv == 0, SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: head_dim must be 128 and hq a multiple of hkv");
+  const int G = hq / hkv;
+  SWL_CHECK(G == 1 || G == 2 || G == 4 || G == 8, SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: hq / hkv must be 1, 2, 4 or 8");
+  SWL_CHECK(nseq >= 0 && q_len >= 1 && (int64_t)nseq * q_len <= kSkinnyMaxTok, SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: at most 64 token rows");
+  SWL_CHECK(block_size > 0 && num_blocks > 0 && max_blocks > 0, SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: bad page geometry");
+  SWL_CHECK(!rope || (cos_sin && positions && max_pos > 0), SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: rope needs positions and cos_sin");
+  if (nseq == 0) return SWL_OK;
+  AttnArgs a{};
+  a.rowmode = 1;
+  for (int t = 0; t < nseq * q_len; ++t) {
+    SWL_CHECK(qkv_rows[t] && out_rows[t] && (reinterpret_cast<uintptr_t>(qkv_rows[t]) & 15) == 0, SWL_ERR_INVALID,
+              "swl_paged_attention_rows_bf16: rows must be non-null and 16-byte aligned");
+    a.qkv_row[t] = reinterpret_cast<bf16*>(qkv_rows[t]);
+    a.out_row[t] = reinterpret_cast<bf16*>(out_rows[t]);
+  }
+  a.kc = reinterpret_cast<bf16*>(k_cache);
+  a.vc = reinterpret_cast<bf16*>(v_cache);
+  a.bt = block_table;
+  a.seqlens = cache_seqlens;
+  a.pos = positions;
+  a.cs = reinterpret_cast<const bf16*>(cos_sin);
+  a.num_blocks = num_blocks;
+  a.max_blocks = max_blocks;
+  a.max_pos = max_pos;
+  a.nseq = nseq;
+  a.L = q_len;
+  a.hq = hq;
+  a.hkv = hkv;
+  a.bs = block_size;
+  a.rope = rope;
+  a.scale = softmax_scale;
+  return launch_attention(a, G, (hipStream_t)stream);
 }

@@ -324,3 +324,104 @@ def zero_blocks(caches: Sequence[torch.Tensor], block_ids: torch.Tensor):
     ids = block_ids.contiguous()
     arr = _ptr_array(caches)
     _lib.check(_lib.load().swl_zero_blocks_bf16(arr, len(caches), _ptr(ids), ids.numel(), per_block, _stream()))
+
+
+# ------------------------------------------------------- token-row ops ---
+class RowSet:
+    """A fixed list of per-token bf16 rows (1-D views of at least `width`
+    elements each, 16-byte aligned), validated once and kept as a host array
+    of device pointers so a decode loop can reuse it every step."""
+
+    MAX_ROWS = 64
+
+    def __init__(self, rows: Sequence[torch.Tensor], width: int):
+        if len(rows) > self.MAX_ROWS:
+            raise ValueError(f"at most {self.MAX_ROWS} rows")
+        for i, r in enumerate(rows):
+            _need(r, f"row[{i}]")
+            if r.dim() != 1 or r.numel() < width or r.stride(0) != 1:
+                raise ValueError(f"row[{i}] must be a contiguous 1-D view of >= {width} elements")
+            if r.data_ptr() % 16:
+                raise ValueError(f"row[{i}] must be 16-byte aligned")
+        self.rows = list(rows)  # keeps the storage alive
+        self.width = width
+        self.array = _ptr_array(self.rows)
+
+    def __len__(self):
+        return len(self.rows)
+
+
+def _rowset(rows, width: int) -> RowSet:
+    if isinstance(rows, RowSet):
+        if rows.width < width:
+            raise ValueError(f"rows are {rows.width} wide, need {width}")
+        return rows
+    return RowSet(rows, width)
+
+
+def rmsnorm_rows(h: torch.Tensor, weight: torch.Tensor, eps: float, out_rows, add_rows=None):
+    """Residual stream h [ntok, d] (contiguous, updated in place): when
+    add_rows is given h[t] = h[t] + add_rows[t] (bf16); then out_rows[t] =
+    LlamaRMSNorm(h[t]) * weight."""
+    _need(h, "h")
+    _need(weight, "weight")
+    if h.dim() != 2 or not h.is_contiguous():
+        raise ValueError("h must be contiguous [ntok, d]")
+    ntok, d = h.shape
+    if weight.numel() != d or not weight.is_contiguous():
+        raise ValueError("weight must be contiguous [d]")
+    out = _rowset(out_rows, d)
+    add = _rowset(add_rows, d) if add_rows is not None else None
+    if len(out) != ntok or (add is not None and len(add) != ntok):
+        raise ValueError("one out (and add) row per token")
+    _lib.check(_lib.load().swl_rmsnorm_rows_bf16(_ptr(h), ntok, d, add.array if add is not None else None,
+                                                 _ptr(weight), float(eps), out.array, _stream()))
+
+
+def silu_mul_rows(in_rows, out_rows, inter: int):
+    """out_rows[t] = silu(in_rows[t][:inter]) * in_rows[t][inter:2*inter]."""
+    src = _rowset(in_rows, 2 * inter)
+    dst = _rowset(out_rows, inter)
+    if len(src) != len(dst):
+        raise ValueError("one out row per in row")
+    _lib.check(_lib.load().swl_silu_mul_rows_bf16(src.array, dst.array, len(src), inter, _stream()))
+
+
+def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: int, k_cache: torch.Tensor,
+                         v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
+                         positions: Optional[torch.Tensor], cos_sin: Optional[torch.Tensor], softmax_scale: float,
+                         rope: bool = True):
+    """paged_attention over per-token rows: token t = seq * q_len + i has
+    its fused [q | k | v] row at qkv_rows[t] (rotated in place) and gets its
+    [hq * d] output at out_rows[t]."""
+    qkv = _rowset(qkv_rows, (hq + 2 * hkv) * d)
+    out = _rowset(out_rows, hq * d)
+    if len(qkv) != len(out) or len(qkv) % q_len:
+        raise ValueError("rows must be nseq * q_len, one out row per qkv row")
+    nseq = len(qkv) // q_len
+    for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _need(t, nm)
+        if not t.is_contiguous():
+            raise ValueError(f"{nm} must be contiguous")
+    _need(block_table, "block_table", torch.int32)
+    _need(cache_seqlens, "cache_seqlens", torch.int32)
+    nb, bs, hkv2, d2 = k_cache.shape
+    if v_cache.shape != k_cache.shape or hkv2 != hkv or d2 != d:
+        raise ValueError("cache geometry mismatch")
+    if block_table.dim() != 2 or block_table.shape[0] < nseq or not block_table.is_contiguous():
+        raise ValueError("block_table must be contiguous [nseq, max_blocks]")
+    if cache_seqlens.numel() < nseq:
+        raise ValueError("cache_seqlens must have nseq entries")
+    max_pos = 0
+    if rope:
+        _need(positions, "positions", torch.int64)
+        _need(cos_sin, "cos_sin")
+        if positions.numel() != nseq * q_len:
+            raise ValueError("positions must have nseq * q_len entries")
+        if cos_sin.shape[-1] != d or not cos_sin.is_contiguous():
+            raise ValueError("cos_sin must be contiguous [max_pos, d]")
+        max_pos = cos_sin.shape[0]
+    _lib.check(_lib.load().swl_paged_attention_rows_bf16(
+        qkv.array, out.array, nseq, q_len, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs, _ptr(block_table),
+        block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope else None),
+        _ptr(cos_sin if rope else None), max_pos, 1 if rope else 0, float(softmax_scale), _stream()))
