@@ -181,6 +181,19 @@ int swl_sample_bf16(const void* logits, int64_t n, int64_t vocab, void* const* o
                     const float* temperature, const int32_t* top_k, const float* top_p, uint64_t seed,
                     void* stream);
 
+/* ------------------------------------------------------ launch timer ----
+ * Benchmark instrumentation (no counterpart in the reference).  After
+ * swl_timer_arm(capacity), each decode-shaped projection (a round or gemm of
+ * at most 64 token rows) launched outside graph capture records HIP events on
+ * its stream around its base kernel and its epilogue kernel, for up to
+ * `capacity` launches.  swl_timer_collect waits for them, disarms, and returns
+ * per launch: base/epilogue milliseconds, N, K, token rows and the base
+ * kernel's algorithmic bytes (W + token rows + distinct stacked LoRA A).
+ * Single-threaded use only. */
+int swl_timer_arm(int capacity);
+int swl_timer_collect(int max_records, float* base_ms, float* epilogue_ms, int64_t* n, int64_t* k, int32_t* ntok,
+                      int64_t* bytes, int* count);
+
 /* ----------------------------------------------- worker-side row ops ----
  * Token-row variants of the worker's per-layer elementwise work, so the
  * batched decode step reads and writes slot buffers directly (at most 64

@@ -129,7 +129,8 @@ int swl_agg_clear_adapters(void);
 /* One batched round over the slot pool: execute_batched_gemm_slots
  * (ext_aggregator.cpp:470-626) for n slots in arrival order, plus the pooled
  * adapters' LoRA delta.  tokens[i] = bx*tx of slot i's command; adapter_ids
- * may be NULL (or hold -1) for no adapter. */
+ * may be NULL (or hold -1) for no adapter.  Kernels go to `stream` as given
+ * (NULL is the device's null stream, ordered with other null-stream work). */
 int swl_agg_execute_round(int op_type, int layer_idx, int n, const int32_t* slot_ids, const int32_t* worker_ids,
                           const int64_t* tokens, const int32_t* adapter_ids, void* stream);
 

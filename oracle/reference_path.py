@@ -282,3 +282,77 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """F.silu(gate) * up in bf16, worker_sync.py:158, :1397."""
     return torch.nn.functional.silu(gate) * up
+
+
+# ------------------------------------------------------- batched decode step --
+def decode_step(cfg, weights, adapters, k_caches, v_caches, block_table, seqlens, ids, cos_sin,
+                layers: Optional[int] = None):
+    """One token for W workers, in the order of the reference's per-token
+    driver (worker_sync.py:1337-1420) with the aggregator's batched rounds
+    (ext_aggregator.cpp:545-621: cat of the W token rows, x @ W^T, per-worker
+    rows back): embed, per layer input RMSNorm -> QKV round + FusedLoRA delta
+    -> RoPE/append/attention -> O round + delta + residual -> post RMSNorm ->
+    Gate+Up round + FusedLoRA delta -> SiLU*up -> Down round + delta +
+    residual; final norm; LM head (greedy uses argmax of these logits).
+
+    cfg: hidden, heads, kv_heads, head_dim, inter, eps, scale (LoRA scaling).
+    weights: {"layers": [{q,k,v,o,gate,up,down,input_norm,post_norm}],
+    "embed", "lm_head", "final_norm"} (CPU bf16).  adapters[w]: {layer: {proj:
+    (A [r, in], B [out, r])}} or None.  k/v_caches: per-layer page pools
+    [num_blocks, bs, kv_heads, head_dim], appended IN PLACE.  seqlens: int32
+    [W] context before the step; ids: int64 [W].  layers limits the layer
+    count (a partial step, for timing samples).
+    Returns (final-norm hidden [W, hidden], logits [W, vocab])."""
+    W = ids.numel()
+    hq, hkv, hd = cfg.heads, cfg.kv_heads, cfg.head_dim
+    kvd = hkv * hd
+    dims_qkv = [hq * hd, kvd, kvd]
+    dims_gu = [cfg.inter, cfg.inter]
+    h = weights["embed"][ids.reshape(-1)]                       # [W, hidden]
+    pos = seqlens.long()
+    n_layers = len(weights["layers"]) if layers is None else layers
+    for li in range(n_layers):
+        w = weights["layers"][li]
+        res = h
+        x = rms_norm(h, w["input_norm"], cfg.eps)
+        Wqkv, Wgu = fuse_layer_weights(w["q"], w["k"], w["v"], w["gate"], w["up"])
+        base = base_gemm(x, Wqkv)
+        q, k, v = [], [], []
+        for s in range(W):
+            ad = adapters[s][li] if adapters[s] is not None else None
+            deltas = None
+            if ad is not None:
+                fA, fB = fused_lora_weights([(*ad[p], cfg.scale) for p in ("q", "k", "v")], dims_qkv)
+                deltas = fused_lora_forward(x[s:s + 1], fA, fB, dims_qkv)
+            qs, ks, vs = qkv_get(base[s:s + 1], dims_qkv, deltas)
+            q.append(qs), k.append(ks), v.append(vs)
+        q = torch.cat(q).reshape(W, 1, hq, hd)
+        k = torch.cat(k).reshape(W, 1, hkv, hd)
+        v = torch.cat(v).reshape(W, 1, hkv, hd)
+        attn, _, _ = paged_attention(q, k, v, k_caches[li], v_caches[li], block_table, seqlens, pos, cos_sin,
+                                     1.0 / math.sqrt(hd))
+        xa = attn.reshape(W, hq * hd)
+        o = base_gemm(xa, w["o"])
+        h = torch.cat([o_down_get(o[s:s + 1], res[s:s + 1],
+                                  remote_lora_delta(xa[s:s + 1], *adapters[s][li]["o"], cfg.scale)
+                                  if adapters[s] is not None else None) for s in range(W)])
+        res = h
+        x = rms_norm(h, w["post_norm"], cfg.eps)
+        gu = base_gemm(x, Wgu)
+        m = []
+        for s in range(W):
+            deltas = None
+            if adapters[s] is not None:
+                ad = adapters[s][li]
+                fA, fB = fused_lora_weights([(*ad[p], cfg.scale) for p in ("gate", "up")], dims_gu)
+                deltas = fused_lora_forward(x[s:s + 1], fA, fB, dims_gu)
+            g, u = qkv_get(gu[s:s + 1], dims_gu, deltas)
+            m.append(silu_mul(g, u))
+        m = torch.cat(m)
+        d = base_gemm(m, w["down"])
+        h = torch.cat([o_down_get(d[s:s + 1], res[s:s + 1],
+                                  remote_lora_delta(m[s:s + 1], *adapters[s][li]["down"], cfg.scale)
+                                  if adapters[s] is not None else None) for s in range(W)])
+    hn = rms_norm(h, weights["final_norm"], cfg.eps)
+    logits = base_gemm(hn, weights["lm_head"])
+    return hn, logits

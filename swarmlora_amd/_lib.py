@@ -76,6 +76,9 @@ _SIGS = {
     "swl_sample_bf16": (c_int, [c_vp, c_i64, c_i64, P_vp, P_i32, ctypes.POINTER(c_f32), P_i32,
                                 ctypes.POINTER(c_f32), c_u64, c_vp]),
     "swl_zero_blocks_bf16": (c_int, [P_vp, c_int, c_vp, c_i64, c_i64, c_vp]),
+    "swl_timer_arm": (c_int, [c_int]),
+    "swl_timer_collect": (c_int, [c_int, ctypes.POINTER(c_f32), ctypes.POINTER(c_f32), P_i64, P_i64, P_i32, P_i64,
+                                  ctypes.POINTER(c_int)]),
     "swl_rmsnorm_rows_bf16": (c_int, [c_vp, c_i64, c_i64, P_vp, c_vp, c_f32, P_vp, c_vp]),
     "swl_silu_mul_rows_bf16": (c_int, [P_vp, P_vp, c_i64, c_i64, c_vp]),
     "swl_paged_attention_rows_bf16": (c_int, [P_vp, P_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64,

@@ -489,10 +489,6 @@ int swl_agg_execute_round(int op_type, int layer_idx, int n, const int32_t* slot
     }
   }
   hipStream_t st = (hipStream_t)stream;
-  if (!st) {
-    rc = stream_get(&st);
-    if (rc) return rc;
-  }
   if (any_lora) {
     rc = upload_adapters();
     if (rc) return rc;

@@ -1116,6 +1116,34 @@ int scratch_get(size_t need, hipStream_t stream, void** out) {
   return SWL_OK;
 }
 
+// ---------------------------------------------------------- launch timer
+// Optional HIP-event timing of the decode projection: when armed, every
+// launch_skinny call (outside graph capture) records three events on its own
+// stream, before the base kernel, between base and epilogue, and after the
+// epilogue, plus the launch's algorithmic byte count.  Used by benchmarks
+// to compute achieved bandwidth per kernel; single-threaded use only.
+struct LaunchTimer {
+  bool armed = false;
+  int cap = 0;
+  int n = 0;
+  std::vector<hipEvent_t> ev;  // 3 per record
+  std::vector<int64_t> N, K, bytes;
+  std::vector<int32_t> ntok;
+};
+LaunchTimer g_timer;
+
+// Returns the record slot to use for this launch, or -1.
+int timer_slot(hipStream_t st) {
+  if (!g_timer.armed || g_timer.n >= g_timer.cap) return -1;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return -1;
+  return g_timer.n++;
+}
+
+void timer_mark(int slot, int which, hipStream_t st) {
+  if (slot >= 0) (void)hipEventRecord(g_timer.ev[3 * slot + which], st);
+}
+
 // -------------------------------------------------------------- launchers
 int fill_segptrs(SegPtrs& sp, const void* const* ptrs, const int64_t* rows, int n, int64_t d, int64_t* total) {
   SWL_CHECK(n >= 1 && n <= kMaxSeg, SWL_ERR_INVALID, "segment count must be in [1, 128]");
@@ -1271,6 +1299,18 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const size_t lds = sizeof(bf16) * (size_t)TT * 16 * ((size_t)a.ks_steps * 32 + 8);
   const dim3 grid((unsigned)(a.n_shrink_wg + a.n_base_wg));
   const dim3 block((unsigned)(waves * 64));
+  const int tslot = timer_slot(st);
+  if (tslot >= 0) {
+    // algorithmic bytes of the base kernel: W and the token rows once, each
+    // distinct adapter's stacked A once
+    int64_t bytes = 2 * (N * K + (int64_t)ntok * K);
+    for (int g = 0; g < sp.ngroups && has_lora; ++g) bytes += 2 * (int64_t)sp.g_arows[g] * K;
+    g_timer.N[tslot] = N;
+    g_timer.K[tslot] = K;
+    g_timer.ntok[tslot] = ntok;
+    g_timer.bytes[tslot] = bytes;
+  }
+  timer_mark(tslot, 0, st);
   if (waves == 4) {
     switch (TT) {
       case 1: hipLaunchKernelGGL((split_kernel<1, 4>), grid, block, lds, st, a); break;
@@ -1287,6 +1327,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     }
   }
   SWL_LAUNCH_CHECK("split_kernel launch");
+  timer_mark(tslot, 1, st);
 
   EpiArgs e{};
   e.part = a.part;
@@ -1312,6 +1353,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const unsigned eg = (unsigned)(((int64_t)ntok * quads + 255) / 256);
   hipLaunchKernelGGL(epilogue_kernel, dim3(eg), dim3(256), 0, st, e);
   SWL_LAUNCH_CHECK("epilogue_kernel launch");
+  timer_mark(tslot, 2, st);
   return SWL_OK;
 }
 
@@ -1526,6 +1568,45 @@ int swl_paged_attention_bf16(void* q, void* k, const void* v, int64_t q_stride, 
   a.rope = rope;
   a.scale = softmax_scale;
   return launch_attention(a, G, (hipStream_t)stream);
+}
+
+int swl_timer_arm(int capacity) {
+  SWL_CHECK(capacity >= 0 && capacity <= (1 << 20), SWL_ERR_INVALID, "swl_timer_arm: bad capacity");
+  if ((int)g_timer.ev.size() < 3 * capacity) {
+    const size_t have = g_timer.ev.size();
+    g_timer.ev.resize(3 * (size_t)capacity, nullptr);
+    for (size_t i = have; i < g_timer.ev.size(); ++i) SWL_HIP(hipEventCreate(&g_timer.ev[i]));
+    g_timer.N.resize(capacity);
+    g_timer.K.resize(capacity);
+    g_timer.bytes.resize(capacity);
+    g_timer.ntok.resize(capacity);
+  }
+  g_timer.cap = capacity;
+  g_timer.n = 0;
+  g_timer.armed = capacity > 0;
+  return SWL_OK;
+}
+
+int swl_timer_collect(int max_records, float* base_ms, float* epilogue_ms, int64_t* n, int64_t* k, int32_t* ntok,
+                      int64_t* bytes, int* count) {
+  SWL_CHECK(count && max_records >= 0, SWL_ERR_INVALID, "swl_timer_collect: null argument");
+  g_timer.armed = false;
+  const int m = std::min(g_timer.n, max_records);
+  for (int i = 0; i < m; ++i) {
+    SWL_HIP(hipEventSynchronize(g_timer.ev[3 * i + 2]));
+    float a = 0.f, b = 0.f;
+    SWL_HIP(hipEventElapsedTime(&a, g_timer.ev[3 * i], g_timer.ev[3 * i + 1]));
+    SWL_HIP(hipEventElapsedTime(&b, g_timer.ev[3 * i + 1], g_timer.ev[3 * i + 2]));
+    if (base_ms) base_ms[i] = a;
+    if (epilogue_ms) epilogue_ms[i] = b;
+    if (n) n[i] = g_timer.N[i];
+    if (k) k[i] = g_timer.K[i];
+    if (ntok) ntok[i] = g_timer.ntok[i];
+    if (bytes) bytes[i] = g_timer.bytes[i];
+  }
+  *count = m;
+  g_timer.n = 0;
+  return SWL_OK;
 }
 
 int swl_zero_blocks_bf16(void* const* caches, int ncache, const int64_t* block_ids, int64_t nblocks,

@@ -1,0 +1,267 @@
+"""One batched decode step for W workers on one GPU, as a single HIP stream.
+
+What one token of SwarmLoRA's serving loop does on the GPU, in order: the
+embed round, then per layer input RMSNorm -> fused-QKV round -> RoPE + KV
+append + paged attention -> O round -> residual add + post RMSNorm ->
+Gate+Up round -> SiLU*up -> Down round -> residual add, then the final norm
+and the LM-head round with greedy sampling (reference per-token driver
+src/worker/worker_sync.py:1274-1425, aggregator op sequence
+src/cpp_extensions/ext_aggregator.cpp:1095-1199).
+
+Here every worker is a slot of the aggregator's pool in this process: the
+four projection rounds run through the aggregator runtime
+(swl_agg_execute_round over the slots' buffers, LoRA deltas of each worker's
+pooled adapter added in the round's epilogue), and the worker-side work reads
+and writes the same slot buffers in place (row-mode attention writes the O
+round's input rows, SiLU*up writes the Down round's input rows, RMSNorm adds
+the round's output rows into the residual stream and writes the next round's
+input rows).  The cross-process barrier of the multi-process runtime is
+replaced by stream order, so the whole step can be captured as one HIP graph.
+"""
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict, List, Optional
+
+import torch
+
+from . import _lib
+from . import ext_aggregator as agg
+from . import ops
+from .worker.paged_attention import PagedKVCache
+
+BF16 = torch.bfloat16
+
+PROJ = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+@dataclass
+class DecodeShape:
+    """Llama-3.1-8B shape by default (hidden 4096, 32 q / 8 kv heads of 128,
+    intermediate 14336, vocabulary 128256, 32 layers)."""
+    layers: int = 32
+    hidden: int = 4096
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    inter: int = 14336
+    vocab: int = 128256
+    eps: float = 1e-5
+    theta: float = 500000.0
+    block_size: int = 16
+    rank: int = 16
+    scale: float = 2.0
+
+    @property
+    def qkv(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+    def proj_dims(self) -> Dict[str, tuple]:
+        """(in, out) of every projection."""
+        h, kv, i = self.hidden, self.kv_heads * self.head_dim, self.inter
+        return {"q": (h, h), "k": (h, kv), "v": (h, kv), "o": (h, h), "gate": (h, i), "up": (h, i), "down": (i, h)}
+
+    def step_bytes(self, ctx_lens: List[int], n_adapters: int) -> int:
+        """Algorithmic HBM bytes of one step: every weight once, each distinct
+        adapter's A and B once, the KV context once, the LM head once."""
+        dims = self.proj_dims()
+        base = sum(i * o for i, o in dims.values()) * 2 * self.layers
+        lora = sum(self.rank * (i + o) for i, o in dims.values()) * 2 * self.layers * n_adapters
+        kv = sum(ctx_lens) * 2 * self.kv_heads * self.head_dim * 2 * self.layers
+        return base + lora + kv + self.vocab * self.hidden * 2
+
+
+def synthetic_weights(shape: DecodeShape, device, seed: int = 0, std: float = 0.02) -> dict:
+    """Random-init weights on `device`: projections, embedding and LM head
+    ~N(0, std), RMSNorm weights 1."""
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def rn(*s):
+        return (torch.randn(*s, generator=g, device=device, dtype=torch.float32) * std).to(BF16)
+
+    dims = shape.proj_dims()
+    layers = []
+    for _ in range(shape.layers):
+        w = {p: rn(o, i) for p, (i, o) in dims.items()}
+        w["input_norm"] = torch.ones(shape.hidden, dtype=BF16, device=device)
+        w["post_norm"] = torch.ones(shape.hidden, dtype=BF16, device=device)
+        layers.append(w)
+    return {"layers": layers, "embed": rn(shape.vocab, shape.hidden), "lm_head": rn(shape.vocab, shape.hidden),
+            "final_norm": torch.ones(shape.hidden, dtype=BF16, device=device)}
+
+
+def synthetic_adapter(shape: DecodeShape, device, seed: int, std: float = 0.02) -> dict:
+    """{layer: {proj: (A [rank, in], B [out, rank])}}, ~N(0, std)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = {}
+    for li in range(shape.layers):
+        out[li] = {}
+        for p, (i, o) in shape.proj_dims().items():
+            a = (torch.randn(shape.rank, i, generator=g, device=device) * std).to(BF16)
+            b = (torch.randn(o, shape.rank, generator=g, device=device) * std).to(BF16)
+            out[li][p] = (a, b)
+    return out
+
+
+class BatchedDecoder:
+    """W one-token decode slots over a shared slot pool and paged KV cache.
+
+    weights: as returned by synthetic_weights (tensors may live on the CPU;
+    they are copied to `device`).  adapters[w]: as returned by
+    synthetic_adapter, or None for a worker without an adapter.
+    ctx_lens[w]: tokens already in worker w's KV pages; kv_fill(layer, k_cache,
+    v_cache, block_tables) fills the pages (default: leave them zero).
+    Capacity for `max_new` generated tokens is reserved up front.
+    """
+
+    def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
+                 first_ids: List[int], device, max_new: int = 64, kv_fill=None):
+        self.shape = s = shape
+        self.device = dev = torch.device(device)
+        self.W = W = len(ctx_lens)
+        if not 1 <= W <= ops.RowSet.MAX_ROWS:
+            raise ValueError(f"1..{ops.RowSet.MAX_ROWS} workers")
+        if len(adapters) != W or len(first_ids) != W:
+            raise ValueError("one adapter entry and one first token per worker")
+        self.max_new = max_new
+        self.steps_done = 0
+        self.graph = None
+        dev_index = dev.index if dev.index is not None else torch.cuda.current_device()
+
+        # ---- slot pool: one slot per worker (1 token per step)
+        agg.init_slot_pool(W, dev_index, s.hidden, s.inter, s.kv_heads, s.head_dim, 1, 2)
+        self.slot_ids, self.worker_ids = [], []
+        for w in range(W):
+            info = agg.claim_slot(w)
+            self.slot_ids.append(info["slot_id"])
+            self.worker_ids.append(w)
+        views = [agg.slot_tensors(sid) for sid in self.slot_ids]
+        self.slot_in = [v[0] for v in views]
+        self.slot_out = [v[1] for v in views]
+
+        # ---- weights (the aggregator fuses q|k|v and gate|up into its own copies)
+        agg.init_aggregator_begin(s.layers, dev_index)
+        self.norms = []
+        for li, lw in enumerate(weights["layers"]):
+            t = {k: v.to(dev) for k, v in lw.items()}
+            agg.init_aggregator_layer(li, t["q"], t["k"], t["v"], t["o"], None, t["gate"], t["up"], t["down"], None)
+            self.norms.append((t["input_norm"].contiguous(), t["post_norm"].contiguous()))
+            del t
+        agg.init_aggregator_finalize()
+        self.embed = weights["embed"].to(dev).contiguous()
+        self.lm_head = weights["lm_head"].to(dev).contiguous()
+        self.final_norm = weights["final_norm"].to(dev).contiguous()
+        agg.init_embed_lm_head_weights(self.embed, self.lm_head)
+
+        # ---- adapters: pooled, adapter id = worker index
+        agg.clear_adapters()
+        self.adapter_ids = []
+        for w, ad in enumerate(adapters):
+            if ad is None:
+                self.adapter_ids.append(-1)
+                continue
+            self.adapter_ids.append(w)
+            for li in range(s.layers):
+                a = ad[li]
+                for op, projs in ((agg.OP_QKV_FUSED, ("q", "k", "v")), (agg.OP_O_PROJ, ("o",)),
+                                  (agg.OP_GATE_UP_FUSED, ("gate", "up")), (agg.OP_DOWN_PROJ, ("down",))):
+                    A = torch.cat([a[p][0].to(dev) for p in projs], 0).contiguous()
+                    Bs = [a[p][1].to(dev).contiguous() for p in projs]
+                    agg.register_adapter(w, li, op, A, Bs, s.scale)
+
+        # ---- paged KV: the reference keeps one cache per worker; here one
+        # pool of pages with a block table per worker
+        self.kv = PagedKVCache(s.layers, s.kv_heads, s.head_dim, s.block_size, W, max(ctx_lens) + max_new, dev, BF16)
+        for w, c in enumerate(ctx_lens):
+            self.kv.ensure_blocks_for_length(w, c + max_new)
+            self.kv.slot_seq_lens[w] = c
+        self.block_tables = self.kv.get_block_table_tensor(list(range(W)))
+        if kv_fill is not None:
+            for li in range(s.layers):
+                kv_fill(li, self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables)
+        self.seqlens = self.kv.get_seq_lens_tensor(list(range(W)))
+        self.positions = torch.zeros(W, dtype=torch.int64, device=dev)
+        from .worker.paged_attention import RotaryInvFreq, build_vllm_cos_sin_cache
+        self.cos_sin = build_vllm_cos_sin_cache(RotaryInvFreq(s.head_dim, s.theta), self.kv.max_blocks_per_seq *
+                                                s.block_size, dev, BF16)
+
+        # ---- per-step state
+        self.ids = torch.tensor(first_ids, dtype=torch.int64, device=dev).reshape(W, 1)
+        self.h = torch.zeros(W, s.hidden, dtype=BF16, device=dev)        # residual stream
+        self.lm_in = torch.zeros(W, s.hidden, dtype=BF16, device=dev)    # final-norm output
+        self.logits = torch.zeros(W, s.vocab, dtype=BF16, device=dev)
+        self.rows_in_h = ops.RowSet([t[:s.hidden] for t in self.slot_in], s.hidden)
+        self.rows_in_i = ops.RowSet([t[:s.inter] for t in self.slot_in], s.inter)
+        self.rows_out_h = ops.RowSet([t[:s.hidden] for t in self.slot_out], s.hidden)
+        self.rows_out_qkv = ops.RowSet([t[:s.qkv] for t in self.slot_out], s.qkv)
+        self.rows_out_gu = ops.RowSet([t[:2 * s.inter] for t in self.slot_out], 2 * s.inter)
+        self.rows_lm = ops.RowSet([self.lm_in[w] for w in range(W)], s.hidden)
+        self._ids_rows = [self.ids[w] for w in range(W)]
+        self._h_rows = [self.h[w:w + 1] for w in range(W)]
+        self._round_args = ((ctypes.c_int32 * W)(*self.slot_ids), (ctypes.c_int32 * W)(*self.worker_ids),
+                            (ctypes.c_int64 * W)(*([1] * W)), (ctypes.c_int32 * W)(*self.adapter_ids))
+        self._scale = 1.0 / (s.head_dim ** 0.5)
+
+    # ------------------------------------------------------------ one step
+    def _round(self, op: int, layer: int):
+        s_arr, w_arr, t_arr, a_arr = self._round_args
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(_lib.load().swl_agg_execute_round(op, layer, self.W, s_arr, w_arr, t_arr, a_arr, st))
+
+    def _body(self):
+        s = self.shape
+        self.positions.copy_(self.seqlens)
+        ops.embed(self._ids_rows, self.embed, self._h_rows)
+        for li in range(s.layers):
+            in_norm, post_norm = self.norms[li]
+            ops.rmsnorm_rows(self.h, in_norm, s.eps, self.rows_in_h, add_rows=self.rows_out_h if li else None)
+            self._round(agg.OP_QKV_FUSED, li)
+            ops.paged_attention_rows(self.rows_out_qkv, self.rows_in_h, 1, s.heads, s.kv_heads, s.head_dim,
+                                     self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
+                                     self.seqlens, self.positions, self.cos_sin, self._scale)
+            self._round(agg.OP_O_PROJ, li)
+            ops.rmsnorm_rows(self.h, post_norm, s.eps, self.rows_in_h, add_rows=self.rows_out_h)
+            self._round(agg.OP_GATE_UP_FUSED, li)
+            ops.silu_mul_rows(self.rows_out_gu, self.rows_in_i, s.inter)
+            self._round(agg.OP_DOWN_PROJ, li)
+        ops.rmsnorm_rows(self.h, self.final_norm, s.eps, self.rows_lm, add_rows=self.rows_out_h)
+        ops.gemm(self.lm_in, self.lm_head, out=self.logits)
+        W = self.W
+        ops.sample(self.logits, self._ids_rows, [False] * W, [1.0] * W, [0] * W, [1.0] * W, 0)
+        self.seqlens.add_(1)
+
+    def _check_capacity(self):
+        if self.steps_done >= self.max_new:
+            raise RuntimeError(f"BatchedDecoder: KV pages reserved for {self.max_new} new tokens are used up")
+
+    def step_eager(self):
+        """Launch one step's kernels on the current stream."""
+        self._check_capacity()
+        self._body()
+        self.steps_done += 1
+
+    def capture(self):
+        """Capture one step as a HIP graph (call after one eager step, which
+        sizes the library's scratch and uploads the adapter table)."""
+        if self.steps_done == 0:
+            raise RuntimeError("run step_eager() once before capture()")
+        # the captured body is not executed; the graph is replayed by step()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._body()
+        self.graph = g
+
+    def step(self):
+        """One decode step: graph replay if captured, else eager."""
+        if self.graph is None:
+            return self.step_eager()
+        self._check_capacity()
+        self.graph.replay()
+        self.steps_done += 1
+
+    def close(self):
+        self.graph = None
+        for sid, wid in zip(self.slot_ids, self.worker_ids):
+            agg.release_slot(sid, wid)
+        agg.clear_adapters()
+        agg.cleanup_slot_pool()

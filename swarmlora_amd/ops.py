@@ -425,3 +425,23 @@ def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: i
         qkv.array, out.array, nseq, q_len, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs, _ptr(block_table),
         block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope else None),
         _ptr(cos_sin if rope else None), max_pos, 1 if rope else 0, float(softmax_scale), _stream()))
+
+
+# -------------------------------------------------------------- timing ---
+def timer_arm(capacity: int):
+    """Record HIP events around the next `capacity` decode-projection launches
+    (base kernel and epilogue) issued outside graph capture."""
+    _lib.check(_lib.load().swl_timer_arm(int(capacity)))
+
+
+def timer_collect(max_records: int = 1 << 16):
+    """Wait for the armed launches; returns a list of dicts with base_ms,
+    epilogue_ms, n, k, ntok and the base kernel's algorithmic bytes."""
+    m = int(max_records)
+    fa, fb = (ctypes.c_float * m)(), (ctypes.c_float * m)()
+    n, k, b = (ctypes.c_int64 * m)(), (ctypes.c_int64 * m)(), (ctypes.c_int64 * m)()
+    t = (ctypes.c_int32 * m)()
+    cnt = ctypes.c_int(0)
+    _lib.check(_lib.load().swl_timer_collect(m, fa, fb, n, k, t, b, ctypes.byref(cnt)))
+    return [{"base_ms": fa[i], "epilogue_ms": fb[i], "n": n[i], "k": k[i], "ntok": t[i], "bytes": b[i]}
+            for i in range(cnt.value)]
