@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Decode throughput of the batched SwarmLoRA step on one MI355X.
+
+Workload: a 32-layer Llama-3.1-8B-shaped decode step for
+28 workers, one token each, every worker with its own rank-16 LoRA adapter on
+all seven projections (scale 2.0), a paged bf16 KV cache per worker (page 16,
+8 kv heads of 128) holding U{128..2048} tokens of ~N(0,1) context, RMSNorm
+weights 1, RoPE theta 500000, embedding / LM head / projections ~N(0,0.02),
+greedy sampling.  One step = embed + 32 x (QKV, O, Gate+Up, Down rounds with
+attention and the worker-side elementwise work) + LM head = 130 rounds, one
+token per worker.  Synthetic random-init weights (seeded), no checkpoint.
+
+`value` is tokens/s over the timed replays of the captured step (inputs and
+weights resident in HBM).  `roofline` is the decode projection's base
+kernel (every projection round and the LM head use it): algorithmic bytes
+per launch over its mean duration, both from HIP events recorded around each
+launch on its stream during eager steps of the same workload (HIP events
+inside a replayed graph carry no timestamps on ROCm).  `cpu_baseline` times
+the CPU oracle's decode_step (torch-CPU bf16, the reference's op order) on a
+bounded sample: the LM head and one layer, scaled to 32 layers.
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "split_kernel_decode_config4_traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100, help="timed decode steps")
+    ap.add_argument("--warmup", type=int, default=10, help="untimed decode steps before timing")
+    ap.add_argument("--workers", type=int, default=28)
+    ap.add_argument("--timer-steps", type=int, default=3, help="eager steps with per-launch HIP events")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(workers, budget_s):
+    """The CPU oracle's batched decode_step (torch-CPU, bf16) at config-4
+    shapes on this host's cores: the LM head alone (layers=0) and with one
+    layer, repeated within the budget; per step = t0 + 32 * (t1 - t0)."""
+    import torch
+    from oracle import reference_path as ref
+    from swarmlora_amd.decode import DecodeShape
+    threads = torch.get_num_threads()
+    s = DecodeShape()
+    g = torch.Generator().manual_seed(0)
+
+    def rn(*shape, std=0.02):
+        return torch.randn(*shape, generator=g, dtype=torch.bfloat16).mul_(std)
+
+    layer = {p: rn(o, i) for p, (i, o) in s.proj_dims().items()}
+    layer["input_norm"] = torch.ones(s.hidden, dtype=torch.bfloat16)
+    layer["post_norm"] = torch.ones(s.hidden, dtype=torch.bfloat16)
+    weights = {"layers": [layer], "embed": rn(s.vocab, s.hidden), "lm_head": rn(s.vocab, s.hidden),
+               "final_norm": torch.ones(s.hidden, dtype=torch.bfloat16)}
+    adapters = [{0: {p: (rn(s.rank, i), rn(o, s.rank)) for p, (i, o) in s.proj_dims().items()}}
+                for _ in range(workers)]
+    ctx = torch.randint(128, 2049, (workers,), generator=torch.Generator().manual_seed(3))
+    mb = (2048 + 16 + s.block_size - 1) // s.block_size
+    kc = [rn(workers * mb, s.block_size, s.kv_heads, s.head_dim, std=1.0)]
+    vc = [rn(workers * mb, s.block_size, s.kv_heads, s.head_dim, std=1.0)]
+    bt = torch.arange(workers * mb, dtype=torch.int32).reshape(workers, mb)
+    cs = ref.cos_sin_cache(ref.rope_inv_freq(s.head_dim, s.theta), mb * s.block_size)
+    ids = torch.randint(0, s.vocab, (workers,), generator=torch.Generator().manual_seed(4))
+    seq = ctx.to(torch.int32)
+    times = {0: [], 1: []}
+    t_start = time.perf_counter()
+    while True:
+        for L in (0, 1):
+            t0 = time.perf_counter()
+            ref.decode_step(s, weights, adapters, [kc[0].clone()], [vc[0].clone()], bt, seq, ids, cs, layers=L)
+            times[L].append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s and len(times[1]) >= 2:
+            break
+    t0 = statistics.median(times[0])
+    t1 = statistics.median(times[1])
+    step_s = t0 + s.layers * max(t1 - t0, 0.0)
+    return {"value": workers / step_s, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle decode_step (torch-CPU bf16) at config-4 shapes, {workers} workers: LM head alone "
+                       f"{t0 * 1e3:.0f} ms and with one layer {t1 * 1e3:.0f} ms (medians of {len(times[1])}); "
+                       f"step = LM head + 32 x layer = {step_s * 1e3:.0f} ms; includes the per-step page clone; "
+                       f"CPU-seeded weights of the same shapes")}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU (one aggregator per GPU; workers and aggregator share it "
+              "through same-device IPC). --gpus must be 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    from swarmlora_amd import ops
+    from swarmlora_amd.decode import BatchedDecoder, DecodeShape, synthetic_adapter, synthetic_weights
+
+    dev = torch.device("cuda:0")
+    W = args.workers
+    s = DecodeShape()
+    ctx = torch.randint(128, 2049, (W,), generator=torch.Generator().manual_seed(3)).tolist()
+    first = torch.randint(0, s.vocab, (W,), generator=torch.Generator().manual_seed(4)).tolist()
+    weights = synthetic_weights(s, dev, seed=0)
+    adapters = [synthetic_adapter(s, dev, seed=1000 + w) for w in range(W)]
+    kv_gen = torch.Generator(device=dev).manual_seed(5)
+
+    def kv_fill(li, kc, vc, bt):
+        kc.copy_(torch.randn(kc.shape, generator=kv_gen, device=dev, dtype=torch.bfloat16))
+        vc.copy_(torch.randn(vc.shape, generator=kv_gen, device=dev, dtype=torch.bfloat16))
+
+    max_new = 1 + args.warmup + args.steps + args.timer_steps + 1
+    dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill)
+    del weights, adapters
+    torch.cuda.synchronize()
+
+    dec.step_eager()  # sizes scratch, uploads the adapter table
+    dec.capture()
+    for _ in range(args.warmup):
+        dec.step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        dec.step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    ms_per_step = gpu_ms / args.steps
+    value = W * args.steps / (gpu_ms / 1e3)
+
+    # per-launch HIP events on eager steps of the same workload
+    n_rounds = 4 * s.layers
+    ops.timer_arm(args.timer_steps * (n_rounds + 1))
+    for _ in range(args.timer_steps):
+        dec.step_eager()
+    recs = ops.timer_collect()
+    base_ms = [r["base_ms"] for r in recs]
+    base_bytes = [r["bytes"] for r in recs]
+    mean_ms = statistics.fmean(base_ms)
+    mean_bytes = statistics.fmean(base_bytes)
+    achieved = mean_bytes / (mean_ms * 1e-3) / 1e9
+    rounds = [r for r in recs if r["n"] != s.vocab]
+    us_round = statistics.fmean([(r["base_ms"] + r["epilogue_ms"]) * 1e3 for r in rounds])
+    per_op = {}
+    names = {(s.qkv, s.hidden): "qkv", (s.hidden, s.hidden): "o", (2 * s.inter, s.hidden): "gate_up",
+             (s.hidden, s.inter): "down", (s.vocab, s.hidden): "lm_head"}
+    for r in recs:
+        nm = names.get((r["n"], r["k"]), f"{r['n']}x{r['k']}")
+        per_op.setdefault(nm, []).append(r)
+    breakdown = {nm: {"base_us": round(statistics.fmean([x["base_ms"] for x in v]) * 1e3, 2),
+                      "epilogue_us": round(statistics.fmean([x["epilogue_ms"] for x in v]) * 1e3, 2),
+                      "base_GBps": round(statistics.fmean([x["bytes"] for x in v]) /
+                                         (statistics.fmean([x["base_ms"] for x in v]) * 1e-3) / 1e9, 1)}
+                 for nm, v in per_op.items()}
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    step_bytes = s.step_bytes(ctx, W)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(W, args.cpu_seconds)
+
+    line = {
+        "metric": "tok/s at 28 workers, 8B-shape decode; µs per gather-GEMM-scatter round",
+        "value": round(value, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights, adapters, KV pages and token ids)",
+        "config": {"workload": "config4: 32-layer Llama-3.1-8B-shaped batched decode step, 28 workers x 1 token, "
+                               "rank-16 adapter per worker on q/k/v/o/gate/up/down, paged KV ctx U{128..2048}, "
+                               "130 rounds per token, greedy sampling, captured as one HIP graph",
+                   "workers": W, "layers": s.layers, "rounds_per_token": 2 + n_rounds,
+                   "us_per_round": round(us_round, 2),
+                   "us_per_round_of_step": round(ms_per_step * 1e3 / (2 + n_rounds), 2),
+                   "step_algorithmic_GB": round(step_bytes / 1e9, 3),
+                   "step_GBps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+                   "wall_s": round(wall, 3),
+                   "rounds": breakdown},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "split_kernel (decode projection base kernel, all 128 rounds + LM head)",
+                     "mean_launch_us": round(mean_ms * 1e3, 3), "bytes_per_launch": int(mean_bytes)},
+        "cpu_baseline": cpu,
+    }
+    dec.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -136,6 +136,8 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(SegPtrs sp, int64_t d
 // ------------------------------------------------------- LoRA epilogue ----
 // Column blocks of a fused projection output and the LoRA state a round
 // carries into the base kernel's epilogue.
+constexpr int kMaxURow = SWL_MAX_LORA_BLOCKS * 64;  // shrink row: blocks x rank (<= 64)
+
 struct LoraEpi {
   const swl_lora_entry* table;  // device
   const float* u;               // [usplit][u_rows][u_ld] fp32 shrink partials
@@ -264,7 +266,6 @@ __device__ __forceinline__ void epilogue_store4(float (&v)[4], int64_t n, int64_
 //                    rounds once to bf16 and stores each token's row into its
 //                    slot buffer (the scatter).
 constexpr int kKDepth = 8;            // k-steps of W in flight per wave
-constexpr int kLdsBudget = 64 * 1024;  // activation slice bytes per workgroup (default dynamic LDS limit)
 
 struct SplitArgs {
   // base projection -> part[ks][tok][N]
@@ -303,36 +304,44 @@ struct EpiArgs {
 
 __device__ __forceinline__ u32x4 lds16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(1))) void* gbl_ptr;
+// s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: expcnt and lgkmcnt
+// at their maxima, i.e. not waited on)
+constexpr unsigned kWaitVm0 = 0x0F70;
+
+// W fragment of k-step s of a K-slice with `n` steps: steps past the end
+// read the slice's last step again (in bounds) and are zeroed, so a padded
+// pipeline adds nothing.
+__device__ __forceinline__ u32x4 ld_w_step(const bf16* wp, int s, int n) {
+  const u32x4 v = ld16(wp + 32 * (s < n ? s : n - 1));
+  return s < n ? v : u32x4{0u, 0u, 0u, 0u};
+}
+
 // W (one row per lane, k-group per lane quarter) streamed through a D-deep
-// register pipeline; B-fragments of TT token tiles read from LDS.  The caller
-// has already issued the first D W-fragments into w[] (so their latency
-// overlaps the activation staging).  The steady-state body is branch-free so
-// s_waitcnt counts are exact.
+// register pipeline; B-fragments of TT token tiles read from LDS (fragment
+// order: step s, tile t at xl + (s * TT + t) * tstride).  The caller has
+// already issued the first D W-fragments into w[].  nsteps (a multiple of D)
+// are run; W steps from nw on are zero, so every step is pipelined and the
+// body is branch-free (s_waitcnt counts are exact).
 template <int TT, int D>
 __device__ __forceinline__ void kloop_lds(f32x4 (&acc)[TT], u32x4 (&w)[D], const bf16* wp, const bf16* xl,
-                                          int tstride, int nsteps) {
-  const int niter = nsteps / D;
-  if (niter > 0) {
-    for (int it = 0; it + 1 < niter; ++it) {
-      const int base = it * D, nxt = base + D;
+                                          int tstride, int nsteps, int nw) {
+  const int niter = (nsteps + D - 1) / D;
+  for (int it = 0; it + 1 < niter; ++it) {
+    const int base = it * D, nxt = base + D;
 #pragma unroll
-      for (int d = 0; d < D; ++d) {
+    for (int d = 0; d < D; ++d) {
 #pragma unroll
-        for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + t * tstride + 32 * (base + d)), acc[t]);
-        w[d] = ld16(wp + 32 * (nxt + d));
-      }
+      for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + ((base + d) * TT + t) * tstride), acc[t]);
+      w[d] = ld_w_step(wp, nxt + d, nw);
     }
-    const int base = (niter - 1) * D;
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-#pragma unroll
-      for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + t * tstride + 32 * (base + d)), acc[t]);
   }
-  for (int s = niter * D; s < nsteps; ++s) {
-    const u32x4 w1 = ld16(wp + 32 * s);
+  const int base = (niter - 1) * D;
 #pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w1, lds16(xl + t * tstride + 32 * s), acc[t]);
-  }
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + ((base + d) * TT + t) * tstride), acc[t]);
 }
 
 // Same pipeline with B-fragments loaded from global memory (LoRA shrink: a
@@ -428,39 +437,45 @@ __global__ __launch_bounds__(WAVES * 64, 16 / WAVES) void split_kernel(SplitArgs
     else shrink_item<4>(a, item, lane);
     return;
   }
+  // K-slice index runs fastest so the n_ks workgroups of one row group are
+  // dispatched together
   const int b = blockIdx.x - a.n_shrink_wg;
-  const int rg = b % a.n_rg, ks = b / a.n_rg;
+  const int ks = b % a.n_ks, rg = b / a.n_ks;
   const int st0 = (int)((int64_t)a.total_steps * ks / a.n_ks);
   const int st1 = (int)((int64_t)a.total_steps * (ks + 1) / a.n_ks);
   const int nst = st1 - st0;
+  const int npad = (nst + kKDepth - 1) / kKDepth * kKDepth;
   const int64_t kbeg = (int64_t)st0 * 32;
-  const int ld = a.ks_steps * 32 + 8;  // LDS row stride (elements), +16 B against bank conflicts
+
+  // Stage the activation K-slice in LDS in MFMA B-fragment order: block
+  // (step s, token tile t) holds 64 lanes x 16 B, lane l = token 16t + l%16,
+  // k-group l/16, so the k-loop's ds_read_b128 is conflict-free.  Moved with
+  // LDS-DMA loads (global_load_lds_dwordx4), no VGPR round trip.  Token rows
+  // past ntok load row 0 (their results are never stored); steps past the
+  // slice reload its last step (the matching W fragments are zero).
+  {
+    for (int i = wv; i < npad * TT; i += WAVES) {
+      const int st = i / TT, t = i - st * TT;
+      const int tk = 16 * t + (lane & 15);
+      const bf16* src = a.x[tk < a.ntok ? tk : 0] + kbeg + 32 * (st < nst ? st : nst - 1) + 8 * (lane >> 4);
+      __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
+    }
+  }
 
   const int64_t r0 = (int64_t)rg * (16 * WAVES) + wv * 16;
   const int64_t wrow = (r0 + (lane & 15) < a.N) ? r0 + (lane & 15) : a.N - 1;
   const bf16* wp = a.w + wrow * a.K + kbeg + 8 * (lane >> 4);
-  // first W fragments go out before the activation staging
   u32x4 w[kKDepth];
-  if (nst >= kKDepth) {
 #pragma unroll
-    for (int d = 0; d < kKDepth; ++d) w[d] = ld16(wp + 32 * d);
-  }
-
-  // stage x[:, kbeg : kbeg + 32*nst] for TT*16 token rows (zeros past ntok)
-  const int cpr = nst * 4;  // 16-byte chunks per row
-  for (int c = threadIdx.x; c < TT * 16 * cpr; c += WAVES * 64) {
-    const int r = c / cpr, cc = c - r * cpr;
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (r < a.ntok) v = ld16(a.x[r] + kbeg + cc * 8);
-    *reinterpret_cast<u32x4*>(xs + r * ld + cc * 8) = v;
-  }
+  for (int d = 0; d < kKDepth; ++d) w[d] = ld_w_step(wp, d, nst);
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's LDS-DMA (and W) loads have landed
   __syncthreads();
 
-  const bf16* xl = xs + (lane & 15) * ld + 8 * (lane >> 4);
+  const bf16* xl = xs + 8 * lane;  // block (s, t) at xs + (s * TT + t) * 512 elements
   f32x4 acc[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  kloop_lds<TT, kKDepth>(acc, w, wp, xl, 16 * ld, nst);
+  kloop_lds<TT, kKDepth>(acc, w, wp, xl, 512, npad, nst);
 
   const int64_t n0 = r0 + 4 * (lane >> 4);
   if (n0 < a.N) {
@@ -480,17 +495,52 @@ __global__ __launch_bounds__(WAVES * 64, 16 / WAVES) void split_kernel(SplitArgs
   }
 }
 
+// scale * sum_q u[q] * B[nin][q] for one output column (u: the token's
+// reduced shrink row for block blk, in LDS).
+__device__ __forceinline__ float lora_col(const swl_lora_entry* ep, const float* ub, int blk, int64_t nin) {
+  const int r = ep->rank;
+  const bf16* b0 = reinterpret_cast<const bf16*>(ep->b[blk]) + nin * r;
+  float d = 0.f;
+  for (int q = 0; q < r; ++q) d += ub[q] * bf2f(b0[q]);
+  return d * ep->scale;
+}
+
+// One workgroup per (256 column quads, token): sums the n_ks K-slice
+// partials (loads issued 8 at a time), adds bias and the token's LoRA
+// expand (its shrink row reduced over the u splits once, into LDS), rounds
+// once to bf16 and stores into the token's output row.
 __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
+  __shared__ float us[kMaxURow];
+  const int tok = blockIdx.y;
   const int64_t quads = (a.N + 3) >> 2;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int tok = (int)(idx / quads);
-  if (tok >= a.ntok) return;
-  const int64_t n = (idx - (int64_t)tok * quads) * 4;
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  const int64_t qi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int lora = a.has_lora ? a.lora[tok] : -1;
+  if (lora >= 0) {  // uniform over the workgroup
+    const float* up = a.L.u + (int64_t)a.urow[tok] * a.L.u_ld;
+    for (int q = threadIdx.x; q < a.L.u_ld; q += 256) {
+      float v = 0.f;
+      for (int sp = 0; sp < a.L.usplit; ++sp) v += up[sp * a.L.u_split_stride + q];
+      us[q] = v;
+    }
+    __syncthreads();
+  }
+  if (qi >= quads) return;
+  const int64_t n = qi * 4;
   const int64_t kstride = (int64_t)a.ntok * a.N;
   const float* p = a.part + (int64_t)tok * a.N + n;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
   if (n + 3 < a.N && (a.N & 3) == 0) {
-    for (int ks = 0; ks < a.n_ks; ++ks) {
+    int ks = 0;
+    for (; ks + 8 <= a.n_ks; ks += 8) {
+      f32x4 q[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = *reinterpret_cast<const f32x4*>(p + (ks + j) * kstride);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[0] += q[j][0]; v[1] += q[j][1]; v[2] += q[j][2]; v[3] += q[j][3];
+      }
+    }
+    for (; ks < a.n_ks; ++ks) {
       const f32x4 q = *reinterpret_cast<const f32x4*>(p + ks * kstride);
       v[0] += q[0]; v[1] += q[1]; v[2] += q[2]; v[3] += q[3];
     }
@@ -499,7 +549,52 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
       for (int j = 0; j < 4; ++j)
         if (n + j < a.N) v[j] += p[ks * kstride + j];
   }
-  epilogue_store4(v, n, a.N, a.bias, a.L, a.has_lora ? a.lora[tok] : -1, a.urow[tok], a.y[tok]);
+  if (a.bias) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (n + j < a.N) v[j] += bf2f(a.bias[n + j]);
+  }
+  if (lora >= 0) {
+    const swl_lora_entry* ep = a.L.table + lora;
+    const int blk = find_blk(a.L, n);
+    const int64_t bs = blk_start_of(a.L, blk), be = blk_start_of(a.L, blk + 1);
+    const int r = ep->rank;
+    if (n + 3 < a.N && n + 3 < be && (r & 7) == 0) {
+      const bf16* b0 = reinterpret_cast<const bf16*>(ep->b[blk]) + (n - bs) * r;
+      const float* ub = us + blk * r;
+      float d[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < r; q += 8) {
+        float uq[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) uq[i] = ub[q + i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float bv[8];
+          unpack8(ld16(b0 + (int64_t)j * r + q), bv);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d[j] += uq[i] * bv[i];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += d[j] * ep->scale;
+    } else {
+      for (int j = 0; j < 4; ++j) {
+        if (n + j >= a.N) break;
+        const int bj = find_blk(a.L, n + j);
+        v[j] += lora_col(ep, us + bj * r, bj, n + j - blk_start_of(a.L, bj));
+      }
+    }
+  }
+  bf16* yrow = a.y[tok];
+  if (n + 3 < a.N && ((reinterpret_cast<uintptr_t>(yrow + n) & 7) == 0)) {
+    u32x2 pk;
+    pk[0] = (uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[0])) | ((uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[1])) << 16);
+    pk[1] = (uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[2])) | ((uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[3])) << 16);
+    *reinterpret_cast<u32x2*>(yrow + n) = pk;
+  } else {
+    for (int j = 0; j < 4; ++j)
+      if (n + j < a.N) yrow[n + j] = f2bf(v[j]);
+  }
 }
 
 // ------------------------------------------------------- tiled (M>64) -----
@@ -829,6 +924,154 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     const float r = (l > 0.f) ? o / l : 0.f;
     tok_out(a, (int64_t)s * a.L + i)[(h * G + g) * 128 + d] = f2bf(r);
   }
+}
+
+// ---- decode attention, split over the context (flash-decoding) ----------
+// One workgroup per (kv head, chunk of kAttnChunk<G> keys, sequence) of a
+// one-token query: every lane issues all of its K and V loads for the chunk
+// at once (16 lanes per key, 8 dims each), scores for the G query heads
+// sharing the kv head, softmax within the chunk, then P.V.  Writes the
+// chunk's max, sum and unnormalised output; attn_combine_kernel merges the
+// chunks.  Keys past the context are masked.
+template <int G> struct AttnChunk { static constexpr int U = (G <= 4) ? 8 : 4; static constexpr int C = 16 * U; };
+constexpr int kAttnRec = 130;  // floats per (chunk, head): max, sum, 128 dims
+
+__device__ __forceinline__ int64_t key_offset(const AttnArgs& a, const int32_t* bt, int64_t key, int h) {
+  const int64_t bi = key / a.bs;
+  int32_t blk = (bi < a.max_blocks) ? bt[bi] : 0;
+  blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;
+  return ((int64_t)blk * a.bs + key % a.bs) * a.hkv * 128 + h * 128;
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a, float* part, int maxch) {
+  constexpr int U = AttnChunk<G>::U, C = AttnChunk<G>::C;
+  const int h = blockIdx.x, c = blockIdx.y, s = blockIdx.z;
+  const int64_t ctx = (int64_t)a.seqlens[s] + 1;
+  const int64_t k0 = (int64_t)c * C;
+  if (k0 >= ctx) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int quarter = tid >> 4;  // 0..15: keys k0 + quarter + 16 j
+  const int dl = (lane & 15) * 8;
+  const int32_t* bt = a.bt + (int64_t)s * a.max_blocks;
+
+  u32x4 kr[U], vr[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int64_t key = k0 + quarter + 16 * j;
+    const int64_t off = key_offset(a, bt, key < ctx ? key : k0, h) + dl;
+    kr[j] = ld16(a.kc + off);
+  }
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int64_t key = k0 + quarter + 16 * j;
+    const int64_t off = key_offset(a, bt, key < ctx ? key : k0, h) + dl;
+    vr[j] = ld16(a.vc + off);
+  }
+  float qv[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    unpack8(ld16(tok_q(a, s) + (h * G + g) * 128 + dl), qv[g]);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) qv[g][d] *= a.scale;
+  }
+
+  __shared__ float sp[G][C];         // scores, then probabilities
+  __shared__ float sred[4][G][128];  // per-wave P.V partials
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    float kf[8];
+    unpack8(kr[j], kf);
+    const int64_t key = k0 + quarter + 16 * j;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float t = 0.f;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) t += qv[g][d] * kf[d];
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) t += __shfl_xor(t, o, 16);
+      if ((lane & 15) == 0) sp[g][quarter + 16 * j] = (key < ctx) ? t : -INFINITY;
+    }
+  }
+  __syncthreads();
+  // softmax within the chunk: one wave per head (C <= 128 keys, 2 per lane)
+  float* rec = part + (((int64_t)s * a.hkv + h) * maxch + c) * G * kAttnRec;
+  for (int g = wv; g < G; g += 4) {
+    const float s0 = sp[g][lane], s1 = (lane + 64 < C) ? sp[g][lane + 64] : -INFINITY;
+    float m = fmaxf(s0, s1);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float p0 = __expf(s0 - m), p1 = (lane + 64 < C) ? __expf(s1 - m) : 0.f;
+    sp[g][lane] = p0;
+    if (lane + 64 < C) sp[g][lane + 64] = p1;
+    float l = p0 + p1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+    if (lane == 0) {
+      rec[g * kAttnRec] = m;
+      rec[g * kAttnRec + 1] = l;
+    }
+  }
+  __syncthreads();
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.f;
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    float vf[8];
+    unpack8(vr[j], vf);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float pj = sp[g][quarter + 16 * j];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[g][d] += pj * vf[d];
+    }
+  }
+  // the 4 quarters of a wave hold the same dims: fold them with shuffles
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      float v = acc[g][d];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      acc[g][d] = v;
+    }
+  if (lane < 16) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) sred[wv][g][dl + d] = acc[g][d];
+  }
+  __syncthreads();
+  for (int it = tid; it < G * 128; it += 256) {
+    const int g = it >> 7, d = it & 127;
+    rec[g * kAttnRec + 2 + d] = sred[0][g][d] + sred[1][g][d] + sred[2][g][d] + sred[3][g][d];
+  }
+}
+
+// Merges the chunk records of one (sequence, query head): out = sum_c o_c
+// e^(m_c - M) / sum_c l_c e^(m_c - M).
+__global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const float* part, int maxch, int G) {
+  const int s = blockIdx.y, hqi = blockIdx.x;
+  const int h = hqi / G, g = hqi - h * G;
+  const int d = threadIdx.x;
+  const int64_t ctx = (int64_t)a.seqlens[s] + 1;
+  const int C = (G <= 4) ? AttnChunk<4>::C : AttnChunk<8>::C;
+  const int nch = (int)((ctx + C - 1) / C);
+  const float* rec = part + ((int64_t)s * a.hkv + h) * maxch * G * kAttnRec + g * kAttnRec;
+  const int64_t cstride = (int64_t)G * kAttnRec;
+  float M = -INFINITY;
+  for (int c = 0; c < nch; ++c) M = fmaxf(M, rec[c * cstride]);
+  float L = 0.f, O = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    const float e = __expf(rec[c * cstride] - M);
+    L += rec[c * cstride + 1] * e;
+    O += rec[c * cstride + 2 + d] * e;
+  }
+  tok_out(a, s)[hqi * 128 + d] = f2bf(L > 0.f ? O / L : 0.f);
 }
 
 __global__ void zero_blocks_kernel(bf16* cache, const int64_t* ids, int64_t nblocks, int64_t block_elems) {
@@ -1168,16 +1411,30 @@ int fill_segptrs(SegPtrs& sp, const void* const* ptrs, const int64_t* rows, int 
 // sweeps.
 struct Tuning {
   int waves = 8;
-  int target_wg = 256;
+  int target_wg = 512;
+  int lds_kb = 96;  // activation-slice LDS per workgroup (16..160 KiB)
+  int nks = 0;      // forced K-slice count (0: chosen per shape)
 };
 const Tuning& tuning() {
   static Tuning t = [] {
     Tuning v;
     if (const char* e = getenv("SWL_SKINNY_WAVES")) v.waves = (atoi(e) == 4) ? 4 : 8;
     if (const char* e = getenv("SWL_SKINNY_TARGET_WG")) v.target_wg = std::max(1, atoi(e));
+    if (const char* e = getenv("SWL_SKINNY_LDS_KB")) v.lds_kb = std::min(160, std::max(16, atoi(e)));
+    if (const char* e = getenv("SWL_SKINNY_NKS")) v.nks = std::max(0, atoi(e));
     return v;
   }();
   return t;
+}
+
+// Dynamic LDS above the default 64 KiB must be allowed per kernel.
+template <typename K>
+int allow_lds(K kernel, size_t bytes, size_t* allowed) {
+  if (bytes <= 64 * 1024 || bytes <= *allowed) return SWL_OK;
+  SWL_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)bytes));
+  *allowed = bytes;
+  return SWL_OK;
 }
 
 // Adapter groups for the LoRA shrink: tokens that share a lora table entry.
@@ -1262,12 +1519,22 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const Tuning& tu = tuning();
   const int waves = tu.waves;
   a.n_rg = (int)((N + 16 * waves - 1) / (16 * waves));
-  const int64_t max_steps_lds = ((int64_t)kLdsBudget / (TT * 16 * 2) - 8) / 32;
-  int64_t n_ks = std::max<int64_t>((tu.target_wg + a.n_rg - 1) / a.n_rg,
-                                   (total_steps + max_steps_lds - 1) / max_steps_lds);
+  // K-slices: a power of two (slice starts on aligned byte offsets stream
+  // best from HBM), enough for target_wg workgroups, doubled once more for
+  // wide projections below 1024 workgroups; then as many more as the LDS cap
+  // on the staged activation slice (padded steps x TT x 1 KiB) requires.
+  int64_t n_ks = 1;
+  if (tu.nks > 0) {
+    n_ks = tu.nks;
+  } else {
+    while (n_ks < total_steps && a.n_rg * n_ks < tu.target_wg) n_ks *= 2;
+    if (a.n_rg >= 128 && a.n_rg * n_ks < 1024 && n_ks < total_steps) n_ks *= 2;
+  }
+  auto padded = [&](int64_t nk) { return ((total_steps + nk - 1) / nk + kKDepth - 1) / kKDepth * kKDepth; };
+  while (n_ks < total_steps && padded(n_ks) * TT * 1024 > (int64_t)tu.lds_kb * 1024) n_ks *= 2;
   n_ks = std::min<int64_t>(n_ks, total_steps);
   a.n_ks = (int)n_ks;
-  a.ks_steps = (int)((total_steps + n_ks - 1) / n_ks);
+  a.ks_steps = (int)padded(n_ks);  // the widest slice, padded to whole pipeline iterations
   a.n_base_wg = a.n_rg * a.n_ks;
   for (int i = 0; i < ntok; ++i) a.x[i] = xrows[i];
 
@@ -1283,6 +1550,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     a.n_items = sp.tiles * a.u_ks;
     a.n_shrink_wg = (a.n_items + waves - 1) / waves;
     a.u_ld = ((max_r * nblk + 15) / 16) * 16;
+    SWL_CHECK(a.u_ld <= kMaxURow, SWL_ERR_INVALID, "round: LoRA rank x blocks exceeds 256");
     a.u_split_stride = (int64_t)ntok * a.u_ld;
     a.table = table;
     copy_shrink(a, sp);
@@ -1296,7 +1564,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   a.part = reinterpret_cast<float*>(scratch);
   a.u = has_lora ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + part_al) : nullptr;
 
-  const size_t lds = sizeof(bf16) * (size_t)TT * 16 * ((size_t)a.ks_steps * 32 + 8);
+  const size_t lds = (size_t)a.ks_steps * TT * 1024;
   const dim3 grid((unsigned)(a.n_shrink_wg + a.n_base_wg));
   const dim3 block((unsigned)(waves * 64));
   const int tslot = timer_slot(st);
@@ -1311,6 +1579,27 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     g_timer.bytes[tslot] = bytes;
   }
   timer_mark(tslot, 0, st);
+  static size_t allowed[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+  {
+    size_t* al = &allowed[waves == 4 ? 0 : 1][TT - 1];
+    int rc2 = SWL_OK;
+    if (waves == 4) {
+      switch (TT) {
+        case 1: rc2 = allow_lds(split_kernel<1, 4>, lds, al); break;
+        case 2: rc2 = allow_lds(split_kernel<2, 4>, lds, al); break;
+        case 3: rc2 = allow_lds(split_kernel<3, 4>, lds, al); break;
+        default: rc2 = allow_lds(split_kernel<4, 4>, lds, al); break;
+      }
+    } else {
+      switch (TT) {
+        case 1: rc2 = allow_lds(split_kernel<1, 8>, lds, al); break;
+        case 2: rc2 = allow_lds(split_kernel<2, 8>, lds, al); break;
+        case 3: rc2 = allow_lds(split_kernel<3, 8>, lds, al); break;
+        default: rc2 = allow_lds(split_kernel<4, 8>, lds, al); break;
+      }
+    }
+    if (rc2) return rc2;
+  }
   if (waves == 4) {
     switch (TT) {
       case 1: hipLaunchKernelGGL((split_kernel<1, 4>), grid, block, lds, st, a); break;
@@ -1350,8 +1639,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     e.L.u_split_stride = a.u_split_stride;
   }
   const int64_t quads = (N + 3) / 4;
-  const unsigned eg = (unsigned)(((int64_t)ntok * quads + 255) / 256);
-  hipLaunchKernelGGL(epilogue_kernel, dim3(eg), dim3(256), 0, st, e);
+  hipLaunchKernelGGL(epilogue_kernel, dim3((unsigned)((quads + 255) / 256), (unsigned)ntok), dim3(256), 0, st, e);
   SWL_LAUNCH_CHECK("epilogue_kernel launch");
   timer_mark(tslot, 2, st);
   return SWL_OK;
@@ -1381,9 +1669,37 @@ int launch_shrink_only(int64_t K, int ntok, const bf16* const* xrows, const int3
   return SWL_OK;
 }
 
+template <int G>
+int launch_attn_decode(const AttnArgs& a, hipStream_t st) {
+  // chunk count from the longest context: read on the host from the block
+  // table geometry (max_blocks pages), never from device memory
+  constexpr int C = AttnChunk<G>::C;
+  const int maxch = (int)((a.max_blocks * a.bs + C - 1) / C);
+  void* scratch = nullptr;
+  const size_t need = sizeof(float) * (size_t)a.nseq * a.hkv * maxch * G * kAttnRec;
+  int rc = scratch_get(need, st, &scratch);
+  if (rc) return rc;
+  float* part = reinterpret_cast<float*>(scratch);
+  hipLaunchKernelGGL(attn_chunk_kernel<G>, dim3((unsigned)a.hkv, (unsigned)maxch, (unsigned)a.nseq), dim3(256), 0,
+                     st, a, part, maxch);
+  SWL_LAUNCH_CHECK("attn_chunk_kernel launch");
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.hq, (unsigned)a.nseq), dim3(128), 0, st, a,
+                     (const float*)part, maxch, G);
+  SWL_LAUNCH_CHECK("attn_combine_kernel launch");
+  return SWL_OK;
+}
+
 int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
   hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L)), dim3(256), 0, st, a);
   SWL_LAUNCH_CHECK("rope_append_kernel launch");
+  if (a.L == 1) {
+    switch (G) {
+      case 1: return launch_attn_decode<1>(a, st);
+      case 2: return launch_attn_decode<2>(a, st);
+      case 4: return launch_attn_decode<4>(a, st);
+      default: return launch_attn_decode<8>(a, st);
+    }
+  }
   const dim3 grid((unsigned)a.hkv, (unsigned)a.L, (unsigned)a.nseq);
   switch (G) {
     case 1: hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(256), 0, st, a); break;

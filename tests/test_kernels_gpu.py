@@ -274,6 +274,15 @@ def test_paged_attention_matches_oracle(dev, nseq, L, ctx0):
     assert_close(kc_d, kc_r, what="k pages")
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (64, 8), (8, 2)])
+def test_paged_attention_decode_gqa_groups(dev, hq, hkv):
+    """One-token decode over contexts spanning many chunks (and a partial last
+    chunk) for every supported q/kv head ratio."""
+    out, want, got_state, ref_state = _attn_case(dev, 3, 1, [1, 300, 2047], hq=hq, hkv=hkv, seed=5)
+    assert_close(out, want, what=f"attention hq={hq} hkv={hkv}")
+    assert bits_equal(got_state[3], ref_state[3]), "v pages must be a bit-exact append"
+
+
 def test_paged_attention_single_key_returns_v(dev):
     """ctx = 1: softmax over one key is 1, so the output is v exactly."""
     out, want, (q_d, k_d, kc_d, vc_d), _ = _attn_case(dev, 2, 1, [0, 0])
