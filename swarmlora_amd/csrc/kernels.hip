@@ -310,38 +310,41 @@ typedef __attribute__((address_space(1))) void* gbl_ptr;
 // at their maxima, i.e. not waited on)
 constexpr unsigned kWaitVm0 = 0x0F70;
 
-// W fragment of k-step s of a K-slice with `n` steps: steps past the end
-// read the slice's last step again (in bounds) and are zeroed, so a padded
-// pipeline adds nothing.
-__device__ __forceinline__ u32x4 ld_w_step(const bf16* wp, int s, int n) {
-  const u32x4 v = ld16(wp + 32 * (s < n ? s : n - 1));
-  return s < n ? v : u32x4{0u, 0u, 0u, 0u};
+// 16-byte load through a global-address-space pointer (global_load, not flat)
+__device__ __forceinline__ u32x4 ldg16(const void* p) {
+  return *(const __attribute__((address_space(1))) u32x4*)(p);
 }
 
-// W (one row per lane, k-group per lane quarter) streamed through a D-deep
-// register pipeline; B-fragments of TT token tiles read from LDS (fragment
-// order: step s, tile t at xl + (s * TT + t) * tstride).  The caller has
-// already issued the first D W-fragments into w[].  nsteps (a multiple of D)
-// are run; W steps from nw on are zero, so every step is pipelined and the
-// body is branch-free (s_waitcnt counts are exact).
+// W fragment of k-step s of a K-slice with `n` steps; steps past the end read
+// the slice's last step again (in bounds).  The caller zeroes them.
+__device__ __forceinline__ u32x4 ld_w_step(const bf16* wp, int s, int n) {
+  return ldg16(wp + 32 * (s < n ? s : n - 1));
+}
+
+// W (one row per lane, k-group per lane quarter) streamed D steps at a time,
+// the D loads of a group issued back to back (consecutive 64-byte pieces of
+// each row reach the memory controller together, which streams faster from
+// HBM than a rolling one-step-ahead prefetch); B-fragments of TT token tiles
+// read from LDS (fragment order: step s, tile t at xl + (s * TT + t) *
+// tstride).  The caller has already issued the first group into w[].  nsteps
+// (a multiple of D) are run; W steps from nw on contribute zero.
 template <int TT, int D>
 __device__ __forceinline__ void kloop_lds(f32x4 (&acc)[TT], u32x4 (&w)[D], const bf16* wp, const bf16* xl,
                                           int tstride, int nsteps, int nw) {
   const int niter = (nsteps + D - 1) / D;
-  for (int it = 0; it + 1 < niter; ++it) {
-    const int base = it * D, nxt = base + D;
+  for (int it = 0; it < niter; ++it) {
+    const int base = it * D;
+    if (it > 0) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) w[d] = ld_w_step(wp, base + d, nw);
+    }
 #pragma unroll
     for (int d = 0; d < D; ++d) {
+      const u32x4 wd = (base + d < nw) ? w[d] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + ((base + d) * TT + t) * tstride), acc[t]);
-      w[d] = ld_w_step(wp, nxt + d, nw);
+      for (int t = 0; t < TT; ++t) acc[t] = mfma16(wd, lds16(xl + ((base + d) * TT + t) * tstride), acc[t]);
     }
   }
-  const int base = (niter - 1) * D;
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-#pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], lds16(xl + ((base + d) * TT + t) * tstride), acc[t]);
 }
 
 // Same pipeline with B-fragments loaded from global memory (LoRA shrink: a
