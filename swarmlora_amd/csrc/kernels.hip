@@ -510,48 +510,59 @@ __device__ __forceinline__ float lora_col(const swl_lora_entry* ep, const float*
 
 // One workgroup per (256 column quads, token): sums the n_ks K-slice
 // partials (loads issued 8 at a time), adds bias and the token's LoRA
-// expand (its shrink row reduced over the u splits once, into LDS), rounds
-// once to bf16 and stores into the token's output row.
+// expand (its shrink row reduced over the u splits once, into LDS; the
+// partial loads are issued first so both latencies overlap), rounds once to
+// bf16 and stores into the token's output row.
 __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   __shared__ float us[kMaxURow];
   const int tok = blockIdx.y;
   const int64_t quads = (a.N + 3) >> 2;
   const int64_t qi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool live = qi < quads;
   const int lora = a.has_lora ? a.lora[tok] : -1;
-  if (lora >= 0) {  // uniform over the workgroup
-    const float* up = a.L.u + (int64_t)a.urow[tok] * a.L.u_ld;
-    for (int q = threadIdx.x; q < a.L.u_ld; q += 256) {
-      float v = 0.f;
-      for (int sp = 0; sp < a.L.usplit; ++sp) v += up[sp * a.L.u_split_stride + q];
-      us[q] = v;
-    }
-    __syncthreads();
-  }
-  if (qi >= quads) return;
   const int64_t n = qi * 4;
   const int64_t kstride = (int64_t)a.ntok * a.N;
   const float* p = a.part + (int64_t)tok * a.N + n;
   float v[4] = {0.f, 0.f, 0.f, 0.f};
-  if (n + 3 < a.N && (a.N & 3) == 0) {
-    int ks = 0;
-    for (; ks + 8 <= a.n_ks; ks += 8) {
-      f32x4 q[8];
+  if (live) {
+    if (n + 3 < a.N && (a.N & 3) == 0) {
+      int ks = 0;
+      for (; ks + 8 <= a.n_ks; ks += 8) {
+        f32x4 q[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) q[j] = *reinterpret_cast<const f32x4*>(p + (ks + j) * kstride);
+        for (int j = 0; j < 8; ++j) q[j] = *reinterpret_cast<const f32x4*>(p + (ks + j) * kstride);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v[0] += q[j][0]; v[1] += q[j][1]; v[2] += q[j][2]; v[3] += q[j][3];
+        for (int j = 0; j < 8; ++j) {
+          v[0] += q[j][0]; v[1] += q[j][1]; v[2] += q[j][2]; v[3] += q[j][3];
+        }
       }
+      for (; ks < a.n_ks; ++ks) {
+        const f32x4 q = *reinterpret_cast<const f32x4*>(p + ks * kstride);
+        v[0] += q[0]; v[1] += q[1]; v[2] += q[2]; v[3] += q[3];
+      }
+    } else {
+      for (int ks = 0; ks < a.n_ks; ++ks)
+        for (int j = 0; j < 4; ++j)
+          if (n + j < a.N) v[j] += p[ks * kstride + j];
     }
-    for (; ks < a.n_ks; ++ks) {
-      const f32x4 q = *reinterpret_cast<const f32x4*>(p + ks * kstride);
-      v[0] += q[0]; v[1] += q[1]; v[2] += q[2]; v[3] += q[3];
-    }
-  } else {
-    for (int ks = 0; ks < a.n_ks; ++ks)
-      for (int j = 0; j < 4; ++j)
-        if (n + j < a.N) v[j] += p[ks * kstride + j];
   }
+  if (lora >= 0) {  // uniform over the workgroup
+    const float* up = a.L.u + (int64_t)a.urow[tok] * a.L.u_ld;
+    for (int q = threadIdx.x; q < a.L.u_ld; q += 256) {
+      float acc = 0.f;
+      int sp = 0;
+      for (; sp + 8 <= a.L.usplit; sp += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = up[(sp + j) * a.L.u_split_stride + q];
+        acc += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+      }
+      for (; sp < a.L.usplit; ++sp) acc += up[sp * a.L.u_split_stride + q];
+      us[q] = acc;
+    }
+    __syncthreads();
+  }
+  if (!live) return;
   if (a.bias) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -801,38 +812,45 @@ __device__ __forceinline__ bf16* tok_out(const AttnArgs& a, int64_t t) {
   return a.rowmode ? a.out_row[t] : a.out + t * (int64_t)a.hq * 128;
 }
 
-// NeoX rotation of q and k at their positions, then k/v appended to the pages.
-// One workgroup per (sequence, new token); 64 threads per head-pair loop.
-__global__ __launch_bounds__(256) void rope_append_kernel(AttnArgs a) {
+// NeoX rotation of q and k at their positions, k/v appended to the pages.
+// One 64-thread workgroup per (token, head) of the fused row: q heads are
+// rotated in place, k heads rotated in place and copied to the K page, v
+// heads copied to the V page (lane d handles dims d and d + 64).
+__global__ __launch_bounds__(64) void rope_append_kernel(AttnArgs a) {
   const int tokid = blockIdx.x;  // s * L + i
+  const int h = blockIdx.y;      // [0, hq): q, [hq, hq + hkv): k, then v
+  const int d = threadIdx.x;
   const int s = tokid / a.L, i = tokid % a.L;
-  const int64_t pos = a.rope ? a.pos[tokid] : 0;
-  const bool do_rope = a.rope && pos >= 0 && pos < a.max_pos;
-  const bf16* cs = a.cs + (do_rope ? pos : 0) * 128;
-  const int nh = a.hq + a.hkv;
-  for (int it = threadIdx.x; it < nh * 64; it += blockDim.x) {
-    const int h = it >> 6, d = it & 63;
-    bf16* base = (h < a.hq) ? tok_q(a, tokid) + h * 128 : tok_k(a, tokid) + (h - a.hq) * 128;
-    if (do_rope) {
+  const bool is_q = h < a.hq, is_k = !is_q && h < a.hq + a.hkv;
+  bf16* row = is_q ? tok_q(a, tokid) + h * 128
+                   : (is_k ? tok_k(a, tokid) + (h - a.hq) * 128
+                           : const_cast<bf16*>(tok_v(a, tokid)) + (h - a.hq - a.hkv) * 128);
+  float x1 = bf2f(row[d]), x2 = bf2f(row[d + 64]);
+  if (!is_q && !is_k) {
+    // v: copy only
+  } else if (a.rope) {
+    const int64_t pos = a.pos[tokid];
+    if (pos >= 0 && pos < a.max_pos) {
+      const bf16* cs = a.cs + pos * 128;
       const float c = bf2f(cs[d]), sn = bf2f(cs[64 + d]);
-      const float x1 = bf2f(base[d]), x2 = bf2f(base[d + 64]);
-      base[d] = f2bf(x1 * c - x2 * sn);
-      base[d + 64] = f2bf(x2 * c + x1 * sn);
+      const float y1 = x1 * c - x2 * sn, y2 = x2 * c + x1 * sn;
+      const bf16 o1 = f2bf(y1), o2 = f2bf(y2);
+      row[d] = o1;
+      row[d + 64] = o2;
+      x1 = bf2f(o1);
+      x2 = bf2f(o2);
     }
   }
-  __syncthreads();
+  if (is_q) return;
   const int64_t p = (int64_t)a.seqlens[s] + i;
   const int64_t blk_i = p / a.bs;
   if (p < 0 || blk_i >= a.max_blocks) return;
   const int32_t blk = a.bt[(int64_t)s * a.max_blocks + blk_i];
   if (blk < 0 || blk >= a.num_blocks) return;
-  const int64_t dst = ((int64_t)blk * a.bs + p % a.bs) * a.hkv * 128;
-  const bf16* ksrc = tok_k(a, tokid);
-  const bf16* vsrc = tok_v(a, tokid);
-  for (int e = threadIdx.x; e < a.hkv * 16; e += blockDim.x) {
-    reinterpret_cast<u32x4*>(a.kc + dst)[e] = reinterpret_cast<const u32x4*>(ksrc)[e];
-    reinterpret_cast<u32x4*>(a.vc + dst)[e] = reinterpret_cast<const u32x4*>(vsrc)[e];
-  }
+  const int kvh = is_k ? h - a.hq : h - a.hq - a.hkv;
+  bf16* dst = (is_k ? a.kc : a.vc) + ((int64_t)blk * a.bs + p % a.bs) * a.hkv * 128 + kvh * 128;
+  dst[d] = f2bf(x1);
+  dst[d + 64] = f2bf(x2);
 }
 
 // Attention of one query token over its causal context for one kv head and
@@ -1066,13 +1084,32 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const flo
   const int nch = (int)((ctx + C - 1) / C);
   const float* rec = part + ((int64_t)s * a.hkv + h) * maxch * G * kAttnRec + g * kAttnRec;
   const int64_t cstride = (int64_t)G * kAttnRec;
-  float M = -INFINITY;
-  for (int c = 0; c < nch; ++c) M = fmaxf(M, rec[c * cstride]);
-  float L = 0.f, O = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const float e = __expf(rec[c * cstride] - M);
-    L += rec[c * cstride + 1] * e;
-    O += rec[c * cstride + 2 + d] * e;
+  // loads issued 8 chunks at a time
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += 8) {
+    float m[8], l[8], o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + j < nch ? c0 + j : nch - 1;
+      m[j] = rec[c * cstride];
+      l[j] = rec[c * cstride + 1];
+      o[j] = rec[c * cstride + 2 + d];
+    }
+    float mn = M;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (c0 + j < nch) mn = fmaxf(mn, m[j]);
+    const float corr = (M == -INFINITY) ? 0.f : __expf(M - mn);
+    L *= corr;
+    O *= corr;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (c0 + j >= nch) break;
+      const float e = __expf(m[j] - mn);
+      L += l[j] * e;
+      O += o[j] * e;
+    }
+    M = mn;
   }
   tok_out(a, s)[hqi * 128 + d] = f2bf(L > 0.f ? O / L : 0.f);
 }
@@ -1364,15 +1401,16 @@ int scratch_get(size_t need, hipStream_t stream, void** out) {
 
 // ---------------------------------------------------------- launch timer
 // Optional HIP-event timing of the decode projection: when armed, every
-// launch_skinny call (outside graph capture) records three events on its own
-// stream, before the base kernel, between base and epilogue, and after the
-// epilogue, plus the launch's algorithmic byte count.  Used by benchmarks
-// to compute achieved bandwidth per kernel; single-threaded use only.
+// launch_skinny call (outside graph capture) records HIP events on its own
+// stream right before and after its base kernel and its epilogue kernel,
+// and keeps the launch's algorithmic byte count.  With the stream kept busy
+// ahead of the host (so launches run back to back) the event pairs measure
+// the kernels.  Used by benchmarks; single-threaded use only.
 struct LaunchTimer {
   bool armed = false;
   int cap = 0;
   int n = 0;
-  std::vector<hipEvent_t> ev;  // 3 per record
+  std::vector<hipEvent_t> ev;  // 4 per record: base start/stop, epilogue start/stop
   std::vector<int64_t> N, K, bytes;
   std::vector<int32_t> ntok;
 };
@@ -1386,8 +1424,15 @@ int timer_slot(hipStream_t st) {
   return g_timer.n++;
 }
 
-void timer_mark(int slot, int which, hipStream_t st) {
-  if (slot >= 0) (void)hipEventRecord(g_timer.ev[3 * slot + which], st);
+hipEvent_t timer_event(int slot, int which) { return slot >= 0 ? g_timer.ev[4 * slot + which] : nullptr; }
+
+// hipLaunchKernelGGL, bracketed by the given events when timing
+template <typename K, typename... Args>
+void launch_maybe_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
+                        Args... args) {
+  if (e0) (void)hipEventRecord(e0, st);
+  hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+  if (e1) (void)hipEventRecord(e1, st);
 }
 
 // -------------------------------------------------------------- launchers
@@ -1581,7 +1626,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     g_timer.ntok[tslot] = ntok;
     g_timer.bytes[tslot] = bytes;
   }
-  timer_mark(tslot, 0, st);
+  hipEvent_t tb0 = timer_event(tslot, 0), tb1 = timer_event(tslot, 1);
   static size_t allowed[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
   {
     size_t* al = &allowed[waves == 4 ? 0 : 1][TT - 1];
@@ -1605,21 +1650,20 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   }
   if (waves == 4) {
     switch (TT) {
-      case 1: hipLaunchKernelGGL((split_kernel<1, 4>), grid, block, lds, st, a); break;
-      case 2: hipLaunchKernelGGL((split_kernel<2, 4>), grid, block, lds, st, a); break;
-      case 3: hipLaunchKernelGGL((split_kernel<3, 4>), grid, block, lds, st, a); break;
-      default: hipLaunchKernelGGL((split_kernel<4, 4>), grid, block, lds, st, a); break;
+      case 1: launch_maybe_timed(split_kernel<1, 4>, grid, block, lds, st, tb0, tb1, a); break;
+      case 2: launch_maybe_timed(split_kernel<2, 4>, grid, block, lds, st, tb0, tb1, a); break;
+      case 3: launch_maybe_timed(split_kernel<3, 4>, grid, block, lds, st, tb0, tb1, a); break;
+      default: launch_maybe_timed(split_kernel<4, 4>, grid, block, lds, st, tb0, tb1, a); break;
     }
   } else {
     switch (TT) {
-      case 1: hipLaunchKernelGGL((split_kernel<1, 8>), grid, block, lds, st, a); break;
-      case 2: hipLaunchKernelGGL((split_kernel<2, 8>), grid, block, lds, st, a); break;
-      case 3: hipLaunchKernelGGL((split_kernel<3, 8>), grid, block, lds, st, a); break;
-      default: hipLaunchKernelGGL((split_kernel<4, 8>), grid, block, lds, st, a); break;
+      case 1: launch_maybe_timed(split_kernel<1, 8>, grid, block, lds, st, tb0, tb1, a); break;
+      case 2: launch_maybe_timed(split_kernel<2, 8>, grid, block, lds, st, tb0, tb1, a); break;
+      case 3: launch_maybe_timed(split_kernel<3, 8>, grid, block, lds, st, tb0, tb1, a); break;
+      default: launch_maybe_timed(split_kernel<4, 8>, grid, block, lds, st, tb0, tb1, a); break;
     }
   }
   SWL_LAUNCH_CHECK("split_kernel launch");
-  timer_mark(tslot, 1, st);
 
   EpiArgs e{};
   e.part = a.part;
@@ -1642,9 +1686,9 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     e.L.u_split_stride = a.u_split_stride;
   }
   const int64_t quads = (N + 3) / 4;
-  hipLaunchKernelGGL(epilogue_kernel, dim3((unsigned)((quads + 255) / 256), (unsigned)ntok), dim3(256), 0, st, e);
+  launch_maybe_timed(epilogue_kernel, dim3((unsigned)((quads + 255) / 256), (unsigned)ntok), dim3(256), 0, st,
+                     timer_event(tslot, 2), timer_event(tslot, 3), e);
   SWL_LAUNCH_CHECK("epilogue_kernel launch");
-  timer_mark(tslot, 2, st);
   return SWL_OK;
 }
 
@@ -1693,7 +1737,8 @@ int launch_attn_decode(const AttnArgs& a, hipStream_t st) {
 }
 
 int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
-  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L), (unsigned)(a.hq + 2 * a.hkv)), dim3(64), 0,
+                     st, a);
   SWL_LAUNCH_CHECK("rope_append_kernel launch");
   if (a.L == 1) {
     switch (G) {
@@ -1891,9 +1936,9 @@ int swl_paged_attention_bf16(void* q, void* k, const void* v, int64_t q_stride, 
 
 int swl_timer_arm(int capacity) {
   SWL_CHECK(capacity >= 0 && capacity <= (1 << 20), SWL_ERR_INVALID, "swl_timer_arm: bad capacity");
-  if ((int)g_timer.ev.size() < 3 * capacity) {
+  if ((int)g_timer.ev.size() < 4 * capacity) {
     const size_t have = g_timer.ev.size();
-    g_timer.ev.resize(3 * (size_t)capacity, nullptr);
+    g_timer.ev.resize(4 * (size_t)capacity, nullptr);
     for (size_t i = have; i < g_timer.ev.size(); ++i) SWL_HIP(hipEventCreate(&g_timer.ev[i]));
     g_timer.N.resize(capacity);
     g_timer.K.resize(capacity);
@@ -1912,10 +1957,10 @@ int swl_timer_collect(int max_records, float* base_ms, float* epilogue_ms, int64
   g_timer.armed = false;
   const int m = std::min(g_timer.n, max_records);
   for (int i = 0; i < m; ++i) {
-    SWL_HIP(hipEventSynchronize(g_timer.ev[3 * i + 2]));
+    SWL_HIP(hipEventSynchronize(g_timer.ev[4 * i + 3]));
     float a = 0.f, b = 0.f;
-    SWL_HIP(hipEventElapsedTime(&a, g_timer.ev[3 * i], g_timer.ev[3 * i + 1]));
-    SWL_HIP(hipEventElapsedTime(&b, g_timer.ev[3 * i + 1], g_timer.ev[3 * i + 2]));
+    SWL_HIP(hipEventElapsedTime(&a, g_timer.ev[4 * i], g_timer.ev[4 * i + 1]));
+    SWL_HIP(hipEventElapsedTime(&b, g_timer.ev[4 * i + 2], g_timer.ev[4 * i + 3]));
     if (base_ms) base_ms[i] = a;
     if (epilogue_ms) epilogue_ms[i] = b;
     if (n) n[i] = g_timer.N[i];

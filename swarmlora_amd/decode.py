@@ -91,14 +91,20 @@ def synthetic_weights(shape: DecodeShape, device, seed: int = 0, std: float = 0.
 
 
 def synthetic_adapter(shape: DecodeShape, device, seed: int, std: float = 0.02) -> dict:
-    """{layer: {proj: (A [rank, in], B [out, rank])}}, ~N(0, std)."""
+    """{layer: {proj: (A [rank, in], B [out, rank])}}, ~N(0, std); all of an
+    adapter's matrices are views of one buffer filled by a single draw."""
     g = torch.Generator(device=device).manual_seed(seed)
-    out = {}
+    dims = shape.proj_dims()
+    per_layer = sum(shape.rank * (i + o) for i, o in dims.values())
+    flat = (torch.randn(shape.layers * per_layer, generator=g, device=device) * std).to(BF16)
+    out, off = {}, 0
     for li in range(shape.layers):
         out[li] = {}
-        for p, (i, o) in shape.proj_dims().items():
-            a = (torch.randn(shape.rank, i, generator=g, device=device) * std).to(BF16)
-            b = (torch.randn(o, shape.rank, generator=g, device=device) * std).to(BF16)
+        for p, (i, o) in dims.items():
+            a = flat[off:off + shape.rank * i].view(shape.rank, i)
+            off += shape.rank * i
+            b = flat[off:off + o * shape.rank].view(o, shape.rank)
+            off += o * shape.rank
             out[li][p] = (a, b)
     return out
 
