@@ -948,13 +948,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 }
 
 // ---- decode attention, split over the context (flash-decoding) ----------
-// One workgroup per (kv head, chunk of kAttnChunk<G> keys, sequence) of a
-// one-token query: every lane issues all of its K and V loads for the chunk
-// at once (16 lanes per key, 8 dims each), scores for the G query heads
-// sharing the kv head, softmax within the chunk, then P.V.  Writes the
-// chunk's max, sum and unnormalised output; attn_combine_kernel merges the
-// chunks.  Keys past the context are masked.
-template <int G> struct AttnChunk { static constexpr int U = (G <= 4) ? 8 : 4; static constexpr int C = 16 * U; };
+// One workgroup (WAVES waves) per (kv head, chunk of C keys, sequence) of a
+// one-token query: 16 lanes per key (8 dims each), every lane issues all of
+// its U K-loads and U V-loads for the chunk at once (page offsets computed
+// first), scores for the G query heads sharing the kv head, softmax within
+// the chunk, then P.V.  Writes the chunk's max, sum and unnormalised output;
+// attn_combine_kernel merges the chunks.  Keys past the context are masked.
 constexpr int kAttnRec = 130;  // floats per (chunk, head): max, sum, 128 dims
 
 __device__ __forceinline__ int64_t key_offset(const AttnArgs& a, const int32_t* bt, int64_t key, int h) {
@@ -964,31 +963,29 @@ __device__ __forceinline__ int64_t key_offset(const AttnArgs& a, const int32_t* 
   return ((int64_t)blk * a.bs + key % a.bs) * a.hkv * 128 + h * 128;
 }
 
-template <int G>
-__global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a, float* part, int maxch) {
-  constexpr int U = AttnChunk<G>::U, C = AttnChunk<G>::C;
+template <int G, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void attn_chunk_kernel(AttnArgs a, float* part, int maxch) {
+  constexpr int NQ = 4 * WAVES, C = NQ * U, KPL = (C + 63) / 64;
   const int h = blockIdx.x, c = blockIdx.y, s = blockIdx.z;
   const int64_t ctx = (int64_t)a.seqlens[s] + 1;
   const int64_t k0 = (int64_t)c * C;
   if (k0 >= ctx) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int quarter = tid >> 4;  // 0..15: keys k0 + quarter + 16 j
+  const int quarter = tid >> 4;  // keys k0 + quarter + NQ * j
   const int dl = (lane & 15) * 8;
   const int32_t* bt = a.bt + (int64_t)s * a.max_blocks;
 
+  int64_t off[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int64_t key = k0 + quarter + NQ * j;
+    off[j] = key_offset(a, bt, key < ctx ? key : k0, h) + dl;
+  }
   u32x4 kr[U], vr[U];
 #pragma unroll
-  for (int j = 0; j < U; ++j) {
-    const int64_t key = k0 + quarter + 16 * j;
-    const int64_t off = key_offset(a, bt, key < ctx ? key : k0, h) + dl;
-    kr[j] = ld16(a.kc + off);
-  }
+  for (int j = 0; j < U; ++j) kr[j] = ldg16(a.kc + off[j]);
 #pragma unroll
-  for (int j = 0; j < U; ++j) {
-    const int64_t key = k0 + quarter + 16 * j;
-    const int64_t off = key_offset(a, bt, key < ctx ? key : k0, h) + dl;
-    vr[j] = ld16(a.vc + off);
-  }
+  for (int j = 0; j < U; ++j) vr[j] = ldg16(a.vc + off[j]);
   float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -997,13 +994,13 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a, float* part
     for (int d = 0; d < 8; ++d) qv[g][d] *= a.scale;
   }
 
-  __shared__ float sp[G][C];         // scores, then probabilities
-  __shared__ float sred[4][G][128];  // per-wave P.V partials
+  __shared__ float sp[G][C];             // scores, then probabilities
+  __shared__ float sred[WAVES][G][128];  // per-wave P.V partials
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     float kf[8];
     unpack8(kr[j], kf);
-    const int64_t key = k0 + quarter + 16 * j;
+    const int64_t key = k0 + quarter + NQ * j;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float t = 0.f;
@@ -1011,21 +1008,30 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a, float* part
       for (int d = 0; d < 8; ++d) t += qv[g][d] * kf[d];
 #pragma unroll
       for (int o = 8; o >= 1; o >>= 1) t += __shfl_xor(t, o, 16);
-      if ((lane & 15) == 0) sp[g][quarter + 16 * j] = (key < ctx) ? t : -INFINITY;
+      if ((lane & 15) == 0) sp[g][quarter + NQ * j] = (key < ctx) ? t : -INFINITY;
     }
   }
   __syncthreads();
-  // softmax within the chunk: one wave per head (C <= 128 keys, 2 per lane)
+  // softmax within the chunk: one wave per head, ceil(C / 64) keys per lane
   float* rec = part + (((int64_t)s * a.hkv + h) * maxch + c) * G * kAttnRec;
-  for (int g = wv; g < G; g += 4) {
-    const float s0 = sp[g][lane], s1 = (lane + 64 < C) ? sp[g][lane + 64] : -INFINITY;
-    float m = fmaxf(s0, s1);
+  for (int g = wv; g < G; g += WAVES) {
+    float sv[KPL];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      sv[i] = (lane + 64 * i < C) ? sp[g][lane + 64 * i] : -INFINITY;
+      m = fmaxf(m, sv[i]);
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    const float p0 = __expf(s0 - m), p1 = (lane + 64 < C) ? __expf(s1 - m) : 0.f;
-    sp[g][lane] = p0;
-    if (lane + 64 < C) sp[g][lane + 64] = p1;
-    float l = p0 + p1;
+    float l = 0.f;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      if (lane + 64 * i >= C) break;
+      const float pi = __expf(sv[i] - m);
+      sp[g][lane + 64 * i] = pi;
+      l += pi;
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
     if (lane == 0) {
@@ -1045,7 +1051,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a, float* part
     unpack8(vr[j], vf);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float pj = sp[g][quarter + 16 * j];
+      const float pj = sp[g][quarter + NQ * j];
 #pragma unroll
       for (int d = 0; d < 8; ++d) acc[g][d] += pj * vf[d];
     }
@@ -1067,20 +1073,22 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a, float* part
       for (int d = 0; d < 8; ++d) sred[wv][g][dl + d] = acc[g][d];
   }
   __syncthreads();
-  for (int it = tid; it < G * 128; it += 256) {
+  for (int it = tid; it < G * 128; it += WAVES * 64) {
     const int g = it >> 7, d = it & 127;
-    rec[g * kAttnRec + 2 + d] = sred[0][g][d] + sred[1][g][d] + sred[2][g][d] + sred[3][g][d];
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) o += sred[w][g][d];
+    rec[g * kAttnRec + 2 + d] = o;
   }
 }
 
 // Merges the chunk records of one (sequence, query head): out = sum_c o_c
 // e^(m_c - M) / sum_c l_c e^(m_c - M).
-__global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const float* part, int maxch, int G) {
+__global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const float* part, int maxch, int G, int C) {
   const int s = blockIdx.y, hqi = blockIdx.x;
   const int h = hqi / G, g = hqi - h * G;
   const int d = threadIdx.x;
   const int64_t ctx = (int64_t)a.seqlens[s] + 1;
-  const int C = (G <= 4) ? AttnChunk<4>::C : AttnChunk<8>::C;
   const int nch = (int)((ctx + C - 1) / C);
   const float* rec = part + ((int64_t)s * a.hkv + h) * maxch * G * kAttnRec + g * kAttnRec;
   const int64_t cstride = (int64_t)G * kAttnRec;
@@ -1716,24 +1724,45 @@ int launch_shrink_only(int64_t K, int ntok, const bf16* const* xrows, const int3
   return SWL_OK;
 }
 
-template <int G>
+template <int G, int WAVES, int U>
 int launch_attn_decode(const AttnArgs& a, hipStream_t st) {
-  // chunk count from the longest context: read on the host from the block
-  // table geometry (max_blocks pages), never from device memory
-  constexpr int C = AttnChunk<G>::C;
+  // chunk count from the longest context the block table can hold (host
+  // side geometry, never device memory)
+  constexpr int C = 4 * WAVES * U;
   const int maxch = (int)((a.max_blocks * a.bs + C - 1) / C);
   void* scratch = nullptr;
   const size_t need = sizeof(float) * (size_t)a.nseq * a.hkv * maxch * G * kAttnRec;
   int rc = scratch_get(need, st, &scratch);
   if (rc) return rc;
   float* part = reinterpret_cast<float*>(scratch);
-  hipLaunchKernelGGL(attn_chunk_kernel<G>, dim3((unsigned)a.hkv, (unsigned)maxch, (unsigned)a.nseq), dim3(256), 0,
-                     st, a, part, maxch);
+  hipLaunchKernelGGL((attn_chunk_kernel<G, WAVES, U>), dim3((unsigned)a.hkv, (unsigned)maxch, (unsigned)a.nseq),
+                     dim3(WAVES * 64), 0, st, a, part, maxch);
   SWL_LAUNCH_CHECK("attn_chunk_kernel launch");
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.hq, (unsigned)a.nseq), dim3(128), 0, st, a,
-                     (const float*)part, maxch, G);
+                     (const float*)part, maxch, G, C);
   SWL_LAUNCH_CHECK("attn_combine_kernel launch");
   return SWL_OK;
+}
+
+// keys per lane of the decode attention chunk (SWL_ATTN_U: 4, 8 or 16;
+// G = 8 uses at most 8)
+int attn_u() {
+  static int u = [] {
+    const char* e = getenv("SWL_ATTN_U");
+    const int v = e ? atoi(e) : 8;
+    return (v == 4 || v == 16) ? v : 8;
+  }();
+  return u;
+}
+
+template <int G>
+int launch_attn_decode_u(const AttnArgs& a, hipStream_t st) {
+  const int u = (G == 8 && attn_u() > 8) ? 8 : attn_u();
+  switch (u) {
+    case 4: return launch_attn_decode<G, 4, 4>(a, st);
+    case 16: return launch_attn_decode<G, 4, (G == 8 ? 8 : 16)>(a, st);
+    default: return launch_attn_decode<G, 4, 8>(a, st);
+  }
 }
 
 int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
@@ -1742,10 +1771,10 @@ int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
   SWL_LAUNCH_CHECK("rope_append_kernel launch");
   if (a.L == 1) {
     switch (G) {
-      case 1: return launch_attn_decode<1>(a, st);
-      case 2: return launch_attn_decode<2>(a, st);
-      case 4: return launch_attn_decode<4>(a, st);
-      default: return launch_attn_decode<8>(a, st);
+      case 1: return launch_attn_decode_u<1>(a, st);
+      case 2: return launch_attn_decode_u<2>(a, st);
+      case 4: return launch_attn_decode_u<4>(a, st);
+      default: return launch_attn_decode_u<8>(a, st);
     }
   }
   const dim3 grid((unsigned)a.hkv, (unsigned)a.L, (unsigned)a.nseq);
