@@ -255,34 +255,50 @@ __device__ __forceinline__ void epilogue_store4(float (&v)[4], int64_t n, int64_
 
 // ------------------------------------------------------ skinny (M<=64) ----
 // Decode-shaped projections (<= 64 tokens) run as two kernels:
-//   split_kernel     workgroup = 8 waves over 128 rows of W and one K-slice.
-//                    The K-slice of every token's activation row is staged once
-//                    in LDS and shared by the 8 waves (activation fetch is
-//                    tokens/128 of the weight bytes); each wave streams its 16
-//                    W rows from HBM into MFMA A-fragments and writes fp32
-//                    partial sums for its K-slice.  Workgroups below
-//                    n_shrink_wg instead run LoRA-shrink items, one per wave.
+//   split_kernel     workgroup = 8 waves over 8 row tiles (16 rows each) and
+//                    one K-slice.  The K-slice of every token's activation row
+//                    is staged once in LDS and shared by the 8 waves
+//                    (activation fetch is tokens/128 of the weight bytes);
+//                    each wave streams its 16 rows from HBM into MFMA
+//                    A-fragments and writes fp32 partial sums for its K-slice.
+//                    The LoRA shrink rides along: the stacked A of each
+//                    distinct adapter of the round forms extra row tiles after
+//                    W's, streamed and multiplied the same way, and each token
+//                    keeps only the columns of its own adapter's rows.
 //   epilogue_kernel  sums the K-slice partials, adds bias and the LoRA expand,
 //                    rounds once to bf16 and stores each token's row into its
 //                    slot buffer (the scatter).
 constexpr int kKDepth = 8;            // k-steps of W in flight per wave
 
 struct SplitArgs {
-  // base projection -> part[ks][tok][N]
+  // base projection -> part[ks][tok][N]; LoRA shrink -> u[ks][tok][u_ld]
   const bf16* w;
   int64_t N, K;
   int32_t ntok;
-  int32_t n_rg, n_ks, n_base_wg;
+  int32_t n_ks, n_workers;            // grid = n_ks x n_workers workgroups
   int32_t total_steps, ks_steps;      // k-steps of 32 in K; max per K-slice
+  int32_t n_wtiles, n_tiles;          // W row tiles (ceil(N / 16)); all tiles incl. adapter rows
+  int32_t ngroups, u_ld;
   float* part;
+  float* u;
+  int64_t u_split_stride;             // ntok * u_ld
   const bf16* x[kSkinnyMaxTok];
-  // LoRA shrink items -> u[uks][urow][u_ld]
-  int32_t n_items, n_shrink_wg, u_ks, u_ld;
+  const bf16* g_a[kSkinnyMaxTok];     // stacked lora_A [g_arows][K] of adapter group g
+  int32_t g_arows[kSkinnyMaxTok];
+  int32_t g_tile0[kSkinnyMaxTok + 1]; // first row tile of group g past W's; [ngroups] = total
+  int8_t tok_grp[kSkinnyMaxTok];      // adapter group of each token, -1 for none
+};
+
+// LoRA shrink alone (prefill path): one wave per (16-row tile of stacked A,
+// K-slice), B-fragments of up to 64 packed token rows read from global memory.
+struct ShrinkArgs {
+  int64_t K;
+  int32_t total_steps;
+  int32_t n_items, u_ks, u_ld;
   int64_t u_split_stride;
   float* u;
-  const swl_lora_entry* table;
   int32_t ngroups;
-  int32_t g_entry[kSkinnyMaxTok];
+  const bf16* g_a[kSkinnyMaxTok];
   int32_t g_arows[kSkinnyMaxTok];
   int32_t g_tile0[kSkinnyMaxTok + 1];
   int32_t g_tok0[kSkinnyMaxTok + 1];
@@ -385,18 +401,17 @@ __device__ __forceinline__ void kloop_global(f32x4 (&acc)[TT], const bf16* wp, c
 }
 
 template <int TT>
-__device__ __forceinline__ void shrink_item(const SplitArgs& a, int item, int lane) {
+__device__ __forceinline__ void shrink_item(const ShrinkArgs& a, int item, int lane) {
   const int tile = item / a.u_ks;
   const int uks = item - tile * a.u_ks;
   int g = 0;
   while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
   const int rt = tile - a.g_tile0[g];
-  const bf16* amat = reinterpret_cast<const bf16*>(a.table[a.g_entry[g]].a);
   const int arow = min(rt * 16 + (lane & 15), a.g_arows[g] - 1);
   const int st0 = (int)((int64_t)a.total_steps * uks / a.u_ks);
   const int st1 = (int)((int64_t)a.total_steps * (uks + 1) / a.u_ks);
   const int64_t koff = (int64_t)st0 * 32 + 8 * (lane >> 4);
-  const bf16* wp = amat + (int64_t)arow * a.K + koff;
+  const bf16* wp = a.g_a[g] + (int64_t)arow * a.K + koff;
   const int t0 = a.g_tok0[g], cnt = a.g_tok0[g + 1] - t0;
   const bf16* xp[TT];
 #pragma unroll
@@ -419,36 +434,73 @@ __device__ __forceinline__ void shrink_item(const SplitArgs& a, int item, int la
   }
 }
 
+// Independent wave items, no workgroup barrier.
+__global__ __launch_bounds__(512) void shrink_kernel(ShrinkArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 8 + (threadIdx.x >> 6);
+  if (item >= a.n_items) return;
+  int cnt_max = 0;
+  {
+    const int tile = item / a.u_ks;
+    int g = 0;
+    while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
+    cnt_max = a.g_tok0[g + 1] - a.g_tok0[g];
+  }
+  if (cnt_max <= 16) shrink_item<1>(a, item, lane);
+  else if (cnt_max <= 32) shrink_item<2>(a, item, lane);
+  else shrink_item<4>(a, item, lane);
+}
+
+// Row pointer (this lane's row, at the K-slice start) of row tile `tile`: a
+// tile of W, or a tile of one adapter group's stacked A (rows past the end of
+// either re-read its last row; their results are never stored).  grp: -1 for
+// W, the group for adapter rows.
+__device__ __forceinline__ const bf16* tile_rows(const SplitArgs& a, int tile, int lane, int64_t kbeg, int& grp,
+                                                 int& qrow0) {
+  const bf16* row;
+  grp = -1;
+  qrow0 = 0;
+  if (tile < a.n_wtiles) {
+    const int64_t r = (int64_t)tile * 16 + (lane & 15);
+    row = a.w + (r < a.N ? r : a.N - 1) * a.K;
+  } else {
+    const int lt = tile - a.n_wtiles;
+    int g = 0;
+    while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= lt) ++g;
+    qrow0 = (lt - a.g_tile0[g]) * 16;
+    row = a.g_a[g] + (int64_t)min(qrow0 + (lane & 15), a.g_arows[g] - 1) * a.K;
+    grp = g;
+  }
+  return row + kbeg + 8 * (lane >> 4);
+}
+
+// Workgroup (K-slice ks, worker j): stages the K-slice of every token row in
+// LDS once, then each wave walks row tiles j*WAVES + wv, + n_workers*WAVES,
+// ... (W's tiles, then the adapter tiles), issuing the next tile's first W
+// group before storing the current tile's partials so the stores and the
+// loads overlap.  No workgroup waits on another.
 template <int TT, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, 16 / WAVES) void split_kernel(SplitArgs a) {
+__global__ __launch_bounds__(WAVES * 64, WAVES >= 16 ? 1 : 16 / WAVES) void split_kernel(SplitArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16 xs[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  if ((int)blockIdx.x < a.n_shrink_wg) {
-    // LoRA shrink: independent wave items, no workgroup barrier on this path
-    const int item = blockIdx.x * WAVES + wv;
-    if (item >= a.n_items) return;
-    int cnt_max = 0;
-    {
-      const int tile = item / a.u_ks;
-      int g = 0;
-      while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
-      cnt_max = a.g_tok0[g + 1] - a.g_tok0[g];
-    }
-    if (cnt_max <= 16) shrink_item<1>(a, item, lane);
-    else if (cnt_max <= 32) shrink_item<2>(a, item, lane);
-    else shrink_item<4>(a, item, lane);
-    return;
-  }
-  // K-slice index runs fastest so the n_ks workgroups of one row group are
-  // dispatched together
-  const int b = blockIdx.x - a.n_shrink_wg;
-  const int ks = b % a.n_ks, rg = b / a.n_ks;
+  const int ks = blockIdx.x % a.n_ks, wk = blockIdx.x / a.n_ks;
   const int st0 = (int)((int64_t)a.total_steps * ks / a.n_ks);
   const int st1 = (int)((int64_t)a.total_steps * (ks + 1) / a.n_ks);
   const int nst = st1 - st0;
   const int npad = (nst + kKDepth - 1) / kKDepth * kKDepth;
   const int64_t kbeg = (int64_t)st0 * 32;
+  const int tstride = a.n_workers * WAVES;
+
+  int tile = wk * WAVES + wv;
+  int grp = -1, qrow0 = 0;
+  const bf16* wp = nullptr;
+  u32x4 w[kKDepth];
+  if (tile < a.n_tiles) {
+    wp = tile_rows(a, tile, lane, kbeg, grp, qrow0);
+#pragma unroll
+    for (int d = 0; d < kKDepth; ++d) w[d] = ld_w_step(wp, d, nst);
+  }
 
   // Stage the activation K-slice in LDS in MFMA B-fragment order: block
   // (step s, token tile t) holds 64 lanes x 16 B, lane l = token 16t + l%16,
@@ -456,43 +508,56 @@ __global__ __launch_bounds__(WAVES * 64, 16 / WAVES) void split_kernel(SplitArgs
   // LDS-DMA loads (global_load_lds_dwordx4), no VGPR round trip.  Token rows
   // past ntok load row 0 (their results are never stored); steps past the
   // slice reload its last step (the matching W fragments are zero).
-  {
-    for (int i = wv; i < npad * TT; i += WAVES) {
-      const int st = i / TT, t = i - st * TT;
-      const int tk = 16 * t + (lane & 15);
-      const bf16* src = a.x[tk < a.ntok ? tk : 0] + kbeg + 32 * (st < nst ? st : nst - 1) + 8 * (lane >> 4);
-      __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
-    }
+  for (int i = wv; i < npad * TT; i += WAVES) {
+    const int st = i / TT, t = i - st * TT;
+    const int tk = 16 * t + (lane & 15);
+    const bf16* src = a.x[tk < a.ntok ? tk : 0] + kbeg + 32 * (st < nst ? st : nst - 1) + 8 * (lane >> 4);
+    __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
   }
-
-  const int64_t r0 = (int64_t)rg * (16 * WAVES) + wv * 16;
-  const int64_t wrow = (r0 + (lane & 15) < a.N) ? r0 + (lane & 15) : a.N - 1;
-  const bf16* wp = a.w + wrow * a.K + kbeg + 8 * (lane >> 4);
-  u32x4 w[kKDepth];
-#pragma unroll
-  for (int d = 0; d < kKDepth; ++d) w[d] = ld_w_step(wp, d, nst);
   __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's LDS-DMA (and W) loads have landed
   __syncthreads();
 
   const bf16* xl = xs + 8 * lane;  // block (s, t) at xs + (s * TT + t) * 512 elements
-  f32x4 acc[TT];
+  while (tile < a.n_tiles) {
+    f32x4 acc[TT];
 #pragma unroll
-  for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  kloop_lds<TT, kKDepth>(acc, w, wp, xl, 512, npad, nst);
+    for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    kloop_lds<TT, kKDepth>(acc, w, wp, xl, 512, npad, nst);
 
-  const int64_t n0 = r0 + 4 * (lane >> 4);
-  if (n0 < a.N) {
-    const bool vec = (n0 + 3 < a.N) && ((a.N & 3) == 0);
+    const int cur = tile, cgrp = grp, cq = qrow0;
+    tile += tstride;
+    if (tile < a.n_tiles) {
+      wp = tile_rows(a, tile, lane, kbeg, grp, qrow0);
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      const int tok = 16 * t + (lane & 15);
-      if (tok >= a.ntok) continue;
-      float* dst = a.part + ((int64_t)ks * a.ntok + tok) * a.N + n0;
-      if (vec) {
-        *reinterpret_cast<f32x4*>(dst) = acc[t];
-      } else {
-        for (int j = 0; j < 4; ++j)
-          if (n0 + j < a.N) dst[j] = acc[t][j];
+      for (int d = 0; d < kKDepth; ++d) w[d] = ld_w_step(wp, d, nst);
+    }
+
+    if (cgrp < 0) {
+      const int64_t n0 = (int64_t)cur * 16 + 4 * (lane >> 4);
+      if (n0 < a.N) {
+        const bool vec = (n0 + 3 < a.N) && ((a.N & 3) == 0);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          const int tok = 16 * t + (lane & 15);
+          if (tok >= a.ntok) continue;
+          float* dst = a.part + ((int64_t)ks * a.ntok + tok) * a.N + n0;
+          if (vec) {
+            *reinterpret_cast<f32x4*>(dst) = acc[t];
+          } else {
+            for (int j = 0; j < 4; ++j)
+              if (n0 + j < a.N) dst[j] = acc[t][j];
+          }
+        }
+      }
+    } else {
+      // shrink rows cq.. of adapter group cgrp: only that group's tokens keep
+      // them (u_ld covers every padded tile, so the f32x4 store stays in the row)
+      const int q = cq + 4 * (lane >> 4);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const int tok = 16 * t + (lane & 15);
+        if (tok < a.ntok && a.tok_grp[tok] == cgrp)
+          *reinterpret_cast<f32x4*>(a.u + ks * a.u_split_stride + (int64_t)tok * a.u_ld + q) = acc[t];
       }
     }
   }
@@ -1463,24 +1528,40 @@ int fill_segptrs(SegPtrs& sp, const void* const* ptrs, const int64_t* rows, int 
 }
 
 // Launch-shape tuning of the decode path.  Defaults are the measured best on
-// MI355X; SWL_SKINNY_WAVES (4 or 8) and SWL_SKINNY_TARGET_WG override them for
-// sweeps.
+// MI355X; SWL_SKINNY_WAVES (4, 8 or 16), SWL_SKINNY_WGCU (resident workgroups per
+// CU the grid is sized for), SWL_SKINNY_LDS_KB and SWL_SKINNY_NKS override
+// them for sweeps.
 struct Tuning {
   int waves = 8;
-  int target_wg = 512;
-  int lds_kb = 96;  // activation-slice LDS per workgroup (16..160 KiB)
-  int nks = 0;      // forced K-slice count (0: chosen per shape)
+  int wg_per_cu = 3;
+  int lds_kb = 96;      // activation-slice LDS per workgroup (16..160 KiB)
+  int slice_steps = 16; // K-slices hold at most this many 32-wide k-steps
+  int nks = 0;          // forced K-slice count (0: chosen per shape)
 };
 const Tuning& tuning() {
   static Tuning t = [] {
     Tuning v;
-    if (const char* e = getenv("SWL_SKINNY_WAVES")) v.waves = (atoi(e) == 4) ? 4 : 8;
-    if (const char* e = getenv("SWL_SKINNY_TARGET_WG")) v.target_wg = std::max(1, atoi(e));
+    if (const char* e = getenv("SWL_SKINNY_WAVES")) v.waves = (atoi(e) == 4 || atoi(e) == 16) ? atoi(e) : 8;
+    if (const char* e = getenv("SWL_SKINNY_WGCU")) v.wg_per_cu = std::min(8, std::max(1, atoi(e)));
     if (const char* e = getenv("SWL_SKINNY_LDS_KB")) v.lds_kb = std::min(160, std::max(16, atoi(e)));
     if (const char* e = getenv("SWL_SKINNY_NKS")) v.nks = std::max(0, atoi(e));
+    if (const char* e = getenv("SWL_SKINNY_SLICE")) v.slice_steps = std::max(1, atoi(e));
     return v;
   }();
   return t;
+}
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
 }
 
 // Dynamic LDS above the default 64 KiB must be allowed per kernel.
@@ -1495,68 +1576,60 @@ int allow_lds(K kernel, size_t bytes, size_t* allowed) {
 
 // Adapter groups for the LoRA shrink: tokens that share a lora table entry.
 struct ShrinkPlan {
-  int ngroups = 0, tiles = 0, max_cnt = 0;
+  int ngroups = 0, tiles = 0;
   int32_t g_entry[kSkinnyMaxTok];
   int32_t g_arows[kSkinnyMaxTok];
   int32_t g_tile0[kSkinnyMaxTok + 1];
   int32_t g_tok0[kSkinnyMaxTok + 1];
-  int32_t g_tok[kSkinnyMaxTok];
-  const bf16* g_x[kSkinnyMaxTok];
+  int32_t g_tok[kSkinnyMaxTok];       // token index (in input order) of each grouped token
+  int8_t tok_grp[kSkinnyMaxTok];      // group of each token, -1 for none
 };
 
-// tok_lora[i] >= 0: token i uses entry tok_lora[i]; u row of token i is
-// urow0 + i.  Tokens are grouped per entry so each adapter's A is read once.
-int plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const bf16* const* xrows, int urow0,
-                const swl_lora_entry* host_entries, int nblk) {
+// tok_lora[i] >= 0: token i uses entry tok_lora[i].  Tokens are grouped per
+// entry so each adapter's A is read once per K-slice.
+void plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const swl_lora_entry* host_entries, int nblk) {
   p.ngroups = 0;
   p.tiles = 0;
-  p.max_cnt = 0;
   int nt = 0;
+  for (int i = 0; i < ntok; ++i) p.tok_grp[i] = -1;
   for (int i = 0; i < ntok; ++i) {
     const int e = tok_lora[i];
-    if (e < 0) continue;
-    bool seen = false;
-    for (int g = 0; g < p.ngroups; ++g) seen |= (p.g_entry[g] == e);
-    if (seen) continue;
+    if (e < 0 || p.tok_grp[i] >= 0) continue;
     const int g = p.ngroups++;
     p.g_entry[g] = e;
     p.g_arows[g] = host_entries[e].rank * nblk;
     p.g_tile0[g] = p.tiles;
     p.g_tok0[g] = nt;
     p.tiles += (p.g_arows[g] + 15) / 16;
-    int cnt = 0;
     for (int j = i; j < ntok; ++j)
       if (tok_lora[j] == e) {
-        p.g_tok[nt] = urow0 + j;
-        p.g_x[nt] = xrows[j];
-        ++nt;
-        ++cnt;
+        p.tok_grp[j] = (int8_t)g;
+        p.g_tok[nt++] = j;
       }
-    p.max_cnt = std::max(p.max_cnt, cnt);
   }
   p.g_tile0[p.ngroups] = p.tiles;
   p.g_tok0[p.ngroups] = nt;
+}
+
+template <int TT, int W>
+int launch_split_tw(const SplitArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t tb0, hipEvent_t tb1) {
+  static size_t allowed = 0;
+  int rc = allow_lds(split_kernel<TT, W>, lds, &allowed);
+  if (rc) return rc;
+  launch_maybe_timed(split_kernel<TT, W>, grid, dim3(W * 64), lds, st, tb0, tb1, a);
   return SWL_OK;
 }
 
-void copy_shrink(SplitArgs& a, const ShrinkPlan& p) {
-  a.ngroups = p.ngroups;
-  for (int g = 0; g < p.ngroups; ++g) {
-    a.g_entry[g] = p.g_entry[g];
-    a.g_arows[g] = p.g_arows[g];
-    a.g_tile0[g] = p.g_tile0[g];
-    a.g_tok0[g] = p.g_tok0[g];
-  }
-  a.g_tile0[p.ngroups] = p.g_tile0[p.ngroups];
-  a.g_tok0[p.ngroups] = p.g_tok0[p.ngroups];
-  for (int i = 0; i < p.g_tok0[p.ngroups]; ++i) {
-    a.g_tok[i] = p.g_tok[i];
-    a.g_x[i] = p.g_x[i];
+template <int W>
+int launch_split_w(int TT, const SplitArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t tb0,
+                   hipEvent_t tb1) {
+  switch (TT) {
+    case 1: return launch_split_tw<1, W>(a, grid, lds, st, tb0, tb1);
+    case 2: return launch_split_tw<2, W>(a, grid, lds, st, tb0, tb1);
+    case 3: return launch_split_tw<3, W>(a, grid, lds, st, tb0, tb1);
+    default: return launch_split_tw<4, W>(a, grid, lds, st, tb0, tb1);
   }
 }
-
-// K-slices per LoRA-shrink item: ~16 k-steps of A per wave.
-int shrink_ksplit(int64_t total_steps) { return (int)std::max<int64_t>(1, total_steps / 16); }
 
 // Decode-shaped projection of ntok (<= 64) token rows: y[i] = x[i] . W^T
 // (+ bias) (+ LoRA delta of entry tok_lora[i]).  xrows[i] / yrows[i] are the
@@ -1572,48 +1645,60 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   a.K = K;
   a.ntok = ntok;
   a.total_steps = (int)total_steps;
-  const Tuning& tu = tuning();
-  const int waves = tu.waves;
-  a.n_rg = (int)((N + 16 * waves - 1) / (16 * waves));
-  // K-slices: a power of two (slice starts on aligned byte offsets stream
-  // best from HBM), enough for target_wg workgroups, doubled once more for
-  // wide projections below 1024 workgroups; then as many more as the LDS cap
-  // on the staged activation slice (padded steps x TT x 1 KiB) requires.
-  int64_t n_ks = 1;
-  if (tu.nks > 0) {
-    n_ks = tu.nks;
-  } else {
-    while (n_ks < total_steps && a.n_rg * n_ks < tu.target_wg) n_ks *= 2;
-    if (a.n_rg >= 128 && a.n_rg * n_ks < 1024 && n_ks < total_steps) n_ks *= 2;
-  }
-  auto padded = [&](int64_t nk) { return ((total_steps + nk - 1) / nk + kKDepth - 1) / kKDepth * kKDepth; };
-  while (n_ks < total_steps && padded(n_ks) * TT * 1024 > (int64_t)tu.lds_kb * 1024) n_ks *= 2;
-  n_ks = std::min<int64_t>(n_ks, total_steps);
-  a.n_ks = (int)n_ks;
-  a.ks_steps = (int)padded(n_ks);  // the widest slice, padded to whole pipeline iterations
-  a.n_base_wg = a.n_rg * a.n_ks;
+  a.n_wtiles = (int)((N + 15) / 16);
   for (int i = 0; i < ntok; ++i) a.x[i] = xrows[i];
 
   bool has_lora = false;
   if (tok_lora)
     for (int i = 0; i < ntok; ++i) has_lora |= tok_lora[i] >= 0;
-  int max_r = 0;
   ShrinkPlan sp;
+  int max_r = 0;
   if (has_lora) {
-    plan_shrink(sp, ntok, tok_lora, xrows, 0, host_entries, nblk);
-    for (int g = 0; g < sp.ngroups; ++g) max_r = std::max(max_r, host_entries[sp.g_entry[g]].rank);
-    a.u_ks = shrink_ksplit(total_steps);
-    a.n_items = sp.tiles * a.u_ks;
-    a.n_shrink_wg = (a.n_items + waves - 1) / waves;
+    plan_shrink(sp, ntok, tok_lora, host_entries, nblk);
+    a.ngroups = sp.ngroups;
+    for (int g = 0; g < sp.ngroups; ++g) {
+      a.g_a[g] = reinterpret_cast<const bf16*>(host_entries[sp.g_entry[g]].a);
+      a.g_arows[g] = sp.g_arows[g];
+      a.g_tile0[g] = sp.g_tile0[g];
+      max_r = std::max(max_r, host_entries[sp.g_entry[g]].rank);
+    }
+    a.g_tile0[sp.ngroups] = sp.g_tile0[sp.ngroups];
+    for (int i = 0; i < ntok; ++i) a.tok_grp[i] = sp.tok_grp[i];
     a.u_ld = ((max_r * nblk + 15) / 16) * 16;
     SWL_CHECK(a.u_ld <= kMaxURow, SWL_ERR_INVALID, "round: LoRA rank x blocks exceeds 256");
     a.u_split_stride = (int64_t)ntok * a.u_ld;
-    a.table = table;
-    copy_shrink(a, sp);
   }
+
+  const Tuning& tu = tuning();
+  const int waves = tu.waves;
+  a.n_tiles = a.n_wtiles + sp.tiles;
+  const int64_t tile_groups = (a.n_tiles + waves - 1) / waves;
+  const int64_t slots = (int64_t)cu_count() * tu.wg_per_cu;
+  // K-slices: a power of two (slice starts on aligned byte offsets stream
+  // best from HBM), the smallest whose slices hold at most slice_steps
+  // k-steps and whose workers fill at least half the resident workgroup
+  // slots (longer slices write fewer fp32 partials but stage more activation
+  // rows per workgroup and leave fewer workers; 16 steps measured best), then
+  // as many more as the LDS cap on the staged activation slice (padded steps
+  // x TT x 1 KiB) requires.
+  auto padded = [&](int64_t nk) { return ((total_steps + nk - 1) / nk + kKDepth - 1) / kKDepth * kKDepth; };
+  int64_t n_ks = 1;
+  if (tu.nks > 0) {
+    n_ks = tu.nks;
+  } else {
+    while (n_ks < total_steps &&
+           ((total_steps + n_ks - 1) / n_ks > tu.slice_steps || 2 * n_ks * tile_groups < slots))
+      n_ks *= 2;
+  }
+  while (n_ks < total_steps && padded(n_ks) * TT * 1024 > (int64_t)tu.lds_kb * 1024) n_ks *= 2;
+  n_ks = std::min<int64_t>(n_ks, total_steps);
+  a.n_ks = (int)n_ks;
+  a.ks_steps = (int)padded(n_ks);  // the widest slice, padded to whole pipeline iterations
+  a.n_workers = (int)std::max<int64_t>(1, std::min<int64_t>(tile_groups, slots / n_ks));
+
   const size_t part_bytes = sizeof(float) * (size_t)a.n_ks * ntok * N;
   const size_t part_al = (part_bytes + 255) & ~(size_t)255;
-  const size_t u_bytes = has_lora ? sizeof(float) * (size_t)a.u_ks * a.u_split_stride : 0;
+  const size_t u_bytes = has_lora ? sizeof(float) * (size_t)a.n_ks * a.u_split_stride : 0;
   void* scratch = nullptr;
   int rc = scratch_get(part_al + u_bytes, st, &scratch);
   if (rc) return rc;
@@ -1621,8 +1706,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   a.u = has_lora ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + part_al) : nullptr;
 
   const size_t lds = (size_t)a.ks_steps * TT * 1024;
-  const dim3 grid((unsigned)(a.n_shrink_wg + a.n_base_wg));
-  const dim3 block((unsigned)(waves * 64));
+  const dim3 grid((unsigned)(a.n_ks * a.n_workers));
   const int tslot = timer_slot(st);
   if (tslot >= 0) {
     // algorithmic bytes of the base kernel: W and the token rows once, each
@@ -1635,41 +1719,14 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     g_timer.bytes[tslot] = bytes;
   }
   hipEvent_t tb0 = timer_event(tslot, 0), tb1 = timer_event(tslot, 1);
-  static size_t allowed[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
   {
-    size_t* al = &allowed[waves == 4 ? 0 : 1][TT - 1];
     int rc2 = SWL_OK;
-    if (waves == 4) {
-      switch (TT) {
-        case 1: rc2 = allow_lds(split_kernel<1, 4>, lds, al); break;
-        case 2: rc2 = allow_lds(split_kernel<2, 4>, lds, al); break;
-        case 3: rc2 = allow_lds(split_kernel<3, 4>, lds, al); break;
-        default: rc2 = allow_lds(split_kernel<4, 4>, lds, al); break;
-      }
-    } else {
-      switch (TT) {
-        case 1: rc2 = allow_lds(split_kernel<1, 8>, lds, al); break;
-        case 2: rc2 = allow_lds(split_kernel<2, 8>, lds, al); break;
-        case 3: rc2 = allow_lds(split_kernel<3, 8>, lds, al); break;
-        default: rc2 = allow_lds(split_kernel<4, 8>, lds, al); break;
-      }
+    switch (waves) {
+      case 4: rc2 = launch_split_w<4>(TT, a, grid, lds, st, tb0, tb1); break;
+      case 16: rc2 = launch_split_w<16>(TT, a, grid, lds, st, tb0, tb1); break;
+      default: rc2 = launch_split_w<8>(TT, a, grid, lds, st, tb0, tb1); break;
     }
     if (rc2) return rc2;
-  }
-  if (waves == 4) {
-    switch (TT) {
-      case 1: launch_maybe_timed(split_kernel<1, 4>, grid, block, lds, st, tb0, tb1, a); break;
-      case 2: launch_maybe_timed(split_kernel<2, 4>, grid, block, lds, st, tb0, tb1, a); break;
-      case 3: launch_maybe_timed(split_kernel<3, 4>, grid, block, lds, st, tb0, tb1, a); break;
-      default: launch_maybe_timed(split_kernel<4, 4>, grid, block, lds, st, tb0, tb1, a); break;
-    }
-  } else {
-    switch (TT) {
-      case 1: launch_maybe_timed(split_kernel<1, 8>, grid, block, lds, st, tb0, tb1, a); break;
-      case 2: launch_maybe_timed(split_kernel<2, 8>, grid, block, lds, st, tb0, tb1, a); break;
-      case 3: launch_maybe_timed(split_kernel<3, 8>, grid, block, lds, st, tb0, tb1, a); break;
-      default: launch_maybe_timed(split_kernel<4, 8>, grid, block, lds, st, tb0, tb1, a); break;
-    }
   }
   SWL_LAUNCH_CHECK("split_kernel launch");
 
@@ -1689,7 +1746,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     e.L = *Lblk;
     e.L.table = table;
     e.L.u = a.u;
-    e.L.usplit = a.u_ks;
+    e.L.usplit = a.n_ks;
     e.L.u_ld = a.u_ld;
     e.L.u_split_stride = a.u_split_stride;
   }
@@ -1701,26 +1758,37 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
 }
 
 // LoRA shrink alone for up to 64 tokens of the packed prefill batch
-// (u rows are packed rows); used by the tiled path.
+// (xrows[i] is packed row urow0 + i; u rows are packed rows); used by the
+// tiled path.
 int launch_shrink_only(int64_t K, int ntok, const bf16* const* xrows, const int32_t* tok_lora, int urow0,
-                       const swl_lora_entry* table, const swl_lora_entry* host_entries, int nblk, float* u,
-                       int u_ld, int64_t u_split_stride, int u_ks, hipStream_t st) {
+                       const swl_lora_entry* host_entries, int nblk, float* u, int u_ld, int64_t u_split_stride,
+                       int u_ks, hipStream_t st) {
   ShrinkPlan sp;
-  plan_shrink(sp, ntok, tok_lora, xrows, urow0, host_entries, nblk);
+  plan_shrink(sp, ntok, tok_lora, host_entries, nblk);
   if (sp.ngroups == 0) return SWL_OK;
-  SplitArgs a{};
+  ShrinkArgs a{};
   a.K = K;
   a.total_steps = (int)(K / 32);
   a.u_ks = u_ks;
   a.n_items = sp.tiles * u_ks;
-  a.n_shrink_wg = (a.n_items + 7) / 8;
   a.u_ld = u_ld;
   a.u_split_stride = u_split_stride;
   a.u = u;
-  a.table = table;
-  copy_shrink(a, sp);
-  hipLaunchKernelGGL((split_kernel<1, 8>), dim3((unsigned)a.n_shrink_wg), dim3(8 * 64), 0, st, a);
-  SWL_LAUNCH_CHECK("split_kernel (shrink) launch");
+  a.ngroups = sp.ngroups;
+  for (int g = 0; g < sp.ngroups; ++g) {
+    a.g_a[g] = reinterpret_cast<const bf16*>(host_entries[sp.g_entry[g]].a);
+    a.g_arows[g] = sp.g_arows[g];
+    a.g_tile0[g] = sp.g_tile0[g];
+    a.g_tok0[g] = sp.g_tok0[g];
+  }
+  a.g_tile0[sp.ngroups] = sp.g_tile0[sp.ngroups];
+  a.g_tok0[sp.ngroups] = sp.g_tok0[sp.ngroups];
+  for (int i = 0; i < sp.g_tok0[sp.ngroups]; ++i) {
+    a.g_tok[i] = urow0 + sp.g_tok[i];
+    a.g_x[i] = xrows[sp.g_tok[i]];
+  }
+  hipLaunchKernelGGL(shrink_kernel, dim3((unsigned)((a.n_items + 7) / 8)), dim3(512), 0, st, a);
+  SWL_LAUNCH_CHECK("shrink_kernel launch");
   return SWL_OK;
 }
 
@@ -2126,7 +2194,7 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
           xr[j] = packed + (prow0 + j) * K;
           tl[j] = seg_lora[i];
         }
-        rc = launch_shrink_only(K, cnt, xr, tl, (int)prow0, lora_table, host_entries, nblk, u, u_ld,
+        rc = launch_shrink_only(K, cnt, xr, tl, (int)prow0, host_entries, nblk, u, u_ld,
                                 (int64_t)T * u_ld, 1, st);
         if (rc) return rc;
       }
