@@ -122,6 +122,60 @@ int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
                    const swl_lora_entry* lora_table_host, int nblk,
                    const int64_t* blk_cols, void* stream);
 
+/* Optional fusions of a decode-shaped round (<= 64 token rows) with the
+ * worker-side elementwise work on either side of it, for the in-process
+ * batched decode step.  No counterpart in the reference: its worker runs this
+ * work between rounds (worker_sync.py:158, :169-205, :314-319, :383-389,
+ * :1344-1350, :1397); the results are the same up to fp32 summation order.
+ *
+ * Input side (norm_weight != NULL): the rows given as seg_in hold the residual
+ * stream h [k]; the round multiplies LlamaRMSNorm(h) = bf16(bf16(h * r) * w),
+ * r = rsqrt(sum(ss_in[t][0 .. ss_in_n)) / k + eps), instead of h.  ss_in
+ * [ntok][ss_in_stride] fp32 holds partial sums of squares of each row, as an
+ * out_mode 1 round writes them.
+ *
+ * Output side (out_mode):
+ *   0  plain: seg_out rows get the round output.
+ *   1  residual: seg_out rows hold h [n]; h = bf16(h + out), and the partial
+ *      sums of squares of the new row go to ss_out [ntok][ss_out_stride]
+ *      (ceil(n / 256) of them: ss_out_stride must be at least that).
+ *   2  SiLU-mul: n = 2 * inter (gate | up); seg_out rows [inter] get
+ *      bf16(bf16(silu(gate)) * up).
+ *   3  RoPE + KV append (decode, one token per sequence; token t is sequence
+ *      t): n = (hq + 2 * hkv) * 128; q columns of seg_out rows get the rotated
+ *      q, the rotated k and the v of token t are written to its page slot
+ *      (position cache_seqlens[t]) in k_cache / v_cache [num_blocks,
+ *      block_size, hkv, 128] through block_table [ntok, max_blocks]; RoPE
+ *      (NeoX halves) at positions[t] from cos_sin [max_pos, 128]. */
+typedef struct swl_round_fusion {
+  const void* norm_weight;
+  float eps;
+  const float* ss_in;
+  int32_t ss_in_n, ss_in_stride;
+  int32_t out_mode;
+  float* ss_out;
+  int32_t ss_out_stride;
+  void* k_cache;
+  void* v_cache;
+  int32_t hq, hkv, block_size;
+  const int32_t* block_table;
+  int64_t max_blocks, num_blocks;
+  const int32_t* cache_seqlens;
+  const int64_t* positions;
+  const void* cos_sin;
+  int64_t max_pos;
+} swl_round_fusion;
+
+/* swl_round_bf16 with fusions (fusion may be NULL; a non-NULL fusion needs
+ * at most 64 token rows). */
+int swl_round_ex_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
+                      void* const* seg_out, const void* w, const void* bias,
+                      int64_t n, int64_t k, const int32_t* seg_lora,
+                      const swl_lora_entry* lora_table,
+                      const swl_lora_entry* lora_table_host, int nblk,
+                      const int64_t* blk_cols, const swl_round_fusion* fusion,
+                      void* stream);
+
 /* Row-major matrix product with an explicit layout, used by the worker-side
  * LoRA modules: y[m, n] = alpha * x[m, k] . B where B is b[k, n] (trans_b = 0,
  * ldb = row stride of b) or b[n, k]^T (trans_b = 1).  fp32 accumulation,
@@ -216,7 +270,9 @@ int swl_silu_mul_rows_bf16(const void* const* in_rows, void* const* out_rows, in
 
 /* swl_paged_attention_bf16 with per-token rows: token t = seq * q_len + i
  * reads its fused [q | k | v] row at qkv_rows[t] (RoPE applied in place) and
- * writes its [hq * d] output row at out_rows[t]. */
+ * writes its [hq * d] output row at out_rows[t].  rope = 2: q in the rows is
+ * already rotated and k / v already appended to the pages (an out_mode 3
+ * round), so only the attention itself runs. */
 int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len, int hq,
                                   int hkv, int d, void* k_cache, void* v_cache, int64_t num_blocks,
                                   int block_size, const int32_t* block_table, int64_t max_blocks,

@@ -43,6 +43,32 @@ class LoraEntry(ctypes.Structure):
     ]
 
 
+class RoundFusion(ctypes.Structure):
+    """swl_round_fusion (include/swl.h)."""
+    _fields_ = [
+        ("norm_weight", c_vp),
+        ("eps", c_f32),
+        ("ss_in", c_vp),
+        ("ss_in_n", ctypes.c_int32),
+        ("ss_in_stride", ctypes.c_int32),
+        ("out_mode", ctypes.c_int32),
+        ("ss_out", c_vp),
+        ("ss_out_stride", ctypes.c_int32),
+        ("k_cache", c_vp),
+        ("v_cache", c_vp),
+        ("hq", ctypes.c_int32),
+        ("hkv", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("block_table", c_vp),
+        ("max_blocks", c_i64),
+        ("num_blocks", c_i64),
+        ("cache_seqlens", c_vp),
+        ("positions", c_vp),
+        ("cos_sin", c_vp),
+        ("max_pos", c_i64),
+    ]
+
+
 class PoolStatus(ctypes.Structure):
     """Mirror of swl_pool_status (include/swl_runtime.h)."""
     _fields_ = [
@@ -67,6 +93,8 @@ _SIGS = {
     "swl_gemm_bf16": (c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
     "swl_round_bf16": (c_int, [c_int, P_i64, P_vp, P_vp, c_vp, c_vp, c_i64, c_i64, P_i32, c_vp, c_vp, c_int,
                                P_i64, c_vp]),
+    "swl_round_ex_bf16": (c_int, [c_int, P_i64, P_vp, P_vp, c_vp, c_vp, c_i64, c_i64, P_i32, c_vp, c_vp, c_int,
+                                  P_i64, ctypes.POINTER(RoundFusion), c_vp]),
     "swl_matmul_bf16": (c_int, [c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
                                 c_vp]),
     "swl_paged_attention_bf16": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_int, c_int,

@@ -32,7 +32,8 @@
 namespace swl {
 int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
                  const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
-                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st);
+                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
+                 const swl_round_fusion* fz = nullptr);
 }  // namespace swl
 
 using swl::AtomicMask;

@@ -283,6 +283,12 @@ struct SplitArgs {
   float* u;
   int64_t u_split_stride;             // ntok * u_ld
   const bf16* x[kSkinnyMaxTok];
+  // RMSNorm on staging (gamma != null): x = bf16(bf16(h * r) * gamma),
+  // r = rsqrt(sum(ss[tok][0 .. ss_n)) / K + eps)
+  const bf16* gamma;
+  const float* ss;
+  int32_t ss_n, ss_stride;
+  float eps;
   const bf16* g_a[kSkinnyMaxTok];     // stacked lora_A [g_arows][K] of adapter group g
   int32_t g_arows[kSkinnyMaxTok];
   int32_t g_tile0[kSkinnyMaxTok + 1]; // first row tile of group g past W's; [ngroups] = total
@@ -312,6 +318,19 @@ struct EpiArgs {
   int64_t N;
   const bf16* bias;
   int32_t has_lora;
+  // output fusions (swl_round_fusion.out_mode): 1 residual + sums of squares,
+  // 2 SiLU-mul of the gate | up halves, 3 RoPE + KV-page append
+  float* ss_out;
+  int32_t ss_stride;
+  int64_t inter;
+  bf16* kc;
+  bf16* vc;
+  const int32_t* bt;
+  const int32_t* seqlens;
+  const int64_t* pos;
+  const bf16* cs;
+  int64_t max_blocks, num_blocks, max_pos;
+  int32_t hq, hkv, bs;
   bf16* y[kSkinnyMaxTok];
   int32_t lora[kSkinnyMaxTok];
   int32_t urow[kSkinnyMaxTok];
@@ -480,7 +499,7 @@ __device__ __forceinline__ const bf16* tile_rows(const SplitArgs& a, int tile, i
 // group before storing the current tile's partials so the stores and the
 // loads overlap.  No workgroup waits on another.
 template <int TT, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, WAVES >= 16 ? 1 : 16 / WAVES) void split_kernel(SplitArgs a) {
+__global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(SplitArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16 xs[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -504,18 +523,59 @@ __global__ __launch_bounds__(WAVES * 64, WAVES >= 16 ? 1 : 16 / WAVES) void spli
 
   // Stage the activation K-slice in LDS in MFMA B-fragment order: block
   // (step s, token tile t) holds 64 lanes x 16 B, lane l = token 16t + l%16,
-  // k-group l/16, so the k-loop's ds_read_b128 is conflict-free.  Moved with
-  // LDS-DMA loads (global_load_lds_dwordx4), no VGPR round trip.  Token rows
+  // k-group l/16, so the k-loop's ds_read_b128 is conflict-free.  Token rows
   // past ntok load row 0 (their results are never stored); steps past the
   // slice reload its last step (the matching W fragments are zero).
-  for (int i = wv; i < npad * TT; i += WAVES) {
+  const int nblk = npad * TT;
+  auto xsrc = [&](int i) {
     const int st = i / TT, t = i - st * TT;
     const int tk = 16 * t + (lane & 15);
-    const bf16* src = a.x[tk < a.ntok ? tk : 0] + kbeg + 32 * (st < nst ? st : nst - 1) + 8 * (lane >> 4);
-    __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
+    return a.x[tk < a.ntok ? tk : 0] + kbeg + 32 * (st < nst ? st : nst - 1) + 8 * (lane >> 4);
+  };
+  // LDS-DMA loads (global_load_lds_dwordx4), no VGPR round trip
+  for (int i = wv; i < nblk; i += WAVES)
+    __builtin_amdgcn_global_load_lds((gbl_ptr)xsrc(i), (lds_ptr)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
+  // Residual-stream rows are RMS-normalised in place after staging: the
+  // slice of gamma (512 elements per DMA block, clamped to the slice) and
+  // each token row's r = rsqrt(sum of its partial sums of squares / K + eps)
+  // go to LDS past the activation blocks; after the barrier every wave
+  // rescales the blocks it staged: h * r rounded to bf16, times gamma,
+  // rounded again, as LlamaRMSNorm does.
+  char* gs = reinterpret_cast<char*>(xs) + a.ks_steps * TT * 1024;
+  float* rs = reinterpret_cast<float*>(gs + (a.ks_steps * 32 + 511) / 512 * 1024);
+  if (a.gamma) {
+    for (int i = wv; i < (npad * 32 + 511) / 512; i += WAVES) {
+      const int64_t k = min(kbeg + (int64_t)i * 512 + 8 * lane, kbeg + (int64_t)nst * 32 - 8);
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(a.gamma + k), (lds_ptr)(gs + i * 1024), 16, 0, 0);
+    }
+    if (threadIdx.x < 64) {
+      const int tk = threadIdx.x;
+      float r = 0.f;
+      if (tk < a.ntok) {
+        float ss = 0.f;
+        for (int j = 0; j < a.ss_n; ++j) ss += a.ss[(int64_t)tk * a.ss_stride + j];
+        r = rsqrtf(ss / (float)a.K + a.eps);
+      }
+      rs[tk] = r;
+    }
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's LDS-DMA (and W) loads have landed
   __syncthreads();
+  if (a.gamma) {
+    for (int i = wv; i < nblk; i += WAVES) {
+      const int st = i / TT, t = i - st * TT;
+      const float r = rs[16 * t + (lane & 15)];
+      u32x4* px = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(xs) + i * 1024 + 16 * lane);
+      float hv[8], gv[8];
+      unpack8(*px, hv);
+      unpack8(*reinterpret_cast<const u32x4*>(gs + (32 * st + 8 * (lane >> 4)) * 2), gv);
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(f2bf(hv[j] * r)) * gv[j]);
+      *px = __builtin_bit_cast(u32x4, o);
+    }
+    __syncthreads();
+  }
 
   const bf16* xl = xs + 8 * lane;  // block (s, t) at xs + (s * TT + t) * 512 elements
   while (tile < a.n_tiles) {
@@ -563,116 +623,197 @@ __global__ __launch_bounds__(WAVES * 64, WAVES >= 16 ? 1 : 16 / WAVES) void spli
   }
 }
 
-// scale * sum_q u[q] * B[nin][q] for one output column (u: the token's
-// reduced shrink row for block blk, in LDS).
-__device__ __forceinline__ float lora_col(const swl_lora_entry* ep, const float* ub, int blk, int64_t nin) {
-  const int r = ep->rank;
-  const bf16* b0 = reinterpret_cast<const bf16*>(ep->b[blk]) + nin * r;
-  float d = 0.f;
-  for (int q = 0; q < r; ++q) d += ub[q] * bf2f(b0[q]);
-  return d * ep->scale;
-}
-
-// One workgroup per (256 column quads, token): sums the n_ks K-slice
-// partials (loads issued 8 at a time), adds bias and the token's LoRA
-// expand (its shrink row reduced over the u splits once, into LDS; the
-// partial loads are issued first so both latencies overlap), rounds once to
-// bf16 and stores into the token's output row.
+// One workgroup per (64 column quads, token); the four lane groups of a wave
+// (lanes l, l^16, l^32, l^48) share 16 quads.  Each lane group sums every
+// fourth K-slice partial of the quads (all its loads issued at once), the
+// groups fold with shuffles and lane group g keeps column g of each quad.
+// The token's LoRA shrink row is reduced over the K-slices by the whole
+// workgroup into LDS, the lane's row of lora_B having been requested before
+// the reductions; bias and the expand are added and the result is rounded
+// once to bf16.  MODE (swl_round_fusion.out_mode) then decides what is
+// stored: 0 the row (the scatter), 1 the residual update and its sum of
+// squares, 2 SiLU(gate) * up (each lane owns a gate and an up column), 3 the
+// row with RoPE on q and k, k and v also appended to their KV pages.
+template <int MODE>
 __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
+  constexpr int C = MODE == 2 ? 2 : 1;  // column sets per lane (gate, up)
   __shared__ float us[kMaxURow];
+  __shared__ float ured[256];
+  __shared__ float xch[256];
   const int tok = blockIdx.y;
-  const int64_t quads = (a.N + 3) >> 2;
-  const int64_t qi = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const bool live = qi < quads;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int kg = lane >> 4;
+  const int64_t ncols = MODE == 2 ? a.inter : a.N;  // output columns
+  const int64_t nq = (((int64_t)blockIdx.x * 4 + wv) * 16 + (lane & 15)) * 4;  // first column of the quad
+  const int64_t n = nq + kg;                                                   // this lane's column
+  const bool live = n < ncols;
   const int lora = a.has_lora ? a.lora[tok] : -1;
-  const int64_t n = qi * 4;
-  const int64_t kstride = (int64_t)a.ntok * a.N;
-  const float* p = a.part + (int64_t)tok * a.N + n;
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
-    if (n + 3 < a.N && (a.N & 3) == 0) {
-      int ks = 0;
-      for (; ks + 8 <= a.n_ks; ks += 8) {
-        f32x4 q[8];
+  const bool vec = (a.N & 3) == 0 && (MODE != 2 || (a.inter & 3) == 0);
+
+  // lora_B rows of this lane's column(s) (rank <= 16, multiple of 8: registers)
+  const swl_lora_entry* ep = lora >= 0 ? a.L.table + lora : nullptr;
+  int r = 0, blk[C];
+  const bf16* brow[C];
+  u32x4 bq[C][2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) q[j] = *reinterpret_cast<const f32x4*>(p + (ks + j) * kstride);
+  for (int c = 0; c < C; ++c) {
+    blk[c] = 0;
+    brow[c] = nullptr;
+    bq[c][0] = bq[c][1] = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (ep) {
+    r = ep->rank;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          v[0] += q[j][0]; v[1] += q[j][1]; v[2] += q[j][2]; v[3] += q[j][3];
-        }
+    for (int c = 0; c < C; ++c) {
+      const int64_t nc = (live ? n : 0) + c * a.inter;
+      blk[c] = find_blk(a.L, nc);
+      brow[c] = reinterpret_cast<const bf16*>(ep->b[blk[c]]) + (nc - blk_start_of(a.L, blk[c])) * r;
+      if (live && r <= 16 && (r & 7) == 0) {
+        bq[c][0] = ld16(brow[c]);
+        if (r == 16) bq[c][1] = ld16(brow[c] + 8);
       }
-      for (; ks < a.n_ks; ++ks) {
-        const f32x4 q = *reinterpret_cast<const f32x4*>(p + ks * kstride);
-        v[0] += q[0]; v[1] += q[1]; v[2] += q[2]; v[3] += q[3];
-      }
-    } else {
-      for (int ks = 0; ks < a.n_ks; ++ks)
-        for (int j = 0; j < 4; ++j)
-          if (n + j < a.N) v[j] += p[ks * kstride + j];
     }
   }
-  if (lora >= 0) {  // uniform over the workgroup
-    const float* up = a.L.u + (int64_t)a.urow[tok] * a.L.u_ld;
-    for (int q = threadIdx.x; q < a.L.u_ld; q += 256) {
-      float acc = 0.f;
-      int sp = 0;
-      for (; sp + 8 <= a.L.usplit; sp += 8) {
-        float t[8];
+
+  // partial sums of the quad(s) over K-slices kg, kg + 4, ...
+  const int64_t kstride = (int64_t)a.ntok * a.N;
+  f32x4 s[C];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = up[(sp + j) * a.L.u_split_stride + q];
-        acc += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+  for (int c = 0; c < C; ++c) {
+    s[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int64_t qc = nq + c * a.inter;
+    if (nq >= ncols) continue;
+    const float* p = a.part + (int64_t)tok * a.N + qc;
+    for (int ks0 = kg; ks0 < a.n_ks; ks0 += 32) {
+      f32x4 q[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int ks = ks0 + 4 * j;
+        q[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (ks < a.n_ks) {
+          const float* pk = p + ks * kstride;
+          if (vec) {
+            q[j] = *reinterpret_cast<const f32x4*>(pk);
+          } else {
+            for (int e = 0; e < 4; ++e)
+              if (nq + e < ncols) q[j][e] = pk[e];
+          }
+        }
       }
-      for (; sp < a.L.usplit; ++sp) acc += up[sp * a.L.u_split_stride + q];
-      us[q] = acc;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[c] += q[j];
+    }
+  }
+
+  // the token's shrink row, reduced over the K-slices: thread (split sp, row q)
+  if (ep) {  // uniform over the workgroup
+    const int ur = a.L.u_ld, nsp = 256 / ur;
+    const int q = threadIdx.x % ur, sp = threadIdx.x / ur;
+    const float* up = a.L.u + (int64_t)a.urow[tok] * a.L.u_ld + q;
+    if (sp < nsp) {
+      float acc = 0.f;
+      for (int k = sp; k < a.L.usplit; k += nsp) acc += up[k * a.L.u_split_stride];
+      ured[threadIdx.x] = acc;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < ur) {
+      float acc = 0.f;
+      for (int i = 0; i < nsp; ++i) acc += ured[i * ur + threadIdx.x];
+      us[threadIdx.x] = acc;
     }
     __syncthreads();
   }
-  if (!live) return;
-  if (a.bias) {
+
+  // fold the four lane groups; lane group kg keeps component kg; then bias
+  // and the LoRA expand
+  float v[C];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (n + j < a.N) v[j] += bf2f(a.bias[n + j]);
-  }
-  if (lora >= 0) {
-    const swl_lora_entry* ep = a.L.table + lora;
-    const int blk = find_blk(a.L, n);
-    const int64_t bs = blk_start_of(a.L, blk), be = blk_start_of(a.L, blk + 1);
-    const int r = ep->rank;
-    if (n + 3 < a.N && n + 3 < be && (r & 7) == 0) {
-      const bf16* b0 = reinterpret_cast<const bf16*>(ep->b[blk]) + (n - bs) * r;
-      const float* ub = us + blk * r;
-      float d[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int q = 0; q < r; q += 8) {
-        float uq[8];
+  for (int c = 0; c < C; ++c) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) uq[i] = ub[q + i];
+    for (int e = 0; e < 4; ++e) {
+      s[c][e] += __shfl_xor(s[c][e], 16, 64);
+      s[c][e] += __shfl_xor(s[c][e], 32, 64);
+    }
+    v[c] = kg == 0 ? s[c][0] : kg == 1 ? s[c][1] : kg == 2 ? s[c][2] : s[c][3];
+    if (!live) continue;
+    const int64_t nc = n + c * a.inter;
+    if (a.bias) v[c] += bf2f(a.bias[nc]);
+    if (ep) {
+      const float* ub = us + blk[c] * r;
+      float d = 0.f;
+      if (r <= 16 && (r & 7) == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int h = 0; h < 2; ++h) {
+          if (8 * h >= r) break;
           float bv[8];
-          unpack8(ld16(b0 + (int64_t)j * r + q), bv);
+          unpack8(bq[c][h], bv);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) d[j] += uq[i] * bv[i];
+          for (int i = 0; i < 8; ++i) d += ub[8 * h + i] * bv[i];
         }
-      }
+      } else if ((r & 7) == 0) {
+        for (int q = 0; q < r; q += 8) {
+          float bv[8];
+          unpack8(ld16(brow[c] + q), bv);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] += d[j] * ep->scale;
-    } else {
-      for (int j = 0; j < 4; ++j) {
-        if (n + j >= a.N) break;
-        const int bj = find_blk(a.L, n + j);
-        v[j] += lora_col(ep, us + bj * r, bj, n + j - blk_start_of(a.L, bj));
+          for (int i = 0; i < 8; ++i) d += ub[q + i] * bv[i];
+        }
+      } else {
+        for (int q = 0; q < r; ++q) d += ub[q] * bf2f(brow[c][q]);
       }
+      v[c] += d * ep->scale;
     }
   }
+
   bf16* yrow = a.y[tok];
-  if (n + 3 < a.N && ((reinterpret_cast<uintptr_t>(yrow + n) & 7) == 0)) {
-    u32x2 pk;
-    pk[0] = (uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[0])) | ((uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[1])) << 16);
-    pk[1] = (uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[2])) | ((uint32_t)__builtin_bit_cast(uint16_t, f2bf(v[3])) << 16);
-    *reinterpret_cast<u32x2*>(yrow + n) = pk;
+  if constexpr (MODE == 0) {
+    if (live) yrow[n] = f2bf(v[0]);
+  } else if constexpr (MODE == 1) {
+    // h = bf16(h + out); the workgroup's sum of squares of the new h
+    float sq = 0.f;
+    if (live) {
+      const bf16 hn = f2bf(bf2f(yrow[n]) + bf2f(f2bf(v[0])));
+      yrow[n] = hn;
+      sq = bf2f(hn) * bf2f(hn);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if (lane == 0) ured[wv] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      a.ss_out[(int64_t)tok * a.ss_stride + blockIdx.x] = (ured[0] + ured[1]) + (ured[2] + ured[3]);
+  } else if constexpr (MODE == 2) {
+    if (live) {
+      const float g = bf2f(f2bf(v[0])), u = bf2f(f2bf(v[1]));
+      yrow[n] = f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u);
+    }
   } else {
-    for (int j = 0; j < 4; ++j)
-      if (n + j < a.N) yrow[n + j] = f2bf(v[j]);
+    // columns of this workgroup: 2 heads of 128; RoPE pairs (d, d + 64)
+    const int cl = (wv * 16 + (lane & 15)) * 4 + kg;
+    float x = bf2f(f2bf(v[0]));
+    xch[cl] = x;
+    __syncthreads();
+    if (!live) return;
+    const int d = (int)(n & 127);
+    const int hh = (int)(n >> 7);
+    const bool is_q = hh < a.hq, is_k = !is_q && hh < a.hq + a.hkv;
+    if (is_q || is_k) {
+      const int64_t pos = a.pos[tok];
+      if (pos >= 0 && pos < a.max_pos) {
+        const int dd = d & 63;
+        const float c = bf2f(a.cs[pos * 128 + dd]), sn = bf2f(a.cs[pos * 128 + 64 + dd]);
+        const float other = xch[d < 64 ? cl + 64 : cl - 64];
+        x = bf2f(f2bf(d < 64 ? x * c - other * sn : x * c + other * sn));
+      }
+    }
+    yrow[n] = f2bf(x);
+    if (is_q) return;
+    const int64_t p = a.seqlens[tok];
+    const int64_t blk_i = p / a.bs;
+    if (p < 0 || blk_i >= a.max_blocks) return;
+    const int32_t pb = a.bt[(int64_t)tok * a.max_blocks + blk_i];
+    if (pb < 0 || pb >= a.num_blocks) return;
+    const int kvh = is_k ? hh - a.hq : hh - a.hq - a.hkv;
+    (is_k ? a.kc : a.vc)[((int64_t)pb * a.bs + p % a.bs) * a.hkv * 128 + kvh * 128 + d] = f2bf(x);
   }
 }
 
@@ -1636,8 +1777,26 @@ int launch_split_w(int TT, const SplitArgs& a, dim3 grid, size_t lds, hipStream_
 // token's input / output rows (slot buffers).
 int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok, const bf16* const* xrows,
                   bf16* const* yrows, const int32_t* tok_lora, const swl_lora_entry* table,
-                  const swl_lora_entry* host_entries, const LoraEpi* Lblk, int nblk, hipStream_t st) {
+                  const swl_lora_entry* host_entries, const LoraEpi* Lblk, int nblk, const swl_round_fusion* fz,
+                  hipStream_t st) {
   const int TT = (ntok + 15) / 16;
+  const int mode = fz ? fz->out_mode : 0;
+  const int64_t epi_cols = mode == 2 ? N / 2 : N;
+  if (fz) {
+    SWL_CHECK(mode >= 0 && mode <= 3, SWL_ERR_INVALID, "round fusion: out_mode must be 0..3");
+    if (fz->norm_weight)
+      SWL_CHECK(fz->ss_in && fz->ss_in_n >= 1 && fz->ss_in_stride >= fz->ss_in_n, SWL_ERR_INVALID,
+                "round fusion: norm_weight needs ss_in with ss_in_n >= 1 partial sums per row");
+    if (mode == 1)
+      SWL_CHECK(fz->ss_out && fz->ss_out_stride >= (N + 255) / 256, SWL_ERR_INVALID,
+                "round fusion: out_mode 1 needs ss_out with ss_out_stride >= ceil(n / 256)");
+    if (mode == 2) SWL_CHECK(N % 2 == 0, SWL_ERR_INVALID, "round fusion: out_mode 2 needs n = 2 * inter");
+    if (mode == 3)
+      SWL_CHECK(fz->hq > 0 && fz->hkv > 0 && N == (int64_t)(fz->hq + 2 * fz->hkv) * 128 && fz->k_cache &&
+                    fz->v_cache && fz->block_table && fz->cache_seqlens && fz->positions && fz->cos_sin &&
+                    fz->block_size > 0 && fz->max_blocks > 0 && fz->max_pos > 0,
+                SWL_ERR_INVALID, "round fusion: out_mode 3 needs n = (hq + 2 hkv) * 128 and the KV / RoPE arguments");
+  }
   const int64_t total_steps = K / 32;
   SplitArgs a{};
   a.w = w;
@@ -1647,6 +1806,13 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   a.total_steps = (int)total_steps;
   a.n_wtiles = (int)((N + 15) / 16);
   for (int i = 0; i < ntok; ++i) a.x[i] = xrows[i];
+  if (fz && fz->norm_weight) {
+    a.gamma = reinterpret_cast<const bf16*>(fz->norm_weight);
+    a.ss = fz->ss_in;
+    a.ss_n = fz->ss_in_n;
+    a.ss_stride = fz->ss_in_stride;
+    a.eps = fz->eps;
+  }
 
   bool has_lora = false;
   if (tok_lora)
@@ -1673,7 +1839,9 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const int waves = tu.waves;
   a.n_tiles = a.n_wtiles + sp.tiles;
   const int64_t tile_groups = (a.n_tiles + waves - 1) / waves;
-  const int64_t slots = (int64_t)cu_count() * tu.wg_per_cu;
+  // resident workgroups: the kernel keeps 6 waves per SIMD up to 32 token
+  // rows (80 VGPRs), 4 beyond (wider accumulators)
+  const int64_t slots = (int64_t)cu_count() * (TT <= 2 ? tu.wg_per_cu : std::min(tu.wg_per_cu, 16 / waves));
   // K-slices: a power of two (slice starts on aligned byte offsets stream
   // best from HBM), the smallest whose slices hold at most slice_steps
   // k-steps and whose workers fill at least half the resident workgroup
@@ -1705,7 +1873,9 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   a.part = reinterpret_cast<float*>(scratch);
   a.u = has_lora ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + part_al) : nullptr;
 
-  const size_t lds = (size_t)a.ks_steps * TT * 1024;
+  size_t lds = (size_t)a.ks_steps * TT * 1024;
+  if (a.gamma) lds += (size_t)(a.ks_steps * 32 + 511) / 512 * 1024 + 64 * sizeof(float);
+  SWL_CHECK(lds <= 160 * 1024, SWL_ERR_INVALID, "round: staged activation slice exceeds LDS");
   const dim3 grid((unsigned)(a.n_ks * a.n_workers));
   const int tslot = timer_slot(st);
   if (tslot >= 0) {
@@ -1750,9 +1920,32 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     e.L.u_ld = a.u_ld;
     e.L.u_split_stride = a.u_split_stride;
   }
-  const int64_t quads = (N + 3) / 4;
-  launch_maybe_timed(epilogue_kernel, dim3((unsigned)((quads + 255) / 256), (unsigned)ntok), dim3(256), 0, st,
-                     timer_event(tslot, 2), timer_event(tslot, 3), e);
+  if (fz) {
+    e.ss_out = fz->ss_out;
+    e.ss_stride = fz->ss_out_stride;
+    e.inter = N / 2;
+    e.kc = reinterpret_cast<bf16*>(fz->k_cache);
+    e.vc = reinterpret_cast<bf16*>(fz->v_cache);
+    e.bt = fz->block_table;
+    e.seqlens = fz->cache_seqlens;
+    e.pos = fz->positions;
+    e.cs = reinterpret_cast<const bf16*>(fz->cos_sin);
+    e.max_blocks = fz->max_blocks;
+    e.num_blocks = fz->num_blocks;
+    e.max_pos = fz->max_pos;
+    e.hq = fz->hq;
+    e.hkv = fz->hkv;
+    e.bs = fz->block_size;
+  }
+  const int64_t quads = (epi_cols + 3) / 4;
+  const dim3 egrid((unsigned)((quads + 63) / 64), (unsigned)ntok);
+  hipEvent_t te0 = timer_event(tslot, 2), te1 = timer_event(tslot, 3);
+  switch (mode) {
+    case 1: launch_maybe_timed(epilogue_kernel<1>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    case 2: launch_maybe_timed(epilogue_kernel<2>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    case 3: launch_maybe_timed(epilogue_kernel<3>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    default: launch_maybe_timed(epilogue_kernel<0>, egrid, dim3(256), 0, st, te0, te1, e); break;
+  }
   SWL_LAUNCH_CHECK("epilogue_kernel launch");
   return SWL_OK;
 }
@@ -1834,9 +2027,11 @@ int launch_attn_decode_u(const AttnArgs& a, hipStream_t st) {
 }
 
 int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
-  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L), (unsigned)(a.hq + 2 * a.hkv)), dim3(64), 0,
-                     st, a);
-  SWL_LAUNCH_CHECK("rope_append_kernel launch");
+  if (a.rope != 2) {  // 2: q rotated and k / v appended by the QKV round's epilogue
+    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L), (unsigned)(a.hq + 2 * a.hkv)), dim3(64),
+                       0, st, a);
+    SWL_LAUNCH_CHECK("rope_append_kernel launch");
+  }
   if (a.L == 1) {
     switch (G) {
       case 1: return launch_attn_decode_u<1>(a, st);
@@ -1876,7 +2071,8 @@ int hip_fail(hipError_t e, const char* where) {
 // shrink + base kernels for n_seg segments given host-side lora metadata.
 int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
                  const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
-                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st);
+                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
+                 const swl_round_fusion* fz = nullptr);
 }  // namespace swl
 
 extern "C" {
@@ -1936,7 +2132,7 @@ int swl_gemm_bf16(const void* x, const void* w, const void* bias, void* y, int64
       yr[i] = reinterpret_cast<bf16*>(y) + (int64_t)i * n;
     }
     return launch_skinny(reinterpret_cast<const bf16*>(w), reinterpret_cast<const bf16*>(bias), n, k, (int)m, xr, yr,
-                         nullptr, nullptr, nullptr, nullptr, 1, st);
+                         nullptr, nullptr, nullptr, nullptr, 1, nullptr, st);
   }
   SWL_CHECK(k % TK == 0, SWL_ERR_INVALID, "swl_gemm_bf16: k must be a multiple of 64 for m > 64");
   TiledArgs a{};
@@ -1964,6 +2160,18 @@ int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in, vo
   }
   return swl::round_launch(n_seg, rows, seg_in, seg_out, w, bias, n, k, seg_lora, lora_table, lora_table_host, nblk,
                            blk_cols, (hipStream_t)stream);
+}
+
+int swl_round_ex_bf16(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
+                      const void* bias, int64_t n, int64_t k, const int32_t* seg_lora,
+                      const swl_lora_entry* lora_table, const swl_lora_entry* lora_table_host, int nblk,
+                      const int64_t* blk_cols, const swl_round_fusion* fusion, void* stream) {
+  if (seg_lora) {
+    SWL_CHECK(lora_table != nullptr && lora_table_host != nullptr, SWL_ERR_INVALID,
+              "swl_round_ex_bf16: seg_lora needs lora_table and lora_table_host");
+  }
+  return swl::round_launch(n_seg, rows, seg_in, seg_out, w, bias, n, k, seg_lora, lora_table, lora_table_host, nblk,
+                           blk_cols, (hipStream_t)stream, fusion);
 }
 
 int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int trans_b, void* y, int64_t ldy,
@@ -1995,6 +2203,7 @@ int swl_paged_attention_bf16(void* q, void* k, const void* v, int64_t q_stride, 
   SWL_CHECK(nseq >= 0 && q_len >= 1 && q_len <= 1024, SWL_ERR_INVALID, "swl_paged_attention_bf16: bad q_len");
   SWL_CHECK(block_size > 0 && num_blocks > 0 && max_blocks > 0, SWL_ERR_INVALID,
             "swl_paged_attention_bf16: bad page geometry");
+  SWL_CHECK(rope == 0 || rope == 1, SWL_ERR_INVALID, "swl_paged_attention_bf16: rope must be 0 or 1");
   SWL_CHECK(!rope || (cos_sin && positions && max_pos > 0), SWL_ERR_INVALID,
             "swl_paged_attention_bf16: rope needs positions and cos_sin");
   SWL_CHECK(q_stride >= hq * d && k_stride >= hkv * d && v_stride >= hkv * d, SWL_ERR_INVALID,
@@ -2090,7 +2299,8 @@ namespace swl {
 
 int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
                  const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
-                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st) {
+                 const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
+                 const swl_round_fusion* fz) {
   SWL_CHECK(rows && seg_in && seg_out && w, SWL_ERR_INVALID, "round: null argument");
   SWL_CHECK(n_seg >= 1 && n_seg <= kMaxSeg, SWL_ERR_INVALID, "round: segment count must be in [1, 128]");
   SWL_CHECK(N > 0 && K > 0 && K % 32 == 0, SWL_ERR_INVALID, "round: K must be a positive multiple of 32");
@@ -2137,6 +2347,11 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   }
 
   const int u_ld = ((max_r * std::max(nblk, 1) + 15) / 16) * 16;  // A rows padded to 16-row tiles
+  const bool fused = fz && (fz->norm_weight || fz->out_mode != 0);
+  const int64_t out_cols = (fz && fz->out_mode == 2) ? N / 2 : N;
+  if (fz && fz->out_mode == 3)
+    for (int i = 0; i < n_seg; ++i)
+      SWL_CHECK(rows[i] == 1, SWL_ERR_INVALID, "round fusion: out_mode 3 takes one token row per sequence");
 
   if (T <= kSkinnyMaxTok) {
     // ---------------------------------------------------- decode regime
@@ -2147,13 +2362,14 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
     for (int i = 0; i < n_seg; ++i) {
       for (int64_t j = 0; j < rows[i]; ++j, ++t) {
         xr[t] = reinterpret_cast<const bf16*>(seg_in[i]) + j * K;
-        yr[t] = reinterpret_cast<bf16*>(seg_out[i]) + j * N;
+        yr[t] = reinterpret_cast<bf16*>(seg_out[i]) + j * out_cols;
         tl[t] = (has_lora && seg_lora[i] >= 0) ? seg_lora[i] : -1;
       }
     }
     return launch_skinny(reinterpret_cast<const bf16*>(w), reinterpret_cast<const bf16*>(bias), N, K, (int)T, xr, yr,
-                         has_lora ? tl : nullptr, lora_table, host_entries, &L, nblk, st);
+                         has_lora ? tl : nullptr, lora_table, host_entries, &L, nblk, fz, st);
   }
+  SWL_CHECK(!fused, SWL_ERR_INVALID, "round fusion: at most 64 token rows");
 
   // ------------------------------------------------------ prefill regime
   SWL_CHECK(K % TK == 0, SWL_ERR_INVALID, "round: K must be a multiple of 64 for > 64 tokens");
@@ -2354,7 +2570,9 @@ extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const*
             "swl_paged_attention_rows_bf16: at most 64 token rows");
   SWL_CHECK(block_size > 0 && num_blocks > 0 && max_blocks > 0, SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: bad page geometry");
-  SWL_CHECK(!rope || (cos_sin && positions && max_pos > 0), SWL_ERR_INVALID,
+  SWL_CHECK(rope >= 0 && rope <= 2 && (rope != 2 || q_len == 1), SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: rope must be 0, 1 or 2 (2: decode rows only)");
+  SWL_CHECK(rope != 1 || (cos_sin && positions && max_pos > 0), SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: rope needs positions and cos_sin");
   if (nseq == 0) return SWL_OK;
   AttnArgs a{};

@@ -121,7 +121,7 @@ class BatchedDecoder:
     """
 
     def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
-                 first_ids: List[int], device, max_new: int = 64, kv_fill=None):
+                 first_ids: List[int], device, max_new: int = 64, kv_fill=None, fused: bool = True):
         self.shape = s = shape
         self.device = dev = torch.device(device)
         self.W = W = len(ctx_lens)
@@ -132,6 +132,10 @@ class BatchedDecoder:
         self.max_new = max_new
         self.steps_done = 0
         self.graph = None
+        self.fused = fused
+        if fused:
+            self._init_fused(weights, adapters, ctx_lens, first_ids, kv_fill)
+            return
         dev_index = dev.index if dev.index is not None else torch.cuda.current_device()
 
         # ---- slot pool: one slot per worker (1 token per step)
@@ -177,19 +181,7 @@ class BatchedDecoder:
 
         # ---- paged KV: the reference keeps one cache per worker; here one
         # pool of pages with a block table per worker
-        self.kv = PagedKVCache(s.layers, s.kv_heads, s.head_dim, s.block_size, W, max(ctx_lens) + max_new, dev, BF16)
-        for w, c in enumerate(ctx_lens):
-            self.kv.ensure_blocks_for_length(w, c + max_new)
-            self.kv.slot_seq_lens[w] = c
-        self.block_tables = self.kv.get_block_table_tensor(list(range(W)))
-        if kv_fill is not None:
-            for li in range(s.layers):
-                kv_fill(li, self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables)
-        self.seqlens = self.kv.get_seq_lens_tensor(list(range(W)))
-        self.positions = torch.zeros(W, dtype=torch.int64, device=dev)
-        from .worker.paged_attention import RotaryInvFreq, build_vllm_cos_sin_cache
-        self.cos_sin = build_vllm_cos_sin_cache(RotaryInvFreq(s.head_dim, s.theta), self.kv.max_blocks_per_seq *
-                                                s.block_size, dev, BF16)
+        self._init_kv(ctx_lens, kv_fill)
 
         # ---- per-step state
         self.ids = torch.tensor(first_ids, dtype=torch.int64, device=dev).reshape(W, 1)
@@ -207,6 +199,135 @@ class BatchedDecoder:
         self._round_args = ((ctypes.c_int32 * W)(*self.slot_ids), (ctypes.c_int32 * W)(*self.worker_ids),
                             (ctypes.c_int64 * W)(*([1] * W)), (ctypes.c_int32 * W)(*self.adapter_ids))
         self._scale = 1.0 / (s.head_dim ** 0.5)
+
+    def _init_kv(self, ctx_lens, kv_fill):
+        s, dev, W = self.shape, self.device, self.W
+        self.kv = PagedKVCache(s.layers, s.kv_heads, s.head_dim, s.block_size, W, max(ctx_lens) + self.max_new, dev,
+                               BF16)
+        for w, c in enumerate(ctx_lens):
+            self.kv.ensure_blocks_for_length(w, c + self.max_new)
+            self.kv.slot_seq_lens[w] = c
+        self.block_tables = self.kv.get_block_table_tensor(list(range(W)))
+        if kv_fill is not None:
+            for li in range(s.layers):
+                kv_fill(li, self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables)
+        self.seqlens = self.kv.get_seq_lens_tensor(list(range(W)))
+        self.positions = torch.zeros(W, dtype=torch.int64, device=dev)
+        from .worker.paged_attention import RotaryInvFreq, build_vllm_cos_sin_cache
+        self.cos_sin = build_vllm_cos_sin_cache(RotaryInvFreq(s.head_dim, s.theta), self.kv.max_blocks_per_seq *
+                                                s.block_size, dev, BF16)
+
+    def _init_fused(self, weights, adapters, ctx_lens, first_ids, kv_fill):
+        """In-process step over explicit token rows with the round fusions
+        (swl_round_fusion): the input RMSNorm applied while the round stages
+        its activation rows, RoPE and the KV append in the QKV round's
+        epilogue, the residual adds in the O and Down epilogues and SiLU*up in
+        the Gate+Up epilogue."""
+        s, dev, W = self.shape, self.device, self.W
+        self.layers_w = []
+        self.norms = []
+        for lw in weights["layers"]:
+            t = {k: v.to(dev) for k, v in lw.items()}
+            self.layers_w.append({
+                "qkv": torch.cat([t["q"], t["k"], t["v"]], 0).contiguous(),
+                "o": t["o"].contiguous(),
+                "gu": torch.cat([t["gate"], t["up"]], 0).contiguous(),
+                "down": t["down"].contiguous(),
+            })
+            self.norms.append((t["input_norm"].contiguous(), t["post_norm"].contiguous()))
+            del t
+        self.embed = weights["embed"].to(dev).contiguous()
+        self.lm_head = weights["lm_head"].to(dev).contiguous()
+        self.final_norm = weights["final_norm"].to(dev).contiguous()
+
+        # adapters: one table entry per (worker, layer, fused projection)
+        self.table = ops.LoraTable(dev)
+        groups = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")), ("down", ("down",)))
+        self.seg_lora = [{g: [-1] * W for g, _ in groups} for _ in range(s.layers)]
+        for w, ad in enumerate(adapters):
+            if ad is None:
+                continue
+            for li in range(s.layers):
+                for g, projs in groups:
+                    A = torch.cat([ad[li][p][0].to(dev) for p in projs], 0).contiguous()
+                    Bs = [ad[li][p][1].to(dev).contiguous() for p in projs]
+                    self.seg_lora[li][g][w] = self.table.add(A, Bs, s.rank, s.scale)
+        has_lora = any(ad is not None for ad in adapters)
+        blk = {"qkv": [s.hidden, s.kv_heads * s.head_dim, s.kv_heads * s.head_dim], "o": [s.hidden],
+               "gu": [s.inter, s.inter], "down": [s.hidden]}
+
+        self._init_kv(ctx_lens, kv_fill)
+
+        # per-step buffers: one row per worker
+        nss = (s.hidden + 255) // 256
+        self.ids = torch.tensor(first_ids, dtype=torch.int64, device=dev).reshape(W, 1)
+        self.h = torch.zeros(W, s.hidden, dtype=BF16, device=dev)        # residual stream
+        self.x0 = torch.zeros(W, s.hidden, dtype=BF16, device=dev)       # layer 0's normed input
+        self.qkv = torch.zeros(W, s.qkv, dtype=BF16, device=dev)
+        self.attn = torch.zeros(W, s.heads * s.head_dim, dtype=BF16, device=dev)
+        self.act = torch.zeros(W, s.inter, dtype=BF16, device=dev)
+        self.logits = torch.zeros(W, s.vocab, dtype=BF16, device=dev)
+        self.ss_o = torch.zeros(W, nss, dtype=torch.float32, device=dev)
+        self.ss_d = torch.zeros(W, nss, dtype=torch.float32, device=dev)
+        rows = lambda t: [t[w:w + 1] for w in range(W)]  # noqa: E731
+        self.rows_x0 = ops.RowSet([self.x0[w] for w in range(W)], s.hidden)
+        self.rows_qkv = ops.RowSet([self.qkv[w] for w in range(W)], s.qkv)
+        self.rows_attn = ops.RowSet([self.attn[w] for w in range(W)], s.heads * s.head_dim)
+        self._ids_rows = [self.ids[w] for w in range(W)]
+        self._h_rows = rows(self.h)
+
+        # the 4 rounds of every layer and the LM head, arguments built once
+        one = [1] * W
+        self._calls = []
+        for li in range(s.layers):
+            lw, (in_norm, post_norm) = self.layers_w[li], self.norms[li]
+            kv = dict(k_cache=self.kv.key_caches[li], v_cache=self.kv.value_caches[li], hq=s.heads, hkv=s.kv_heads,
+                      block_table=self.block_tables, cache_seqlens=self.seqlens, positions=self.positions,
+                      cos_sin=self.cos_sin)
+            plan = (
+                ("qkv", rows(self.x0) if li == 0 else rows(self.h), rows(self.qkv),
+                 ops.round_fusion(out_mode=3, **kv) if li == 0 else
+                 ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, out_mode=3, **kv)),
+                ("o", rows(self.attn), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_o)),
+                ("gu", rows(self.h), rows(self.act),
+                 ops.round_fusion(norm_weight=post_norm, eps=s.eps, ss_in=self.ss_o, out_mode=2)),
+                ("down", rows(self.act), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_d)),
+            )
+            layer_calls = []
+            for g, xin, yout, fz in plan:
+                args = ops._round_args(xin, yout, one, lw[g], None, self.seg_lora[li][g] if has_lora else None,
+                                       self.table if has_lora else None, blk[g] if has_lora else None,
+                                       out_div=2 if fz.out_mode == 2 else 1)
+                layer_calls.append((args, fz))
+            self._calls.append(layer_calls)
+        lm_fz = ops.round_fusion(norm_weight=self.final_norm, eps=s.eps, ss_in=self.ss_d)
+        self._lm_call = (ops._round_args(rows(self.h), rows(self.logits), one, self.lm_head, None, None, None, None),
+                         lm_fz)
+        self._scale = 1.0 / (s.head_dim ** 0.5)
+
+    def _round_ex(self, call):
+        args, fz = call
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(_lib.load().swl_round_ex_bf16(*args, ctypes.byref(fz), st))
+
+    def _body_fused(self):
+        s = self.shape
+        self.positions.copy_(self.seqlens)
+        ops.embed(self._ids_rows, self.embed, self._h_rows)
+        ops.rmsnorm_rows(self.h, self.norms[0][0], s.eps, self.rows_x0)
+        for li in range(s.layers):
+            qkv, o, gu, down = self._calls[li]
+            self._round_ex(qkv)
+            ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
+                                     self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
+                                     self.seqlens, None, None, self._scale, rope=2)
+            self._round_ex(o)
+            self._round_ex(gu)
+            self._round_ex(down)
+        self._round_ex(self._lm_call)
+        W = self.W
+        ops.sample(self.logits, self._ids_rows, [False] * W, [1.0] * W, [0] * W, [1.0] * W, 0)
+        self.seqlens.add_(1)
 
     # ------------------------------------------------------------ one step
     def _round(self, op: int, layer: int):
@@ -240,10 +361,16 @@ class BatchedDecoder:
         if self.steps_done >= self.max_new:
             raise RuntimeError(f"BatchedDecoder: KV pages reserved for {self.max_new} new tokens are used up")
 
+    def _step_body(self):
+        if self.fused:
+            self._body_fused()
+        else:
+            self._body()
+
     def step_eager(self):
         """Launch one step's kernels on the current stream."""
         self._check_capacity()
-        self._body()
+        self._step_body()
         self.steps_done += 1
 
     def capture(self):
@@ -254,7 +381,7 @@ class BatchedDecoder:
         # the captured body is not executed; the graph is replayed by step()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._body()
+            self._step_body()
         self.graph = g
 
     def step(self):
@@ -267,6 +394,8 @@ class BatchedDecoder:
 
     def close(self):
         self.graph = None
+        if self.fused:
+            return
         for sid, wid in zip(self.slot_ids, self.worker_ids):
             agg.release_slot(sid, wid)
         agg.clear_adapters()

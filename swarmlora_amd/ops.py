@@ -162,11 +162,7 @@ class LoraTable:
         return len(self._entries)
 
 
-def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], rows: Sequence[int],
-                w: torch.Tensor, bias: Optional[torch.Tensor] = None,
-                seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
-                blk_cols: Optional[Sequence[int]] = None):
-    """One gather -> GEMM -> (+LoRA) -> scatter round over slot buffers."""
+def _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols, out_div=1):
     _need(w, "w")
     n, k = w.shape
     if len(seg_in) != len(rows) or len(seg_out) != len(rows):
@@ -174,7 +170,7 @@ def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor],
     for i in range(len(rows)):
         _need(seg_in[i], f"seg_in[{i}]")
         _need(seg_out[i], f"seg_out[{i}]")
-        if seg_in[i].numel() < rows[i] * k or seg_out[i].numel() < rows[i] * n:
+        if seg_in[i].numel() < rows[i] * k or seg_out[i].numel() < rows[i] * (n // out_div):
             raise ValueError(f"segment {i} buffers are smaller than rows * dim")
         if not (seg_in[i].is_contiguous() and seg_out[i].is_contiguous()):
             raise ValueError("segment buffers must be contiguous")
@@ -195,9 +191,82 @@ def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor],
         host_tab = ctypes.cast(table.host_table(), ctypes.c_void_p)
         blk = _i64_array(blk_cols)
         nblk = len(blk_cols)
-    _lib.check(_lib.load().swl_round_bf16(len(rows), _i64_array(rows), _ptr_array(seg_in), _ptr_array(seg_out),
-                                          _ptr(w), _ptr(bias), n, k, lora_arr, tab_ptr, host_tab, nblk, blk,
-                                          _stream()))
+    return (len(rows), _i64_array(rows), _ptr_array(seg_in), _ptr_array(seg_out), _ptr(w), _ptr(bias), n, k,
+            lora_arr, tab_ptr, host_tab, nblk, blk)
+
+
+def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], rows: Sequence[int],
+                w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
+                blk_cols: Optional[Sequence[int]] = None):
+    """One gather -> GEMM -> (+LoRA) -> scatter round over slot buffers."""
+    args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols)
+    _lib.check(_lib.load().swl_round_bf16(*args, _stream()))
+
+
+RoundFusion = _lib.RoundFusion
+
+
+def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
+                 ss_in: Optional[torch.Tensor] = None, out_mode: int = 0, ss_out: Optional[torch.Tensor] = None,
+                 k_cache: Optional[torch.Tensor] = None, v_cache: Optional[torch.Tensor] = None, hq: int = 0,
+                 hkv: int = 0, block_table: Optional[torch.Tensor] = None,
+                 cache_seqlens: Optional[torch.Tensor] = None, positions: Optional[torch.Tensor] = None,
+                 cos_sin: Optional[torch.Tensor] = None) -> RoundFusion:
+    """swl_round_fusion for round_ex (include/swl.h documents each mode).
+    ss_in / ss_out: fp32 [ntok, n_partial] (n_partial = ceil(n / 256) of the
+    producing round); the record keeps the tensors it points to alive."""
+    f = RoundFusion()
+    keep = []
+    if norm_weight is not None:
+        _need(norm_weight, "norm_weight")
+        _need(ss_in, "ss_in", torch.float32)
+        if ss_in.dim() != 2 or ss_in.stride(1) != 1:
+            raise ValueError("ss_in must be [ntok, n_partial] with unit column stride")
+        f.norm_weight, f.eps = norm_weight.data_ptr(), float(eps)
+        f.ss_in, f.ss_in_n, f.ss_in_stride = ss_in.data_ptr(), ss_in.shape[1], ss_in.stride(0)
+        keep += [norm_weight, ss_in]
+    if out_mode not in (0, 1, 2, 3):
+        raise ValueError("out_mode must be 0..3")
+    f.out_mode = out_mode
+    if out_mode == 1:
+        _need(ss_out, "ss_out", torch.float32)
+        if ss_out.dim() != 2 or ss_out.stride(1) != 1:
+            raise ValueError("ss_out must be [ntok, n_partial] with unit column stride")
+        f.ss_out, f.ss_out_stride = ss_out.data_ptr(), ss_out.stride(0)
+        keep.append(ss_out)
+    if out_mode == 3:
+        for t, nm in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+            _need(t, nm)
+            if not t.is_contiguous() or t.dim() != 4 or t.shape[2] != hkv or t.shape[3] != 128:
+                raise ValueError(f"{nm} must be contiguous [num_blocks, block_size, hkv, 128]")
+        _need(block_table, "block_table", torch.int32)
+        _need(cache_seqlens, "cache_seqlens", torch.int32)
+        _need(positions, "positions", torch.int64)
+        _need(cos_sin, "cos_sin")
+        if block_table.dim() != 2 or not block_table.is_contiguous():
+            raise ValueError("block_table must be contiguous [nseq, max_blocks]")
+        if cos_sin.dim() != 2 or cos_sin.shape[1] != 128 or not cos_sin.is_contiguous():
+            raise ValueError("cos_sin must be contiguous [max_pos, 128]")
+        f.k_cache, f.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+        f.hq, f.hkv, f.block_size = hq, hkv, k_cache.shape[1]
+        f.block_table, f.max_blocks, f.num_blocks = block_table.data_ptr(), block_table.shape[1], k_cache.shape[0]
+        f.cache_seqlens, f.positions = cache_seqlens.data_ptr(), positions.data_ptr()
+        f.cos_sin, f.max_pos = cos_sin.data_ptr(), cos_sin.shape[0]
+        keep += [k_cache, v_cache, block_table, cache_seqlens, positions, cos_sin]
+    f._keep = keep
+    return f
+
+
+def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], rows: Sequence[int],
+             w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+             seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
+             blk_cols: Optional[Sequence[int]] = None, fusion: Optional[RoundFusion] = None):
+    """round_fused with the decode-step fusions of `fusion` (round_fusion())."""
+    args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols,
+                       out_div=2 if fusion is not None and fusion.out_mode == 2 else 1)
+    _lib.check(_lib.load().swl_round_ex_bf16(*args, ctypes.byref(fusion) if fusion is not None else None,
+                                             _stream()))
 
 
 def matmul(x: torch.Tensor, b: torch.Tensor, trans_b: bool, alpha: float = 1.0,
@@ -390,10 +459,12 @@ def silu_mul_rows(in_rows, out_rows, inter: int):
 def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: int, k_cache: torch.Tensor,
                          v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
                          positions: Optional[torch.Tensor], cos_sin: Optional[torch.Tensor], softmax_scale: float,
-                         rope: bool = True):
+                         rope=True):
     """paged_attention over per-token rows: token t = seq * q_len + i has
     its fused [q | k | v] row at qkv_rows[t] (rotated in place) and gets its
-    [hq * d] output at out_rows[t]."""
+    [hq * d] output at out_rows[t].  rope=2: q already rotated and k / v
+    already appended by an out_mode 3 round (decode rows only)."""
+    rope = 2 if rope == 2 else (1 if rope else 0)
     qkv = _rowset(qkv_rows, (hq + 2 * hkv) * d)
     out = _rowset(out_rows, hq * d)
     if len(qkv) != len(out) or len(qkv) % q_len:
@@ -413,7 +484,7 @@ def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: i
     if cache_seqlens.numel() < nseq:
         raise ValueError("cache_seqlens must have nseq entries")
     max_pos = 0
-    if rope:
+    if rope == 1:
         _need(positions, "positions", torch.int64)
         _need(cos_sin, "cos_sin")
         if positions.numel() != nseq * q_len:
@@ -423,8 +494,8 @@ def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: i
         max_pos = cos_sin.shape[0]
     _lib.check(_lib.load().swl_paged_attention_rows_bf16(
         qkv.array, out.array, nseq, q_len, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs, _ptr(block_table),
-        block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope else None),
-        _ptr(cos_sin if rope else None), max_pos, 1 if rope else 0, float(softmax_scale), _stream()))
+        block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope == 1 else None),
+        _ptr(cos_sin if rope == 1 else None), max_pos, rope, float(softmax_scale), _stream()))
 
 
 # -------------------------------------------------------------- timing ---

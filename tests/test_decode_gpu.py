@@ -4,7 +4,10 @@ CPU oracle's decode_step, teacher-forced with the tokens the GPU chose.
 Small Llama-shaped model (tests/_tiny_model.py: hidden 512, GQA 4/2 heads of
 128, 2 layers), five workers with different KV context lengths (one with no
 history, one without an adapter), random KV pages.  Eager steps, then steps
-replayed from a captured HIP graph.
+replayed from a captured HIP graph.  Both step forms: the one over the
+aggregator's slot pool with separate worker-side kernels, and the fused one
+(RMSNorm on the rounds' staging, RoPE + KV append / residual adds / SiLU*up in
+the round epilogues).
 """
 
 import pytest
@@ -19,7 +22,7 @@ CTX = [0, 3, 17, 40, 100]
 TOL = 1e-2  # normalised max error of the final hidden state and the logits
 
 
-def _setup(dev):
+def _setup(dev, fused):
     from swarmlora_amd.decode import BatchedDecoder, DecodeShape
     from tests._tiny_model import CFG as c, adapter, base_weights
     shape = DecodeShape(layers=c.layers, hidden=c.hidden, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
@@ -45,7 +48,7 @@ def _setup(dev):
         vc.copy_(v)
 
     first = [5, 77, 300, 639, 0]
-    dec = BatchedDecoder(shape, wts, ads, CTX, first, dev, max_new=8, kv_fill=kv_fill)
+    dec = BatchedDecoder(shape, wts, ads, CTX, first, dev, max_new=8, kv_fill=kv_fill, fused=fused)
     kc = [pages[li][0] for li in range(c.layers)]
     vc = [pages[li][1] for li in range(c.layers)]
     return dec, shape, wts, ads, kc, vc
@@ -58,7 +61,10 @@ def _check_step(dec, shape, wts, ads, kc, vc, cs, bt, step):
     dec.step()
     torch.cuda.synchronize()
     hn, lg = ref.decode_step(shape, wts, ads, kc, vc, bt, seq, ids, cs)
-    got_h = dec.lm_in.cpu()
+    if dec.fused:  # the final norm runs inside the LM-head round: check the residual stream through it
+        got_h = ref.rms_norm(dec.h.cpu(), wts["final_norm"], shape.eps)
+    else:
+        got_h = dec.lm_in.cpu()
     got_l = dec.logits.cpu()
     assert rel_err(got_h, hn) <= TOL, f"step {step}: final hidden"
     assert rel_err(got_l, lg) <= TOL, f"step {step}: logits"
@@ -70,8 +76,9 @@ def _check_step(dec, shape, wts, ads, kc, vc, cs, bt, step):
     assert dec.seqlens.cpu().tolist() == (seq + 1).tolist()
 
 
-def test_decode_steps_eager_then_graph(dev):
-    dec, shape, wts, ads, kc, vc = _setup(dev)
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_steps_eager_then_graph(dev, fused):
+    dec, shape, wts, ads, kc, vc = _setup(dev, fused)
     try:
         cs = ref.cos_sin_cache(ref.rope_inv_freq(shape.head_dim, shape.theta), dec.cos_sin.shape[0])
         bt = dec.block_tables.cpu()
@@ -89,8 +96,9 @@ def test_decode_steps_eager_then_graph(dev):
         dec.close()
 
 
-def test_decode_capacity_is_enforced(dev):
-    dec, *_ = _setup(dev)
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_capacity_is_enforced(dev, fused):
+    dec, *_ = _setup(dev, fused)
     try:
         dec.max_new = 1
         dec.step()
