@@ -997,6 +997,7 @@ struct AttnArgs {
   bf16* out;             // [nseq, L, hq*128]
   int64_t num_blocks, max_blocks, max_pos;
   int32_t nseq, L, hq, hkv, bs, rope;
+  int32_t bs_shift;      // log2(bs) when bs is a power of two, else -1
   float scale;
   // row mode (rowmode != 0): token t reads its fused [q | k | v] row at
   // qkv_row[t] and writes its output row at out_row[t]
@@ -1163,10 +1164,17 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 constexpr int kAttnRec = 130;  // floats per (chunk, head): max, sum, 128 dims
 
 __device__ __forceinline__ int64_t key_offset(const AttnArgs& a, const int32_t* bt, int64_t key, int h) {
-  const int64_t bi = key / a.bs;
+  int64_t bi, in;
+  if (a.bs_shift >= 0) {
+    bi = key >> a.bs_shift;
+    in = key & (a.bs - 1);
+  } else {
+    bi = key / a.bs;
+    in = key - bi * a.bs;
+  }
   int32_t blk = (bi < a.max_blocks) ? bt[bi] : 0;
   blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;
-  return ((int64_t)blk * a.bs + key % a.bs) * a.hkv * 128 + h * 128;
+  return ((int64_t)blk * a.bs + in) * a.hkv * 128 + h * 128;
 }
 
 template <int G, int WAVES, int U>
@@ -2235,6 +2243,7 @@ int swl_paged_attention_bf16(void* q, void* k, const void* v, int64_t q_stride, 
   a.hq = hq;
   a.hkv = hkv;
   a.bs = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.rope = rope;
   a.scale = softmax_scale;
   return launch_attention(a, G, (hipStream_t)stream);
@@ -2597,6 +2606,7 @@ extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const*
   a.hq = hq;
   a.hkv = hkv;
   a.bs = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.rope = rope;
   a.scale = softmax_scale;
   return launch_attention(a, G, (hipStream_t)stream);
