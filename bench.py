@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, copy a buffer of this many MiB (a kernel of known HBM traffic for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+                    help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
+                         "rounds on the MFMA path, a line of its own")
     return ap.parse_args()
 
 
@@ -113,6 +116,86 @@ def cpu_baseline(workers, budget_s):
                        f"CPU-seeded weights of the same shapes")}
 
 
+def prefill(args):
+    """one 8B-shaped layer's four rounds (QKV, O,
+    Gate+Up, Down) over 16 slots, half of them one token, the rest
+    U{32..512} tokens (seeded), each slot with its own adapter of rank drawn
+    from {8, 16, 32, 64}; > 64 token rows, so the rounds take the packed
+    MFMA path (gather, LoRA shrink, tiled_kernel with the expand in its
+    epilogue, scatter).  `value` is the base-GEMM TFLOP/s of the four rounds
+    (2*T*N*K each) over their measured time; `roofline` is bf16 MFMA."""
+    import torch
+    from swarmlora_amd import ops
+    dev = torch.device("cuda:0")
+    H, KV, HD, I = 4096, 8, 128, 14336
+    g = torch.Generator().manual_seed(3)
+    rows = [1] * 8 + torch.randint(32, 513, (8,), generator=g).tolist()
+    ranks = [[8, 16, 32, 64][int(i)] for i in torch.randint(0, 4, (16,), generator=g)]
+    T = sum(rows)
+    gd = torch.Generator(device=dev).manual_seed(0)
+
+    def rn(*shape, std=0.02):
+        return torch.randn(*shape, generator=gd, device=dev, dtype=torch.bfloat16) * std
+
+    rounds = [("qkv", H, [H, KV * HD, KV * HD]), ("o", H, [H]), ("gate_up", H, [I, I]), ("down", I, [H])]
+    plan = []
+    for nm, k, dims in rounds:
+        n = sum(dims)
+        table = ops.LoraTable(dev)
+        for i, r in enumerate(ranks):
+            table.add(rn(r * len(dims), k).contiguous(), [rn(d, r).contiguous() for d in dims], r, 2.0)
+        xs = [rn(t, k, std=1.0) for t in rows]
+        ys = [torch.empty(t, n, dtype=torch.bfloat16, device=dev) for t in rows]
+        plan.append((nm, n, k, dims, rn(n, k), table, xs, ys))
+
+    def run(p):
+        nm, n, k, dims, w, table, xs, ys = p
+        ops.round_fused(xs, ys, rows, w, None, seg_lora=list(range(len(rows))), table=table, blk_cols=dims)
+
+    for p in plan:
+        for _ in range(3):
+            run(p)
+    torch.cuda.synchronize()
+    per = {}
+    flops = 0
+    tot_ms = 0.0
+    for p in plan:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            run(p)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        f = 2.0 * T * p[1] * p[2]
+        per[p[0]] = {"ms": round(ms, 4), "TFLOPs": round(f / (ms * 1e-3) / 1e12, 1)}
+        flops += f
+        tot_ms += ms
+    tflops = flops / (tot_ms * 1e-3) / 1e12
+    line = {
+        "metric": "prefill-shape round TFLOP/s (BASELINE config 3)",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": 3,
+        "ms_per_step": round(tot_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights, adapters and activations)",
+        "config": {"workload": "config3: one 8B-shaped layer's QKV, O, Gate+Up and Down rounds over 16 ragged "
+                               "slots (8 x 1 token, 8 x U{32..512}), per-slot adapter rank in {8,16,32,64}",
+                   "token_rows": T, "slot_rows": rows, "ranks": ranks, "rounds": per},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "kernel": "round (gather + shrink + tiled_kernel + scatter), base-GEMM flops"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -125,6 +208,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.workload == "prefill":
+        return prefill(args)
     from swarmlora_amd import ops
     from swarmlora_amd.decode import BatchedDecoder, DecodeShape, synthetic_adapter, synthetic_weights
 

@@ -295,21 +295,18 @@ struct SplitArgs {
   int8_t tok_grp[kSkinnyMaxTok];      // adapter group of each token, -1 for none
 };
 
-// LoRA shrink alone (prefill path): one wave per (16-row tile of stacked A,
-// K-slice), B-fragments of up to 64 packed token rows read from global memory.
-struct ShrinkArgs {
-  int64_t K;
-  int32_t total_steps;
-  int32_t n_items, u_ks, u_ld;
-  int64_t u_split_stride;
-  float* u;
-  int32_t ngroups;
-  const bf16* g_a[kSkinnyMaxTok];
-  int32_t g_arows[kSkinnyMaxTok];
-  int32_t g_tile0[kSkinnyMaxTok + 1];
-  int32_t g_tok0[kSkinnyMaxTok + 1];
-  int32_t g_tok[kSkinnyMaxTok];
-  const bf16* g_x[kSkinnyMaxTok];
+// LoRA shrink of the packed prefill batch: u[ks][row][q] = x[row] . A[q]
+// over K-slice ks, for every segment with an adapter.  Work items are
+// (64-row tile of the segment, 64-row block of its stacked A) pairs, item0 is
+// their prefix over the segments.
+struct ShrinkGemmArgs {
+  const bf16* x;          // packed [T, K]
+  float* u;               // [n_ks][T][u_ld]
+  int64_t K, u_split_stride;
+  int32_t n_seg, n_ks, u_ld, total_steps;
+  int32_t item0[kMaxSeg + 1];
+  int32_t row0[kMaxSeg], rows[kMaxSeg], arows[kMaxSeg];
+  const bf16* a[kMaxSeg];
 };
 
 struct EpiArgs {
@@ -382,92 +379,71 @@ __device__ __forceinline__ void kloop_lds(f32x4 (&acc)[TT], u32x4 (&w)[D], const
   }
 }
 
-// Same pipeline with B-fragments loaded from global memory (LoRA shrink: a
-// handful of tokens per adapter, so the activation traffic is small).
-template <int TT, int D>
-__device__ __forceinline__ void kloop_global(f32x4 (&acc)[TT], const bf16* wp, const bf16* const (&xp)[TT],
-                                             int nsteps) {
-  const int niter = nsteps / D;
-  if (niter > 0) {
-    u32x4 w[D], x[D][TT];
+// One workgroup per (item, K-slice): 4 waves, each 16 token rows x the 64
+// A rows of the item's block (4 MFMA tiles, A rows as the A-operand so the
+// fp32 results land as 4 consecutive q per lane), 4 k-steps of loads in
+// flight; A is shared by the 4 waves through the L1.
+__global__ __launch_bounds__(256) void shrink_gemm_kernel(ShrinkGemmArgs a) {
+  constexpr int D = 4;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int ks = blockIdx.x % a.n_ks, item = blockIdx.x / a.n_ks;
+  int lo = 0, hi = a.n_seg - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a.item0[mid] <= item) lo = mid; else hi = mid - 1;
+  }
+  const int s = lo;
+  const int nab = (a.arows[s] + 63) / 64;
+  const int li = item - a.item0[s];
+  const int rt = li / nab, ab = li - rt * nab;
+  const int st0 = (int)((int64_t)a.total_steps * ks / a.n_ks);
+  const int st1 = (int)((int64_t)a.total_steps * (ks + 1) / a.n_ks);
+  const int nst = st1 - st0;
+  const int64_t kbeg = (int64_t)st0 * 32 + 8 * (lane >> 4);
+  const int tr = rt * 64 + wv * 16 + (lane & 15);  // token row of this lane within the segment
+  const bf16* xp = a.x + (int64_t)(a.row0[s] + min(tr, a.rows[s] - 1)) * a.K + kbeg;
+  const bf16* ap[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = ab * 64 + 16 * j + (lane & 15);
+    ap[j] = a.a[s] + (int64_t)min(q, a.arows[s] - 1) * a.K + kbeg;
+  }
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < nst; i += D) {
+    u32x4 xv[D], av[D][4];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      w[d] = ld16(wp + 32 * d);
+      const int st = 32 * (i + d < nst ? i + d : nst - 1);
+      xv[d] = ldg16(xp + st);
 #pragma unroll
-      for (int t = 0; t < TT; ++t) x[d][t] = ld16(xp[t] + 32 * d);
-    }
-    for (int it = 0; it + 1 < niter; ++it) {
-      const int nxt = (it + 1) * D;
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-#pragma unroll
-        for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], x[d][t], acc[t]);
-        w[d] = ld16(wp + 32 * (nxt + d));
-#pragma unroll
-        for (int t = 0; t < TT; ++t) x[d][t] = ld16(xp[t] + 32 * (nxt + d));
-      }
+      for (int j = 0; j < 4; ++j) av[d][j] = ldg16(ap[j] + st);
     }
 #pragma unroll
-    for (int d = 0; d < D; ++d)
+    for (int d = 0; d < D; ++d) {
+      if (i + d >= nst) break;
 #pragma unroll
-      for (int t = 0; t < TT; ++t) acc[t] = mfma16(w[d], x[d][t], acc[t]);
+      for (int j = 0; j < 4; ++j) acc[j] = mfma16(av[d][j], xv[d], acc[j]);
+    }
   }
-  for (int s = niter * D; s < nsteps; ++s) {
-    const u32x4 w1 = ld16(wp + 32 * s);
+  if (tr >= a.rows[s]) return;
+  float* urow = a.u + ks * a.u_split_stride + (int64_t)(a.row0[s] + tr) * a.u_ld;
 #pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = mfma16(w1, ld16(xp[t] + 32 * s), acc[t]);
+  for (int j = 0; j < 4; ++j) {
+    const int q0 = ab * 64 + 16 * j + 4 * (lane >> 4);
+    if (q0 < a.u_ld) *reinterpret_cast<f32x4*>(urow + q0) = acc[j];
   }
 }
 
-template <int TT>
-__device__ __forceinline__ void shrink_item(const ShrinkArgs& a, int item, int lane) {
-  const int tile = item / a.u_ks;
-  const int uks = item - tile * a.u_ks;
-  int g = 0;
-  while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
-  const int rt = tile - a.g_tile0[g];
-  const int arow = min(rt * 16 + (lane & 15), a.g_arows[g] - 1);
-  const int st0 = (int)((int64_t)a.total_steps * uks / a.u_ks);
-  const int st1 = (int)((int64_t)a.total_steps * (uks + 1) / a.u_ks);
-  const int64_t koff = (int64_t)st0 * 32 + 8 * (lane >> 4);
-  const bf16* wp = a.g_a[g] + (int64_t)arow * a.K + koff;
-  const int t0 = a.g_tok0[g], cnt = a.g_tok0[g + 1] - t0;
-  const bf16* xp[TT];
-#pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    const int i = min(16 * t + (lane & 15), cnt - 1);
-    xp[t] = a.g_x[t0 + i] + koff;
-  }
-  f32x4 acc[TT];
-#pragma unroll
-  for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  kloop_global<TT, (TT >= 4 ? 2 : 4)>(acc, wp, xp, st1 - st0);
-  const int q = rt * 16 + 4 * (lane >> 4);
-#pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    const int i = 16 * t + (lane & 15);
-    if (i < cnt) {
-      float* dst = a.u + uks * a.u_split_stride + (int64_t)a.g_tok[t0 + i] * a.u_ld + q;
-      *reinterpret_cast<f32x4*>(dst) = acc[t];
-    }
-  }
-}
-
-// Independent wave items, no workgroup barrier.
-__global__ __launch_bounds__(512) void shrink_kernel(ShrinkArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 8 + (threadIdx.x >> 6);
-  if (item >= a.n_items) return;
-  int cnt_max = 0;
-  {
-    const int tile = item / a.u_ks;
-    int g = 0;
-    while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= tile) ++g;
-    cnt_max = a.g_tok0[g + 1] - a.g_tok0[g];
-  }
-  if (cnt_max <= 16) shrink_item<1>(a, item, lane);
-  else if (cnt_max <= 32) shrink_item<2>(a, item, lane);
-  else shrink_item<4>(a, item, lane);
+// u[0] += u[1] + ... + u[n_ks - 1] over [nvec] float4 (the shrink partials
+// folded once, so the tiled epilogue's expand reads a single split).
+__global__ __launch_bounds__(256) void u_fold_kernel(float* u, int64_t split_stride, int n_ks, int64_t nvec) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nvec) return;
+  f32x4 s = reinterpret_cast<const f32x4*>(u)[i];
+  for (int k = 1; k < n_ks; ++k) s += reinterpret_cast<const f32x4*>(u + k * split_stride)[i];
+  reinterpret_cast<f32x4*>(u)[i] = s;
 }
 
 // Row pointer (this lane's row, at the K-slice start) of row tile `tile`: a
@@ -1729,8 +1705,6 @@ struct ShrinkPlan {
   int32_t g_entry[kSkinnyMaxTok];
   int32_t g_arows[kSkinnyMaxTok];
   int32_t g_tile0[kSkinnyMaxTok + 1];
-  int32_t g_tok0[kSkinnyMaxTok + 1];
-  int32_t g_tok[kSkinnyMaxTok];       // token index (in input order) of each grouped token
   int8_t tok_grp[kSkinnyMaxTok];      // group of each token, -1 for none
 };
 
@@ -1739,7 +1713,6 @@ struct ShrinkPlan {
 void plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const swl_lora_entry* host_entries, int nblk) {
   p.ngroups = 0;
   p.tiles = 0;
-  int nt = 0;
   for (int i = 0; i < ntok; ++i) p.tok_grp[i] = -1;
   for (int i = 0; i < ntok; ++i) {
     const int e = tok_lora[i];
@@ -1748,16 +1721,11 @@ void plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const swl_lor
     p.g_entry[g] = e;
     p.g_arows[g] = host_entries[e].rank * nblk;
     p.g_tile0[g] = p.tiles;
-    p.g_tok0[g] = nt;
     p.tiles += (p.g_arows[g] + 15) / 16;
     for (int j = i; j < ntok; ++j)
-      if (tok_lora[j] == e) {
-        p.tok_grp[j] = (int8_t)g;
-        p.g_tok[nt++] = j;
-      }
+      if (tok_lora[j] == e) p.tok_grp[j] = (int8_t)g;
   }
   p.g_tile0[p.ngroups] = p.tiles;
-  p.g_tok0[p.ngroups] = nt;
 }
 
 template <int TT, int W>
@@ -1958,38 +1926,41 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   return SWL_OK;
 }
 
-// LoRA shrink alone for up to 64 tokens of the packed prefill batch
-// (xrows[i] is packed row urow0 + i; u rows are packed rows); used by the
-// tiled path.
-int launch_shrink_only(int64_t K, int ntok, const bf16* const* xrows, const int32_t* tok_lora, int urow0,
-                       const swl_lora_entry* host_entries, int nblk, float* u, int u_ld, int64_t u_split_stride,
-                       int u_ks, hipStream_t st) {
-  ShrinkPlan sp;
-  plan_shrink(sp, ntok, tok_lora, host_entries, nblk);
-  if (sp.ngroups == 0) return SWL_OK;
-  ShrinkArgs a{};
-  a.K = K;
-  a.total_steps = (int)(K / 32);
-  a.u_ks = u_ks;
-  a.n_items = sp.tiles * u_ks;
-  a.u_ld = u_ld;
-  a.u_split_stride = u_split_stride;
+// LoRA shrink of the packed prefill batch (one launch for all segments with
+// an adapter): seg_off / seg_rows are packed row offsets and counts; the u
+// rows are packed rows; n_ks K-slices of partials, folded into the first.
+int launch_shrink_gemm(const bf16* x, int64_t K, int n_seg, const int64_t* seg_off, const int64_t* seg_rows,
+                       const int32_t* seg_lora, const swl_lora_entry* host_entries, int nblk, float* u, int u_ld,
+                       int64_t u_split_stride, int n_ks, hipStream_t st) {
+  ShrinkGemmArgs a{};
+  a.x = x;
   a.u = u;
-  a.ngroups = sp.ngroups;
-  for (int g = 0; g < sp.ngroups; ++g) {
-    a.g_a[g] = reinterpret_cast<const bf16*>(host_entries[sp.g_entry[g]].a);
-    a.g_arows[g] = sp.g_arows[g];
-    a.g_tile0[g] = sp.g_tile0[g];
-    a.g_tok0[g] = sp.g_tok0[g];
+  a.K = K;
+  a.u_split_stride = u_split_stride;
+  a.n_ks = n_ks;
+  a.u_ld = u_ld;
+  a.total_steps = (int)(K / 32);
+  int items = 0;
+  for (int i = 0; i < n_seg; ++i) {
+    if (seg_lora[i] < 0 || seg_rows[i] == 0) continue;
+    const int j = a.n_seg++;
+    a.item0[j] = items;
+    a.row0[j] = (int32_t)seg_off[i];
+    a.rows[j] = (int32_t)seg_rows[i];
+    a.arows[j] = host_entries[seg_lora[i]].rank * nblk;
+    a.a[j] = reinterpret_cast<const bf16*>(host_entries[seg_lora[i]].a);
+    items += (int)((seg_rows[i] + 63) / 64) * ((a.arows[j] + 63) / 64);
   }
-  a.g_tile0[sp.ngroups] = sp.g_tile0[sp.ngroups];
-  a.g_tok0[sp.ngroups] = sp.g_tok0[sp.ngroups];
-  for (int i = 0; i < sp.g_tok0[sp.ngroups]; ++i) {
-    a.g_tok[i] = urow0 + sp.g_tok[i];
-    a.g_x[i] = xrows[sp.g_tok[i]];
+  if (a.n_seg == 0) return SWL_OK;
+  a.item0[a.n_seg] = items;
+  hipLaunchKernelGGL(shrink_gemm_kernel, dim3((unsigned)(items * n_ks)), dim3(256), 0, st, a);
+  SWL_LAUNCH_CHECK("shrink_gemm_kernel launch");
+  if (n_ks > 1) {
+    const int64_t nvec = u_split_stride / 4;  // u_ld is a multiple of 16
+    hipLaunchKernelGGL(u_fold_kernel, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, st, u, u_split_stride,
+                       n_ks, nvec);
+    SWL_LAUNCH_CHECK("u_fold_kernel launch");
   }
-  hipLaunchKernelGGL(shrink_kernel, dim3((unsigned)((a.n_items + 7) / 8)), dim3(512), 0, st, a);
-  SWL_LAUNCH_CHECK("shrink_kernel launch");
   return SWL_OK;
 }
 
@@ -2254,7 +2225,10 @@ int swl_timer_arm(int capacity) {
   if ((int)g_timer.ev.size() < 4 * capacity) {
     const size_t have = g_timer.ev.size();
     g_timer.ev.resize(4 * (size_t)capacity, nullptr);
-    for (size_t i = have; i < g_timer.ev.size(); ++i) SWL_HIP(hipEventCreate(&g_timer.ev[i]));
+    // timestamp-only markers: no system-scope cache writeback / invalidate
+    // around the timed kernels
+    for (size_t i = have; i < g_timer.ev.size(); ++i)
+      SWL_HIP(hipEventCreateWithFlags(&g_timer.ev[i], hipEventReleaseToDevice));
     g_timer.N.resize(capacity);
     g_timer.K.resize(capacity);
     g_timer.bytes.resize(capacity);
@@ -2384,8 +2358,17 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   SWL_CHECK(K % TK == 0, SWL_ERR_INVALID, "round: K must be a multiple of 64 for > 64 tokens");
   const size_t xbytes = sizeof(bf16) * (size_t)T * (size_t)K;
   const size_t xbytes_al = (xbytes + 255) & ~(size_t)255;
+  // LoRA shrink K-slices: enough (item, slice) workgroups to fill the chip
+  int u_ks = 1;
+  if (has_lora) {
+    int64_t items = 0;
+    for (int i = 0; i < n_seg; ++i)
+      if (seg_lora[i] >= 0 && rows[i] > 0)
+        items += (rows[i] + 63) / 64 * ((host_entries[seg_lora[i]].rank * nblk + 63) / 64);
+    while (u_ks < 16 && items * u_ks < 1024 && (K / 32) / (2 * u_ks) >= 8) u_ks *= 2;
+  }
   size_t ubytes = 0;
-  if (has_lora) ubytes = sizeof(float) * (size_t)T * (size_t)u_ld;
+  if (has_lora) ubytes = sizeof(float) * (size_t)u_ks * (size_t)T * (size_t)u_ld;
   void* scratch = nullptr;
   int rc = scratch_get(xbytes_al + ubytes, st, &scratch);
   if (rc) return rc;
@@ -2406,28 +2389,18 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   if (rc) return rc;
   if (has_lora) {
     float* u = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + xbytes_al);
-    // shrink per segment in chunks of <= 64 packed rows (A re-read per chunk)
+    int64_t rws[kMaxSeg];
     for (int i = 0; i < n_seg; ++i) {
+      rws[i] = rows[i];
       a.seg_lora[i] = (seg_lora[i] >= 0 && rows[i] > 0) ? seg_lora[i] : -1;
-      if (a.seg_lora[i] < 0) continue;
-      for (int64_t c0 = 0; c0 < rows[i]; c0 += kSkinnyMaxTok) {
-        const int cnt = (int)std::min<int64_t>(kSkinnyMaxTok, rows[i] - c0);
-        const bf16* xr[kSkinnyMaxTok];
-        int32_t tl[kSkinnyMaxTok];
-        const int64_t prow0 = a.out.off[i] + c0;
-        for (int j = 0; j < cnt; ++j) {
-          xr[j] = packed + (prow0 + j) * K;
-          tl[j] = seg_lora[i];
-        }
-        rc = launch_shrink_only(K, cnt, xr, tl, (int)prow0, host_entries, nblk, u, u_ld,
-                                (int64_t)T * u_ld, 1, st);
-        if (rc) return rc;
-      }
     }
+    rc = launch_shrink_gemm(packed, K, n_seg, a.out.off, rws, a.seg_lora, host_entries, nblk, u, u_ld,
+                            (int64_t)T * u_ld, u_ks, st);
+    if (rc) return rc;
     a.has_lora = 1;
     a.L = L;
     a.L.u = u;
-    a.L.usplit = 1;
+    a.L.usplit = 1;  // folded into split 0
     a.L.u_ld = u_ld;
     a.L.u_split_stride = (int64_t)T * u_ld;
   }
