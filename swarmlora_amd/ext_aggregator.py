@@ -61,9 +61,11 @@ _lib.register_signatures({
 })
 
 # Tensors whose memory the library points at (o/down weights, biases, embed
-# and LM-head tables, pooled adapters): kept alive for the process lifetime,
-# as the reference keeps its detach()-shared tensors.
+# and LM-head tables): kept alive for the process lifetime, as the reference
+# keeps its detach()-shared tensors.  Pooled adapters are kept per pool entry
+# and released when the entry is replaced or the pool cleared.
 _keep = []
+_adapter_keep = {}
 _pool_info = {}
 
 
@@ -225,13 +227,21 @@ def register_adapter(adapter_id, layer_idx, op_type, lora_a, lora_b: Sequence[to
     if a.shape[0] != rank * len(bs) or any(b.shape[1] != rank for b in bs):
         raise RuntimeError("register_adapter: lora_a must be [nblk*rank, in] and every lora_b [cols, rank]")
     arr = (c_vp * len(bs))(*[b.data_ptr() for b in bs])
+    key = (int(adapter_id), int(layer_idx), int(op_type))
+    old = _adapter_keep.get(key)
+    if old is not None and any(t.data_ptr() != n.data_ptr() for t, n in zip(old, [a, *bs])):
+        torch.cuda.synchronize()  # rounds already queued may still read the tensors being replaced
     _lib.check(_L().swl_agg_register_adapter(int(adapter_id), int(layer_idx), int(op_type), a.data_ptr(), arr,
                                              len(bs), int(rank), float(scale)))
-    _keep.extend([a, *bs])
+    _adapter_keep[key] = [a, *bs]
 
 
 def clear_adapters():
     _lib.check(_L().swl_agg_clear_adapters())
+    if _adapter_keep:
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+        _adapter_keep.clear()
 
 
 def execute_round(op_type, layer_idx, slot_ids, worker_ids, tokens, adapter_ids: Optional[Sequence[int]] = None,
