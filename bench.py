@@ -51,9 +51,15 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, copy a buffer of this many MiB (a kernel of known HBM traffic for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "ipc"), default="decode",
                     help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
-                         "rounds on the MFMA path, a line of its own")
+                         "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
+                         "shared-memory ring, IPC slots), host-synchronised vs GPU-ordered rounds. The last two "
+                         "print lines of their own")
+    ap.add_argument("--ipc-layers", type=int, default=4, help="ipc: 8B-shaped layers")
+    ap.add_argument("--ipc-tokens", type=int, default=8, help="ipc: decode tokens per worker (after 2 warm-up)")
+    ap.add_argument("--ipc-pooled", action="store_true",
+                    help="ipc: adapters pooled in the aggregator (delta added in the round) instead of on the worker")
     return ap.parse_args()
 
 
@@ -196,6 +202,173 @@ def prefill(args):
     print(json.dumps(line), flush=True)
 
 
+def _ipc_worker(shm_name, claim, wid, layers, n_tok, gpu_ordered, pooled, out):
+    """One worker process of the ipc workload: 8B-shaped layer modules with a
+    rank-16 adapter, decoding n_tok + 2 tokens through the aggregator."""
+    try:
+        from types import SimpleNamespace
+        import torch
+        from swarmlora_amd import ext_ipc_queue as extq
+        from swarmlora_amd import ext_unified_barrier as ub
+        from swarmlora_amd.decode import DecodeShape, synthetic_adapter
+        from swarmlora_amd.worker.batched_ops import BatchedAggregatorOps, SlotState
+        from swarmlora_amd.worker.engine import LayerModules, WorkerEngine
+        from swarmlora_amd.worker.model_builder import (FastLoRAModule, FusedLoRA, SyncFusedGateUp, SyncFusedQKV,
+                                                        SyncRemoteLoRALinear)
+        from swarmlora_amd.worker.paged_attention import PagedKVCache, RotaryInvFreq, build_vllm_cos_sin_cache
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(0)
+        s = DecodeShape(layers=layers)
+        kvd = s.kv_heads * s.head_dim
+        extq.open_queue(shm_name, 1024, 1024)
+        ub.init_worker_slot_manager(wid, 0, 0, s.hidden, s.inter, s.qkv)
+        sid = claim["slot_id"]
+        ub.open_slot(sid, claim["input_handle"], claim["output_handle"], claim["input_buffer_size"],
+                     claim["output_buffer_size"])
+        ad = synthetic_adapter(s, dev, seed=1000 + wid)
+        ones = torch.ones(s.hidden, dtype=torch.bfloat16, device=dev)
+        mods = []
+        for li in range(layers):
+            m = {p: FastLoRAModule(a.contiguous(), b.contiguous(), s.scale) for p, (a, b) in ad[li].items()}
+            mods.append(LayerModules(ones, ones,
+                                     SyncFusedQKV(li, [s.hidden, kvd, kvd], FusedLoRA([m["q"], m["k"], m["v"]],
+                                                                                      [s.hidden, kvd, kvd], dev,
+                                                                                      torch.bfloat16)),
+                                     SyncRemoteLoRALinear(3, li, s.hidden, m["o"]),
+                                     SyncFusedGateUp(li, [s.inter, s.inter], FusedLoRA([m["gate"], m["up"]],
+                                                                                       [s.inter, s.inter], dev,
+                                                                                       torch.bfloat16)),
+                                     SyncRemoteLoRALinear(6, li, s.hidden, m["down"])))
+        kv = PagedKVCache(layers, s.kv_heads, s.head_dim, s.block_size, 1, 64, dev, torch.bfloat16)
+        cs = build_vllm_cos_sin_cache(RotaryInvFreq(s.head_dim, s.theta), 64, dev, torch.bfloat16)
+        bops = BatchedAggregatorOps(SimpleNamespace(base_client=SimpleNamespace(hidden_dim=s.hidden)), wid, 15,
+                                    pooled_adapter=wid if pooled else None, gpu_ordered=gpu_ordered)
+        eng = WorkerEngine(mods, ones, s.eps, s.heads, s.kv_heads, s.head_dim, kv, cs, bops)
+        extq.slot_signal_join(sid)
+        t0 = time.time()
+        while not extq.slot_is_active(sid):
+            if time.time() - t0 > 120:
+                raise RuntimeError("slot never became active")
+            time.sleep(0.001)
+        st = SlotState(sid, torch.tensor([[1 + wid]], dtype=torch.int64, device=dev))
+        slots = {sid: st}
+        for _ in range(2):
+            eng.generate_one_token_all(slots)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(n_tok):
+            eng.generate_one_token_all(slots)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t1
+        extq.slot_signal_leave(sid)
+        ub.close_slot(sid)
+        out.put((wid, dt, None))
+    except Exception:
+        import traceback
+        out.put((wid, None, traceback.format_exc()))
+
+
+def ipc(args):
+    """The multi-process serving path: this process is the aggregator (native
+    main loop on a thread, 8B-shaped weights for --ipc-layers layers, embed
+    and LM head), --workers worker processes (at most 8 here) decode one
+    token per step each through the shared-memory ring and IPC-mapped slots.
+    Runs the same decode twice: host-synchronised rounds (the reference's
+    protocol) and GPU-ordered rounds (sequence words in the slot buffers
+    waited on by the streams).  `value` is tokens/s of the GPU-ordered run."""
+    import multiprocessing as mp
+    import threading
+    import torch
+    from swarmlora_amd import ext_aggregator as agg
+    from swarmlora_amd import ext_ipc_queue as extq
+    from swarmlora_amd.decode import DecodeShape, synthetic_weights
+    dev = torch.device("cuda:0")
+    W = min(args.workers, 8)
+    L = args.ipc_layers
+    s = DecodeShape(layers=L)
+    wts = synthetic_weights(s, dev, seed=0)
+    res = {}
+    for mode in ("host_sync", "gpu_ordered"):
+        q = extq.create_queue(1024, 1024)
+        extq.init_batch_control(W)
+        agg.init_slot_pool(W, 0, s.hidden, s.inter, s.kv_heads, s.head_dim, 1, 2)
+        agg.init_aggregator_begin(L, 0)
+        for li, w in enumerate(wts["layers"]):
+            agg.init_aggregator_layer(li, w["q"], w["k"], w["v"], w["o"], torch.empty(0), w["gate"], w["up"],
+                                      w["down"], torch.empty(0))
+        agg.init_aggregator_finalize()
+        agg.init_embed_lm_head_weights(wts["embed"], wts["lm_head"])
+        agg.init_aggregator_queue(q["shm_name"], 1024)
+        if args.ipc_pooled:
+            from swarmlora_amd.decode import synthetic_adapter
+            agg.clear_adapters()
+            for wid in range(W):
+                ad = synthetic_adapter(s, dev, seed=1000 + wid)
+                for li in range(L):
+                    for op, projs in ((agg.OP_QKV_FUSED, ("q", "k", "v")), (agg.OP_O_PROJ, ("o",)),
+                                      (agg.OP_GATE_UP_FUSED, ("gate", "up")), (agg.OP_DOWN_PROJ, ("down",))):
+                        agg.register_adapter(wid, li, op, torch.cat([ad[li][p][0] for p in projs], 0).contiguous(),
+                                             [ad[li][p][1].contiguous() for p in projs], s.scale)
+        claims = {wid: agg.claim_slot(wid) for wid in range(W)}
+        loop = threading.Thread(target=agg.aggregator_main_loop_slots, args=(W, 15), daemon=True)
+        loop.start()
+        ctx = mp.get_context("spawn")
+        out = ctx.Queue()
+        procs = [ctx.Process(target=_ipc_worker, args=(q["shm_name"], claims[w], w, L, args.ipc_tokens,
+                                                       mode == "gpu_ordered", args.ipc_pooled, out))
+                 for w in range(W)]
+        times = []
+        try:
+            for p in procs:
+                p.start()
+            for _ in procs:
+                wid, dt, err = out.get(timeout=600)
+                if err:
+                    raise RuntimeError(f"worker {wid}: {err}")
+                times.append(dt)
+        finally:
+            extq.set_quit(1)
+            loop.join(timeout=60)
+            for p in procs:
+                p.join(timeout=60)
+                if p.is_alive():
+                    p.kill()
+            for wid in range(W):
+                try:
+                    agg.release_slot(claims[wid]["slot_id"], wid)
+                except RuntimeError:
+                    pass
+            agg.clear_adapters()
+            agg.cleanup_slot_pool()
+            extq.close_queue()
+        rounds = 2 + 4 * L
+        step_s = max(times) / args.ipc_tokens
+        res[mode] = {"tok_s": round(W / step_s, 1), "ms_per_step": round(step_s * 1e3, 3),
+                     "us_per_round": round(step_s * 1e6 / rounds, 1)}
+    line = {
+        "metric": "multi-process decode tok/s (ipc path, GPU-ordered rounds)",
+        "value": res["gpu_ordered"]["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.ipc_tokens,
+        "warmup": 2,
+        "ms_per_step": res["gpu_ordered"]["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights and adapters)",
+        "config": {"workload": f"{W} worker processes x 1 decode token, {L} Llama-3.1-8B-shaped layers, rank-16 "
+                               "adapter per worker " + ("pooled in the aggregator's rounds" if args.ipc_pooled else
+                                                        "applied on the worker") +
+                               ", aggregator main loop in this process",
+                   "workers": W, "layers": L, "rounds_per_token": 2 + 4 * L, "modes": res},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -210,6 +383,8 @@ def main():
         sys.exit(1)
     if args.workload == "prefill":
         return prefill(args)
+    if args.workload == "ipc":
+        return ipc(args)
     from swarmlora_amd import ops
     from swarmlora_amd.decode import BatchedDecoder, DecodeShape, synthetic_adapter, synthetic_weights
 

@@ -63,6 +63,16 @@ int64_t swl_q_get_epoch(void);
  * before reserving a ring entry; "command ring buffer FULL" when full. */
 int swl_q_submit(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
                  uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id);
+/* submit_slot_command of a GPU-ordered worker (no counterpart in the
+ * reference, whose worker waits for its input copy on the host before
+ * submitting, ext_unified_barrier.cpp:262-266): in_seq is the slot's input
+ * sequence value the worker's stream writes after the copy
+ * (swl_w_input_seq); the aggregator's stream waits for it before the round
+ * and writes it to the slot's output sequence word after the round, instead
+ * of synchronising its stream before signalling done. */
+int swl_q_submit_seq(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
+                     uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id,
+                     uint64_t in_seq);
 /* Layout sizes of the shared segment (for tests). */
 size_t swl_q_control_bytes(void);
 size_t swl_q_command_bytes(void);
@@ -147,6 +157,10 @@ int swl_agg_drain_commands(uint64_t active_lo, uint64_t active_hi, int want, int
                            int32_t* ops, int32_t* layers, int64_t* tokens, uint64_t* x_keys, int* got);
 /* Eviction and leave-check periods of the barrier (defaults 500 ms, 10 ms). */
 int swl_agg_set_barrier_timeouts(int evict_ms, int leave_check_ms);
+/* Slots whose GPU-ordered input did not arrive within the stream wait's
+ * limit (2 s) since the last call: writes up to 128 slot ids, returns the
+ * count and clears them (such slots are also evicted by the main loop). */
+int swl_agg_take_seq_timeouts(int32_t* slot_ids, int max_ids);
 /* aggregator_main_loop_slots (ext_aggregator.cpp:1024-1210): blocks until the
  * quit flag is set.  dtype_code 15 (bfloat16) only. */
 int swl_agg_main_loop(int num_slots, int dtype_code);
@@ -184,6 +198,14 @@ int swl_w_get_next_token(int slot_id, int64_t* token, void* stream);
 int swl_w_cleanup(void);
 /* Buffer sizes of an open slot (for shape checks in the Python shim). */
 int swl_w_slot_sizes(int slot_id, size_t* input_buffer_size, size_t* output_buffer_size);
+/* GPU-ordered mode for every slot of this worker (no counterpart in the
+ * reference): prepare_* no longer wait on the host; they write the slot's
+ * next input sequence value on the stream after the copy.  Output reads
+ * (copy_output, get_next_token) first wait on the stream for the
+ * aggregator's output sequence word to reach the last input value. */
+int swl_w_set_gpu_ordered(int enable);
+/* The input sequence value of the slot's last prepare_* (0 before any). */
+int swl_w_input_seq(int slot_id, uint64_t* seq);
 
 #ifdef __cplusplus
 }

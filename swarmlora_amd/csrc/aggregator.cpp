@@ -60,8 +60,12 @@ struct Pool {
   int max_seq_per_step = 0;
   size_t in_size = 0, out_size = 0;
   bool initialized = false;
+  uint32_t* seq_timeout = nullptr;  // host-visible, one word per slot (GPU-ordered input waits that timed out)
 };
 Pool g_pool;
+
+// Limit of the aggregator stream's wait for a GPU-ordered worker's input.
+constexpr uint32_t kSeqWaitLimitUs = 2000000;
 
 struct LayerW {
   void* qkv = nullptr;      // owned: [q+k+v, hidden]
@@ -147,6 +151,11 @@ int upload_adapters() {
 
 }  // namespace
 
+namespace {
+int drain_impl(uint64_t active_lo, uint64_t active_hi, int want, int32_t* slot_ids, int32_t* worker_ids, int32_t* ops,
+               int32_t* layers, int64_t* tokens, uint64_t* x_keys, uint64_t* in_seqs, int* got);
+}  // namespace
+
 extern "C" {
 
 // ------------------------------------------------------------- slot pool
@@ -177,10 +186,14 @@ int swl_agg_init_slot_pool(int num_slots, int device_index, int hidden_dim, int 
     SWL_HIP(hipMalloc(&s.in, p.in_size));
     SWL_HIP(hipMemset(s.in, 0, p.in_size));
     SWL_HIP(hipIpcGetMemHandle(&s.in_handle, s.in));
-    SWL_HIP(hipMalloc(&s.out, p.out_size));
-    SWL_HIP(hipMemset(s.out, 0, p.out_size));
+    // the output buffer carries the slot's two sequence words in a tail past
+    // out_size (GPU-ordered rounds)
+    SWL_HIP(hipMalloc(&s.out, p.out_size + swl::kSeqTailBytes));
+    SWL_HIP(hipMemset(s.out, 0, p.out_size + swl::kSeqTailBytes));
     SWL_HIP(hipIpcGetMemHandle(&s.out_handle, s.out));
   }
+  SWL_HIP(hipHostMalloc((void**)&p.seq_timeout, SWL_MAX_SLOTS * sizeof(uint32_t), hipHostMallocDefault));
+  std::memset(p.seq_timeout, 0, SWL_MAX_SLOTS * sizeof(uint32_t));
   p.initialized = true;
   if (input_buffer_size) *input_buffer_size = p.in_size;
   if (output_buffer_size) *output_buffer_size = p.out_size;
@@ -238,7 +251,7 @@ int swl_agg_release_slot(int slot_id, int worker_id) {
   int rc = stream_get(&st);
   if (rc) return rc;
   SWL_HIP(hipMemsetAsync(s.in, 0, g_pool.in_size, st));
-  SWL_HIP(hipMemsetAsync(s.out, 0, g_pool.out_size, st));
+  SWL_HIP(hipMemsetAsync(s.out, 0, g_pool.out_size + swl::kSeqTailBytes, st));  // sequence words restart at 0
   SWL_HIP(hipStreamSynchronize(st));
   g_pool.free_mask.set_bit(slot_id);
   g_pool.active_mask.clear_bits(Mask::bit(slot_id));
@@ -278,6 +291,8 @@ int swl_agg_cleanup_slot_pool(void) {
     s.in = s.out = nullptr;
     s.owner.store(-1);
   }
+  if (g_pool.seq_timeout) SWL_HIP(hipHostFree(g_pool.seq_timeout));
+  g_pool.seq_timeout = nullptr;
   g_pool.initialized = false;
   g_pool.num_slots = 0;
   std::printf("[Aggregator] Slot pool cleaned up\n");
@@ -588,6 +603,25 @@ int swl_agg_signal_done(void) {
 
 int swl_agg_drain_commands(uint64_t active_lo, uint64_t active_hi, int want, int32_t* slot_ids, int32_t* worker_ids,
                            int32_t* ops, int32_t* layers, int64_t* tokens, uint64_t* x_keys, int* got) {
+  return drain_impl(active_lo, active_hi, want, slot_ids, worker_ids, ops, layers, tokens, x_keys, nullptr, got);
+}
+
+int swl_agg_take_seq_timeouts(int32_t* slot_ids, int max_ids) {
+  if (!g_pool.initialized || !g_pool.seq_timeout) return 0;
+  int n = 0;
+  for (int i = 0; i < SWL_MAX_SLOTS; ++i) {
+    if (__atomic_exchange_n(&g_pool.seq_timeout[i], 0u, __ATOMIC_ACQ_REL) == 0) continue;
+    if (slot_ids && n < max_ids) slot_ids[n] = i;
+    ++n;
+  }
+  return n;
+}
+
+}  // extern "C"
+
+namespace {
+int drain_impl(uint64_t active_lo, uint64_t active_hi, int want, int32_t* slot_ids, int32_t* worker_ids, int32_t* ops,
+               int32_t* layers, int64_t* tokens, uint64_t* x_keys, uint64_t* in_seqs, int* got) {
   SWL_CHECK(g_agg_q.ctrl && g_agg_q.ring, SWL_ERR_STATE, "Aggregator queue not initialized");
   swl::Control* c = g_agg_q.ctrl;
   const Mask active{{active_lo, active_hi}};
@@ -621,6 +655,7 @@ int swl_agg_drain_commands(uint64_t active_lo, uint64_t active_hi, int want, int
       layers[n] = cmd.layer_idx;
       tokens[n] = cmd.bx * cmd.tx;
       x_keys[n] = cmd.x_key;
+      if (in_seqs) in_seqs[n] = cmd.in_seq;
       if (cmd.op_type == SWL_OP_SET_SAMPLING) {
         swl::SamplingParams p;
         p.do_sample = (cmd.x_key & 1) ? 1 : 0;
@@ -639,8 +674,7 @@ int swl_agg_drain_commands(uint64_t active_lo, uint64_t active_hi, int want, int
   *got = n;
   return SWL_OK;
 }
-
-}  // extern "C"
+}  // namespace
 
 // ----------------------------------------------------------- main loop ops
 namespace swl {
@@ -717,7 +751,7 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
   SWL_CHECK(dtype_code == 15, SWL_ERR_UNSUPPORTED, "aggregator_main_loop_slots: only bfloat16 (dtype_code 15)");
   (void)num_slots;
   SWL_HIP(hipSetDevice(g_device));
-  hipStream_t st;
+  hipStream_t st = nullptr;
   int rc = stream_get(&st);
   if (rc) return rc;
   swl::Control* c = g_agg_q.ctrl;
@@ -728,7 +762,10 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
   std::fflush(stdout);
   int32_t sids[SWL_MAX_SLOTS], wids[SWL_MAX_SLOTS], ops[SWL_MAX_SLOTS], layers[SWL_MAX_SLOTS];
   int64_t toks[SWL_MAX_SLOTS];
-  uint64_t keys[SWL_MAX_SLOTS];
+  uint64_t keys[SWL_MAX_SLOTS], seqs[SWL_MAX_SLOTS];
+  auto seq_word = [](int sid, size_t off) {
+    return reinterpret_cast<uint64_t*>(static_cast<char*>(g_pool.slots[sid].out) + g_pool.out_size + off);
+  };
   while (c->quit.load(std::memory_order_acquire) == 0) {
     // token boundary: leaves first, then joins
     if (!c->leaves.load().empty()) {
@@ -771,7 +808,7 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
       N = cnt;
       if (c->quit.load(std::memory_order_acquire) != 0) break;
       int got = 0;
-      rc = swl_agg_drain_commands(active.w[0], active.w[1], N, sids, wids, ops, layers, toks, keys, &got);
+      rc = drain_impl(active.w[0], active.w[1], N, sids, wids, ops, layers, toks, keys, seqs, &got);
       if (rc) return rc;
       if (got == 0 || c->quit.load(std::memory_order_acquire) != 0) {
         if (c->quit.load(std::memory_order_acquire) != 0) swl_agg_signal_done();
@@ -784,14 +821,36 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
         int m = 0;
         for (int i = 0; i < got; ++i) {
           if (ops[i] == op && layers[i] == layers[0]) {
-            sids[m] = sids[i]; wids[m] = wids[i]; toks[m] = toks[i]; keys[m] = keys[i];
+            sids[m] = sids[i]; wids[m] = wids[i]; toks[m] = toks[i]; keys[m] = keys[i]; seqs[m] = seqs[i];
             ++m;
           } else {
             c->evicted.set_bit(sids[i]);
             active.clear(sids[i]);
           }
         }
+        // GPU-ordered commands: the stream waits for each such slot's input
+        // sequence word instead of the worker having waited on its host
+        const uint64_t* wflag[SWL_MAX_SLOTS];
+        uint64_t want[SWL_MAX_SLOTS];
+        int32_t wtag[SWL_MAX_SLOTS];
+        int nord = 0;
+        for (int i = 0; i < m; ++i)
+          if (seqs[i] > 0) {
+            wflag[nord] = seq_word(sids[i], swl::kInSeqOffset);
+            want[nord] = seqs[i];
+            wtag[nord] = sids[i];
+            ++nord;
+          }
+        if (nord > 0) {
+          rc = swl::seq_wait_launch(nord, wflag, want, wtag, g_pool.seq_timeout, kSeqWaitLimitUs, st);
+          if (rc) return rc;
+        }
         rc = run_op(op, layers[0], m, sids, wids, toks, keys, st, step++);
+        // ... and each ordered slot's output sequence word follows the round
+        // on the stream (written even if the round failed, so no worker waits
+        // out its limit on an evicted slot)
+        for (int i = 0; i < m; ++i)
+          if (seqs[i] > 0) SWL_HIP(hipStreamWriteValue64(st, seq_word(sids[i], swl::kOutSeqOffset), seqs[i], 0));
         if (rc) {
           // a malformed command must not take every co-tenant down: evict the
           // slots of this round and keep serving the others
@@ -804,7 +863,20 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
           }
           c->active.store(active);
         }
-        SWL_HIP(hipStreamSynchronize(st));
+        // rounds of GPU-ordered commands only are not waited for on the host
+        if (nord < m) SWL_HIP(hipStreamSynchronize(st));
+        int32_t late[SWL_MAX_SLOTS];
+        const int nlate = swl_agg_take_seq_timeouts(late, SWL_MAX_SLOTS);
+        for (int i = 0; i < nlate && i < SWL_MAX_SLOTS; ++i) {
+          std::fprintf(stderr, "[Aggregator] slot %d: GPU-ordered input not written within %u ms; evicting\n",
+                       late[i], kSeqWaitLimitUs / 1000);
+          c->evicted.set_bit(late[i]);
+          active.clear(late[i]);
+        }
+        if (nlate) {
+          std::fflush(stderr);
+          c->active.store(active);
+        }
       }
       swl_agg_signal_done();
       ++ops_done;

@@ -11,7 +11,7 @@
 namespace swl {
 
 constexpr uint32_t kQueueMagic = 0x53574C51u;  // "SWLQ"
-constexpr uint32_t kQueueLayoutVersion = 1;
+constexpr uint32_t kQueueLayoutVersion = 2;
 constexpr int kSlotWords = SWL_MAX_SLOTS / 64;
 
 // 128-bit slot set held in registers.
@@ -85,6 +85,7 @@ struct alignas(64) Command {
   int32_t ticket_id;
   int64_t bx, tx, dx;
   uint64_t x_key, y0_key, y1_key, y2_key;
+  uint64_t in_seq;  // > 0: GPU-ordered command (the slot's input sequence word reaches this value)
 };
 
 // Control block at offset 0 of the segment; the ring follows it.  Producer

@@ -2277,6 +2277,54 @@ int swl_zero_blocks_bf16(void* const* caches, int ncache, const int64_t* block_i
 
 }  // extern "C"
 
+// ============================================== GPU-ordered round flags ===
+namespace {
+struct SeqWaitArgs {
+  int32_t n;
+  uint32_t limit_ticks;  // s_memrealtime runs at 100 MHz
+  uint32_t* timed_out;
+  const uint64_t* flag[SWL_MAX_SLOTS];
+  uint64_t want[SWL_MAX_SLOTS];
+  int32_t tag[SWL_MAX_SLOTS];
+};
+
+// One lane per flag; every lane exits: when its flag reaches the wanted value
+// or when the time limit has passed (then it reports its tag).
+__global__ __launch_bounds__(SWL_MAX_SLOTS) void seq_wait_kernel(SeqWaitArgs a) {
+  const int i = threadIdx.x;
+  if (i >= a.n) return;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (__hip_atomic_load(a.flag[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) < a.want[i]) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 > a.limit_ticks) {
+      __hip_atomic_store(a.timed_out + a.tag[i], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(32);
+  }
+}
+}  // namespace
+
+namespace swl {
+int seq_wait_launch(int n, const uint64_t* const* flag, const uint64_t* want, const int32_t* tag, uint32_t* timed_out,
+                    uint32_t limit_us, hipStream_t stream) {
+  SWL_CHECK(n >= 0 && n <= SWL_MAX_SLOTS, SWL_ERR_INVALID, "seq_wait: at most 128 flags");
+  if (n == 0) return SWL_OK;
+  SeqWaitArgs a{};
+  a.n = n;
+  a.limit_ticks = (uint32_t)std::min<uint64_t>((uint64_t)limit_us * 100, 0xFFFFFFFFull);
+  a.timed_out = timed_out;
+  for (int i = 0; i < n; ++i) {
+    SWL_CHECK(flag[i] != nullptr && tag[i] >= 0 && tag[i] < SWL_MAX_SLOTS, SWL_ERR_INVALID, "seq_wait: bad flag");
+    a.flag[i] = flag[i];
+    a.want[i] = want[i];
+    a.tag[i] = tag[i];
+  }
+  hipLaunchKernelGGL(seq_wait_kernel, dim3(1), dim3(SWL_MAX_SLOTS), 0, stream, a);
+  SWL_LAUNCH_CHECK("seq_wait_kernel launch");
+  return SWL_OK;
+}
+}  // namespace swl
+
 // ======================================================== round planner ===
 namespace swl {
 

@@ -20,6 +20,21 @@ int fail(int code, const std::string& msg);
 // keep working.
 int hip_fail(hipError_t e, const char* where);
 
+// GPU-ordered rounds: per slot two 64-bit sequence words live in a tail
+// past the slot's output buffer (both processes map that buffer).  The
+// worker's stream writes in_seq after its input copy; the aggregator's stream
+// waits for it, runs the round and writes out_seq; the worker's stream waits
+// for out_seq before reading the outputs.
+constexpr size_t kSeqTailBytes = 256;
+constexpr size_t kInSeqOffset = 0, kOutSeqOffset = 128;
+
+// Waits on `stream` until *flag[i] >= want[i] for every i < n (one lane per
+// flag, polled with system-scope loads and a sleep).  A flag still short after
+// limit_us microseconds stops the wait for that flag and stores 1 into
+// timed_out[tag[i]] (host-visible, one word per tag); the stream continues.
+int seq_wait_launch(int n, const uint64_t* const* flag, const uint64_t* want, const int32_t* tag, uint32_t* timed_out,
+                    uint32_t limit_us, hipStream_t stream);
+
 }  // namespace swl
 
 #define SWL_HIP(call)                                   \

@@ -22,7 +22,12 @@ struct SlotCtx {
   void* out = nullptr;
   size_t in_size = 0, out_size = 0;
   int64_t bx = 0, tx = 0, dx = 0;
+  uint64_t seq = 0;  // GPU-ordered mode: input sequence value of the last prepare_*
 };
+
+// Limit of this worker's stream wait for a round's outputs (the aggregator's
+// own input wait is 2 s; a round that long has already been evicted).
+constexpr uint32_t kOutWaitLimitUs = 4000000;
 
 struct Manager {
   int worker_id = -1;
@@ -32,7 +37,24 @@ struct Manager {
   SlotCtx slots[kMaxSlotsPerWorker];
   int nopen = 0;
   bool initialized = false;
+  bool gpu_ordered = false;
+  uint32_t* out_timeout = nullptr;  // host-visible words, one per slot id
 } g_w;
+
+uint64_t* seq_word(SlotCtx* c, size_t off) {
+  return reinterpret_cast<uint64_t*>(static_cast<char*>(c->out) + c->out_size + off);
+}
+
+// GPU-ordered mode: the stream waits until the aggregator has written this
+// slot's output sequence word for the last submitted input.
+int wait_outputs(const char* fn, SlotCtx* c, hipStream_t st) {
+  if (!g_w.gpu_ordered || c->seq == 0) return SWL_OK;
+  const uint64_t* flag = seq_word(c, swl::kOutSeqOffset);
+  const int32_t tag = c->slot_id;
+  int rc = swl::seq_wait_launch(1, &flag, &c->seq, &tag, g_w.out_timeout, kOutWaitLimitUs, st);
+  if (rc) return swl::fail(rc, std::string(fn) + ": " + swl::last_error());
+  return SWL_OK;
+}
 
 SlotCtx* find_slot(int slot_id) {
   for (auto& s : g_w.slots)
@@ -53,6 +75,12 @@ int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream
                                           " bytes) exceeds slot buffer size (" + std::to_string(c->in_size) +
                                           " bytes)");
   SWL_HIP(hipMemcpyAsync(c->in, src, bytes, hipMemcpyDeviceToDevice, st));
+  if (g_w.gpu_ordered) {
+    // the aggregator's stream waits for this value before reading the buffer
+    ++c->seq;
+    SWL_HIP(hipStreamWriteValue64(st, seq_word(c, swl::kInSeqOffset), c->seq, 0));
+    return SWL_OK;
+  }
   // the aggregator reads the buffer from another process once this worker
   // signals ready: the copy must be complete, not just ordered
   SWL_HIP(hipStreamSynchronize(st));
@@ -74,6 +102,7 @@ int swl_w_init(int worker_id, int worker_device, int aggregator_device, int hidd
   g_w.qkv = qkv_dim;
   for (auto& s : g_w.slots) s = SlotCtx();
   g_w.nopen = 0;
+  g_w.gpu_ordered = false;
   g_w.initialized = true;
   std::printf("[Worker-%d] Slot manager initialized (worker_device=%d, aggregator_device=%d)\n", worker_id,
               worker_device, aggregator_device);
@@ -192,6 +221,8 @@ int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream) {
   SWL_CHECK(bytes <= c->out_size, SWL_ERR_INVALID,
             "get_outputs_slot: output (" + std::to_string(bytes) + " bytes) exceeds slot output buffer (" +
                 std::to_string(c->out_size) + " bytes)");
+  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
+  if (rc) return rc;
   // stream-ordered; consumers of dst on the same stream see the copy
   SWL_HIP(hipMemcpyAsync(dst, c->out, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
   return SWL_OK;
@@ -229,9 +260,29 @@ int swl_w_get_next_token(int slot_id, int64_t* token, void* stream) {
   int rc = need_slot("get_next_token_slot", slot_id, &c);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
+  rc = wait_outputs("get_next_token_slot", c, st);
+  if (rc) return rc;
   SWL_HIP(hipStreamSynchronize(st));
   SWL_HIP(hipMemcpyAsync(token, c->out, sizeof(int64_t), hipMemcpyDeviceToHost, st));
   SWL_HIP(hipStreamSynchronize(st));
+  return SWL_OK;
+}
+
+int swl_w_set_gpu_ordered(int enable) {
+  SWL_CHECK(g_w.initialized, SWL_ERR_STATE, "set_gpu_ordered: worker slot manager not initialized");
+  if (enable && !g_w.out_timeout) {
+    SWL_HIP(hipHostMalloc((void**)&g_w.out_timeout, SWL_MAX_SLOTS * sizeof(uint32_t), hipHostMallocDefault));
+    std::memset(g_w.out_timeout, 0, SWL_MAX_SLOTS * sizeof(uint32_t));
+  }
+  g_w.gpu_ordered = enable != 0;
+  return SWL_OK;
+}
+
+int swl_w_input_seq(int slot_id, uint64_t* seq) {
+  SlotCtx* c;
+  int rc = need_slot("input_seq", slot_id, &c);
+  if (rc) return rc;
+  *seq = c->seq;
   return SWL_OK;
 }
 
@@ -247,6 +298,9 @@ int swl_w_cleanup(void) {
   }
   g_w.nopen = 0;
   g_w.initialized = false;
+  g_w.gpu_ordered = false;
+  if (g_w.out_timeout) (void)hipHostFree(g_w.out_timeout);
+  g_w.out_timeout = nullptr;
   return SWL_OK;
 }
 

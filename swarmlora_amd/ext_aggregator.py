@@ -58,6 +58,7 @@ _lib.register_signatures({
                                        ctypes.POINTER(c_int)]),
     "swl_agg_set_barrier_timeouts": (c_int, [c_int, c_int]),
     "swl_agg_main_loop": (c_int, [c_int, c_int]),
+    "swl_agg_take_seq_timeouts": (c_int, [ctypes.POINTER(ctypes.c_int32), c_int]),
 })
 
 # Tensors whose memory the library points at (o/down weights, biases, embed
@@ -234,6 +235,14 @@ def register_adapter(adapter_id, layer_idx, op_type, lora_a, lora_b: Sequence[to
     _lib.check(_L().swl_agg_register_adapter(int(adapter_id), int(layer_idx), int(op_type), a.data_ptr(), arr,
                                              len(bs), int(rank), float(scale)))
     _adapter_keep[key] = [a, *bs]
+
+
+def take_seq_timeouts():
+    """Slots whose GPU-ordered input did not arrive within the aggregator
+    stream's wait limit since the last call (the main loop evicts them)."""
+    arr = (ctypes.c_int32 * 128)()
+    n = _L().swl_agg_take_seq_timeouts(arr, 128)
+    return list(arr[:min(n, 128)])
 
 
 def clear_adapters():

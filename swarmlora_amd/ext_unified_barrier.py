@@ -40,6 +40,8 @@ _lib.register_signatures({
     "swl_w_prepare_hidden_lm": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, ctypes.c_size_t, c_vp]),
     "swl_w_get_next_token": (c_int, [c_int, _P_i64, c_vp]),
     "swl_w_cleanup": (c_int, []),
+    "swl_w_set_gpu_ordered": (c_int, [c_int]),
+    "swl_w_input_seq": (c_int, [c_int, ctypes.POINTER(ctypes.c_uint64)]),
 })
 
 _state = {"device": 0, "hidden_dim": 0}
@@ -131,3 +133,19 @@ def get_next_token_slot(slot_id):
 
 def cleanup_worker_slots():
     _lib.check(_L().swl_w_cleanup())
+
+
+# ------------------------------------------------ additions (no reference counterpart)
+def set_gpu_ordered(enable=True):
+    """GPU-ordered slots: prepare_* stop waiting for their copy on the host
+    and write the slot's next input sequence value on the stream instead;
+    output reads first wait on the stream for the aggregator's output
+    sequence word.  Commands must then carry input_seq(slot_id)."""
+    _lib.check(_L().swl_w_set_gpu_ordered(1 if enable else 0))
+
+
+def input_seq(slot_id):
+    """Input sequence value written by the slot's last prepare_* call."""
+    v = ctypes.c_uint64(0)
+    _lib.check(_L().swl_w_input_seq(int(slot_id), ctypes.byref(v)))
+    return v.value

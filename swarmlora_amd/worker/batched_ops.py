@@ -66,9 +66,17 @@ class WorkerBatchedOps:
 class BatchedAggregatorOps:
     """submit -> signal_ready -> (local LoRA delta) -> wait epoch -> read."""
 
-    def __init__(self, slot_manager, worker_id: int, dtype_code: int, pooled_adapter: Optional[int] = None):
+    def __init__(self, slot_manager, worker_id: int, dtype_code: int, pooled_adapter: Optional[int] = None,
+                 gpu_ordered: bool = False):
         self.slot_manager = slot_manager
         self.worker_id = worker_id
+        # gpu_ordered (an addition): slot copies are ordered against the
+        # aggregator's rounds on the GPU (sequence words in the slot buffer)
+        # instead of by host waits; barrier_sync then returns once the round
+        # is launched, not finished
+        self.gpu_ordered = gpu_ordered
+        if gpu_ordered:
+            ub.set_gpu_ordered(True)
         self.dtype_code = dtype_code
         self.dtype = torch.bfloat16 if dtype_code == 15 else torch.float16
         self.hidden_dim = slot_manager.base_client.hidden_dim
@@ -82,10 +90,14 @@ class BatchedAggregatorOps:
         slot_id, state = next(iter(slots.items()))
         return {slot_id: ub.get_outputs_slot(slot_id, dims, state.hidden)}
 
+    def _seq(self, slot_id):
+        return ub.input_seq(slot_id) if self.gpu_ordered else 0
+
     def _submit(self, op, layer_idx, slot_id, x):
         b, t, d = x.shape
         ub.prepare_input_slot(slot_id, op, x)
-        extq.submit_slot_command(op, layer_idx, slot_id, self.worker_id, b, t, d, self._x_key, 0, 0, 0, 0)
+        extq.submit_slot_command(op, layer_idx, slot_id, self.worker_id, b, t, d, self._x_key, 0, 0, 0, 0,
+                                 in_seq=self._seq(slot_id))
         extq.slot_signal_ready(slot_id)
 
     # ---------------------------------------------------------------- embed
@@ -94,7 +106,8 @@ class BatchedAggregatorOps:
         slot_id, state = next(iter(slots.items()))
         ub.prepare_token_ids_slot(slot_id, state.input_ids)
         b, t = state.input_ids.shape
-        extq.submit_slot_command(OP_EMBED, 0, slot_id, self.worker_id, b, t, self.hidden_dim, 0, 0, 0, 0, 0)
+        extq.submit_slot_command(OP_EMBED, 0, slot_id, self.worker_id, b, t, self.hidden_dim, 0, 0, 0, 0, 0,
+                                 in_seq=self._seq(slot_id))
         extq.slot_signal_ready(slot_id)
         return epoch
 
@@ -189,7 +202,8 @@ class BatchedAggregatorOps:
         slot_id, state = next(iter(slots.items()))
         ub.prepare_hidden_for_lm_head_slot(slot_id, state.hidden)
         b, t, d = state.hidden.shape
-        extq.submit_slot_command(OP_LM_HEAD, 0, slot_id, self.worker_id, b, t, d, 0, 0, 0, 0, 0)
+        extq.submit_slot_command(OP_LM_HEAD, 0, slot_id, self.worker_id, b, t, d, 0, 0, 0, 0, 0,
+                                 in_seq=self._seq(slot_id))
         extq.slot_signal_ready(slot_id)
         return epoch
 

@@ -117,7 +117,7 @@ def test_execute_round_with_pooled_adapters(pool, dev):
 
 
 # ------------------------------------------------------------ end to end
-def _worker_proc(shm_name, claim, worker_id, prompt, n_new, pooled, out):
+def _worker_proc(shm_name, claim, worker_id, prompt, n_new, pooled, out, gpu_ordered=False):
     try:
         from types import SimpleNamespace
         import torch
@@ -154,7 +154,7 @@ def _worker_proc(shm_name, claim, worker_id, prompt, n_new, pooled, out):
         kv = PagedKVCache(c.layers, c.kv_heads, c.head_dim, c.block, 1, c.max_seq, dev, torch.bfloat16)
         cs = build_vllm_cos_sin_cache(RotaryInvFreq(c.head_dim, c.theta), c.max_seq, dev, torch.bfloat16)
         bops = BatchedAggregatorOps(SimpleNamespace(base_client=SimpleNamespace(hidden_dim=c.hidden)), worker_id, 15,
-                                    pooled_adapter=worker_id if pooled else None)
+                                    pooled_adapter=worker_id if pooled else None, gpu_ordered=gpu_ordered)
         eng = WorkerEngine(layers, W["final_norm"].to(dev), c.eps, c.heads, c.kv_heads, c.head_dim, kv, cs, bops)
         extq.slot_signal_join(sid)
         t0 = time.time()
@@ -183,14 +183,16 @@ def _worker_proc(shm_name, claim, worker_id, prompt, n_new, pooled, out):
         out.put((worker_id, None, None, traceback.format_exc()))
 
 
-@pytest.mark.parametrize("pooled", [False, True])
-def test_end_to_end_workers_through_ipc(dev, pooled):
+@pytest.mark.parametrize("pooled,gpu_ordered", [(False, False), (True, False), (False, True), (True, True)])
+def test_end_to_end_workers_through_ipc(dev, pooled, gpu_ordered):
     """Two worker processes (one 20-token prompt in two prefill chunks + 3
     decode tokens each) run the per-token 130-round-style sequence through
     the shared-memory ring and IPC slots; this process runs the native main
     loop.  Each step's final hidden state is checked against the CPU oracle
     fed the same tokens.  pooled=True moves the LoRA delta into the
-    aggregator's round epilogue."""
+    aggregator's round epilogue; gpu_ordered=True orders the slot copies
+    against the rounds with sequence words waited on by the streams instead
+    of host waits."""
     from swarmlora_amd import ext_ipc_queue as extq
     from tests._tiny_model import CFG, KVD, PROJ, adapter, base_weights, oracle_steps
     agg = _agg()
@@ -224,7 +226,8 @@ def test_end_to_end_workers_through_ipc(dev, pooled):
     out = ctx.Queue()
     g = torch.Generator().manual_seed(3)
     prompts = {wid: torch.randint(0, c.vocab, (20,), generator=g).tolist() for wid in workers}
-    procs = [ctx.Process(target=_worker_proc, args=(q["shm_name"], claims[w], w, prompts[w], 3, pooled, out))
+    procs = [ctx.Process(target=_worker_proc,
+                         args=(q["shm_name"], claims[w], w, prompts[w], 3, pooled, out, gpu_ordered))
              for w in workers]
     results = {}
     try:
