@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="after timing, copy a buffer of this many MiB (a kernel of known HBM traffic for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--weights", choices=("packed", "row-major"), default="packed",
+                    help="decode: projection weights in fragment tiles (default) or row-major")
     ap.add_argument("--workload", choices=("decode", "prefill", "ipc"), default="decode",
                     help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
                          "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
@@ -402,7 +404,8 @@ def main():
         vc.copy_(torch.randn(vc.shape, generator=kv_gen, device=dev, dtype=torch.bfloat16))
 
     max_new = 1 + args.warmup + args.steps + args.timer_steps + 1
-    dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill)
+    dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill,
+                         packed=args.weights == "packed")
     del weights, adapters
     torch.cuda.synchronize()
 
@@ -484,6 +487,7 @@ def main():
                                "rank-16 adapter per worker on q/k/v/o/gate/up/down, paged KV ctx U{128..2048}, "
                                "130 rounds per token, greedy sampling, captured as one HIP graph",
                    "workers": W, "layers": s.layers, "rounds_per_token": 2 + n_rounds,
+                   "weight_layout": args.weights,
                    "us_per_round": round(us_round, 2),
                    "us_per_round_of_step": round(ms_per_step * 1e3 / (2 + n_rounds), 2),
                    "step_algorithmic_GB": round(step_bytes / 1e9, 3),

@@ -164,7 +164,22 @@ typedef struct swl_round_fusion {
   const int64_t* positions;
   const void* cos_sin;
   int64_t max_pos;
+  /* w_layout 1: w is in the fragment-tile layout of swl_pack_weight_bf16
+   * (decode-shaped rounds only); 0: row-major [n, k]. */
+  int32_t w_layout;
 } swl_round_fusion;
+
+/* Fragment-tile layout of a row-major weight w [n, k] (k a multiple of 32)
+ * for decode-shaped rounds: 16-row tiles, each tile stored whole (16 x k),
+ * k-step by k-step (32 columns); one k-step block is the 1 KiB A operand of a
+ * 16x16x32 bf16 MFMA for those rows (lane l: row l % 16, columns
+ * 8 (l / 16) .. + 7), so a wave streams each block with one fully coalesced
+ * 16-byte load per lane.  Rows past n are zero.  out holds
+ * ceil(n / 16) * 16 * k elements (16-byte aligned).  No counterpart in the
+ * reference (its weights stay row-major torch tensors, ext_aggregator.cpp:
+ * 347-376); the round results are bit-identical to the row-major ones. */
+int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out,
+                         void* stream);
 
 /* swl_round_bf16 with fusions (fusion may be NULL; a non-NULL fusion needs
  * at most 64 token rows). */

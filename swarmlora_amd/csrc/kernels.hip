@@ -29,6 +29,7 @@
 // same for A and B, so any consistent assignment of memory k to (group, j)
 // computes the same dot products.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -272,9 +273,10 @@ constexpr int kKDepth = 8;            // k-steps of W in flight per wave
 
 struct SplitArgs {
   // base projection -> part[ks][tok][N]; LoRA shrink -> u[ks][tok][u_ld]
-  const bf16* w;
+  const bf16* w;                      // row-major [N][K], or fragment tiles (w_packed)
   int64_t N, K;
   int32_t ntok;
+  int32_t w_packed;
   int32_t n_ks, n_workers;            // grid = n_ks x n_workers workgroups
   int32_t total_steps, ks_steps;      // k-steps of 32 in K; max per K-slice
   int32_t n_wtiles, n_tiles;          // W row tiles (ceil(N / 16)); all tiles incl. adapter rows
@@ -349,8 +351,17 @@ __device__ __forceinline__ u32x4 ldg16(const void* p) {
 
 // W fragment of k-step s of a K-slice with `n` steps; steps past the end read
 // the slice's last step again (in bounds).  The caller zeroes them.
+// SS: elements between consecutive k-steps (32 for a row-major row, 512 for
+// fragment tiles).
+template <int SS>
 __device__ __forceinline__ u32x4 ld_w_step(const bf16* wp, int s, int n) {
-  return ldg16(wp + 32 * (s < n ? s : n - 1));
+  return ldg16(wp + SS * (s < n ? s : n - 1));
+}
+
+template <int SS, int D>
+__device__ __forceinline__ void issue_w(u32x4 (&w)[D], const bf16* wp, int n) {
+#pragma unroll
+  for (int d = 0; d < D; ++d) w[d] = ld_w_step<SS>(wp, d, n);
 }
 
 // W (one row per lane, k-group per lane quarter) streamed D steps at a time,
@@ -360,7 +371,7 @@ __device__ __forceinline__ u32x4 ld_w_step(const bf16* wp, int s, int n) {
 // read from LDS (fragment order: step s, tile t at xl + (s * TT + t) *
 // tstride).  The caller has already issued the first group into w[].  nsteps
 // (a multiple of D) are run; W steps from nw on contribute zero.
-template <int TT, int D>
+template <int TT, int D, int SS>
 __device__ __forceinline__ void kloop_lds(f32x4 (&acc)[TT], u32x4 (&w)[D], const bf16* wp, const bf16* xl,
                                           int tstride, int nsteps, int nw) {
   const int niter = (nsteps + D - 1) / D;
@@ -368,7 +379,7 @@ __device__ __forceinline__ void kloop_lds(f32x4 (&acc)[TT], u32x4 (&w)[D], const
     const int base = it * D;
     if (it > 0) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) w[d] = ld_w_step(wp, base + d, nw);
+      for (int d = 0; d < D; ++d) w[d] = ld_w_step<SS>(wp, base + d, nw);
     }
 #pragma unroll
     for (int d = 0; d < D; ++d) {
@@ -455,6 +466,10 @@ __device__ __forceinline__ const bf16* tile_rows(const SplitArgs& a, int tile, i
   const bf16* row;
   grp = -1;
   qrow0 = 0;
+  if (tile < a.n_wtiles && a.w_packed) {
+    // fragment tiles: this lane's 16 bytes of the slice's first k-step block
+    return a.w + ((int64_t)tile * a.total_steps + (kbeg >> 5)) * 512 + 8 * lane;
+  }
   if (tile < a.n_wtiles) {
     const int64_t r = (int64_t)tile * 16 + (lane & 15);
     row = a.w + (r < a.N ? r : a.N - 1) * a.K;
@@ -491,10 +506,14 @@ __global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(Spli
   int grp = -1, qrow0 = 0;
   const bf16* wp = nullptr;
   u32x4 w[kKDepth];
+  // fragment-tile W: k-steps 512 elements apart (uniform per tile)
+  auto packed = [&](int t) { return a.w_packed && t < a.n_wtiles; };
   if (tile < a.n_tiles) {
     wp = tile_rows(a, tile, lane, kbeg, grp, qrow0);
-#pragma unroll
-    for (int d = 0; d < kKDepth; ++d) w[d] = ld_w_step(wp, d, nst);
+    if (packed(tile))
+      issue_w<512>(w, wp, nst);
+    else
+      issue_w<32>(w, wp, nst);
   }
 
   // Stage the activation K-slice in LDS in MFMA B-fragment order: block
@@ -558,14 +577,19 @@ __global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(Spli
     f32x4 acc[TT];
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    kloop_lds<TT, kKDepth>(acc, w, wp, xl, 512, npad, nst);
+    if (packed(tile))
+      kloop_lds<TT, kKDepth, 512>(acc, w, wp, xl, 512, npad, nst);
+    else
+      kloop_lds<TT, kKDepth, 32>(acc, w, wp, xl, 512, npad, nst);
 
     const int cur = tile, cgrp = grp, cq = qrow0;
     tile += tstride;
     if (tile < a.n_tiles) {
       wp = tile_rows(a, tile, lane, kbeg, grp, qrow0);
-#pragma unroll
-      for (int d = 0; d < kKDepth; ++d) w[d] = ld_w_step(wp, d, nst);
+      if (packed(tile))
+        issue_w<512>(w, wp, nst);
+      else
+        issue_w<32>(w, wp, nst);
     }
 
     if (cgrp < 0) {
@@ -1312,6 +1336,23 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const flo
   tok_out(a, s)[hqi * 128 + d] = f2bf(L > 0.f ? O / L : 0.f);
 }
 
+// Fragment-tile packing of a row-major W [N][K]: output 16-byte chunk c =
+// ((tile * steps + step) * 64 + lane) holds row tile * 16 + lane % 16,
+// columns step * 32 + 8 (lane / 16) .. + 7 (zero past row N).
+__global__ __launch_bounds__(256) void pack_weight_kernel(const bf16* w, int64_t N, int64_t K, u32x4* out,
+                                                         int64_t nchunks) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= nchunks) return;
+  const int64_t steps = K >> 5;
+  const int lane = (int)(c & 63);
+  const int64_t ts = c >> 6;
+  const int64_t tile = ts / steps, step = ts - tile * steps;
+  const int64_t r = tile * 16 + (lane & 15);
+  u32x4 v = u32x4{0u, 0u, 0u, 0u};
+  if (r < N) v = ldg16(w + r * K + step * 32 + 8 * (lane >> 4));
+  out[c] = v;
+}
+
 __global__ void zero_blocks_kernel(bf16* cache, const int64_t* ids, int64_t nblocks, int64_t block_elems) {
   const int64_t b = blockIdx.x;
   if (b >= nblocks) return;
@@ -1599,11 +1640,10 @@ int scratch_get(size_t need, hipStream_t stream, void** out) {
 
 // ---------------------------------------------------------- launch timer
 // Optional HIP-event timing of the decode projection: when armed, every
-// launch_skinny call (outside graph capture) records HIP events on its own
-// stream right before and after its base kernel and its epilogue kernel,
-// and keeps the launch's algorithmic byte count.  With the stream kept busy
-// ahead of the host (so launches run back to back) the event pairs measure
-// the kernels.  Used by benchmarks; single-threaded use only.
+// launch_skinny call (outside graph capture) launches its base kernel and
+// its epilogue kernel with start/stop events that take the dispatches' own
+// timestamps, and keeps the launch's algorithmic byte count.  Used by
+// benchmarks; single-threaded use only.
 struct LaunchTimer {
   bool armed = false;
   int cap = 0;
@@ -1624,13 +1664,16 @@ int timer_slot(hipStream_t st) {
 
 hipEvent_t timer_event(int slot, int which) { return slot >= 0 ? g_timer.ev[4 * slot + which] : nullptr; }
 
-// hipLaunchKernelGGL, bracketed by the given events when timing
+// hipLaunchKernelGGL; when timing, hipExtLaunchKernelGGL with the events
+// taking the dispatch's own start and end timestamps (no marker packets
+// around the kernel)
 template <typename K, typename... Args>
 void launch_maybe_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1,
                         Args... args) {
-  if (e0) (void)hipEventRecord(e0, st);
-  hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
-  if (e1) (void)hipEventRecord(e1, st);
+  if (e0 || e1)
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, st, e0, e1, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
 }
 
 // -------------------------------------------------------------- launchers
@@ -1760,6 +1803,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const int64_t epi_cols = mode == 2 ? N / 2 : N;
   if (fz) {
     SWL_CHECK(mode >= 0 && mode <= 3, SWL_ERR_INVALID, "round fusion: out_mode must be 0..3");
+    SWL_CHECK(fz->w_layout == 0 || fz->w_layout == 1, SWL_ERR_INVALID, "round fusion: w_layout must be 0 or 1");
     if (fz->norm_weight)
       SWL_CHECK(fz->ss_in && fz->ss_in_n >= 1 && fz->ss_in_stride >= fz->ss_in_n, SWL_ERR_INVALID,
                 "round fusion: norm_weight needs ss_in with ss_in_n >= 1 partial sums per row");
@@ -1776,6 +1820,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const int64_t total_steps = K / 32;
   SplitArgs a{};
   a.w = w;
+  a.w_packed = (fz && fz->w_layout == 1) ? 1 : 0;
   a.N = N;
   a.K = K;
   a.ntok = ntok;
@@ -2153,6 +2198,18 @@ int swl_round_ex_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
                            blk_cols, (hipStream_t)stream, fusion);
 }
 
+int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out, void* stream) {
+  SWL_CHECK(w && out, SWL_ERR_INVALID, "swl_pack_weight_bf16: null argument");
+  SWL_CHECK(n > 0 && k > 0 && k % 32 == 0, SWL_ERR_INVALID, "swl_pack_weight_bf16: k must be a positive multiple of 32");
+  SWL_CHECK((reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+            SWL_ERR_INVALID, "swl_pack_weight_bf16: w and out must be 16-byte aligned");
+  const int64_t nchunks = (n + 15) / 16 * 16 * k / 8;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     reinterpret_cast<const bf16*>(w), n, k, reinterpret_cast<u32x4*>(out), nchunks);
+  SWL_LAUNCH_CHECK("pack_weight_kernel launch");
+  return SWL_OK;
+}
+
 int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int trans_b, void* y, int64_t ldy,
                     int64_t m, int64_t n, int64_t k, float alpha, void* stream) {
   SWL_CHECK(x && b && y, SWL_ERR_INVALID, "swl_matmul_bf16: null argument");
@@ -2378,7 +2435,7 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   }
 
   const int u_ld = ((max_r * std::max(nblk, 1) + 15) / 16) * 16;  // A rows padded to 16-row tiles
-  const bool fused = fz && (fz->norm_weight || fz->out_mode != 0);
+  const bool fused = fz && (fz->norm_weight || fz->out_mode != 0 || fz->w_layout != 0);
   const int64_t out_cols = (fz && fz->out_mode == 2) ? N / 2 : N;
   if (fz && fz->out_mode == 3)
     for (int i = 0; i < n_seg; ++i)
@@ -2400,7 +2457,7 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
     return launch_skinny(reinterpret_cast<const bf16*>(w), reinterpret_cast<const bf16*>(bias), N, K, (int)T, xr, yr,
                          has_lora ? tl : nullptr, lora_table, host_entries, &L, nblk, fz, st);
   }
-  SWL_CHECK(!fused, SWL_ERR_INVALID, "round fusion: at most 64 token rows");
+  SWL_CHECK(!fused, SWL_ERR_INVALID, "round fusion / fragment-tile weights: at most 64 token rows");
 
   // ------------------------------------------------------ prefill regime
   SWL_CHECK(K % TK == 0, SWL_ERR_INVALID, "round: K must be a multiple of 64 for > 64 tokens");

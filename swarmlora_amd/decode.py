@@ -118,10 +118,13 @@ class BatchedDecoder:
     ctx_lens[w]: tokens already in worker w's KV pages; kv_fill(layer, k_cache,
     v_cache, block_tables) fills the pages (default: leave them zero).
     Capacity for `max_new` generated tokens is reserved up front.
+    packed (fused step only): projection and LM-head weights kept in the
+    fragment-tile layout (ops.PackedWeight) instead of row-major.
     """
 
     def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
-                 first_ids: List[int], device, max_new: int = 64, kv_fill=None, fused: bool = True):
+                 first_ids: List[int], device, max_new: int = 64, kv_fill=None, fused: bool = True,
+                 packed: bool = True):
         self.shape = s = shape
         self.device = dev = torch.device(device)
         self.W = W = len(ctx_lens)
@@ -133,6 +136,7 @@ class BatchedDecoder:
         self.steps_done = 0
         self.graph = None
         self.fused = fused
+        self.packed = packed and fused
         if fused:
             self._init_fused(weights, adapters, ctx_lens, first_ids, kv_fill)
             return
@@ -226,18 +230,19 @@ class BatchedDecoder:
         s, dev, W = self.shape, self.device, self.W
         self.layers_w = []
         self.norms = []
+        keep = ops.pack_weight if self.packed else (lambda t: t)  # noqa: E731
         for lw in weights["layers"]:
             t = {k: v.to(dev) for k, v in lw.items()}
             self.layers_w.append({
-                "qkv": torch.cat([t["q"], t["k"], t["v"]], 0).contiguous(),
-                "o": t["o"].contiguous(),
-                "gu": torch.cat([t["gate"], t["up"]], 0).contiguous(),
-                "down": t["down"].contiguous(),
+                "qkv": keep(torch.cat([t["q"], t["k"], t["v"]], 0).contiguous()),
+                "o": keep(t["o"].contiguous()),
+                "gu": keep(torch.cat([t["gate"], t["up"]], 0).contiguous()),
+                "down": keep(t["down"].contiguous()),
             })
             self.norms.append((t["input_norm"].contiguous(), t["post_norm"].contiguous()))
             del t
         self.embed = weights["embed"].to(dev).contiguous()
-        self.lm_head = weights["lm_head"].to(dev).contiguous()
+        self.lm_head = keep(weights["lm_head"].to(dev).contiguous())
         self.final_norm = weights["final_norm"].to(dev).contiguous()
 
         # adapters: one table entry per (worker, layer, fused projection)
@@ -284,14 +289,15 @@ class BatchedDecoder:
             kv = dict(k_cache=self.kv.key_caches[li], v_cache=self.kv.value_caches[li], hq=s.heads, hkv=s.kv_heads,
                       block_table=self.block_tables, cache_seqlens=self.seqlens, positions=self.positions,
                       cos_sin=self.cos_sin)
+            wl = 1 if self.packed else 0
             plan = (
                 ("qkv", rows(self.x0) if li == 0 else rows(self.h), rows(self.qkv),
-                 ops.round_fusion(out_mode=3, **kv) if li == 0 else
-                 ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, out_mode=3, **kv)),
-                ("o", rows(self.attn), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_o)),
+                 ops.round_fusion(out_mode=3, w_layout=wl, **kv) if li == 0 else
+                 ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, out_mode=3, w_layout=wl, **kv)),
+                ("o", rows(self.attn), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_o, w_layout=wl)),
                 ("gu", rows(self.h), rows(self.act),
-                 ops.round_fusion(norm_weight=post_norm, eps=s.eps, ss_in=self.ss_o, out_mode=2)),
-                ("down", rows(self.act), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_d)),
+                 ops.round_fusion(norm_weight=post_norm, eps=s.eps, ss_in=self.ss_o, out_mode=2, w_layout=wl)),
+                ("down", rows(self.act), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_d, w_layout=wl)),
             )
             layer_calls = []
             for g, xin, yout, fz in plan:
@@ -300,7 +306,7 @@ class BatchedDecoder:
                                        out_div=2 if fz.out_mode == 2 else 1)
                 layer_calls.append((args, fz))
             self._calls.append(layer_calls)
-        lm_fz = ops.round_fusion(norm_weight=self.final_norm, eps=s.eps, ss_in=self.ss_d)
+        lm_fz = ops.round_fusion(norm_weight=self.final_norm, eps=s.eps, ss_in=self.ss_d, w_layout=1 if self.packed else 0)
         self._lm_call = (ops._round_args(rows(self.h), rows(self.logits), one, self.lm_head, None, None, None, None),
                          lm_fz)
         self._scale = 1.0 / (s.head_dim ** 0.5)

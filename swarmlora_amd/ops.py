@@ -162,8 +162,42 @@ class LoraTable:
         return len(self._entries)
 
 
+class PackedWeight:
+    """Fragment-tile copy of a row-major weight [n, k] for decode-shaped
+    rounds (swl_pack_weight_bf16): 16-row tiles stored whole, k-step by
+    k-step, each k-step block the MFMA A operand of those rows.  `data` is
+    flat bf16 of ceil(n / 16) * 16 * k elements."""
+
+    def __init__(self, w: torch.Tensor):
+        _need(w, "w")
+        if w.dim() != 2 or not w.is_contiguous():
+            raise ValueError("w must be a contiguous [n, k] matrix")
+        self.n, self.k = w.shape
+        if self.k % 32:
+            raise ValueError("k must be a multiple of 32")
+        self.data = torch.empty((self.n + 15) // 16 * 16 * self.k, dtype=BF16, device=w.device)
+        _lib.check(_lib.load().swl_pack_weight_bf16(_ptr(w), self.n, self.k, _ptr(self.data), _stream()))
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    def data_ptr(self):
+        return self.data.data_ptr()
+
+
+def pack_weight(w: torch.Tensor) -> PackedWeight:
+    """Fragment-tile copy of w [n, k] (see PackedWeight)."""
+    return PackedWeight(w)
+
+
 def _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols, out_div=1):
-    _need(w, "w")
+    if not isinstance(w, PackedWeight):
+        _need(w, "w")
     n, k = w.shape
     if len(seg_in) != len(rows) or len(seg_out) != len(rows):
         raise ValueError("one input, output and row count per segment")
@@ -200,6 +234,8 @@ def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor],
                 seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
                 blk_cols: Optional[Sequence[int]] = None):
     """One gather -> GEMM -> (+LoRA) -> scatter round over slot buffers."""
+    if isinstance(w, PackedWeight):
+        return round_ex(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols)
     args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols)
     _lib.check(_lib.load().swl_round_bf16(*args, _stream()))
 
@@ -212,12 +248,15 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
                  k_cache: Optional[torch.Tensor] = None, v_cache: Optional[torch.Tensor] = None, hq: int = 0,
                  hkv: int = 0, block_table: Optional[torch.Tensor] = None,
                  cache_seqlens: Optional[torch.Tensor] = None, positions: Optional[torch.Tensor] = None,
-                 cos_sin: Optional[torch.Tensor] = None) -> RoundFusion:
+                 cos_sin: Optional[torch.Tensor] = None, w_layout: int = 0) -> RoundFusion:
     """swl_round_fusion for round_ex (include/swl.h documents each mode).
     ss_in / ss_out: fp32 [ntok, n_partial] (n_partial = ceil(n / 256) of the
     producing round); the record keeps the tensors it points to alive."""
     f = RoundFusion()
     keep = []
+    if w_layout not in (0, 1):
+        raise ValueError("w_layout must be 0 (row-major) or 1 (fragment tiles)")
+    f.w_layout = w_layout
     if norm_weight is not None:
         _need(norm_weight, "norm_weight")
         _need(ss_in, "ss_in", torch.float32)
@@ -262,7 +301,15 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
              w: torch.Tensor, bias: Optional[torch.Tensor] = None,
              seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
              blk_cols: Optional[Sequence[int]] = None, fusion: Optional[RoundFusion] = None):
-    """round_fused with the decode-step fusions of `fusion` (round_fusion())."""
+    """round_fused with the decode-step fusions of `fusion` (round_fusion()).
+    A PackedWeight w sets the fusion's w_layout to 1 (decode-shaped rounds
+    only)."""
+    if isinstance(w, PackedWeight):
+        if fusion is None:
+            fusion = RoundFusion()
+        fusion.w_layout = 1
+    elif fusion is not None and fusion.w_layout != 0:
+        raise ValueError("fusion.w_layout = 1 needs a PackedWeight")
     args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols,
                        out_div=2 if fusion is not None and fusion.out_mode == 2 else 1)
     _lib.check(_lib.load().swl_round_ex_bf16(*args, ctypes.byref(fusion) if fusion is not None else None,

@@ -1,0 +1,130 @@
+"""GPU tests of the fragment-tile weight layout (swl_pack_weight_bf16,
+swl_round_fusion.w_layout, include/swl.h).
+
+The packing is a pure permutation, checked bit-exactly against the layout
+restated with torch indexing on the CPU.  A round over the packed weight
+multiplies the same numbers in the same order as the row-major round, so its
+outputs are checked bit-identical to the row-major round's (shapes with N not
+a multiple of 16, LoRA adapters, the norm-on-staging and residual fusions),
+and against the oracle at the usual tolerance.
+"""
+
+import pytest
+import torch
+
+from oracle import reference_path as ref
+from tests._util import BF16, SEED_W, SEED_X, assert_close, bits_equal, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from swarmlora_amd import ops
+    return ops
+
+
+def _pack_cpu(w: torch.Tensor) -> torch.Tensor:
+    """Fragment tiles of w [n, k]: [tile][step][lane][8], lane l holding row
+    16 * tile + l % 16 and columns 32 * step + 8 * (l // 16) .. + 7."""
+    n, k = w.shape
+    tiles = (n + 15) // 16
+    wp = torch.zeros(tiles * 16, k, dtype=w.dtype)
+    wp[:n] = w
+    # [tile, r, step, q, e] -> [tile, step, q, r, e] (lane = q * 16 + r)
+    v = wp.view(tiles, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4)
+    return v.contiguous().view(-1)
+
+
+@pytest.mark.parametrize("n,k", [(64, 64), (40, 96), (4096, 4096), (1000, 14336)])
+def test_pack_is_the_fragment_permutation(dev, n, k):
+    ops = _ops()
+    w = randn((n, k), SEED_W + n, std=0.02)
+    pw = ops.pack_weight(w.to(dev))
+    torch.cuda.synchronize()
+    assert pw.shape == (n, k)
+    assert bits_equal(pw.data.cpu(), _pack_cpu(w))
+
+
+def _table(dev, in_dim, out_dims, n, r=16, scale=2.0):
+    ops = _ops()
+    table = ops.LoraTable(dev)
+    ads = []
+    for i in range(n):
+        blocks = [(randn((r, in_dim), 9000 + 10 * i + 2 * j, std=0.02),
+                   randn((od, r), 9000 + 10 * i + 2 * j + 1, std=0.02)) for j, od in enumerate(out_dims)]
+        table.add(torch.cat([A for A, _ in blocks], 0).contiguous().to(dev), [B.contiguous().to(dev) for _, B in blocks],
+                  r, scale)
+        ads.append([(A, B, scale) for A, B in blocks])
+    return table, ads
+
+
+@pytest.mark.parametrize("T,in_dim,out_dims,lora", [
+    (28, 4096, [4096, 1024, 1024], True),   # QKV with adapters
+    (1, 4096, [4096], False),
+    (5, 256, [200], True),                  # N not a multiple of 16
+    (64, 512, [96, 96], True),              # 4 token tiles
+    (17, 14336, [4096], False),             # long K (Down shape)
+])
+def test_packed_round_matches_row_major_bitwise(dev, T, in_dim, out_dims, lora):
+    ops = _ops()
+    n = sum(out_dims)
+    w = randn((n, in_dim), SEED_W, std=0.02)
+    xs = [randn((1, in_dim), SEED_X * 100 + i) for i in range(T)]
+    table, ads = _table(dev, in_dim, out_dims, 3) if lora else (None, None)
+    ids = [i % 3 for i in range(T)] if lora else None
+    kw = dict(seg_lora=ids, table=table, blk_cols=out_dims) if lora else {}
+    wd = w.to(dev)
+    pw = ops.pack_weight(wd)
+    got_rm = [torch.zeros(1, n, dtype=BF16, device=dev) for _ in range(T)]
+    got_pk = [torch.zeros(1, n, dtype=BF16, device=dev) for _ in range(T)]
+    xd = [x.to(dev) for x in xs]
+    ops.round_fused(xd, got_rm, [1] * T, wd, None, **kw)
+    ops.round_ex(xd, got_pk, [1] * T, pw, None, **kw)
+    torch.cuda.synchronize()
+    for i in range(T):
+        assert bits_equal(got_pk[i].cpu(), got_rm[i].cpu()), f"token {i}"
+    op = {3: ref.OP_QKV_FUSED, 2: ref.OP_GATE_UP_FUSED}.get(len(out_dims), ref.OP_O_PROJ)
+    want = ref.round_with_lora(op, xs, [1] * T, w, [ads[j] for j in ids] if lora else [None] * T, out_dims)
+    for i in range(T):
+        assert_close(got_pk[i].cpu(), want[i], what=f"token {i}")
+
+
+def test_packed_round_with_norm_and_residual_fusions(dev):
+    """Fused forms over packed weights equal the same fusions over row-major
+    weights bit for bit."""
+    ops = _ops()
+    H, T = 4096, 28
+    w = randn((H, H), SEED_W + 1, std=0.02)
+    gamma = (1 + randn((H,), 77, std=0.1).float()).to(BF16).to(dev)
+    hs = torch.cat([randn((1, H), SEED_X + i, std=3.0) for i in range(T)], 0).to(dev)
+    ss = torch.stack([hs.float()[:, j:j + 256].pow(2).sum(1) for j in range(0, H, 256)], 1).contiguous()
+    wd = w.to(dev)
+    pw = ops.pack_weight(wd)
+    outs = []
+    for wt, layout in ((wd, 0), (pw, 1)):
+        h2 = hs.clone()
+        ss_out = torch.zeros(T, 16, dtype=torch.float32, device=dev)
+        y = [torch.zeros(1, H, dtype=BF16, device=dev) for _ in range(T)]
+        ops.round_ex([hs[i:i + 1] for i in range(T)], y, [1] * T, wt, None,
+                     fusion=ops.round_fusion(norm_weight=gamma, eps=1e-5, ss_in=ss, w_layout=layout))
+        ops.round_ex([y[i] for i in range(T)], [h2[i:i + 1] for i in range(T)], [1] * T, wt, None,
+                     fusion=ops.round_fusion(out_mode=1, ss_out=ss_out, w_layout=layout))
+        torch.cuda.synchronize()
+        outs.append((torch.cat(y, 0).cpu(), h2.cpu(), ss_out.cpu()))
+    assert bits_equal(outs[0][0], outs[1][0])
+    assert bits_equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][2], outs[1][2])
+
+
+def test_packed_weight_rejected_where_unsupported(dev):
+    ops = _ops()
+    w = randn((64, 64), 5).to(dev)
+    pw = ops.pack_weight(w)
+    xs = [torch.zeros(65, 64, dtype=BF16, device=dev)]
+    ys = [torch.zeros(65, 64, dtype=BF16, device=dev)]
+    with pytest.raises(RuntimeError, match="at most 64 token rows"):
+        ops.round_ex(xs, ys, [65], pw)
+    with pytest.raises(ValueError, match="PackedWeight"):
+        ops.round_ex(xs, ys, [1], w, fusion=ops.round_fusion(w_layout=1))
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ops.pack_weight(torch.zeros(16, 48, dtype=BF16, device=dev))
