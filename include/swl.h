@@ -253,10 +253,10 @@ int swl_sample_bf16(const void* logits, int64_t n, int64_t vocab, void* const* o
 /* ------------------------------------------------------ launch timer ----
  * Benchmark instrumentation (no counterpart in the reference).  After
  * swl_timer_arm(capacity), each decode-shaped projection (a round or gemm of
- * at most 64 token rows) launched outside graph capture records HIP events
- * on its stream right before and after its base kernel and its epilogue
- * kernel, for up to `capacity` launches (keep the stream busy ahead of the
- * host so the launches run back to back and the pairs time the kernels).  swl_timer_collect waits for them, disarms, and returns per
+ * at most 64 token rows) launched outside graph capture launches its base
+ * kernel and its epilogue kernel with start/stop HIP events that take the
+ * dispatches' own begin/end timestamps (hipExtLaunchKernelGGL), for up to
+ * `capacity` launches.  swl_timer_collect waits for them, disarms, and returns per
  * launch: base/epilogue milliseconds, N, K, token rows and the base kernel's
  * algorithmic bytes (W + token rows + distinct stacked LoRA A).
  * Single-threaded use only. */

@@ -1501,12 +1501,33 @@ __global__ __launch_bounds__(1024) void sample_kernel(SampleArgs a) {
   const int row = blockIdx.x;
   const bf16* lg = a.logits + (int64_t)row * a.vocab;
   const int64_t V = a.vocab;
-  // argmax with first-index tie break: key = (fkey(v) << 32) | ~index
+  // argmax with first-index tie break: key = (fkey(v) << 32) | ~index.
+  // 16-byte loads (8 logits), four per thread in flight, when the row is
+  // 16-byte aligned; scalar loads for the rest.
   unsigned long long best = 0;
-  for (int64_t i = threadIdx.x; i < V; i += blockDim.x) {
-    const unsigned long long k = ((unsigned long long)fkey(bf2f(lg[i])) << 32) | (uint32_t)(~(uint32_t)i);
+  auto take = [&](float v, int64_t i) {
+    const unsigned long long k = ((unsigned long long)fkey(v) << 32) | (uint32_t)(~(uint32_t)i);
     best = k > best ? k : best;
+  };
+  const int64_t nv = (reinterpret_cast<uintptr_t>(lg) & 15) == 0 ? V / 8 : 0;
+  for (int64_t j0 = threadIdx.x; j0 < nv; j0 += 4 * (int64_t)blockDim.x) {
+    u32x4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = j0 + u * (int64_t)blockDim.x;
+      q[u] = j < nv ? ldg16(lg + 8 * j) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = j0 + u * (int64_t)blockDim.x;
+      if (j >= nv) break;
+      float f[8];
+      unpack8(q[u], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) take(f[e], 8 * j + e);
+    }
   }
+  for (int64_t i = 8 * nv + threadIdx.x; i < V; i += blockDim.x) take(bf2f(lg[i]), i);
   best = block_reduce<unsigned long long>(best, [](unsigned long long x, unsigned long long y) { return x > y ? x : y; }, shl);
   const int64_t amax = (int64_t)(~(uint32_t)(best & 0xffffffffull));
   if (!a.do_sample[row]) {
