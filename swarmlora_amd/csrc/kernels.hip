@@ -1297,21 +1297,23 @@ __global__ __launch_bounds__(WAVES * 64) void attn_chunk_kernel(AttnArgs a, floa
 }
 
 // Merges the chunk records of one (sequence, query head): out = sum_c o_c
-// e^(m_c - M) / sum_c l_c e^(m_c - M).
+// e^(m_c - M) / sum_c l_c e^(m_c - M).  Records are read 16 chunks at a
+// time with every load of a batch in flight together (one batch covers
+// 16 chunks of the context).
 __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const float* part, int maxch, int G, int C) {
+  constexpr int B = 16;
   const int s = blockIdx.y, hqi = blockIdx.x;
   const int h = hqi / G, g = hqi - h * G;
   const int d = threadIdx.x;
   const int64_t ctx = (int64_t)a.seqlens[s] + 1;
-  const int nch = (int)((ctx + C - 1) / C);
+  const int nch = (int)min<int64_t>((ctx + C - 1) / C, maxch);  // contexts past the block table: records end there
   const float* rec = part + ((int64_t)s * a.hkv + h) * maxch * G * kAttnRec + g * kAttnRec;
   const int64_t cstride = (int64_t)G * kAttnRec;
-  // loads issued 8 chunks at a time
   float M = -INFINITY, L = 0.f, O = 0.f;
-  for (int c0 = 0; c0 < nch; c0 += 8) {
-    float m[8], l[8], o[8];
+  for (int c0 = 0; c0 < nch; c0 += B) {
+    float m[B], l[B], o[B];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < B; ++j) {
       const int c = c0 + j < nch ? c0 + j : nch - 1;
       m[j] = rec[c * cstride];
       l[j] = rec[c * cstride + 1];
@@ -1319,13 +1321,13 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const flo
     }
     float mn = M;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < B; ++j)
       if (c0 + j < nch) mn = fmaxf(mn, m[j]);
     const float corr = (M == -INFINITY) ? 0.f : __expf(M - mn);
     L *= corr;
     O *= corr;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < B; ++j) {
       if (c0 + j >= nch) break;
       const float e = __expf(m[j] - mn);
       L += l[j] * e;
@@ -1334,6 +1336,227 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const flo
     M = mn;
   }
   tok_out(a, s)[hqi * 128 + d] = f2bf(L > 0.f ? O / L : 0.f);
+}
+
+// ---- decode attention over whole pages (flash-decoding by parts) --------
+// One workgroup of W waves per (kv head, part of a sequence); wave w takes
+// the part's tiles of 16 keys (a page, or a 16-key slice of one) w, w + W,
+// ... and streams them into its own LDS ring with LDS-DMA, S tiles deep, so
+// waves never wait on each other inside the loop.  K is stored group-major
+// ([16-byte dim group][key]: the 16 keys of an MFMA operand read sit in
+// distinct banks), V key-major ([key][dims]).  Scores of the G query heads
+// on MFMA (the 16 K rows as the A operand, q as the B operand, 16x16x32
+// over 4 steps of 32 dims), then online softmax and P.V in-lane (lane group
+// = query head, 8 dims a lane).  The W waves' partial results are merged in
+// LDS into one record (max, sum, unnormalised output) per (part, query
+// head); attn_combine_kernel merges the parts.  Keys past the context are
+// masked and their V rows never read.
+constexpr int kTileKeys = 16;
+constexpr int kTileBytes = 2 * kTileKeys * 256;  // one head's K and V rows of a tile
+
+__host__ __device__ constexpr unsigned wait_vm_imm(int n) {
+  return 0x0F70u | (unsigned)(n & 15) | ((unsigned)(n >> 4) << 14);
+}
+
+template <int G, int S, int W>
+__global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* part, int maxparts, int tpp) {
+  constexpr int GL = G < 4 ? G : 4;  // lane groups with a query head
+  constexpr int HPG = G / GL;        // query heads per lane group
+  constexpr int WAVE_LDS = S * kTileBytes + G * kTileKeys * 4;
+  static_assert(W * S * kTileBytes >= W * G * kAttnRec * 4, "merge area must fit in the rings");
+  __shared__ __attribute__((aligned(16))) char lds[W * WAVE_LDS];
+  const int h = blockIdx.x, p = blockIdx.y, s = blockIdx.z;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t ctx = (int64_t)a.seqlens[s] + 1;
+  const int64_t ntiles = (ctx + kTileKeys - 1) / kTileKeys;
+  const int64_t tb = (int64_t)p * tpp;  // first tile of the part
+  if (tb >= ntiles) return;             // uniform over the workgroup
+  const int nt = (int)min<int64_t>(tpp, ntiles - tb);
+  const int ntw = nt > w ? (nt - w + W - 1) / W : 0;  // this wave's tiles: w + j W
+  char* ring = lds + w * WAVE_LDS;
+  float* sc = reinterpret_cast<float*>(ring + S * kTileBytes);
+
+  // key row 0 of each tile of the part (lane t holds tile t's), head h
+  const int32_t* bt = a.bt + (int64_t)s * a.max_blocks;
+  const int64_t krow = (int64_t)a.hkv * 128;
+  int64_t tile_base = 0;
+  if (lane < nt) {
+    const int64_t key0 = (tb + lane) * kTileKeys;
+    int64_t bi, ip;
+    if (a.bs_shift >= 0) {
+      bi = key0 >> a.bs_shift;
+      ip = key0 & (a.bs - 1);
+    } else {
+      bi = key0 / a.bs;
+      ip = key0 - bi * a.bs;
+    }
+    int32_t blk = bi < a.max_blocks ? bt[bi] : 0;
+    blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;
+    tile_base = ((int64_t)blk * a.bs + ip) * krow + (int64_t)h * 128;
+  }
+  // K: instruction i, lane c -> key c % 16, dim group 4 i + c / 16 (LDS
+  // offset group * 256 + key * 16); V: key 4 i + c / 16, group c % 16 (LDS
+  // offset key * 256 + group * 16)
+  const int64_t koff = (int64_t)(lane & 15) * krow + 8 * (lane >> 4);
+  const int64_t voff = (int64_t)(lane >> 4) * krow + 8 * (lane & 15);
+  auto issue = [&](int j) {  // this wave's j-th tile into ring slot j % S
+    const int t = w + j * W;
+    const int64_t base = (int64_t)(uint32_t)__builtin_amdgcn_readlane((int)(tile_base & 0xffffffff), t) |
+                         ((int64_t)__builtin_amdgcn_readlane((int)(tile_base >> 32), t) << 32);
+    char* dst = ring + (j % S) * kTileBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(a.kc + base + koff + 32 * i), (lds_ptr)(dst + i * 1024), 16, 0,
+                                       0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(a.vc + base + voff + 4 * i * krow),
+                                       (lds_ptr)(dst + 4096 + i * 1024), 16, 0, 0);
+  };
+
+  // q of the G query heads as the MFMA B operand: lane l holds column l % 16
+  // (query head, zero past G), dims 32 * step + 8 (l / 16) .. + 7
+  u32x4 qf[4];
+  {
+    const int col = lane & 15;
+    const bf16* qp = tok_q(a, s) + (int64_t)(h * G + (col < G ? col : 0)) * 128 + 8 * (lane >> 4);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qf[st] = col < G ? ldg16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+#pragma unroll
+  for (int j = 0; j < S; ++j)
+    if (j < ntw) issue(j);
+
+  const int gg = lane >> 4;  // lane group: query heads gg * HPG ..
+  float m[HPG], l[HPG], acc[HPG][8];
+#pragma unroll
+  for (int j = 0; j < HPG; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[j][d] = 0.f;
+  }
+
+  for (int j = 0; j < ntw; ++j) {
+    switch (min(S - 1, ntw - 1 - j)) {  // tiles issued after j: 8 DMA each
+      case 3: __builtin_amdgcn_s_waitcnt(wait_vm_imm(24)); break;
+      case 2: __builtin_amdgcn_s_waitcnt(wait_vm_imm(16)); break;
+      case 1: __builtin_amdgcn_s_waitcnt(wait_vm_imm(8)); break;
+      default: __builtin_amdgcn_s_waitcnt(wait_vm_imm(0)); break;
+    }
+    const char* kb = ring + (j % S) * kTileBytes;
+    const char* vb = kb + 4096;
+    const int64_t k0 = (tb + w + (int64_t)j * W) * kTileKeys;
+    const int nk = (int)min<int64_t>(kTileKeys, ctx - k0);  // valid keys of the tile
+
+    // scores: S[key 4 (l / 16) + i][query head l % 16]
+    f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (st * 4 + gg) * 256 + (lane & 15) * 16);
+      sv = mfma16(kf, qf[st], sv);
+    }
+    if ((lane & 15) < G) {
+      f32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (4 * gg + i < nk) ? sv[i] * a.scale : -INFINITY;
+      *reinterpret_cast<f32x4*>(sc + (lane & 15) * kTileKeys + 4 * gg) = o;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // online softmax of the lane group's query heads over the tile's keys
+    float pr[HPG][kTileKeys];
+#pragma unroll
+    for (int e = 0; e < HPG; ++e) {
+      const int g = gg < GL ? gg * HPG + e : 0;
+      float x[kTileKeys];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(sc + g * kTileKeys + 4 * q);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * q + i] = v4[i];
+      }
+      float mx = x[0];
+#pragma unroll
+      for (int k = 1; k < kTileKeys; ++k) mx = fmaxf(mx, x[k]);
+      const float mn = fmaxf(m[e], mx);
+      const float corr = __expf(m[e] - mn);
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < kTileKeys; ++k) {
+        pr[e][k] = __expf(x[k] - mn);
+        sum += pr[e][k];
+      }
+      l[e] = l[e] * corr + sum;
+      m[e] = mn;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[e][d] *= corr;
+    }
+    // P.V over the valid keys: a full tile unrolled (all V reads in flight
+    // together), the context's last tile key by key
+    auto pv = [&](int k) {
+      float vf[8];
+      unpack8(*reinterpret_cast<const u32x4*>(vb + k * 256 + (lane & 15) * 16), vf);
+#pragma unroll
+      for (int e = 0; e < HPG; ++e)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[e][d] += pr[e][k] * vf[d];
+    };
+    if (nk == kTileKeys) {
+#pragma unroll
+      for (int k = 0; k < kTileKeys; ++k) pv(k);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kTileKeys; ++k) {
+        if (k >= nk) break;
+        pv(k);
+      }
+    }
+    // every lane's LDS reads of this slot are done before it is refilled
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    if (j + S < ntw) issue(j + S);
+  }
+
+  // merge the W waves (all their DMA has landed) in LDS over the rings
+  float* mg = reinterpret_cast<float*>(lds);  // [W][G][kAttnRec]
+  if (W > 1) __syncthreads();
+  if (gg < GL) {
+#pragma unroll
+    for (int e = 0; e < HPG; ++e) {
+      float* r = mg + (w * G + gg * HPG + e) * kAttnRec;
+      if ((lane & 15) == 0) {
+        r[0] = m[e];
+        r[1] = l[e];
+      }
+#pragma unroll
+      for (int d = 0; d < 8; ++d) r[2 + (lane & 15) * 8 + d] = acc[e][d];
+    }
+  }
+  __syncthreads();
+  for (int it = threadIdx.x; it < G * 128; it += 64 * W) {
+    const int g = it >> 7, d = it & 127;
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < W; ++v) M = fmaxf(M, mg[(v * G + g) * kAttnRec]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {
+      const float* r = mg + (v * G + g) * kAttnRec;
+      const float c = r[0] == -INFINITY ? 0.f : __expf(r[0] - M);
+      L += r[1] * c;
+      O += r[2 + d] * c;
+    }
+    float* rec = part + ((((int64_t)s * a.hkv + h) * maxparts + p) * G + g) * kAttnRec;
+    if (d == 0) {
+      rec[0] = M;
+      rec[1] = L;
+    }
+    rec[2 + d] = O;
+  }
 }
 
 // Fragment-tile packing of a row-major W [N][K]: output 16-byte chunk c =
@@ -2071,11 +2294,85 @@ int launch_attn_decode_u(const AttnArgs& a, hipStream_t st) {
   }
 }
 
+// Page-streaming decode attention geometry: waves per workgroup (W, 1 2 4
+// or 8), tiles of 16 keys per part (SWL_ATTN_TPP), LDS ring depth per wave
+// (SWL_ATTN_STAGES, 2..4); SWL_ATTN_TILE=0 selects the per-chunk kernel.
+struct AttnTileTuning {
+  bool on = true;
+  int waves = 2, tpp = 16, stages = 2;
+};
+const AttnTileTuning& attn_tile_tuning() {
+  static AttnTileTuning t = [] {
+    AttnTileTuning v;
+    if (const char* e = getenv("SWL_ATTN_TILE")) v.on = atoi(e) != 0;
+    if (const char* e = getenv("SWL_ATTN_WAVES")) {
+      const int x = atoi(e);
+      v.waves = (x == 2 || x == 4 || x == 8) ? x : 1;
+    }
+    if (const char* e = getenv("SWL_ATTN_TPP")) v.tpp = std::max(1, std::min(64, atoi(e)));
+    if (const char* e = getenv("SWL_ATTN_STAGES")) v.stages = std::max(2, std::min(4, atoi(e)));
+    v.tpp = std::max(v.tpp, v.waves);
+    return v;
+  }();
+  return t;
+}
+
+template <int G, int S, int W>
+int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp) {
+  const int64_t max_tiles = (a.max_blocks * a.bs + kTileKeys - 1) / kTileKeys;
+  const int maxparts = (int)((max_tiles + tpp - 1) / tpp);
+  void* scratch = nullptr;
+  const size_t need = sizeof(float) * (size_t)a.nseq * a.hkv * maxparts * G * kAttnRec;
+  int rc = scratch_get(need, st, &scratch);
+  if (rc) return rc;
+  float* part = reinterpret_cast<float*>(scratch);
+  hipLaunchKernelGGL((attn_tile_kernel<G, S, W>), dim3((unsigned)a.hkv, (unsigned)maxparts, (unsigned)a.nseq),
+                     dim3(64 * W), 0, st, a, part, maxparts, tpp);
+  SWL_LAUNCH_CHECK("attn_tile_kernel launch");
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.hq, (unsigned)a.nseq), dim3(128), 0, st, a,
+                     (const float*)part, maxparts, G, kTileKeys * tpp);
+  SWL_LAUNCH_CHECK("attn_combine_kernel launch");
+  return SWL_OK;
+}
+
+template <int G, int S>
+int launch_attn_tile_s(const AttnArgs& a, hipStream_t st, const AttnTileTuning& t) {
+  switch (t.waves) {  // 8 waves only with 2 stages (LDS: 160 KiB per CU)
+    case 2: return launch_attn_tile_sw<G, S, 2>(a, st, t.tpp);
+    case 4: return launch_attn_tile_sw<G, S, 4>(a, st, t.tpp);
+    case 8: return launch_attn_tile_sw<G, S, (S == 2 ? 8 : 4)>(a, st, t.tpp);
+    default: return launch_attn_tile_sw<G, S, 1>(a, st, t.tpp);
+  }
+}
+
+template <int G>
+int launch_attn_tile(const AttnArgs& a, hipStream_t st) {
+  const AttnTileTuning& t = attn_tile_tuning();
+  switch (t.stages) {
+    case 3: return launch_attn_tile_s<G, 3>(a, st, t);
+    case 4: return launch_attn_tile_s<G, 4>(a, st, t);
+    default: return launch_attn_tile_s<G, 2>(a, st, t);
+  }
+}
+
+// The page-streaming kernel needs whole 16-key tiles inside a page.
+bool attn_tile_fits(const AttnArgs& a) {
+  return attn_tile_tuning().on && a.L == 1 && a.bs % kTileKeys == 0;
+}
+
 int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
   if (a.rope != 2) {  // 2: q rotated and k / v appended by the QKV round's epilogue
     hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L), (unsigned)(a.hq + 2 * a.hkv)), dim3(64),
                        0, st, a);
     SWL_LAUNCH_CHECK("rope_append_kernel launch");
+  }
+  if (a.L == 1 && attn_tile_fits(a)) {
+    switch (G) {
+      case 1: return launch_attn_tile<1>(a, st);
+      case 2: return launch_attn_tile<2>(a, st);
+      case 4: return launch_attn_tile<4>(a, st);
+      default: return launch_attn_tile<8>(a, st);
+    }
   }
   if (a.L == 1) {
     switch (G) {

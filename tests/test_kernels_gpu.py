@@ -283,6 +283,16 @@ def test_paged_attention_decode_gqa_groups(dev, hq, hkv):
     assert bits_equal(got_state[3], ref_state[3]), "v pages must be a bit-exact append"
 
 
+@pytest.mark.parametrize("bs", [8, 32, 48])
+def test_paged_attention_decode_block_sizes(dev, bs):
+    """Pages of 8 keys (per-chunk kernel), 32 and 48 keys (16-key tiles
+    inside a page, pages not a power of two) over contexts ending inside a
+    tile, on a tile edge and past several parts."""
+    out, want, got_state, ref_state = _attn_case(dev, 4, 1, [15, 16, 143, 1999], bs=bs, seed=9)
+    assert_close(out, want, what=f"attention bs={bs}")
+    assert bits_equal(got_state[3], ref_state[3]), "v pages must be a bit-exact append"
+
+
 def test_paged_attention_single_key_returns_v(dev):
     """ctx = 1: softmax over one key is 1, so the output is v exactly."""
     out, want, (q_d, k_d, kc_d, vc_d), _ = _attn_case(dev, 2, 1, [0, 0])
