@@ -49,6 +49,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxSeg = SWL_MAX_SLOTS;
 constexpr int kSkinnyMaxTok = 64;
@@ -1495,24 +1496,36 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
 #pragma unroll
       for (int d = 0; d < 8; ++d) acc[e][d] *= corr;
     }
-    // P.V over the valid keys: a full tile unrolled (all V reads in flight
-    // together), the context's last tile key by key
-    auto pv = [&](int k) {
-      float vf[8];
-      unpack8(*reinterpret_cast<const u32x4*>(vb + k * 256 + (lane & 15) * 16), vf);
+    // P.V over key pairs (k, k + 1): bf16 dot2 of each dim's two V values
+    // with the pair's probabilities rounded to bf16 (as flash attention's
+    // second product takes P), fp32 accumulation.  A full tile unrolled (all
+    // V reads in flight together); the context's last tile pair by pair, the
+    // V row past its end zeroed.
+    auto pv2 = [&](int k, bool second) {
+      const u32x4 w0 = *reinterpret_cast<const u32x4*>(vb + k * 256 + (lane & 15) * 16);
+      u32x4 w1 = *reinterpret_cast<const u32x4*>(vb + (k + 1) * 256 + (lane & 15) * 16);
+      if (!second) w1 = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int e = 0; e < HPG; ++e)
+      for (int e = 0; e < HPG; ++e) {
+        const bf16x2 pp = {f2bf(pr[e][k]), f2bf(second ? pr[e][k + 1] : 0.f)};
 #pragma unroll
-        for (int d = 0; d < 8; ++d) acc[e][d] += pr[e][k] * vf[d];
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = __builtin_amdgcn_perm(w1[q], w0[q], 0x05040100u);  // dim 2q of keys k, k + 1
+          const uint32_t hi = __builtin_amdgcn_perm(w1[q], w0[q], 0x07060302u);  // dim 2q + 1
+          acc[e][2 * q] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, lo), pp, acc[e][2 * q], false);
+          acc[e][2 * q + 1] =
+              __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, hi), pp, acc[e][2 * q + 1], false);
+        }
+      }
     };
     if (nk == kTileKeys) {
 #pragma unroll
-      for (int k = 0; k < kTileKeys; ++k) pv(k);
+      for (int k = 0; k < kTileKeys; k += 2) pv2(k, true);
     } else {
 #pragma unroll
-      for (int k = 0; k < kTileKeys; ++k) {
+      for (int k = 0; k < kTileKeys; k += 2) {
         if (k >= nk) break;
-        pv(k);
+        pv2(k, k + 1 < nk);
       }
     }
     // every lane's LDS reads of this slot are done before it is refilled
