@@ -1355,6 +1355,26 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const flo
 constexpr int kTileKeys = 16;
 constexpr int kTileBytes = 2 * kTileKeys * 256;  // one head's K and V rows of a tile
 
+// Max / sum over the 16 lanes of a DPP row, every lane receiving the
+// result: xor 1 and xor 2 by quad permutes, then the half-row and row
+// mirrors join the quads and the halves.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  return v + dpp_f<0x140>(v);
+}
+
 __host__ __device__ constexpr unsigned wait_vm_imm(int n) {
   return 0x0F70u | (unsigned)(n & 15) | ((unsigned)(n >> 4) << 14);
 }
@@ -1363,7 +1383,7 @@ template <int G, int S, int W>
 __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* part, int maxparts, int tpp) {
   constexpr int GL = G < 4 ? G : 4;  // lane groups with a query head
   constexpr int HPG = G / GL;        // query heads per lane group
-  constexpr int WAVE_LDS = S * kTileBytes + G * kTileKeys * 4;
+  constexpr int WAVE_LDS = S * kTileBytes + G * kTileKeys * 4 + G * kTileKeys * 2;
   static_assert(W * S * kTileBytes >= W * G * kAttnRec * 4, "merge area must fit in the rings");
   __shared__ __attribute__((aligned(16))) char lds[W * WAVE_LDS];
   const int h = blockIdx.x, p = blockIdx.y, s = blockIdx.z;
@@ -1375,7 +1395,8 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
   const int nt = (int)min<int64_t>(tpp, ntiles - tb);
   const int ntw = nt > w ? (nt - w + W - 1) / W : 0;  // this wave's tiles: w + j W
   char* ring = lds + w * WAVE_LDS;
-  float* sc = reinterpret_cast<float*>(ring + S * kTileBytes);
+  float* sc = reinterpret_cast<float*>(ring + S * kTileBytes);   // [G][16] scores
+  bf16* pb = reinterpret_cast<bf16*>(sc + G * kTileKeys);        // [G][16] probabilities
 
   // key row 0 of each tile of the part (lane t holds tile t's), head h
   const int32_t* bt = a.bt + (int64_t)s * a.max_blocks;
@@ -1468,53 +1489,57 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // online softmax of the lane group's query heads over the tile's keys
-    float pr[HPG][kTileKeys];
+    // online softmax: lane l takes key l % 16 of its lane group's query
+    // head; max and sum over the 16 lanes of the group, the probabilities
+    // rounded to bf16 into LDS for the P.V pairs
 #pragma unroll
     for (int e = 0; e < HPG; ++e) {
       const int g = gg < GL ? gg * HPG + e : 0;
-      float x[kTileKeys];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(sc + g * kTileKeys + 4 * q);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[4 * q + i] = v4[i];
-      }
-      float mx = x[0];
-#pragma unroll
-      for (int k = 1; k < kTileKeys; ++k) mx = fmaxf(mx, x[k]);
-      const float mn = fmaxf(m[e], mx);
+      const float x = sc[g * kTileKeys + (lane & 15)];
+      const float mn = fmaxf(m[e], row16_max(x));
       const float corr = __expf(m[e] - mn);
-      float sum = 0.f;
-#pragma unroll
-      for (int k = 0; k < kTileKeys; ++k) {
-        pr[e][k] = __expf(x[k] - mn);
-        sum += pr[e][k];
-      }
-      l[e] = l[e] * corr + sum;
+      const float pe = __expf(x - mn);
+      l[e] = l[e] * corr + row16_sum(pe);
       m[e] = mn;
 #pragma unroll
       for (int d = 0; d < 8; ++d) acc[e][d] *= corr;
+      if (gg < GL) pb[g * kTileKeys + (lane & 15)] = f2bf(pe);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the lane group's probabilities as bf16 pairs (keys 2i, 2i + 1)
+    uint32_t pp[HPG][kTileKeys / 2];
+#pragma unroll
+    for (int e = 0; e < HPG; ++e) {
+      const int g = gg < GL ? gg * HPG + e : 0;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(pb + g * kTileKeys);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(pb + g * kTileKeys + 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pp[e][i] = a0[i];
+        pp[e][4 + i] = a1[i];
+      }
     }
     // P.V over key pairs (k, k + 1): bf16 dot2 of each dim's two V values
-    // with the pair's probabilities rounded to bf16 (as flash attention's
-    // second product takes P), fp32 accumulation.  A full tile unrolled (all
-    // V reads in flight together); the context's last tile pair by pair, the
-    // V row past its end zeroed.
+    // with the pair's probabilities (bf16, as flash attention's second
+    // product takes P), fp32 accumulation.  A full tile unrolled (all V
+    // reads in flight together); the context's last tile pair by pair, the
+    // V row past its end zeroed (its probability is 0).
     auto pv2 = [&](int k, bool second) {
       const u32x4 w0 = *reinterpret_cast<const u32x4*>(vb + k * 256 + (lane & 15) * 16);
       u32x4 w1 = *reinterpret_cast<const u32x4*>(vb + (k + 1) * 256 + (lane & 15) * 16);
       if (!second) w1 = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int e = 0; e < HPG; ++e) {
-        const bf16x2 pp = {f2bf(pr[e][k]), f2bf(second ? pr[e][k + 1] : 0.f)};
+        const bf16x2 p2 = __builtin_bit_cast(bf16x2, pp[e][k >> 1]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t lo = __builtin_amdgcn_perm(w1[q], w0[q], 0x05040100u);  // dim 2q of keys k, k + 1
           const uint32_t hi = __builtin_amdgcn_perm(w1[q], w0[q], 0x07060302u);  // dim 2q + 1
-          acc[e][2 * q] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, lo), pp, acc[e][2 * q], false);
+          acc[e][2 * q] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, lo), p2, acc[e][2 * q], false);
           acc[e][2 * q + 1] =
-              __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, hi), pp, acc[e][2 * q + 1], false);
+              __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, hi), p2, acc[e][2 * q + 1], false);
         }
       }
     };
