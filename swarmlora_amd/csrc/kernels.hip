@@ -651,6 +651,19 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   const int lora = a.has_lora ? a.lora[tok] : -1;
   const bool vec = (a.N & 3) == 0 && (MODE != 2 || (a.inter & 3) == 0);
 
+  // values the output fusions need after the reduction, requested first:
+  // the residual element (1); the position and the cache length (3)
+  bf16* yrow = a.y[tok];
+  float hres = 0.f;
+  if constexpr (MODE == 1) {
+    if (live) hres = bf2f(yrow[n]);
+  }
+  int64_t pos = -1, slen = -1;
+  if constexpr (MODE == 3) {
+    pos = a.pos[tok];
+    slen = a.seqlens[tok];
+  }
+
   // lora_B rows of this lane's column(s) (rank <= 16, multiple of 8: registers)
   const swl_lora_entry* ep = lora >= 0 ? a.L.table + lora : nullptr;
   int r = 0, blk[C];
@@ -676,31 +689,61 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     }
   }
 
-  // partial sums of the quad(s) over K-slices kg, kg + 4, ...
+  // partial sums of the quad(s) over K-slices kg, kg + 4, ...: the first 8
+  // of each lane group requested together (all of them up to 32 K-slices)
   const int64_t kstride = (int64_t)a.ntok * a.N;
+  auto ld_part = [&](int c, int ks) {
+    f32x4 q = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int64_t qc = nq + c * a.inter;
+    if (nq < ncols && ks < a.n_ks) {
+      const float* pk = a.part + (int64_t)tok * a.N + qc + ks * kstride;
+      if (vec) {
+        q = *reinterpret_cast<const f32x4*>(pk);
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (nq + e < ncols) q[e] = pk[e];
+      }
+    }
+    return q;
+  };
+  f32x4 q0[C][8];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q0[c][j] = ld_part(c, kg + 4 * j);
+
+  // RoPE factors and the KV page slot (3), requested while the partials are
+  // in flight
+  const int d = (int)(n & 127), hh = (int)(n >> 7);
+  const bool is_q = MODE == 3 && hh < a.hq, is_k = MODE == 3 && !is_q && hh < a.hq + a.hkv;
+  float rc = 1.f, rsn = 0.f;
+  bool rot = false;
+  int64_t kv_dst = -1;
+  if constexpr (MODE == 3) {
+    if (live && (is_q || is_k) && pos >= 0 && pos < a.max_pos) {
+      rot = true;
+      rc = bf2f(a.cs[pos * 128 + (d & 63)]);
+      rsn = bf2f(a.cs[pos * 128 + 64 + (d & 63)]);
+    }
+    if (live && !is_q && slen >= 0 && slen / a.bs < a.max_blocks) {
+      const int32_t pb = a.bt[(int64_t)tok * a.max_blocks + slen / a.bs];
+      if (pb >= 0 && pb < a.num_blocks) {
+        const int kvh = is_k ? hh - a.hq : hh - a.hq - a.hkv;
+        kv_dst = ((int64_t)pb * a.bs + slen % a.bs) * a.hkv * 128 + kvh * 128 + d;
+      }
+    }
+  }
+
   f32x4 s[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     s[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int64_t qc = nq + c * a.inter;
-    if (nq >= ncols) continue;
-    const float* p = a.part + (int64_t)tok * a.N + qc;
-    for (int ks0 = kg; ks0 < a.n_ks; ks0 += 32) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[c] += q0[c][j];
+    for (int ks0 = kg + 32; ks0 < a.n_ks; ks0 += 32) {
       f32x4 q[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int ks = ks0 + 4 * j;
-        q[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (ks < a.n_ks) {
-          const float* pk = p + ks * kstride;
-          if (vec) {
-            q[j] = *reinterpret_cast<const f32x4*>(pk);
-          } else {
-            for (int e = 0; e < 4; ++e)
-              if (nq + e < ncols) q[j][e] = pk[e];
-          }
-        }
-      }
+      for (int j = 0; j < 8; ++j) q[j] = ld_part(c, ks0 + 4 * j);
 #pragma unroll
       for (int j = 0; j < 8; ++j) s[c] += q[j];
     }
@@ -765,14 +808,13 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     }
   }
 
-  bf16* yrow = a.y[tok];
   if constexpr (MODE == 0) {
     if (live) yrow[n] = f2bf(v[0]);
   } else if constexpr (MODE == 1) {
     // h = bf16(h + out); the workgroup's sum of squares of the new h
     float sq = 0.f;
     if (live) {
-      const bf16 hn = f2bf(bf2f(yrow[n]) + bf2f(f2bf(v[0])));
+      const bf16 hn = f2bf(hres + bf2f(f2bf(v[0])));
       yrow[n] = hn;
       sq = bf2f(hn) * bf2f(hn);
     }
@@ -794,27 +836,12 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     xch[cl] = x;
     __syncthreads();
     if (!live) return;
-    const int d = (int)(n & 127);
-    const int hh = (int)(n >> 7);
-    const bool is_q = hh < a.hq, is_k = !is_q && hh < a.hq + a.hkv;
-    if (is_q || is_k) {
-      const int64_t pos = a.pos[tok];
-      if (pos >= 0 && pos < a.max_pos) {
-        const int dd = d & 63;
-        const float c = bf2f(a.cs[pos * 128 + dd]), sn = bf2f(a.cs[pos * 128 + 64 + dd]);
-        const float other = xch[d < 64 ? cl + 64 : cl - 64];
-        x = bf2f(f2bf(d < 64 ? x * c - other * sn : x * c + other * sn));
-      }
+    if (rot) {
+      const float other = xch[d < 64 ? cl + 64 : cl - 64];
+      x = bf2f(f2bf(d < 64 ? x * rc - other * rsn : x * rc + other * rsn));
     }
     yrow[n] = f2bf(x);
-    if (is_q) return;
-    const int64_t p = a.seqlens[tok];
-    const int64_t blk_i = p / a.bs;
-    if (p < 0 || blk_i >= a.max_blocks) return;
-    const int32_t pb = a.bt[(int64_t)tok * a.max_blocks + blk_i];
-    if (pb < 0 || pb >= a.num_blocks) return;
-    const int kvh = is_k ? hh - a.hq : hh - a.hq - a.hkv;
-    (is_k ? a.kc : a.vc)[((int64_t)pb * a.bs + p % a.bs) * a.hkv * 128 + kvh * 128 + d] = f2bf(x);
+    if (kv_dst >= 0) (is_k ? a.kc : a.vc)[kv_dst] = f2bf(x);
   }
 }
 
