@@ -689,8 +689,9 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     }
   }
 
-  // partial sums of the quad(s) over K-slices kg, kg + 4, ...: the first 8
-  // of each lane group requested together (all of them up to 32 K-slices)
+  // partial sums of the quad(s) over K-slices kg, kg + 4, ...: the first
+  // batch of each lane group requested together (all of them up to 32
+  // K-slices, 8 with two column sets)
   const int64_t kstride = (int64_t)a.ntok * a.N;
   auto ld_part = [&](int c, int ks) {
     f32x4 q = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -706,11 +707,27 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     }
     return q;
   };
-  f32x4 q0[C][8];
+  constexpr int B0 = C == 2 ? 2 : 8;  // first batch per lane group (two column sets: 8 K-slices)
+  f32x4 q0[C][B0];
 #pragma unroll
   for (int c = 0; c < C; ++c)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) q0[c][j] = ld_part(c, kg + 4 * j);
+    for (int j = 0; j < B0; ++j) q0[c][j] = ld_part(c, kg + 4 * j);
+
+  // the token's shrink row over the K-slices: thread (split sp, row q) sums
+  // splits sp, sp + nsp, ... (the first four requested here, with the
+  // partials)
+  const int ur = ep ? a.L.u_ld : 1, nsp = 256 / ur;
+  const int uq = threadIdx.x % ur, usp = threadIdx.x / ur;
+  const float* up = ep ? a.L.u + (int64_t)a.urow[tok] * a.L.u_ld + uq : nullptr;
+  float u4[4] = {0.f, 0.f, 0.f, 0.f};
+  if (ep && usp < nsp) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = usp + i * nsp;
+      if (k < a.L.usplit) u4[i] = up[k * a.L.u_split_stride];
+    }
+  }
 
   // RoPE factors and the KV page slot (3), requested while the partials are
   // in flight
@@ -739,8 +756,8 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   for (int c = 0; c < C; ++c) {
     s[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s[c] += q0[c][j];
-    for (int ks0 = kg + 32; ks0 < a.n_ks; ks0 += 32) {
+    for (int j = 0; j < B0; ++j) s[c] += q0[c][j];
+    for (int ks0 = kg + 4 * B0; ks0 < a.n_ks; ks0 += 32) {
       f32x4 q[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) q[j] = ld_part(c, ks0 + 4 * j);
@@ -749,14 +766,10 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     }
   }
 
-  // the token's shrink row, reduced over the K-slices: thread (split sp, row q)
   if (ep) {  // uniform over the workgroup
-    const int ur = a.L.u_ld, nsp = 256 / ur;
-    const int q = threadIdx.x % ur, sp = threadIdx.x / ur;
-    const float* up = a.L.u + (int64_t)a.urow[tok] * a.L.u_ld + q;
-    if (sp < nsp) {
-      float acc = 0.f;
-      for (int k = sp; k < a.L.usplit; k += nsp) acc += up[k * a.L.u_split_stride];
+    if (usp < nsp) {
+      float acc = (u4[0] + u4[1]) + (u4[2] + u4[3]);
+      for (int k = usp + 4 * nsp; k < a.L.usplit; k += nsp) acc += up[k * a.L.u_split_stride];
       ured[threadIdx.x] = acc;
     }
     __syncthreads();
