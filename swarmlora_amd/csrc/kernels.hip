@@ -2027,6 +2027,7 @@ struct Tuning {
   int lds_kb = 96;      // activation-slice LDS per workgroup (16..160 KiB)
   int slice_steps = 16; // K-slices hold at most this many 32-wide k-steps
   int nks = 0;          // forced K-slice count (0: chosen per shape)
+  int long_slice = 32;  // slice cap when the row tiles alone overfill the slots (0: off)
 };
 const Tuning& tuning() {
   static Tuning t = [] {
@@ -2036,6 +2037,7 @@ const Tuning& tuning() {
     if (const char* e = getenv("SWL_SKINNY_LDS_KB")) v.lds_kb = std::min(160, std::max(16, atoi(e)));
     if (const char* e = getenv("SWL_SKINNY_NKS")) v.nks = std::max(0, atoi(e));
     if (const char* e = getenv("SWL_SKINNY_SLICE")) v.slice_steps = std::max(1, atoi(e));
+    if (const char* e = getenv("SWL_SKINNY_LONG_SLICE")) v.long_slice = std::max(0, atoi(e));
     return v;
   }();
   return t;
@@ -2192,20 +2194,29 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   // rows per workgroup and leave fewer workers; 16 steps measured best), then
   // as many more as the LDS cap on the staged activation slice (padded steps
   // x TT x 1 KiB) requires.
+  // When the row tiles alone outnumber the slots (the LM head), slices of up
+  // to long_slice steps: half the partials, and the workgroups the larger
+  // staged slice leaves resident still have many tiles each.
   auto padded = [&](int64_t nk) { return ((total_steps + nk - 1) / nk + kKDepth - 1) / kKDepth * kKDepth; };
+  const int slice_cap = (tu.long_slice > 0 && tile_groups > slots) ? tu.long_slice : tu.slice_steps;
   int64_t n_ks = 1;
   if (tu.nks > 0) {
     n_ks = tu.nks;
   } else {
     while (n_ks < total_steps &&
-           ((total_steps + n_ks - 1) / n_ks > tu.slice_steps || 2 * n_ks * tile_groups < slots))
+           ((total_steps + n_ks - 1) / n_ks > slice_cap || 2 * n_ks * tile_groups < slots))
       n_ks *= 2;
   }
   while (n_ks < total_steps && padded(n_ks) * TT * 1024 > (int64_t)tu.lds_kb * 1024) n_ks *= 2;
   n_ks = std::min<int64_t>(n_ks, total_steps);
   a.n_ks = (int)n_ks;
   a.ks_steps = (int)padded(n_ks);  // the widest slice, padded to whole pipeline iterations
-  a.n_workers = (int)std::max<int64_t>(1, std::min<int64_t>(tile_groups, slots / n_ks));
+  // workgroups resident per CU given the staged slice's LDS (160 KiB per CU)
+  size_t lds = (size_t)a.ks_steps * TT * 1024;
+  if (a.gamma) lds += (size_t)(a.ks_steps * 32 + 511) / 512 * 1024 + 64 * sizeof(float);
+  SWL_CHECK(lds <= 160 * 1024, SWL_ERR_INVALID, "round: staged activation slice exceeds LDS");
+  const int64_t res_slots = std::min<int64_t>(slots, (int64_t)cu_count() * std::max<int64_t>(1, (160 * 1024) / lds));
+  a.n_workers = (int)std::max<int64_t>(1, std::min<int64_t>(tile_groups, res_slots / n_ks));
 
   const size_t part_bytes = sizeof(float) * (size_t)a.n_ks * ntok * N;
   const size_t part_al = (part_bytes + 255) & ~(size_t)255;
@@ -2216,9 +2227,6 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   a.part = reinterpret_cast<float*>(scratch);
   a.u = has_lora ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + part_al) : nullptr;
 
-  size_t lds = (size_t)a.ks_steps * TT * 1024;
-  if (a.gamma) lds += (size_t)(a.ks_steps * 32 + 511) / 512 * 1024 + 64 * sizeof(float);
-  SWL_CHECK(lds <= 160 * 1024, SWL_ERR_INVALID, "round: staged activation slice exceeds LDS");
   const dim3 grid((unsigned)(a.n_ks * a.n_workers));
   const int tslot = timer_slot(st);
   if (tslot >= 0) {
