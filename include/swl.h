@@ -169,6 +169,23 @@ typedef struct swl_round_fusion {
   int32_t w_layout;
 } swl_round_fusion;
 
+/* Segmented LoRA delta of a packed batch x [T, k] (segment i = rows
+ * sum(seg_rows[0..i)) .. + seg_rows[i]), replacing the worker-side delta
+ * products of FusedLoRA / SyncRemoteLoRALinear (model_builder.py:193-201,
+ * :217-262; worker_sync.py:305, :375) for callers that keep the base GEMM
+ * and the delta apart.  For a segment with seg_lora[i] >= 0 (an entry of
+ * lora_table), delta = scale * (x . A^T) . B^T over the entry's nblk column
+ * blocks (blk_cols, summing to n); fp32 throughout, one bf16 rounding.
+ * mode 0: y [T, n] = delta (0 for segments without an adapter); mode 1:
+ * y = y + delta in place (segments without an adapter untouched).  k a
+ * multiple of 32, x 16-byte aligned, T <= 65535. */
+int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg,
+                            const int64_t* seg_rows, const int32_t* seg_lora,
+                            const swl_lora_entry* lora_table,
+                            const swl_lora_entry* lora_table_host, int nblk,
+                            const int64_t* blk_cols, void* y, int64_t n,
+                            int mode, void* stream);
+
 /* Fragment-tile layout of a row-major weight w [n, k] (k a multiple of 32)
  * for decode-shaped rounds: 16-row tiles, each tile stored whole (16 x k),
  * k-step by k-step (32 columns); one k-step block is the 1 KiB A operand of a

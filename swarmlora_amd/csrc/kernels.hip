@@ -458,6 +458,35 @@ __global__ __launch_bounds__(256) void u_fold_kernel(float* u, int64_t split_str
   reinterpret_cast<f32x4*>(u)[i] = s;
 }
 
+// LoRA expand of a packed batch (swl_lora_segmented_bf16): one thread per
+// (row, 4 consecutive columns); y = delta (mode 0) or y + delta rounded
+// once (mode 1), delta from the row's folded shrink row and its adapter's
+// lora_B block; rows of segments without an adapter get 0 (mode 0) or are
+// left as they are (mode 1).
+struct ExpandArgs {
+  bf16* y;
+  int64_t N;
+  int32_t mode, n_seg;
+  int64_t off[kMaxSeg + 1];
+  int32_t seg_lora[kMaxSeg];
+  LoraEpi L;
+};
+
+__global__ __launch_bounds__(256) void lora_expand_kernel(ExpandArgs a) {
+  const int64_t t = blockIdx.y;
+  const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n >= a.N) return;
+  const int s = find_seg(a.off, a.n_seg, t);
+  const int lidx = a.seg_lora[s];
+  if (a.mode == 1 && lidx < 0) return;
+  bf16* yrow = a.y + t * a.N;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (a.mode == 1)
+    for (int j = 0; j < 4; ++j)
+      if (n + j < a.N) v[j] = bf2f(yrow[n + j]);
+  epilogue_store4(v, n, a.N, nullptr, a.L, lidx, (int)t, yrow);
+}
+
 // Row pointer (this lane's row, at the K-slice start) of row tile `tile`: a
 // tile of W, or a tile of one adapter group's stacked A (rows past the end of
 // either re-read its last row; their results are never stored).  grp: -1 for
@@ -2501,6 +2530,9 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
                  const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
                  const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
                  const swl_round_fusion* fz = nullptr);
+int plan_lora(int n_seg, const int64_t* rows, int64_t N, const int32_t* seg_lora, const swl_lora_entry* lora_table,
+              const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, LoraEpi* L, bool* has_lora,
+              int* max_r);
 }  // namespace swl
 
 extern "C" {
@@ -2600,6 +2632,63 @@ int swl_round_ex_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
   }
   return swl::round_launch(n_seg, rows, seg_in, seg_out, w, bias, n, k, seg_lora, lora_table, lora_table_host, nblk,
                            blk_cols, (hipStream_t)stream, fusion);
+}
+
+int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg, const int64_t* seg_rows, const int32_t* seg_lora,
+                            const swl_lora_entry* lora_table, const swl_lora_entry* lora_table_host, int nblk,
+                            const int64_t* blk_cols, void* y, int64_t n, int mode, void* stream) {
+  SWL_CHECK(x && seg_rows && seg_lora && lora_table && lora_table_host && y, SWL_ERR_INVALID,
+            "swl_lora_segmented_bf16: null argument");
+  SWL_CHECK(n_seg >= 1 && n_seg <= kMaxSeg, SWL_ERR_INVALID, "swl_lora_segmented_bf16: segment count must be in [1, 128]");
+  SWL_CHECK(k > 0 && k % 32 == 0 && n > 0, SWL_ERR_INVALID, "swl_lora_segmented_bf16: k must be a positive multiple of 32");
+  SWL_CHECK(mode == 0 || mode == 1, SWL_ERR_INVALID, "swl_lora_segmented_bf16: mode must be 0 or 1");
+  SWL_CHECK((reinterpret_cast<uintptr_t>(x) & 15) == 0, SWL_ERR_INVALID, "swl_lora_segmented_bf16: x must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  ExpandArgs e{};
+  e.y = reinterpret_cast<bf16*>(y);
+  e.N = n;
+  e.mode = mode;
+  e.n_seg = n_seg;
+  e.off[0] = 0;
+  for (int i = 0; i < n_seg; ++i) {
+    SWL_CHECK(seg_rows[i] >= 0, SWL_ERR_INVALID, "swl_lora_segmented_bf16: negative row count");
+    e.off[i + 1] = e.off[i] + seg_rows[i];
+    e.seg_lora[i] = (seg_lora[i] >= 0 && seg_rows[i] > 0) ? seg_lora[i] : -1;
+  }
+  const int64_t T = e.off[n_seg];
+  if (T == 0) return SWL_OK;
+  SWL_CHECK(T <= 65535, SWL_ERR_INVALID, "swl_lora_segmented_bf16: at most 65535 rows");
+  bool has_lora = false;
+  int max_r = 0;
+  int rc = swl::plan_lora(n_seg, seg_rows, n, seg_lora, lora_table, lora_table_host, nblk, blk_cols, &e.L, &has_lora,
+                          &max_r);
+  if (rc) return rc;
+  if (has_lora) {
+    const int u_ld = ((max_r * nblk + 15) / 16) * 16;
+    SWL_CHECK(u_ld <= kMaxURow, SWL_ERR_INVALID, "swl_lora_segmented_bf16: LoRA rank x blocks exceeds 256");
+    int64_t items = 0;
+    for (int i = 0; i < n_seg; ++i)
+      if (e.seg_lora[i] >= 0) items += (seg_rows[i] + 63) / 64 * ((lora_table_host[e.seg_lora[i]].rank * nblk + 63) / 64);
+    int u_ks = 1;
+    while (u_ks < 16 && items * u_ks < 1024 && (k / 32) / (2 * u_ks) >= 8) u_ks *= 2;
+    void* scratch = nullptr;
+    rc = scratch_get(sizeof(float) * (size_t)u_ks * (size_t)T * (size_t)u_ld, st, &scratch);
+    if (rc) return rc;
+    float* u = reinterpret_cast<float*>(scratch);
+    rc = launch_shrink_gemm(reinterpret_cast<const bf16*>(x), k, n_seg, e.off, seg_rows, e.seg_lora, lora_table_host,
+                            nblk, u, u_ld, T * u_ld, u_ks, st);
+    if (rc) return rc;
+    e.L.u = u;
+    e.L.usplit = 1;  // folded into split 0
+    e.L.u_ld = u_ld;
+    e.L.u_split_stride = T * u_ld;
+  } else if (mode == 1) {
+    return SWL_OK;  // nothing to add
+  }
+  const dim3 grid((unsigned)((n + 1023) / 1024), (unsigned)T);
+  hipLaunchKernelGGL(lora_expand_kernel, grid, dim3(256), 0, st, e);
+  SWL_LAUNCH_CHECK("lora_expand_kernel launch");
+  return SWL_OK;
 }
 
 int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out, void* stream) {
@@ -2788,6 +2877,40 @@ int seq_wait_launch(int n, const uint64_t* const* flag, const uint64_t* want, co
 
 // ======================================================== round planner ===
 namespace swl {
+// LoRA metadata of a round: column blocks (blk_cols, nblk of them, summing
+// to N) into L, whether any non-empty segment has an adapter, and the largest
+// rank among those (adapter entries checked).
+int plan_lora(int n_seg, const int64_t* rows, int64_t N, const int32_t* seg_lora, const swl_lora_entry* lora_table,
+              const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, LoraEpi* L, bool* has_lora,
+              int* max_r) {
+  *has_lora = false;
+  *max_r = 0;
+  if (!seg_lora) return SWL_OK;
+  SWL_CHECK(nblk >= 1 && nblk <= SWL_MAX_LORA_BLOCKS, SWL_ERR_INVALID, "round: nblk must be in [1, 4]");
+  SWL_CHECK(blk_cols != nullptr, SWL_ERR_INVALID, "round: blk_cols required with LoRA");
+  L->nblk = nblk;
+  L->blk_start[0] = 0;
+  for (int b = 0; b < nblk; ++b) {
+    SWL_CHECK(blk_cols[b] > 0, SWL_ERR_INVALID, "round: column blocks must be positive");
+    L->blk_start[b + 1] = L->blk_start[b] + blk_cols[b];
+  }
+  for (int b = nblk + 1; b <= SWL_MAX_LORA_BLOCKS; ++b) L->blk_start[b] = L->blk_start[nblk];
+  SWL_CHECK(L->blk_start[nblk] == N, SWL_ERR_INVALID, "round: column blocks must sum to N");
+  for (int i = 0; i < n_seg; ++i)
+    if (seg_lora[i] >= 0 && rows[i] > 0) *has_lora = true;
+  L->table = lora_table;
+  if (!*has_lora) return SWL_OK;
+  SWL_CHECK(host_entries != nullptr, SWL_ERR_INVALID, "round: missing adapter metadata");
+  for (int i = 0; i < n_seg; ++i) {
+    if (seg_lora[i] < 0 || rows[i] == 0) continue;
+    const swl_lora_entry& e = host_entries[seg_lora[i]];
+    SWL_CHECK(e.a != nullptr && e.rank > 0 && e.rank <= 256, SWL_ERR_INVALID, "round: bad adapter entry");
+    for (int b = 0; b < nblk; ++b) SWL_CHECK(e.b[b] != nullptr, SWL_ERR_INVALID, "round: adapter missing lora_B");
+    *max_r = std::max(*max_r, (int)e.rank);
+  }
+  return SWL_OK;
+}
+
 
 int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
                  const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
@@ -2810,33 +2933,9 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   // LoRA planning.
   bool has_lora = false;
   LoraEpi L{};
-  if (seg_lora) {
-    SWL_CHECK(nblk >= 1 && nblk <= SWL_MAX_LORA_BLOCKS, SWL_ERR_INVALID, "round: nblk must be in [1, 4]");
-    SWL_CHECK(blk_cols != nullptr, SWL_ERR_INVALID, "round: blk_cols required with LoRA");
-    L.nblk = nblk;
-    L.blk_start[0] = 0;
-    for (int b = 0; b < nblk; ++b) {
-      SWL_CHECK(blk_cols[b] > 0, SWL_ERR_INVALID, "round: column blocks must be positive");
-      L.blk_start[b + 1] = L.blk_start[b] + blk_cols[b];
-    }
-    for (int b = nblk + 1; b <= SWL_MAX_LORA_BLOCKS; ++b) L.blk_start[b] = L.blk_start[nblk];
-    SWL_CHECK(L.blk_start[nblk] == N, SWL_ERR_INVALID, "round: column blocks must sum to N");
-    for (int i = 0; i < n_seg; ++i)
-      if (seg_lora[i] >= 0 && rows[i] > 0) has_lora = true;
-    L.table = lora_table;
-  }
-
   int max_r = 0;
-  if (has_lora) {
-    SWL_CHECK(host_entries != nullptr, SWL_ERR_INVALID, "round: missing adapter metadata");
-    for (int i = 0; i < n_seg; ++i) {
-      if (seg_lora[i] < 0 || rows[i] == 0) continue;
-      const swl_lora_entry& e = host_entries[seg_lora[i]];
-      SWL_CHECK(e.a != nullptr && e.rank > 0 && e.rank <= 256, SWL_ERR_INVALID, "round: bad adapter entry");
-      for (int b = 0; b < nblk; ++b) SWL_CHECK(e.b[b] != nullptr, SWL_ERR_INVALID, "round: adapter missing lora_B");
-      max_r = std::max(max_r, (int)e.rank);
-    }
-  }
+  int rc0 = plan_lora(n_seg, rows, N, seg_lora, lora_table, host_entries, nblk, blk_cols, &L, &has_lora, &max_r);
+  if (rc0) return rc0;
 
   const int u_ld = ((max_r * std::max(nblk, 1) + 15) / 16) * 16;  // A rows padded to 16-row tiles
   const bool fused = fz && (fz->norm_weight || fz->out_mode != 0 || fz->w_layout != 0);

@@ -316,6 +316,29 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
                                              _stream()))
 
 
+def lora_segmented(x: torch.Tensor, seg_rows: Sequence[int], seg_lora: Sequence[int], table: LoraTable,
+                   blk_cols: Sequence[int], y: torch.Tensor, add: bool = False):
+    """Segmented LoRA delta of the packed rows x [T, k] (swl_lora_segmented_bf16):
+    y [T, n] = delta (add=False) or y += delta (add=True); segment i's rows use
+    table entry seg_lora[i] (-1: no adapter)."""
+    _need(x, "x")
+    _need(y, "y")
+    if x.dim() != 2 or not x.is_contiguous() or y.dim() != 2 or not y.is_contiguous():
+        raise ValueError("x and y must be contiguous 2-D tensors")
+    if len(seg_rows) != len(seg_lora):
+        raise ValueError("one adapter index per segment")
+    t = sum(int(r) for r in seg_rows)
+    if x.shape[0] != t or y.shape[0] != t:
+        raise ValueError("x and y need sum(seg_rows) rows")
+    if any(i >= len(table) for i in seg_lora):
+        raise ValueError("seg_lora index out of range")
+    _lib.check(_lib.load().swl_lora_segmented_bf16(
+        _ptr(x), x.shape[1], len(seg_rows), _i64_array(seg_rows), _i32_array(seg_lora), _ptr(table.device_table()),
+        ctypes.cast(table.host_table(), ctypes.c_void_p), len(blk_cols), _i64_array(blk_cols), _ptr(y), y.shape[1],
+        1 if add else 0, _stream()))
+    return y
+
+
 def matmul(x: torch.Tensor, b: torch.Tensor, trans_b: bool, alpha: float = 1.0,
            out: Optional[torch.Tensor] = None):
     """y = alpha * x @ (b.T if trans_b else b) for 2-D views with unit column
