@@ -13,6 +13,13 @@
  *     as void* (NULL = the null stream).  No torch types cross this boundary.
  *   - Kernels are stream-ordered and never synchronise the host unless the
  *     comment says so.
+ *   - Rounds, GEMMs, the segmented LoRA delta and paged attention use one
+ *     library-owned scratch area per device (K-slice partials, shrink rows,
+ *     attention part records, packed prefill rows): calls that use it must
+ *     not overlap on one device, so callers on several streams of a device
+ *     order them.  The area grows (hipMalloc) outside graph capture only;
+ *     run a call once before capturing it.  Outgrown areas stay allocated
+ *     until the process ends, so earlier captured graphs stay valid.
  *
  * Reference citations are relative to SHUs-Lab/SwarmLoRA's tree.
  */

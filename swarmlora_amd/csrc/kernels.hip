@@ -1961,15 +1961,23 @@ __global__ __launch_bounds__(1024) void sample_kernel(SampleArgs a) {
 }
 
 // --------------------------------------------------- library scratch ------
-// One growable device scratch area per device, used for the LoRA shrink
-// partials and the packed activations of the prefill path.  Growth calls
-// hipMalloc and is refused while the stream is being captured.
+// One growable device scratch area per device, used for the decode
+// projection's fp32 K-slice partials, the LoRA shrink partials, the
+// attention part records and the packed activations of the prefill path.
+// Launches that use it must not overlap on one device (calls from several
+// streams of one device are to be ordered by the caller; a graph captured
+// on one stream is sized by an eager call on another).  Growth calls
+// hipMalloc and is refused while the stream is being captured; an outgrown
+// area is kept (not freed) until the process ends, because a graph captured
+// earlier still references it.  Sizes grow by at least half, so the areas
+// kept stay within twice the largest.
 struct Scratch {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 std::mutex g_scratch_mu;
 std::vector<Scratch> g_scratch;
+std::vector<void*> g_scratch_kept;
 
 int scratch_get(size_t need, hipStream_t stream, void** out) {
   int dev = 0;
@@ -1982,15 +1990,12 @@ int scratch_get(size_t need, hipStream_t stream, void** out) {
     if (stream) SWL_HIP(hipStreamIsCapturing(stream, &cs));
     SWL_CHECK(cs == hipStreamCaptureStatusNone, SWL_ERR_STATE,
               "scratch must grow outside graph capture (run the call once before capturing)");
-    if (s.ptr) {
-      SWL_HIP(hipDeviceSynchronize());
-      SWL_HIP(hipFree(s.ptr));
-      s.ptr = nullptr;
-      s.bytes = 0;
-    }
-    size_t nb = std::max(need, (size_t)1 << 20);
+    size_t nb = std::max({need, s.bytes + s.bytes / 2, (size_t)1 << 20});
     nb = (nb + 4095) & ~(size_t)4095;
-    SWL_HIP(hipMalloc(&s.ptr, nb));
+    void* p = nullptr;
+    SWL_HIP(hipMalloc(&p, nb));
+    if (s.ptr) g_scratch_kept.push_back(s.ptr);
+    s.ptr = p;
     s.bytes = nb;
   }
   *out = s.ptr;

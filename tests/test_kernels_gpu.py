@@ -342,3 +342,34 @@ def test_zero_blocks(dev):
         assert float(c[[1, 7, 3]].abs().max()) == 0.0
         assert float(c[[0, 2, 4, 5, 6, 8, 9]].abs().min()) >= 0.0
         assert float(c[0].abs().max()) > 0.0
+
+
+def test_captured_round_survives_scratch_growth(dev):
+    """A decode-shaped round captured in a graph keeps reading valid scratch
+    after later, larger prefill rounds grow the library's scratch area (the
+    outgrown area stays allocated): every replay, with eager growth between
+    replays, equals the eager result bit for bit."""
+    ops = _ops()
+    w = randn((H, H), SEED_W + 3, std=0.02).to(dev)
+    xs = [randn((1, H), SEED_X + i).to(dev) for i in range(28)]
+    want = [torch.zeros(1, H, dtype=BF16, device=dev) for _ in range(28)]
+    ops.round_fused(xs, want, [1] * 28, w)
+    got = [torch.zeros(1, H, dtype=BF16, device=dev) for _ in range(28)]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.round_fused(xs, got, [1] * 28, w)
+    w2 = randn((512, H), SEED_W + 4, std=0.02).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(SEED_X + 50)
+    for i in range(3):
+        t = 4096 * (i + 2)  # each prefill round needs a larger packed staging area
+        xb = torch.randn(t, H, generator=gen, device=dev, dtype=BF16)
+        yb = torch.empty(t, 512, dtype=BF16, device=dev)
+        ops.round_fused([xb], [yb], [t], w2)
+        torch.cuda.synchronize()
+        for o in got:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for j in range(28):
+            assert bits_equal(got[j].cpu(), want[j].cpu()), f"replay {i} row {j}"
