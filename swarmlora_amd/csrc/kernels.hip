@@ -1420,8 +1420,8 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const flo
 // One workgroup of W waves per (kv head, part of a sequence); wave w takes
 // the part's tiles of 16 keys (a page, or a 16-key slice of one) w, w + W,
 // ... and streams them into its own LDS ring with LDS-DMA, S tiles deep, so
-// waves never wait on each other inside the loop.  K is stored group-major
-// ([16-byte dim group][key]: the 16 keys of an MFMA operand read sit in
+// waves never wait on each other inside the loop.  K is stored in blocks of
+// 8 keys x 8 16-byte dim groups (the 16 keys of an MFMA operand read sit in
 // distinct banks), V key-major ([key][dims]).  Scores of the G query heads
 // on MFMA (the 16 K rows as the A operand, q as the B operand, 16x16x32
 // over 4 steps of 32 dims), then online softmax and P.V in-lane (lane group
@@ -1430,7 +1430,13 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const flo
 // head); attn_combine_kernel merges the parts.  Keys past the context are
 // masked and their V rows never read.
 constexpr int kTileKeys = 16;
-constexpr int kTileBytes = 2 * kTileKeys * 256;  // one head's K and V rows of a tile
+// K of a tile: four 1 KiB blocks (dim octet o, key half h at (2 o + h) *
+// 1152): 8 keys x 128 bytes each, so every DMA instruction reads whole
+// 128-byte lines; the 128-byte skew of the odd blocks puts a dim group's
+// two key halves in different banks.  V follows as 16 key rows of 256 bytes.
+constexpr int kTileKBlk = 1152;
+constexpr int kTileKBytes = 4 * kTileKBlk;
+constexpr int kTileBytes = kTileKBytes + kTileKeys * 256;  // one head's K and V rows of a tile
 
 // Max / sum over the 16 lanes of a DPP row, every lane receiving the
 // result: xor 1 and xor 2 by quad permutes, then the half-row and row
@@ -1493,10 +1499,10 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
     blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;
     tile_base = ((int64_t)blk * a.bs + ip) * krow + (int64_t)h * 128;
   }
-  // K: instruction i, lane c -> key c % 16, dim group 4 i + c / 16 (LDS
-  // offset group * 256 + key * 16); V: key 4 i + c / 16, group c % 16 (LDS
-  // offset key * 256 + group * 16)
-  const int64_t koff = (int64_t)(lane & 15) * krow + 8 * (lane >> 4);
+  // K: instruction i, lane c -> key 8 (i % 2) + c % 8, dim group
+  // 8 (i / 2) + c / 8 (LDS block i, offset ((group % 8) * 8 + key % 8) * 16);
+  // V: key 4 i + c / 16, group c % 16 (LDS offset key * 256 + group * 16)
+  const int64_t koff = (int64_t)(lane & 7) * krow + 8 * (lane >> 3);
   const int64_t voff = (int64_t)(lane >> 4) * krow + 8 * (lane & 15);
   auto issue = [&](int j) {  // this wave's j-th tile into ring slot j % S
     const int t = w + j * W;
@@ -1505,12 +1511,12 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
     char* dst = ring + (j % S) * kTileBytes;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds((gbl_ptr)(a.kc + base + koff + 32 * i), (lds_ptr)(dst + i * 1024), 16, 0,
-                                       0);
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(a.kc + base + koff + (i & 1) * 8 * krow + (i >> 1) * 64),
+                                       (lds_ptr)(dst + i * kTileKBlk), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_global_load_lds((gbl_ptr)(a.vc + base + voff + 4 * i * krow),
-                                       (lds_ptr)(dst + 4096 + i * 1024), 16, 0, 0);
+                                       (lds_ptr)(dst + kTileKBytes + i * 1024), 16, 0, 0);
   };
 
   // q of the G query heads as the MFMA B operand: lane l holds column l % 16
@@ -1545,7 +1551,7 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
       default: __builtin_amdgcn_s_waitcnt(wait_vm_imm(0)); break;
     }
     const char* kb = ring + (j % S) * kTileBytes;
-    const char* vb = kb + 4096;
+    const char* vb = kb + kTileKBytes;
     const int64_t k0 = (tb + w + (int64_t)j * W) * kTileKeys;
     const int nk = (int)min<int64_t>(kTileKeys, ctx - k0);  // valid keys of the tile
 
@@ -1553,7 +1559,9 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
     f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (st * 4 + gg) * 256 + (lane & 15) * 16);
+      // dim group 4 st + gg: octet st / 2, index 4 (st % 2) + gg in it
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (2 * (st >> 1) + ((lane >> 3) & 1)) * kTileKBlk +
+                                                       ((4 * (st & 1) + gg) * 8 + (lane & 7)) * 16);
       sv = mfma16(kf, qf[st], sv);
     }
     if ((lane & 15) < G) {

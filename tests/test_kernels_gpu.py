@@ -189,6 +189,45 @@ def test_round_shared_adapters_zipf(dev):
     _run_round(dev, [1] * 64, H, [H, KV * HD, KV * HD], [16], adapter_ids=[remap[a] for a in ids])
 
 
+@pytest.mark.parametrize("out_dims,in_dim", [([H, KV * HD, KV * HD], H), ([H], H), ([I, I], H), ([H], I)],
+                         ids=["qkv", "o", "gate_up", "down"])
+def test_round_config5_pool_of_500(dev, out_dims, in_dim):
+    """BASELINE config 5 at full size, one round of the layer per case: 500
+    rank-16 adapters ~N(0, 0.02) resident in HBM (drawn on the device from a
+    seeded generator), 64 one-token slots drawing adapter ids from Zipf(1.1)
+    over all 500; the table indexes the whole pool.  The oracle receives the
+    adapters the slots use, copied back to the host."""
+    ops = _ops()
+    r, scale, n_pool, n_slots = 16, 2.0, 500, 64
+    g = torch.Generator().manual_seed(SEED_META)
+    p = torch.tensor([(i + 1) ** -1.1 for i in range(n_pool)])
+    ids = torch.multinomial(p / p.sum(), n_slots, replacement=True, generator=g).tolist()
+    gd = torch.Generator(device=dev).manual_seed(SEED_A)
+    table = ops.LoraTable(dev)
+    pool = []
+    for _ in range(n_pool):
+        a = (torch.randn(r * len(out_dims), in_dim, generator=gd, device=dev) * 0.02).to(BF16)
+        bs = [(torch.randn(od, r, generator=gd, device=dev) * 0.02).to(BF16) for od in out_dims]
+        table.add(a, bs, r, scale)
+        pool.append((a, bs))
+    n = sum(out_dims)
+    w = randn((n, in_dim), SEED_W, std=0.02)
+    xs = [randn((1, in_dim), SEED_X * 1000 + i) for i in range(n_slots)]
+    seg_out = [torch.zeros(1, n, dtype=BF16, device=dev) for _ in range(n_slots)]
+    ops.round_fused([x.to(dev) for x in xs], seg_out, [1] * n_slots, w.to(dev), None, seg_lora=ids, table=table,
+                    blk_cols=out_dims)
+    torch.cuda.synchronize()
+    host = {}
+    for a_id in set(ids):
+        a, bs = pool[a_id]
+        host[a_id] = [(a[j * r:(j + 1) * r].cpu(), b.cpu(), scale) for j, b in enumerate(bs)]
+    op = ref.OP_QKV_FUSED if len(out_dims) > 1 else ref.OP_O_PROJ
+    want = ref.round_with_lora(op, xs, [1] * n_slots, w, [host[a] for a in ids], out_dims)
+    assert len(set(ids)) > 8 and max(ids) > 64  # shared adapters, ids beyond the slot count
+    for i in range(n_slots):
+        assert_close(seg_out[i], want[i], what=f"slot {i} (adapter {ids[i]})")
+
+
 @pytest.mark.parametrize("ranks", [[8], [8, 16, 32, 64], [4, 12]])
 def test_round_mixed_ranks_decode(dev, ranks):
     _run_round(dev, [1] * 9, H, [H, KV * HD, KV * HD], ranks)
