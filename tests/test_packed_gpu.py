@@ -64,6 +64,7 @@ def _table(dev, in_dim, out_dims, n, r=16, scale=2.0):
     (5, 256, [200], True),                  # N not a multiple of 16
     (64, 512, [96, 96], True),              # 4 token tiles
     (17, 14336, [4096], False),             # long K (Down shape)
+    (28, 4096, [128256], False),            # LM head: 32-step K-slices, 16-step load groups
 ])
 def test_packed_round_matches_row_major_bitwise(dev, T, in_dim, out_dims, lora):
     ops = _ops()
