@@ -242,6 +242,52 @@ def test_round_prefill_ragged_mixed_ranks(dev):
     _run_round(dev, rows, H, [H, KV * HD, KV * HD], ranks)
 
 
+@pytest.mark.parametrize("out_dims,in_dim", [([H, KV * HD, KV * HD], H), ([H], H), ([I, I], H), ([H], I)],
+                         ids=["qkv", "o", "gate_up", "down"])
+def test_round_config3_full_size(dev, out_dims, in_dim):
+    """BASELINE config 3 at full size, one round of the layer per case: 16
+    slots, half of them 1 token and the rest U{32..512} tokens (seeded),
+    adapter ranks drawn from {8, 16, 32, 64}, scale 2.0.  Every row is checked
+    against a float32 torch evaluation of the same per-slot products on the
+    device; three rows of each slot (first, middle, last) against the oracle's
+    bf16 restatement (rows are independent, so the oracle runs on those rows
+    only)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(SEED_META + 3)
+    rows = [1] * 8 + torch.randint(32, 513, (8,), generator=g).tolist()
+    perm = torch.randperm(16, generator=g).tolist()
+    rows = [rows[i] for i in perm]
+    ranks = [[8, 16, 32, 64][int(i)] for i in torch.randint(0, 4, (16,), generator=g)]
+    scale, n = 2.0, sum(out_dims)
+    w = randn((n, in_dim), SEED_W, std=0.02)
+    xs = [randn((t, in_dim), SEED_X * 1000 + i) for i, t in enumerate(rows)]
+    ads = [_adapter(SEED_A + 7 * i, ranks[i], in_dim, out_dims) for i in range(16)]
+    table = ops.LoraTable(dev)
+    for ad, r in zip(ads, ranks):
+        table.add(torch.cat([A for A, _ in ad], 0).contiguous().to(dev), [B.contiguous().to(dev) for _, B in ad], r,
+                  scale)
+    seg_out = [torch.zeros(t, n, dtype=BF16, device=dev) for t in rows]
+    wd = w.to(dev)
+    ops.round_fused([x.to(dev) for x in xs], seg_out, rows, wd, None, seg_lora=list(range(16)), table=table,
+                    blk_cols=out_dims)
+    torch.cuda.synchronize()
+    wf = wd.float()
+    for i, (x, ad) in enumerate(zip(xs, ads)):
+        xf = x.to(dev).float()
+        want = xf @ wf.t()
+        c0 = 0
+        for (A, B), od in zip(ad, out_dims):
+            want[:, c0:c0 + od] += scale * ((xf @ A.to(dev).float().t()) @ B.to(dev).float().t())
+            c0 += od
+        assert_close(seg_out[i].float().cpu(), want.cpu(), what=f"slot {i} ({rows[i]} rows, rank {ranks[i]}) fp32")
+    pick = [sorted({0, t // 2, t - 1}) for t in rows]
+    op = ref.OP_QKV_FUSED if len(out_dims) > 1 else ref.OP_O_PROJ
+    want = ref.round_with_lora(op, [x[p] for x, p in zip(xs, pick)], [len(p) for p in pick], w,
+                               [[(A, B, scale) for A, B in ad] for ad in ads], out_dims)
+    for i, p in enumerate(pick):
+        assert_close(seg_out[i][p].cpu(), want[i], what=f"slot {i} rows {p} oracle")
+
+
 def test_round_prefill_zero_row_segments(dev):
     _run_round(dev, [40, 0, 30, 0, 1], 1024, [512], [16])
 
