@@ -2730,6 +2730,7 @@ int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out, void* s
   SWL_CHECK((reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
             SWL_ERR_INVALID, "swl_pack_weight_bf16: w and out must be 16-byte aligned");
   const int64_t nchunks = (n + 15) / 16 * 16 * k / 8;
+  SWL_CHECK((nchunks + 255) / 256 < ((int64_t)1 << 31), SWL_ERR_INVALID, "swl_pack_weight_bf16: weight too large");
   hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      reinterpret_cast<const bf16*>(w), n, k, reinterpret_cast<u32x4*>(out), nchunks);
   SWL_LAUNCH_CHECK("pack_weight_kernel launch");
