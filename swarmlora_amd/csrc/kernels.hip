@@ -904,6 +904,9 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
 // workgroup (4 waves in 2x2, 64x64 each = 4x4 MFMA tiles), BK = 64 staged in
 // LDS with a register prefetch of the next stage.
 constexpr int TM = 128, TN = 128, TK = 64;
+// LDS stages of the tiled kernel: one 32 KiB stage (two barriers per k-tile)
+// leaves three workgroups resident per CU instead of two.
+constexpr int kTiledBufs = 1;
 
 struct TiledArgs {
   const bf16* x;          // packed [M, K]
@@ -927,8 +930,11 @@ struct TiledArgs {
 __device__ __forceinline__ int swz(int row, int chunk) { return (chunk ^ ((row >> 1) & 7)) * 8; }
 
 __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2][TM][TK];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2][TN][TK];
+  // one LDS block: the A and B stages, reused by the epilogue (17 KiB)
+  __shared__ __attribute__((aligned(16))) bf16 smem[kTiledBufs * (TM + TN) * TK];
+  static_assert(kTiledBufs * (TM + TN) * TK * 2 >= 4 * 16 * (64 + 4) * 4, "epilogue staging must fit");
+  bf16(*As)[TM][TK] = reinterpret_cast<bf16(*)[TM][TK]>(smem);
+  bf16(*Bs)[TN][TK] = reinterpret_cast<bf16(*)[TN][TK]>(smem + kTiledBufs * TM * TK);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
@@ -990,7 +996,8 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
     }
     if (kt + 1 < nk) {
-      const int nb = buf ^ 1;
+      const int nb = kTiledBufs == 2 ? buf ^ 1 : 0;
+      if (kTiledBufs == 1) __syncthreads();  // every wave is done reading the stage
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
         *reinterpret_cast<u32x4*>(&As[nb][lr + 32 * p][swz(lr + 32 * p, lc >> 3)]) = ra[p];
@@ -1005,7 +1012,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   // column n0+wn*64+j*16+(l%16).  Transpose through LDS so each lane owns 4
   // consecutive columns of one token (8-byte stores, shared epilogue).
   __syncthreads();
-  float* ct = reinterpret_cast<float*>(&As[0][0][0]);  // reuse: 64x(64+4) floats per wave pass
+  float* ct = reinterpret_cast<float*>(smem);  // reuse: 16 x (64 + 4) floats per wave pass
   // Each wave handles its own 64x64 sub-tile in 4 passes of 16 tokens.
   constexpr int CLD = 64 + 4;
   float* cw = ct + wv * 16 * CLD;  // 16 tokens x 64 columns per wave per pass
