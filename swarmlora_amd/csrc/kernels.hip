@@ -2095,7 +2095,8 @@ struct Tuning {
   int lds_kb = 96;      // activation-slice LDS per workgroup (16..160 KiB)
   int slice_steps = 16; // K-slices hold at most this many 32-wide k-steps
   int nks = 0;          // forced K-slice count (0: chosen per shape)
-  int long_slice = 32;  // slice cap when the row tiles alone overfill the slots (0: off)
+  int long_slice = 1 << 20;  // slice cap when the row tiles alone overfill the slots (0: off; default:
+                             // the longest slice the LDS holds)
 };
 const Tuning& tuning() {
   static Tuning t = [] {
@@ -2263,10 +2264,19 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   // as many more as the LDS cap on the staged activation slice (padded steps
   // x TT x 1 KiB) requires.
   // When the row tiles alone outnumber the slots (the LM head), slices of up
-  // to long_slice steps: half the partials, and the workgroups the larger
-  // staged slice leaves resident still have many tiles each.
+  // to long_slice steps, by default the longest the 160 KiB of LDS holds:
+  // fewer fp32 partials, and the one workgroup per CU the staged slice
+  // leaves resident still has many tiles (LM head at 28 rows: 2 slices of
+  // 64 steps 220 us, 4 of 32 steps 246 us).
   auto padded = [&](int64_t nk) { return ((total_steps + nk - 1) / nk + kKDepth - 1) / kKDepth * kKDepth; };
-  const int slice_cap = (tu.long_slice > 0 && tile_groups > slots) ? tu.long_slice : tu.slice_steps;
+  const bool long_rows = tu.long_slice > 0 && tile_groups > slots;
+  const int slice_cap = long_rows ? tu.long_slice : tu.slice_steps;
+  auto lds_of = [&](int64_t nk) {  // staged slice (+ RMSNorm gamma and row factors)
+    int64_t l = padded(nk) * TT * 1024;
+    if (a.gamma) l += (padded(nk) * 32 + 511) / 512 * 1024 + 64 * (int64_t)sizeof(float);
+    return l;
+  };
+  const int64_t lds_cap = long_rows ? 160 * 1024 : (int64_t)tu.lds_kb * 1024;
   int64_t n_ks = 1;
   if (tu.nks > 0) {
     n_ks = tu.nks;
@@ -2275,7 +2285,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
            ((total_steps + n_ks - 1) / n_ks > slice_cap || 2 * n_ks * tile_groups < slots))
       n_ks *= 2;
   }
-  while (n_ks < total_steps && padded(n_ks) * TT * 1024 > (int64_t)tu.lds_kb * 1024) n_ks *= 2;
+  while (n_ks < total_steps && lds_of(n_ks) > lds_cap) n_ks *= 2;
   n_ks = std::min<int64_t>(n_ks, total_steps);
   a.n_ks = (int)n_ks;
   a.ks_steps = (int)padded(n_ks);  // the widest slice, padded to whole pipeline iterations
