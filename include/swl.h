@@ -42,7 +42,8 @@ enum {
   SWL_ERR_FULL = 4,      /* ring buffer full                                   */
   SWL_ERR_QUIT = 5,      /* quit flag observed                                 */
   SWL_ERR_NOT_FOUND = 6, /* slot not open / no free slot                       */
-  SWL_ERR_UNSUPPORTED = 7
+  SWL_ERR_UNSUPPORTED = 7,
+  SWL_ERR_TIMEOUT = 8    /* a bounded device-side wait gave up                 */
 };
 
 /* Constants shared with the reference's ABI (src/cpp_extensions/common/ipc_types.h:16-25). */

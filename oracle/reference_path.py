@@ -78,7 +78,7 @@ def execute_round(slot_inputs, rows, w, bias=None) -> List[torch.Tensor]:
 
 # ----------------------------------------------------------------- LoRA -----
 def fused_lora_weights(modules: Sequence[Optional[Tuple[torch.Tensor, torch.Tensor, float]]],
-                       out_dims: Sequence[int], dtype=BF16):
+                       out_dims: Sequence[int], dtype=None):
     """FusedLoRA.__init__, model_builder.py:217-256.  modules[i] is
     (lora_A [r, in], lora_B [out_i, r], scaling) or None.
     fused_A = cat_i(A_i^T * s_i) (scale folded in bf16); fused_B is
@@ -89,6 +89,7 @@ def fused_lora_weights(modules: Sequence[Optional[Tuple[torch.Tensor, torch.Tens
         return None, None
     rank = valid[0][0].shape[0]
     in_features = valid[0][0].shape[1]
+    dtype = valid[0][0].dtype if dtype is None else dtype
     a_list, b_list = [], []
     for i, m in enumerate(modules):
         if m is not None:
@@ -159,6 +160,18 @@ def round_with_lora(op: int, slot_inputs, rows, w, adapters, dims):
             A, B, s = ad[0]
             outs.append(b + remote_lora_delta(x, A, B, s))
     return outs
+
+
+# ------------------------------------------------------------ embed round --
+def embed_round(slot_ids: Sequence[torch.Tensor], table: torch.Tensor) -> List[torch.Tensor]:
+    """execute_batched_embed_slots, ext_aggregator.cpp:630-706: the int64 token
+    ids of every slot, concatenated in command order, clamped to [0, vocab-1]
+    (:663, :694), looked up with torch::embedding and copied back to each
+    slot's output rows [t_i, hidden]."""
+    counts = [int(t.numel()) for t in slot_ids]
+    ids = torch.cat([t.reshape(-1) for t in slot_ids]).clamp(0, table.shape[0] - 1)
+    emb = torch.nn.functional.embedding(ids, table)
+    return scatter(emb, counts)
 
 
 # ------------------------------------------------------- paged KV cache -----

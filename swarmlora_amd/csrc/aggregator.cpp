@@ -66,6 +66,8 @@ Pool g_pool;
 
 // Limit of the aggregator stream's wait for a GPU-ordered worker's input.
 constexpr uint32_t kSeqWaitLimitUs = 2000000;
+// Largest buffer a hipIpc mapping can take here (2 GiB).
+constexpr size_t kMaxIpcBytes = (size_t)1 << 31;
 
 struct LayerW {
   void* qkv = nullptr;      // owned: [q+k+v, hidden]
@@ -130,12 +132,20 @@ int op_dims(int op, int64_t* K, int64_t* N, int* nblk, int64_t* blk) {
   }
 }
 
+// Device copy of the adapter table.  Rounds already queued on the
+// aggregator stream (GPU-ordered rounds are not host-synchronised) may still
+// read the current table, so the stream is drained before the table is
+// rewritten, and a table that has to grow is replaced by a new allocation
+// while the old one stays allocated until the process ends.
+std::vector<void*> g_adapter_dev_kept;
+
 int upload_adapters() {
   std::lock_guard<std::mutex> lk(g_adapter_mu);
   if (!g_adapter_dirty) return SWL_OK;
+  if (g_stream) SWL_HIP(hipStreamSynchronize(g_stream));
   const size_t need = std::max<size_t>(g_adapter_entries.size(), 1);
   if (g_adapter_dev_cap < need) {
-    if (g_adapter_dev) SWL_HIP(hipFree(g_adapter_dev));
+    if (g_adapter_dev) g_adapter_dev_kept.push_back(g_adapter_dev);
     g_adapter_dev = nullptr;
     size_t cap = 64;
     while (cap < need) cap *= 2;
@@ -167,16 +177,25 @@ int swl_agg_init_slot_pool(int num_slots, int device_index, int hidden_dim, int 
   SWL_CHECK(hidden_dim > 0 && intermediate_dim > 0 && max_seq_per_step > 0 && dtype_size > 0, SWL_ERR_INVALID,
             "init_slot_pool: dimensions must be positive");
   SWL_CHECK(!g_pool.initialized, SWL_ERR_STATE, "init_slot_pool: slot pool already initialized");
+  const int qkv = hidden_dim + num_kv_heads * head_dim * 2;
+  const size_t in_size = (size_t)max_seq_per_step * std::max(intermediate_dim, hidden_dim) * dtype_size;
+  const size_t out_size = (size_t)max_seq_per_step * std::max(intermediate_dim * 2, qkv) * dtype_size;
+  // IPC mappings of 2 GiB or more do not open on these devices: refuse such
+  // buffers here rather than in every worker's open_slot
+  SWL_CHECK(in_size < kMaxIpcBytes && out_size + swl::kSeqTailBytes < kMaxIpcBytes, SWL_ERR_INVALID,
+            "init_slot_pool: slot buffers of " + std::to_string(in_size) + " / " +
+                std::to_string(out_size + swl::kSeqTailBytes) +
+                " bytes reach the 2 GiB limit of an IPC mapping (lower max_seq_per_step)");
   SWL_HIP(hipSetDevice(device_index));
   Pool& p = g_pool;
   p.num_slots = num_slots;
   p.device = device_index;
   p.hidden = hidden_dim;
   p.inter = intermediate_dim;
-  p.qkv = hidden_dim + num_kv_heads * head_dim * 2;
+  p.qkv = qkv;
   p.max_seq_per_step = max_seq_per_step;
-  p.in_size = (size_t)max_seq_per_step * std::max(intermediate_dim, hidden_dim) * dtype_size;
-  p.out_size = (size_t)max_seq_per_step * std::max(intermediate_dim * 2, p.qkv) * dtype_size;
+  p.in_size = in_size;
+  p.out_size = out_size;
   p.free_mask.store(Mask::below(num_slots), std::memory_order_relaxed);
   p.active_mask.store(Mask(), std::memory_order_relaxed);
   p.active_slot_count.store(0, std::memory_order_relaxed);

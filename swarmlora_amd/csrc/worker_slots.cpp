@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -27,7 +28,17 @@ struct SlotCtx {
 
 // Limit of this worker's stream wait for a round's outputs (the aggregator's
 // own input wait is 2 s; a round that long has already been evicted).
+// SWL_OUT_WAIT_US overrides it (tests of the time-out path).
 constexpr uint32_t kOutWaitLimitUs = 4000000;
+
+uint32_t out_wait_limit_us() {
+  static const uint32_t v = [] {
+    const char* e = std::getenv("SWL_OUT_WAIT_US");
+    const long long x = e ? std::atoll(e) : 0;
+    return x > 0 && x < 0xFFFFFFFFll ? (uint32_t)x : kOutWaitLimitUs;
+  }();
+  return v;
+}
 
 struct Manager {
   int worker_id = -1;
@@ -51,9 +62,23 @@ int wait_outputs(const char* fn, SlotCtx* c, hipStream_t st) {
   if (!g_w.gpu_ordered || c->seq == 0) return SWL_OK;
   const uint64_t* flag = seq_word(c, swl::kOutSeqOffset);
   const int32_t tag = c->slot_id;
-  int rc = swl::seq_wait_launch(1, &flag, &c->seq, &tag, g_w.out_timeout, kOutWaitLimitUs, st);
+  int rc = swl::seq_wait_launch(1, &flag, &c->seq, &tag, g_w.out_timeout, out_wait_limit_us(), st);
   if (rc) return swl::fail(rc, std::string(fn) + ": " + swl::last_error());
   return SWL_OK;
+}
+
+// A GPU-ordered output wait that ran out of time sets the slot's word in
+// out_timeout (the copy behind it then read a stale buffer).  The word is
+// checked, and cleared, by every later call on the slot and right after the
+// host synchronises in get_next_token_slot, so the worker learns of it before
+// its next submit and treats the slot as evicted.
+int check_out_timeout(const char* fn, const SlotCtx* c) {
+  if (!g_w.out_timeout || c->slot_id < 0 || c->slot_id >= SWL_MAX_SLOTS) return SWL_OK;
+  volatile uint32_t* word = g_w.out_timeout + c->slot_id;
+  if (*word == 0) return SWL_OK;
+  *word = 0;
+  return swl::fail(SWL_ERR_TIMEOUT, std::string(fn) + ": slot " + std::to_string(c->slot_id) +
+                                        " timed out waiting for the aggregator's output (slot evicted?)");
 }
 
 SlotCtx* find_slot(int slot_id) {
@@ -66,7 +91,7 @@ int need_slot(const char* fn, int slot_id, SlotCtx** out) {
   if (!g_w.initialized) return swl::fail(SWL_ERR_STATE, std::string(fn) + ": worker slot manager not initialized");
   *out = find_slot(slot_id);
   if (!*out) return swl::fail(SWL_ERR_NOT_FOUND, std::string(fn) + ": slot " + std::to_string(slot_id) + " not found");
-  return SWL_OK;
+  return check_out_timeout(fn, *out);
 }
 
 int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream_t st) {
@@ -263,6 +288,8 @@ int swl_w_get_next_token(int slot_id, int64_t* token, void* stream) {
   rc = wait_outputs("get_next_token_slot", c, st);
   if (rc) return rc;
   SWL_HIP(hipStreamSynchronize(st));
+  rc = check_out_timeout("get_next_token_slot", c);
+  if (rc) return rc;
   SWL_HIP(hipMemcpyAsync(token, c->out, sizeof(int64_t), hipMemcpyDeviceToHost, st));
   SWL_HIP(hipStreamSynchronize(st));
   return SWL_OK;

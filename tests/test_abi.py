@@ -41,3 +41,12 @@ def test_error_text_and_no_device_calls():
     # argument validation fails before any HIP call
     rc = lib.swl_gemm_bf16(None, None, None, None, 1, 1, 32, None)
     assert rc != 0 and "null argument" in _lib.last_error()
+
+
+def test_slot_pool_refuses_buffers_past_the_ipc_limit():
+    """init_slot_pool refuses slot buffers of 2 GiB or more (an IPC mapping
+    of that size does not open) before it touches the device."""
+    from swarmlora_amd import ext_aggregator as agg
+    # 8B shapes: out = max_seq x max(2 x 14336, 6144) x 2 B; 37450 rows -> 2.0 GiB
+    with pytest.raises(RuntimeError, match="2 GiB limit of an IPC mapping"):
+        agg.init_slot_pool(4, 0, 4096, 14336, 8, 128, 37450, 2)

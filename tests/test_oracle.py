@@ -48,6 +48,18 @@ def test_round_results_independent_of_arrival_order():
         assert bits_equal(b[i], a[p])
 
 
+def test_embed_round_clamps_and_scatters_bruteforce():
+    """Each slot's rows are table rows of its ids clamped to [0, vocab-1]
+    (negative ids -> row 0, ids >= vocab -> the last row), in slot order."""
+    table = randn((9, 5), 30)
+    ids = [torch.tensor([3, -1, 8]), torch.tensor([], dtype=torch.int64), torch.tensor([9, 100, 0, -7])]
+    got = ref.embed_round(ids, table)
+    assert [g.shape[0] for g in got] == [3, 0, 4]
+    for g, t in zip(got, ids):
+        for j, v in enumerate(t.tolist()):
+            assert bits_equal(g[j], table[min(max(v, 0), 8)])
+
+
 # -------------------------------------------------------------------- GEMM
 def test_base_gemm_one_hot_selects_column():
     w = randn((7, 11), 0)

@@ -64,7 +64,7 @@ def _table(dev, in_dim, out_dims, n, r=16, scale=2.0):
     (5, 256, [200], True),                  # N not a multiple of 16
     (64, 512, [96, 96], True),              # 4 token tiles
     (17, 14336, [4096], False),             # long K (Down shape)
-    (28, 4096, [128256], False),            # LM head: 32-step K-slices, 16-step load groups
+    (28, 4096, [128256], False),            # LM head: long K-slices (as many steps as the LDS holds)
 ])
 def test_packed_round_matches_row_major_bitwise(dev, T, in_dim, out_dims, lora):
     ops = _ops()
@@ -115,6 +115,36 @@ def test_packed_round_with_norm_and_residual_fusions(dev):
     assert bits_equal(outs[0][0], outs[1][0])
     assert bits_equal(outs[0][1], outs[1][1])
     assert torch.equal(outs[0][2], outs[1][2])
+
+
+@pytest.mark.parametrize("T", [28, 64])
+def test_norm_fused_lm_head_packed_matches_row_major_and_oracle(dev, T):
+    """The decode step's LM-head round: vocab 128256, the final RMSNorm on
+    the staged residual rows (norm_weight + ss_in), long K-slices whose LDS
+    holds the slice, gamma and the row factors.  T = 64 runs four token
+    tiles.  Packed equals row-major bit for bit; sampled rows match the
+    oracle's rms_norm -> x @ W^T."""
+    ops = _ops()
+    H, V, eps = 4096, 128256, 1e-5
+    g = torch.Generator(device=dev).manual_seed(SEED_W + T)
+    wd = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(BF16)
+    gamma = (1 + randn((H,), 78, std=0.1).float()).to(BF16)
+    hs = torch.cat([randn((1, H), SEED_X + 300 + i, std=3.0) for i in range(T)], 0)
+    ss = torch.stack([hs.float()[:, j:j + 256].pow(2).sum(1) for j in range(0, H, 256)], 1).contiguous()
+    hd, gd, ssd = hs.to(dev), gamma.to(dev), ss.to(dev)
+    pw = ops.pack_weight(wd)
+    outs = []
+    for wt, layout in ((wd, 0), (pw, 1)):
+        y = torch.zeros(T, V, dtype=BF16, device=dev)
+        ops.round_ex([hd[i:i + 1] for i in range(T)], [y[i:i + 1] for i in range(T)], [1] * T, wt, None,
+                     fusion=ops.round_fusion(norm_weight=gd, eps=eps, ss_in=ssd, w_layout=layout))
+        torch.cuda.synchronize()
+        outs.append(y.cpu())
+    assert bits_equal(outs[0], outs[1])
+    rows = [0, T // 2 + 1, T - 1]
+    w = wd.cpu()
+    want = ref.base_gemm(ref.rms_norm(hs[rows], gamma, eps), w)
+    assert_close(outs[1][rows], want, what=f"LM head T={T}")
 
 
 def test_packed_weight_rejected_where_unsupported(dev):

@@ -269,3 +269,68 @@ def test_end_to_end_workers_through_ipc(dev, pooled, gpu_ordered):
             top2 = logits.topk(2).values[0]
             if float(top2[0] - top2[1]) > 0.05:
                 assert toks[si - 1] == int(logits.argmax())
+
+
+def _timeout_proc(claim, out):
+    try:
+        import os
+        os.environ["SWL_OUT_WAIT_US"] = "200000"  # 0.2 s bounded wait
+        import torch
+        from swarmlora_amd import ext_unified_barrier as ub
+        torch.cuda.set_device(0)
+        dev = torch.device("cuda:0")
+        ub.init_worker_slot_manager(5, 0, 0, H, I, QKV)
+        sid = claim["slot_id"]
+        ub.open_slot(sid, claim["input_handle"], claim["output_handle"], claim["input_buffer_size"],
+                     claim["output_buffer_size"])
+        ub.set_gpu_ordered(True)
+        x = torch.ones(1, 1, H, dtype=torch.bfloat16, device=dev)
+        seen = []
+        # 1: get_outputs_slot does not synchronise; the next call on the slot reports the time-out
+        ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
+        ub.get_outputs_slot(sid, [H], x)
+        torch.cuda.synchronize()
+        try:
+            ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
+            seen.append("no error")
+        except RuntimeError as e:
+            seen.append(str(e))
+        # 2: get_next_token_slot synchronises and reports it itself
+        ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
+        try:
+            ub.get_next_token_slot(sid)
+            seen.append("no error")
+        except RuntimeError as e:
+            seen.append(str(e))
+        # the word was cleared: the slot works again
+        ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
+        torch.cuda.synchronize()
+        ub.close_slot(sid)
+        out.put((seen, None))
+    except Exception:
+        import traceback
+        out.put((None, traceback.format_exc()))
+
+
+def test_gpu_ordered_output_wait_timeout_is_reported(pool):
+    """A GPU-ordered worker whose output sequence word is never written (no
+    aggregator runs): the bounded stream wait gives up, and the time-out is
+    raised by the next call on the slot (get_outputs_slot path) or by
+    get_next_token_slot itself, instead of stale outputs passing silently."""
+    agg = _agg()
+    claim = agg.claim_slot(5)
+    ctx = mp.get_context("spawn")
+    out = ctx.Queue()
+    p = ctx.Process(target=_timeout_proc, args=(claim, out))
+    try:
+        p.start()
+        seen, err = out.get(timeout=180)
+    finally:
+        p.join(timeout=30)
+        if p.is_alive():
+            p.kill()
+        agg.release_slot(claim["slot_id"], 5)
+    assert err is None, err
+    assert len(seen) == 2
+    assert "prepare_input_slot" in seen[0] and "timed out" in seen[0]
+    assert "get_next_token_slot" in seen[1] and "timed out" in seen[1]

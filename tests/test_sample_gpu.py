@@ -98,3 +98,30 @@ def test_sampled_frequencies_follow_softmax(dev):
     # top_k 3 drops token 2 (the smallest)
     q = torch.tensor([p[0], p[1], 0.0, p[3]], dtype=torch.float64)
     check(counts(top_k=3), q / q.sum())
+
+
+@pytest.mark.parametrize("vocab,hidden", [(128256, 4096), (1001, 136)])
+def test_embed_rows_bit_exact_with_clamped_ids(dev, vocab, hidden):
+    """swl_embed_bf16 against the oracle's embed round (ext_aggregator.cpp:
+    630-706): ragged slots, ids below 0 and at or past the vocabulary
+    clamped to the first / last row, every output row bit-identical to the
+    table row (the table holds arbitrary 16-bit patterns)."""
+    from oracle import reference_path as ref
+    from tests._util import bits_equal
+    ops = _ops()
+    g = torch.Generator().manual_seed(vocab)
+    table = torch.randint(-32768, 32768, (vocab, hidden), generator=g, dtype=torch.int32).to(torch.int16)
+    table = table.view(torch.bfloat16)
+    edge = [0, vocab - 1, -1, vocab, -(1 << 40), (1 << 40), vocab + 7]
+    rnd = torch.randint(0, vocab, (40,), generator=g).tolist()
+    ids = [torch.tensor(edge[:3], dtype=torch.int64), torch.tensor(rnd[:16] + edge[3:], dtype=torch.int64),
+           torch.tensor([], dtype=torch.int64), torch.tensor(rnd[16:], dtype=torch.int64)]
+    td = table.to(dev)
+    outs = [torch.full((max(t.numel(), 1), hidden), 7.0, dtype=torch.bfloat16, device=dev) for t in ids]
+    ops.embed([t.to(dev) for t in ids], td, outs)
+    torch.cuda.synchronize()
+    want = ref.embed_round(ids, table)
+    for i, (o, w) in enumerate(zip(outs, want)):
+        assert bits_equal(o[: w.shape[0]].cpu(), w), f"slot {i}"
+    # an empty slot's buffer is not written
+    assert bool((outs[2] == 7.0).all())
