@@ -216,6 +216,26 @@ int swl_round_ex_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
                       const int64_t* blk_cols, const swl_round_fusion* fusion,
                       void* stream);
 
+/* Allocation-free variant of swl_round_ex_bf16.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops and harnesses that forbid hipMalloc).
+ * Same arguments and results as swl_round_ex_bf16 (the same kernels run), for
+ * rounds of at most 64 token rows; the K-slice partials live in a 64 MiB
+ * device array of the library (one copy per GPU, held until the process
+ * ends) instead of the growable library scratch, and the call allocates and
+ * frees nothing.  A round whose partials need more than 64 MiB is refused
+ * with an error (every 8B-shaped round and the LM head fit at 64 rows).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, other threads) race and must be ordered by the
+ * caller. */
+int swl_round_ex_noalloc_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
+                              void* const* seg_out, const void* w, const void* bias,
+                              int64_t n, int64_t k, const int32_t* seg_lora,
+                              const swl_lora_entry* lora_table,
+                              const swl_lora_entry* lora_table_host, int nblk,
+                              const int64_t* blk_cols, const swl_round_fusion* fusion,
+                              void* stream);
+
 /* Row-major matrix product with an explicit layout, used by the worker-side
  * LoRA modules: y[m, n] = alpha * x[m, k] . B where B is b[k, n] (trans_b = 0,
  * ldb = row stride of b) or b[n, k]^T (trans_b = 1).  fp32 accumulation,

@@ -2187,10 +2187,12 @@ int launch_split_w(int TT, const SplitArgs& a, dim3 grid, size_t lds, hipStream_
 // Decode-shaped projection of ntok (<= 64) token rows: y[i] = x[i] . W^T
 // (+ bias) (+ LoRA delta of entry tok_lora[i]).  xrows[i] / yrows[i] are the
 // token's input / output rows (slot buffers).
+// ws / ws_bytes: a fixed workspace to use instead of the library scratch
+// (the allocation-free entry point); the launch is refused if it does not fit.
 int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok, const bf16* const* xrows,
                   bf16* const* yrows, const int32_t* tok_lora, const swl_lora_entry* table,
                   const swl_lora_entry* host_entries, const LoraEpi* Lblk, int nblk, const swl_round_fusion* fz,
-                  hipStream_t st) {
+                  hipStream_t st, void* ws = nullptr, size_t ws_bytes = 0) {
   const int TT = (ntok + 15) / 16;
   const int mode = fz ? fz->out_mode : 0;
   const int64_t epi_cols = mode == 2 ? N / 2 : N;
@@ -2300,11 +2302,17 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   SWL_CHECK(part_bytes < ((size_t)1 << 31), SWL_ERR_INVALID, "round: K-slice partials exceed 2 GiB");
   const size_t part_al = (part_bytes + 255) & ~(size_t)255;
   const size_t u_bytes = has_lora ? sizeof(float) * (size_t)a.n_ks * a.u_split_stride : 0;
-  void* scratch = nullptr;
-  int rc = scratch_get(part_al + u_bytes, st, &scratch);
-  if (rc) return rc;
-  a.part = reinterpret_cast<float*>(scratch);
-  a.u = has_lora ? reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + part_al) : nullptr;
+  void* scr = ws;
+  if (ws) {
+    SWL_CHECK(part_al + u_bytes <= ws_bytes, SWL_ERR_INVALID,
+              "round: needs " + std::to_string(part_al + u_bytes) + " bytes of K-slice partials, more than the " +
+                  std::to_string(ws_bytes) + " bytes of the allocation-free scratch");
+  } else {
+    int rc = scratch_get(part_al + u_bytes, st, &scr);
+    if (rc) return rc;
+  }
+  a.part = reinterpret_cast<float*>(scr);
+  a.u = has_lora ? reinterpret_cast<float*>(reinterpret_cast<char*>(scr) + part_al) : nullptr;
 
   const dim3 grid((unsigned)(a.n_ks * a.n_workers));
   const int tslot = timer_slot(st);
@@ -2424,11 +2432,11 @@ int launch_attn_decode(const AttnArgs& a, hipStream_t st) {
   // side geometry, never device memory)
   constexpr int C = 4 * WAVES * U;
   const int maxch = (int)((a.max_blocks * a.bs + C - 1) / C);
-  void* scratch = nullptr;
+  void* scr = nullptr;
   const size_t need = sizeof(float) * (size_t)a.nseq * a.hkv * maxch * G * kAttnRec;
-  int rc = scratch_get(need, st, &scratch);
+  int rc = scratch_get(need, st, &scr);
   if (rc) return rc;
-  float* part = reinterpret_cast<float*>(scratch);
+  float* part = reinterpret_cast<float*>(scr);
   hipLaunchKernelGGL((attn_chunk_kernel<G, WAVES, U>), dim3((unsigned)a.hkv, (unsigned)maxch, (unsigned)a.nseq),
                      dim3(WAVES * 64), 0, st, a, part, maxch);
   SWL_LAUNCH_CHECK("attn_chunk_kernel launch");
@@ -2486,11 +2494,11 @@ template <int G, int S, int W>
 int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp) {
   const int64_t max_tiles = (a.max_blocks * a.bs + kTileKeys - 1) / kTileKeys;
   const int maxparts = (int)((max_tiles + tpp - 1) / tpp);
-  void* scratch = nullptr;
+  void* scr = nullptr;
   const size_t need = sizeof(float) * (size_t)a.nseq * a.hkv * maxparts * G * kAttnRec;
-  int rc = scratch_get(need, st, &scratch);
+  int rc = scratch_get(need, st, &scr);
   if (rc) return rc;
-  float* part = reinterpret_cast<float*>(scratch);
+  float* part = reinterpret_cast<float*>(scr);
   hipLaunchKernelGGL((attn_tile_kernel<G, S, W>), dim3((unsigned)a.hkv, (unsigned)maxparts, (unsigned)a.nseq),
                      dim3(64 * W), 0, st, a, part, maxparts, tpp);
   SWL_LAUNCH_CHECK("attn_tile_kernel launch");
@@ -2560,6 +2568,43 @@ int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
 
 }  // namespace
 
+// ================================================ allocation-free scratch ===
+// Device memory of swl_round_ex_noalloc_bf16: the decode projection's K-slice
+// partials of one round (64 MiB holds them for every 8B-shaped round and the
+// LM head at 64 token rows).  Every GPU the library runs on holds its own
+// copy, at its own address, from module load until the process ends.  Host
+// code never passes the array's name to a kernel (on the host it is only a
+// stand-in for the symbol): the device address is looked up once per device
+// with hipGetSymbolAddress and used instead.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace swl {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+}  // namespace
+
+// Device address of the current device's copy of `scratch` (looked up on the
+// first call on that device, with the device current).
+int noalloc_scratch(void** out, size_t* bytes) {
+  int dev = 0;
+  SWL_HIP(hipGetDevice(&dev));
+  SWL_CHECK(dev >= 0 && dev < kMaxDevices, SWL_ERR_INVALID, "allocation-free scratch: device index out of range");
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    SWL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    SWL_CHECK(p != nullptr, SWL_ERR_HIP, "allocation-free scratch: hipGetSymbolAddress returned null");
+    g_noalloc_ptr[dev] = p;
+  }
+  *out = g_noalloc_ptr[dev];
+  *bytes = kNoAllocScratchBytes;
+  return SWL_OK;
+}
+}  // namespace swl
+
 // ================================================================ C ABI ===
 namespace swl {
 thread_local std::string t_err;
@@ -2580,6 +2625,11 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
                  const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
                  const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
                  const swl_round_fusion* fz = nullptr);
+int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
+                    const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
+                    const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
+                    const swl_round_fusion* fz, void* ws, size_t ws_bytes);
+int noalloc_scratch(void** out, size_t* bytes);
 int plan_lora(int n_seg, const int64_t* rows, int64_t N, const int32_t* seg_lora, const swl_lora_entry* lora_table,
               const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, LoraEpi* L, bool* has_lora,
               int* max_r);
@@ -2684,6 +2734,22 @@ int swl_round_ex_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
                            blk_cols, (hipStream_t)stream, fusion);
 }
 
+int swl_round_ex_noalloc_bf16(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out,
+                              const void* w, const void* bias, int64_t n, int64_t k, const int32_t* seg_lora,
+                              const swl_lora_entry* lora_table, const swl_lora_entry* lora_table_host, int nblk,
+                              const int64_t* blk_cols, const swl_round_fusion* fusion, void* stream) {
+  if (seg_lora) {
+    SWL_CHECK(lora_table != nullptr && lora_table_host != nullptr, SWL_ERR_INVALID,
+              "swl_round_ex_noalloc_bf16: seg_lora needs lora_table and lora_table_host");
+  }
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  int rc = swl::noalloc_scratch(&ws, &ws_bytes);
+  if (rc) return rc;
+  return swl::round_launch_ws(n_seg, rows, seg_in, seg_out, w, bias, n, k, seg_lora, lora_table, lora_table_host,
+                              nblk, blk_cols, (hipStream_t)stream, fusion, ws, ws_bytes);
+}
+
 int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg, const int64_t* seg_rows, const int32_t* seg_lora,
                             const swl_lora_entry* lora_table, const swl_lora_entry* lora_table_host, int nblk,
                             const int64_t* blk_cols, void* y, int64_t n, int mode, void* stream) {
@@ -2721,10 +2787,10 @@ int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg, const int64_t* 
       if (e.seg_lora[i] >= 0) items += (seg_rows[i] + 63) / 64 * ((lora_table_host[e.seg_lora[i]].rank * nblk + 63) / 64);
     int u_ks = 1;
     while (u_ks < 16 && items * u_ks < 1024 && (k / 32) / (2 * u_ks) >= 8) u_ks *= 2;
-    void* scratch = nullptr;
-    rc = scratch_get(sizeof(float) * (size_t)u_ks * (size_t)T * (size_t)u_ld, st, &scratch);
+    void* scr = nullptr;
+    rc = scratch_get(sizeof(float) * (size_t)u_ks * (size_t)T * (size_t)u_ld, st, &scr);
     if (rc) return rc;
-    float* u = reinterpret_cast<float*>(scratch);
+    float* u = reinterpret_cast<float*>(scr);
     rc = launch_shrink_gemm(reinterpret_cast<const bf16*>(x), k, n_seg, e.off, seg_rows, e.seg_lora, lora_table_host,
                             nblk, u, u_ld, T * u_ld, u_ks, st);
     if (rc) return rc;
@@ -2967,6 +3033,15 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
                  const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
                  const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
                  const swl_round_fusion* fz) {
+  return round_launch_ws(n_seg, rows, seg_in, seg_out, w, bias, N, K, seg_lora, lora_table, host_entries, nblk,
+                         blk_cols, st, fz, nullptr, 0);
+}
+
+// ws != null: the decode regime only, its partials in [ws, ws + ws_bytes).
+int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
+                    const void* bias, int64_t N, int64_t K, const int32_t* seg_lora, const swl_lora_entry* lora_table,
+                    const swl_lora_entry* host_entries, int nblk, const int64_t* blk_cols, hipStream_t st,
+                    const swl_round_fusion* fz, void* ws, size_t ws_bytes) {
   SWL_CHECK(rows && seg_in && seg_out && w, SWL_ERR_INVALID, "round: null argument");
   SWL_CHECK(n_seg >= 1 && n_seg <= kMaxSeg, SWL_ERR_INVALID, "round: segment count must be in [1, 128]");
   SWL_CHECK(N > 0 && K > 0 && K % 32 == 0, SWL_ERR_INVALID, "round: K must be a positive multiple of 32");
@@ -3009,9 +3084,10 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
       }
     }
     return launch_skinny(reinterpret_cast<const bf16*>(w), reinterpret_cast<const bf16*>(bias), N, K, (int)T, xr, yr,
-                         has_lora ? tl : nullptr, lora_table, host_entries, &L, nblk, fz, st);
+                         has_lora ? tl : nullptr, lora_table, host_entries, &L, nblk, fz, st, ws, ws_bytes);
   }
   SWL_CHECK(!fused, SWL_ERR_INVALID, "round fusion / fragment-tile weights: at most 64 token rows");
+  SWL_CHECK(!ws, SWL_ERR_INVALID, "allocation-free round: at most 64 token rows");
 
   // ------------------------------------------------------ prefill regime
   SWL_CHECK(K % TK == 0, SWL_ERR_INVALID, "round: K must be a multiple of 64 for > 64 tokens");
@@ -3028,10 +3104,10 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   }
   size_t ubytes = 0;
   if (has_lora) ubytes = sizeof(float) * (size_t)u_ks * (size_t)T * (size_t)u_ld;
-  void* scratch = nullptr;
-  int rc = scratch_get(xbytes_al + ubytes, st, &scratch);
+  void* scr = nullptr;
+  int rc = scratch_get(xbytes_al + ubytes, st, &scr);
   if (rc) return rc;
-  bf16* packed = reinterpret_cast<bf16*>(scratch);
+  bf16* packed = reinterpret_cast<bf16*>(scr);
   rc = swl_gather_bf16(seg_in, rows, n_seg, K, packed, st);
   if (rc) return rc;
 
@@ -3047,7 +3123,7 @@ int round_launch(int n_seg, const int64_t* rows, const void* const* seg_in, void
   rc = fill_segptrs(a.out, reinterpret_cast<const void* const*>(seg_out), rows, n_seg, N, &dummy);
   if (rc) return rc;
   if (has_lora) {
-    float* u = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + xbytes_al);
+    float* u = reinterpret_cast<float*>(reinterpret_cast<char*>(scr) + xbytes_al);
     int64_t rws[kMaxSeg];
     for (int i = 0; i < n_seg; ++i) {
       rws[i] = rows[i];

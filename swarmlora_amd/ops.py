@@ -300,10 +300,13 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
 def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], rows: Sequence[int],
              w: torch.Tensor, bias: Optional[torch.Tensor] = None,
              seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
-             blk_cols: Optional[Sequence[int]] = None, fusion: Optional[RoundFusion] = None):
+             blk_cols: Optional[Sequence[int]] = None, fusion: Optional[RoundFusion] = None,
+             noalloc: bool = False):
     """round_fused with the decode-step fusions of `fusion` (round_fusion()).
     A PackedWeight w sets the fusion's w_layout to 1 (decode-shaped rounds
-    only)."""
+    only).  noalloc=True calls the allocation-free entry point
+    (swl_round_ex_noalloc_bf16: at most 64 token rows, partials in the
+    library's fixed 64 MiB device array)."""
     if isinstance(w, PackedWeight):
         if fusion is None:
             fusion = RoundFusion()
@@ -312,8 +315,8 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
         raise ValueError("fusion.w_layout = 1 needs a PackedWeight")
     args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols,
                        out_div=2 if fusion is not None and fusion.out_mode == 2 else 1)
-    _lib.check(_lib.load().swl_round_ex_bf16(*args, ctypes.byref(fusion) if fusion is not None else None,
-                                             _stream()))
+    fn = _lib.load().swl_round_ex_noalloc_bf16 if noalloc else _lib.load().swl_round_ex_bf16
+    _lib.check(fn(*args, ctypes.byref(fusion) if fusion is not None else None, _stream()))
 
 
 def lora_segmented(x: torch.Tensor, seg_rows: Sequence[int], seg_lora: Sequence[int], table: LoraTable,
