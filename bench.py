@@ -17,7 +17,15 @@ per launch over its mean duration, both from HIP events recorded around each
 launch on its stream during eager steps of the same workload (HIP events
 inside a replayed graph carry no timestamps on ROCm).  `cpu_baseline` times
 the CPU oracle's decode_step (torch-CPU bf16, the reference's op order) on a
-bounded sample: the LM head and one layer, scaled to 32 layers.
+bounded sample: the LM head and one layer, scaled to 32 layers, on every
+core the process may use (CPU model and bf16-relevant flags reported).
+
+`config.drop_in` is the drop-in (multi-process) path measured after the
+headline: --ipc-workers worker processes and this process as the
+aggregator, the reference's protocol (worker-side LoRA, host-synchronised
+rounds) and GPU-ordered rounds, with tokens/s, µs per round and the mean
+[LAYER_PROFILE] stage split (gather / round wait / scatter / LoRA / norms
+and attention) of stage-timed tokens.
 """
 
 import argparse
@@ -58,6 +66,10 @@ def parse():
                          "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
                          "shared-memory ring, IPC slots), host-synchronised vs GPU-ordered rounds. The last two "
                          "print lines of their own")
+    ap.add_argument("--ipc-workers", type=int, default=8,
+                    help="drop-in leg of the decode line: worker processes (at most 8; with the aggregator's "
+                         "process at most 9 processes use the GPU)")
+    ap.add_argument("--no-ipc", action="store_true", help="decode: skip the drop-in (multi-process) leg")
     ap.add_argument("--ipc-layers", type=int, default=4, help="ipc: 8B-shaped layers")
     ap.add_argument("--ipc-tokens", type=int, default=8, help="ipc: decode tokens per worker (after 2 warm-up)")
     ap.add_argument("--ipc-pooled", action="store_true",
@@ -76,14 +88,49 @@ def read_traffic():
     return None
 
 
+def host_cpu_info():
+    """CPU model, the x86 flags that matter for bf16 matrix work on the host,
+    and the number of cores this process may use: the affinity mask, capped
+    by a cgroup-v2 CPU quota when one is set (the job's CPU share)."""
+    info = {"model": None, "flags": [], "os_cpu_count": os.cpu_count()}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and info["model"] is None:
+                    info["model"] = line.split(":", 1)[1].strip()
+                elif line.startswith("flags"):
+                    fl = set(line.split(":", 1)[1].split())
+                    info["flags"] = sorted(fl & {"avx2", "avx512f", "avx512_bf16", "amx_bf16", "amx_tile",
+                                                 "avx512_vnni", "avx_vnni"})
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    info["affinity_cpus"] = usable
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            info["cgroup_cpus"] = int(quota) / int(period)
+            usable = max(1, min(usable, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    info["usable_cpus"] = usable
+    return info
+
+
 def cpu_baseline(workers, budget_s):
     """The CPU oracle's batched decode_step (torch-CPU, bf16) at config-4
-    shapes on this host's cores: the LM head alone (layers=0) and with one
-    layer, repeated within the budget; per step = t0 + 32 * (t1 - t0)."""
+    shapes on this host's cores (every core the process may use): the LM head
+    alone (layers=0) and with one layer, repeated within the budget; per
+    step = t0 + 32 * (t1 - t0)."""
     import torch
     from oracle import reference_path as ref
     from swarmlora_amd.decode import DecodeShape
-    threads = torch.get_num_threads()
+    host = host_cpu_info()
+    threads = host["usable_cpus"]
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
     s = DecodeShape()
     g = torch.Generator().manual_seed(0)
 
@@ -114,10 +161,13 @@ def cpu_baseline(workers, budget_s):
             times[L].append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > budget_s and len(times[1]) >= 2:
             break
+    torch.set_num_threads(prev_threads)
     t0 = statistics.median(times[0])
     t1 = statistics.median(times[1])
     step_s = t0 + s.layers * max(t1 - t0, 0.0)
     return {"value": workers / step_s, "unit": "tok/s", "cores": threads, "kind": "port",
+            "cpu_model": host["model"], "cpu_flags": host["flags"], "os_cpu_count": host["os_cpu_count"],
+            "affinity_cpus": host["affinity_cpus"], "cgroup_cpus": host.get("cgroup_cpus"),
             "sample": (f"oracle decode_step (torch-CPU bf16) at config-4 shapes, {workers} workers: LM head alone "
                        f"{t0 * 1e3:.0f} ms and with one layer {t1 * 1e3:.0f} ms (medians of {len(times[1])}); "
                        f"step = LM head + 32 x layer = {step_s * 1e3:.0f} ms; includes the per-step page clone; "
@@ -214,7 +264,7 @@ def _ipc_worker(shm_name, claim, wid, layers, n_tok, gpu_ordered, pooled, out):
         from swarmlora_amd import ext_unified_barrier as ub
         from swarmlora_amd.decode import DecodeShape, synthetic_adapter
         from swarmlora_amd.worker.batched_ops import BatchedAggregatorOps, SlotState
-        from swarmlora_amd.worker.engine import LayerModules, WorkerEngine
+        from swarmlora_amd.worker.engine import LayerModules, StageTimer, WorkerEngine
         from swarmlora_amd.worker.model_builder import (FastLoRAModule, FusedLoRA, SyncFusedGateUp, SyncFusedQKV,
                                                         SyncRemoteLoRALinear)
         from swarmlora_amd.worker.paged_attention import PagedKVCache, RotaryInvFreq, build_vllm_cos_sin_cache
@@ -262,22 +312,30 @@ def _ipc_worker(shm_name, claim, wid, layers, n_tok, gpu_ordered, pooled, out):
             eng.generate_one_token_all(slots)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t1
+        # then two tokens through the stage-timed path ([LAYER_PROFILE])
+        eng.profiler = StageTimer()
+        for _ in range(2):
+            eng.generate_one_token_all(slots)
+        prof = eng.profiler.records
+        eng.profiler = None
         extq.slot_signal_leave(sid)
         ub.close_slot(sid)
-        out.put((wid, dt, None))
+        out.put((wid, (dt, prof), None))
     except Exception:
         import traceback
         out.put((wid, None, traceback.format_exc()))
 
 
-def ipc(args):
+def ipc_measure(W, L, n_tok, pooled):
     """The multi-process serving path: this process is the aggregator (native
-    main loop on a thread, 8B-shaped weights for --ipc-layers layers, embed
-    and LM head), --workers worker processes (at most 8 here) decode one
-    token per step each through the shared-memory ring and IPC-mapped slots.
-    Runs the same decode twice: host-synchronised rounds (the reference's
-    protocol) and GPU-ordered rounds (sequence words in the slot buffers
-    waited on by the streams).  `value` is tokens/s of the GPU-ordered run."""
+    main loop on a thread, 8B-shaped weights for L layers, embed and LM
+    head), W worker processes decode one token per step each through the
+    shared-memory ring and IPC-mapped slots.  Runs the same decode twice:
+    host-synchronised rounds (the reference's protocol) and GPU-ordered
+    rounds (sequence words in the slot buffers waited on by the streams).
+    Per mode: tokens/s, step time and µs per round over n_tok timed tokens
+    per worker, then the mean [LAYER_PROFILE] stage split of two stage-timed
+    tokens per worker."""
     import multiprocessing as mp
     import threading
     import torch
@@ -285,8 +343,6 @@ def ipc(args):
     from swarmlora_amd import ext_ipc_queue as extq
     from swarmlora_amd.decode import DecodeShape, synthetic_weights
     dev = torch.device("cuda:0")
-    W = min(args.workers, 8)
-    L = args.ipc_layers
     s = DecodeShape(layers=L)
     wts = synthetic_weights(s, dev, seed=0)
     res = {}
@@ -301,7 +357,7 @@ def ipc(args):
         agg.init_aggregator_finalize()
         agg.init_embed_lm_head_weights(wts["embed"], wts["lm_head"])
         agg.init_aggregator_queue(q["shm_name"], 1024)
-        if args.ipc_pooled:
+        if pooled:
             from swarmlora_amd.decode import synthetic_adapter
             agg.clear_adapters()
             for wid in range(W):
@@ -316,18 +372,19 @@ def ipc(args):
         loop.start()
         ctx = mp.get_context("spawn")
         out = ctx.Queue()
-        procs = [ctx.Process(target=_ipc_worker, args=(q["shm_name"], claims[w], w, L, args.ipc_tokens,
-                                                       mode == "gpu_ordered", args.ipc_pooled, out))
+        procs = [ctx.Process(target=_ipc_worker, args=(q["shm_name"], claims[w], w, L, n_tok,
+                                                       mode == "gpu_ordered", pooled, out))
                  for w in range(W)]
-        times = []
+        times, profs = [], []
         try:
             for p in procs:
                 p.start()
             for _ in procs:
-                wid, dt, err = out.get(timeout=600)
+                wid, r, err = out.get(timeout=600)
                 if err:
                     raise RuntimeError(f"worker {wid}: {err}")
-                times.append(dt)
+                times.append(r[0])
+                profs.extend(r[1])
         finally:
             extq.set_quit(1)
             loop.join(timeout=60)
@@ -344,9 +401,22 @@ def ipc(args):
             agg.cleanup_slot_pool()
             extq.close_queue()
         rounds = 2 + 4 * L
-        step_s = max(times) / args.ipc_tokens
+        step_s = max(times) / n_tok
+        split = {k: round(statistics.fmean(r[k] for r in profs), 1)
+                 for k in ("gather_us", "gemm_us", "scatter_us", "lora_us", "attn_us", "compute_us", "wall_us")}
+        split["ipc_pct"] = round(100.0 * (split["gather_us"] + split["scatter_us"]) / split["wall_us"], 1)
+        split["round_wait_us"] = round(split["gemm_us"] / rounds, 1)
         res[mode] = {"tok_s": round(W / step_s, 1), "ms_per_step": round(step_s * 1e3, 3),
-                     "us_per_round": round(step_s * 1e6 / rounds, 1)}
+                     "us_per_round": round(step_s * 1e6 / rounds, 1), "layer_profile": split}
+    return res
+
+
+def ipc(args):
+    """--workload ipc: ipc_measure's line on its own; `value` is tokens/s of
+    the GPU-ordered run."""
+    W = min(args.workers, 8)
+    L = args.ipc_layers
+    res = ipc_measure(W, L, args.ipc_tokens, args.ipc_pooled)
     line = {
         "metric": "multi-process decode tok/s (ipc path, GPU-ordered rounds)",
         "value": res["gpu_ordered"]["tok_s"],
@@ -501,6 +571,23 @@ def main():
         "cpu_baseline": cpu,
     }
     dec.close()
+    del dec
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    if not args.no_ipc:
+        # the drop-in path: real worker processes, the shared-memory ring and
+        # IPC slot buffers, at the same 8B widths (a few layers)
+        W_ipc = max(1, min(args.ipc_workers, 8))
+        try:
+            res = ipc_measure(W_ipc, args.ipc_layers, args.ipc_tokens, pooled=False)
+            line["config"]["drop_in"] = {
+                "workload": f"{W_ipc} worker processes + this aggregator process, {args.ipc_layers} 8B-shaped "
+                            "layers, rank-16 adapter per worker applied on the worker (the reference's protocol), "
+                            f"{args.ipc_tokens} timed tokens per worker",
+                "workers": W_ipc, "layers": args.ipc_layers, "rounds_per_token": 2 + 4 * args.ipc_layers,
+                **res}
+        except Exception as e:  # the headline line is still printed
+            line["config"]["drop_in"] = {"error": f"{type(e).__name__}: {e}"[:2000]}
     print(json.dumps(line), flush=True)
 
 

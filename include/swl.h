@@ -224,7 +224,8 @@ int swl_round_ex_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
  * device array of the library (one copy per GPU, held until the process
  * ends) instead of the growable library scratch, and the call allocates and
  * frees nothing.  A round whose partials need more than 64 MiB is refused
- * with an error (every 8B-shaped round and the LM head fit at 64 rows).
+ * with an error (every 8B-shaped projection round fits at 64 token rows,
+ * the 128256-wide LM head up to 32).
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (other streams, other threads) race and must be ordered by the
  * caller. */

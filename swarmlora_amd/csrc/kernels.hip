@@ -1078,6 +1078,75 @@ __global__ __launch_bounds__(256) void matmul_generic_kernel(const bf16* __restr
   }
 }
 
+// Few output columns over long rows (the LoRA shrink x . A of a worker's
+// few tokens: N = rank or a fused n * rank, K = hidden or intermediate).
+// One 1024-thread workgroup per row m streams B once with 16-byte loads;
+// x[m, :] is staged in LDS.  NT (B(k, n) = b[n*ldb + k]): wave w owns the
+// columns n = w, w + 16, ..., its lanes stride k in 8-element vectors and a
+// wave reduction finishes each column.  NN (B(k, n) = b[k*ldb + n]): thread
+// t owns 8 adjacent columns (cv = t % N8) over the k-rows p, p + P, ... with
+// P a power of two, and the P partial sums of each column are reduced as a
+// tree in LDS.  fp32 accumulation, alpha applied before the one bf16
+// rounding.  Host-checked: N <= 256, K % 8 == 0, 16-byte aligned rows,
+// N % 8 == 0 (NN), K <= kShrinkMaxK.
+constexpr int64_t kShrinkMaxK = 16384;
+
+template <bool NT>
+__global__ __launch_bounds__(1024) void matmul_shrink_kernel(const bf16* __restrict__ x, int64_t ldx,
+                                                             const bf16* __restrict__ b, int64_t ldb,
+                                                             bf16* __restrict__ y, int64_t ldy, int N, int64_t K,
+                                                             float alpha, int P) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* xs = reinterpret_cast<bf16*>(smem);                      // [K]
+  float* red = reinterpret_cast<float*>(smem + K * sizeof(bf16));  // NN: [P][N]
+  const int64_t m = blockIdx.x;
+  const bf16* xr = x + m * ldx;
+  const int tid = threadIdx.x;
+  const int64_t K8 = K >> 3;
+  for (int64_t i = tid; i < K8; i += 1024)
+    *reinterpret_cast<u32x4*>(xs + 8 * i) = ld16(xr + 8 * i);
+  __syncthreads();
+  if constexpr (NT) {
+    const int w = tid >> 6, lane = tid & 63;
+    for (int n = w; n < N; n += 16) {
+      const bf16* br = b + (int64_t)n * ldb;
+      float acc = 0.f;
+#pragma unroll 4
+      for (int64_t i = lane; i < K8; i += 64) {
+        float xv[8], bv[8];
+        unpack8(*reinterpret_cast<const u32x4*>(xs + 8 * i), xv);
+        unpack8(ld16(br + 8 * i), bv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += xv[j] * bv[j];
+      }
+      for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      if (lane == 0) y[m * ldy + n] = f2bf(alpha * acc);
+    }
+  } else {
+    const int N8 = N >> 3;
+    const int cv = tid % N8, p = tid / N8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (p < P) {
+#pragma unroll 4
+      for (int64_t k = p; k < K; k += P) {
+        float bv[8];
+        unpack8(ld16(b + k * ldb + 8 * cv), bv);
+        const float xv = bf2f(xs[k]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += xv * bv[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red[(int64_t)p * N + 8 * cv + j] = acc[j];
+    }
+    __syncthreads();
+    for (int s = P >> 1; s >= 1; s >>= 1) {
+      for (int e = tid; e < s * N; e += 1024) red[e] += red[e + s * N];
+      __syncthreads();
+    }
+    if (tid < N) y[m * ldy + tid] = f2bf(alpha * red[tid]);
+  }
+}
+
 // ------------------------------------------------------ paged attention ---
 struct AttnArgs {
   bf16* q;               // token t at q + t*qs: [hq, 128]
@@ -2570,9 +2639,10 @@ int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
 
 // ================================================ allocation-free scratch ===
 // Device memory of swl_round_ex_noalloc_bf16: the decode projection's K-slice
-// partials of one round (64 MiB holds them for every 8B-shaped round and the
-// LM head at 64 token rows).  Every GPU the library runs on holds its own
-// copy, at its own address, from module load until the process ends.  Host
+// partials of one round (64 MiB holds them for every 8B-shaped projection
+// round at 64 token rows and for the 128256-wide LM head up to 32 rows).
+// Every GPU the library runs on holds its own copy, at its own address, from
+// module load until the process ends.  Host
 // code never passes the array's name to a kernel (on the host it is only a
 // stand-in for the symbol): the device address is looked up once per device
 // with hipGetSymbolAddress and used instead.
@@ -2826,6 +2896,27 @@ int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int 
   SWL_CHECK(m >= 0 && n > 0 && k > 0, SWL_ERR_INVALID, "swl_matmul_bf16: bad shape");
   SWL_CHECK(m <= 65535, SWL_ERR_INVALID, "swl_matmul_bf16: m too large");
   if (m == 0) return SWL_OK;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(b)) & 15) == 0 &&
+                      ldx % 8 == 0 && ldb % 8 == 0 && k % 8 == 0;
+  if (vec_ok && m <= kSkinnyMaxTok && n <= 256 && k >= 512 && k <= kShrinkMaxK && (trans_b || n % 8 == 0)) {
+    int P = 0;
+    size_t lds = (size_t)k * sizeof(bf16);
+    if (!trans_b) {
+      P = 1;
+      while (P * 2 * (n / 8) <= 1024) P *= 2;
+      lds += (size_t)P * n * sizeof(float);
+    }
+    if (trans_b)
+      hipLaunchKernelGGL(matmul_shrink_kernel<true>, dim3((unsigned)m), dim3(1024), lds, (hipStream_t)stream,
+                         reinterpret_cast<const bf16*>(x), ldx, reinterpret_cast<const bf16*>(b), ldb,
+                         reinterpret_cast<bf16*>(y), ldy, (int)n, k, alpha, P);
+    else
+      hipLaunchKernelGGL(matmul_shrink_kernel<false>, dim3((unsigned)m), dim3(1024), lds, (hipStream_t)stream,
+                         reinterpret_cast<const bf16*>(x), ldx, reinterpret_cast<const bf16*>(b), ldb,
+                         reinterpret_cast<bf16*>(y), ldy, (int)n, k, alpha, P);
+    SWL_LAUNCH_CHECK("matmul_shrink_kernel launch");
+    return SWL_OK;
+  }
   hipLaunchKernelGGL(matmul_generic_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)m), dim3(256), 0,
                      (hipStream_t)stream, reinterpret_cast<const bf16*>(x), ldx, reinterpret_cast<const bf16*>(b),
                      ldb, trans_b, reinterpret_cast<bf16*>(y), ldy, n, k, alpha);

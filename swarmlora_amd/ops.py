@@ -529,6 +529,60 @@ def silu_mul_rows(in_rows, out_rows, inter: int):
     _lib.check(_lib.load().swl_silu_mul_rows_bf16(src.array, dst.array, len(src), inter, _stream()))
 
 
+def _row_ptrs(t: torch.Tensor, c0: int, c1: int):
+    """Host array of the device addresses of rows c0..c1 of a contiguous 2-D
+    bf16 matrix (16-byte aligned rows when the base is and the width is a
+    multiple of 8)."""
+    base, step = t.data_ptr(), t.stride(0) * t.element_size()
+    arr = (ctypes.c_void_p * (c1 - c0))()
+    for i in range(c1 - c0):
+        arr[i] = base + (c0 + i) * step
+    return arr
+
+
+def _rows_matrix(t: torch.Tensor, name: str) -> torch.Tensor:
+    _need(t, name)
+    m = t.reshape(-1, t.shape[-1])
+    if not m.is_contiguous() or m.data_ptr() % 16 or m.shape[-1] % 8:
+        raise ValueError(f"{name} must be contiguous, 16-byte aligned, last dim a multiple of 8")
+    return m
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """LlamaRMSNorm of every row of x [..., d] into a new tensor (the
+    worker's input / post-attention / final norms, worker_sync.py:1344-1350,
+    :314-319), 64 rows per launch of the row kernel."""
+    h = _rows_matrix(x, "x")
+    _need(weight, "weight")
+    n, d = h.shape
+    if weight.numel() != d or not weight.is_contiguous():
+        raise ValueError("weight must be contiguous [d]")
+    out = torch.empty_like(x)
+    o = out.view(n, d)
+    lib, st = _lib.load(), _stream()
+    for c0 in range(0, n, RowSet.MAX_ROWS):
+        c1 = min(n, c0 + RowSet.MAX_ROWS)
+        _lib.check(lib.swl_rmsnorm_rows_bf16(ctypes.c_void_p(h.data_ptr() + c0 * d * 2), c1 - c0, d, None,
+                                             _ptr(weight), float(eps), _row_ptrs(o, c0, c1), st))
+    return out
+
+
+def silu_mul(gu: torch.Tensor, inter: int) -> torch.Tensor:
+    """F.silu(gate) * up for a fused Gate+Up output gu [..., 2*inter] (gate
+    columns first) into a new [..., inter] tensor (worker_sync.py:158)."""
+    m = _rows_matrix(gu, "gu")
+    n = m.shape[0]
+    if m.shape[1] != 2 * inter:
+        raise ValueError(f"gu must be [..., {2 * inter}]")
+    out = torch.empty(*gu.shape[:-1], inter, dtype=gu.dtype, device=gu.device)
+    o = out.view(n, inter)
+    lib, st = _lib.load(), _stream()
+    for c0 in range(0, n, RowSet.MAX_ROWS):
+        c1 = min(n, c0 + RowSet.MAX_ROWS)
+        _lib.check(lib.swl_silu_mul_rows_bf16(_row_ptrs(m, c0, c1), _row_ptrs(o, c0, c1), c1 - c0, inter, st))
+    return out
+
+
 def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: int, k_cache: torch.Tensor,
                          v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
                          positions: Optional[torch.Tensor], cos_sin: Optional[torch.Tensor], softmax_scale: float,

@@ -26,6 +26,29 @@ from .model_builder import OP_DOWN_PROJ, OP_EMBED, OP_GATE_UP_FUSED, OP_LM_HEAD,
 from .model_builder import SyncRemoteLoRALinear
 
 
+class _NoStage:
+    __slots__ = ()
+
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_STAGE = _NoStage()
+
+
+class NullTimer:
+    """Stage timer that times nothing (the unprofiled path)."""
+
+    def stage(self, name):
+        return _NO_STAGE
+
+
+NULL_TIMER = NullTimer()
+
+
 @dataclass
 class SlotState:
     """Per-request state of an active slot (worker_sync.py:100-118)."""
@@ -82,23 +105,27 @@ class BatchedAggregatorOps:
         self.hidden_dim = slot_manager.base_client.hidden_dim
         self.pooled_adapter = pooled_adapter
         self._x_key = 0 if pooled_adapter is None else int(pooled_adapter) + 1
+        # stage timer of WorkerEngine's profiled path (times nothing otherwise)
+        self.timer = NULL_TIMER
 
     def barrier_sync(self, epoch: int):
         extq.wait_for_epoch(epoch)
 
     def _get_outputs_all(self, slots, dims):
         slot_id, state = next(iter(slots.items()))
-        return {slot_id: ub.get_outputs_slot(slot_id, dims, state.hidden)}
+        with self.timer.stage("scatter"):
+            return {slot_id: ub.get_outputs_slot(slot_id, dims, state.hidden)}
 
     def _seq(self, slot_id):
         return ub.input_seq(slot_id) if self.gpu_ordered else 0
 
     def _submit(self, op, layer_idx, slot_id, x):
         b, t, d = x.shape
-        ub.prepare_input_slot(slot_id, op, x)
-        extq.submit_slot_command(op, layer_idx, slot_id, self.worker_id, b, t, d, self._x_key, 0, 0, 0, 0,
-                                 in_seq=self._seq(slot_id))
-        extq.slot_signal_ready(slot_id)
+        with self.timer.stage("gather"):
+            ub.prepare_input_slot(slot_id, op, x)
+            extq.submit_slot_command(op, layer_idx, slot_id, self.worker_id, b, t, d, self._x_key, 0, 0, 0, 0,
+                                     in_seq=self._seq(slot_id))
+            extq.slot_signal_ready(slot_id)
 
     # ---------------------------------------------------------------- embed
     def embed_submit_all(self, slots) -> int:
@@ -121,20 +148,22 @@ class BatchedAggregatorOps:
         slot_id, state = next(iter(slots.items()))
         self._submit(OP_QKV_FUSED, layer_idx, slot_id, state.hidden)
         fq = fused_qkv_modules[layer_idx]
-        if self.pooled_adapter is None and fq.fused_lora is not None and fq.fused_lora.has_lora:
-            deltas = {slot_id: fq.fused_lora(state.hidden)}
-        else:
-            deltas = {slot_id: (None, None, None)}
+        with self.timer.stage("lora"):
+            if self.pooled_adapter is None and fq.fused_lora is not None and fq.fused_lora.has_lora:
+                deltas = {slot_id: fq.fused_lora(state.hidden)}
+            else:
+                deltas = {slot_id: (None, None, None)}
         return epoch, deltas
 
     def qkv_get_all(self, slots, layer_idx: int, deltas, dims: List[int]):
         raw = self._get_outputs_all(slots, dims)
         res = {}
-        for sid in slots:
-            q, k, v = raw[sid]
-            dq, dk, dv = deltas.get(sid, (None, None, None))
-            res[sid] = (q + dq if dq is not None else q, k + dk if dk is not None else k,
-                        v + dv if dv is not None else v)
+        with self.timer.stage("lora"):
+            for sid in slots:
+                q, k, v = raw[sid]
+                dq, dk, dv = deltas.get(sid, (None, None, None))
+                res[sid] = (q + dq if dq is not None else q, k + dk if dk is not None else k,
+                            v + dv if dv is not None else v)
         return res
 
     # -------------------------------------------------------------------- O
@@ -145,16 +174,18 @@ class BatchedAggregatorOps:
         self._submit(OP_O_PROJ, layer_idx, slot_id, x)
         o = o_proj_modules[layer_idx]
         use = self.pooled_adapter is None and isinstance(o, SyncRemoteLoRALinear)
-        return epoch, {slot_id: o.delta(x) if use else None}
+        with self.timer.stage("lora"):
+            return epoch, {slot_id: o.delta(x) if use else None}
 
     def o_proj_get_all(self, slots, layer_idx: int, deltas, out_dim: int):
         raw = self._get_outputs_all(slots, [out_dim])
-        for sid, state in slots.items():
-            r = raw[sid][0]
-            d = deltas.get(sid)
-            if d is not None:
-                r = r + d
-            state.hidden = state.residual + r
+        with self.timer.stage("lora"):
+            for sid, state in slots.items():
+                r = raw[sid][0]
+                d = deltas.get(sid)
+                if d is not None:
+                    r = r + d
+                state.hidden = state.residual + r
 
     # -------------------------------------------------------------- Gate+Up
     def gate_up_submit_all(self, slots, layer_idx: int, fused_gate_up_modules: List):
@@ -162,19 +193,28 @@ class BatchedAggregatorOps:
         slot_id, state = next(iter(slots.items()))
         self._submit(OP_GATE_UP_FUSED, layer_idx, slot_id, state.hidden)
         fg = fused_gate_up_modules[layer_idx]
-        if self.pooled_adapter is None and fg.fused_lora is not None and fg.fused_lora.has_lora:
-            deltas = {slot_id: fg.fused_lora(state.hidden)}
-        else:
-            deltas = {slot_id: (None, None)}
+        with self.timer.stage("lora"):
+            if self.pooled_adapter is None and fg.fused_lora is not None and fg.fused_lora.has_lora:
+                deltas = {slot_id: fg.fused_lora(state.hidden)}
+            else:
+                deltas = {slot_id: (None, None)}
         return epoch, deltas
 
     def gate_up_get_all(self, slots, layer_idx: int, deltas, dims: List[int]):
+        # g and u are the two halves of the freshly copied output; the deltas
+        # are added in place (the values of g + dg, u + du) so the pair stays
+        # one [.., 2 * inter] buffer that the SiLU*up kernel reads directly
         raw = self._get_outputs_all(slots, dims)
         res = {}
-        for sid in slots:
-            g, u = raw[sid]
-            dg, du = deltas.get(sid, (None, None))
-            res[sid] = (g + dg if dg is not None else g, u + du if du is not None else u)
+        with self.timer.stage("lora"):
+            for sid in slots:
+                g, u = raw[sid]
+                dg, du = deltas.get(sid, (None, None))
+                if dg is not None:
+                    g.add_(dg)
+                if du is not None:
+                    u.add_(du)
+                res[sid] = (g, u)
         return res
 
     # ----------------------------------------------------------------- Down
@@ -185,16 +225,18 @@ class BatchedAggregatorOps:
         self._submit(OP_DOWN_PROJ, layer_idx, slot_id, x)
         dp = down_proj_modules[layer_idx]
         use = self.pooled_adapter is None and isinstance(dp, SyncRemoteLoRALinear)
-        return epoch, {slot_id: dp.delta(x) if use else None}
+        with self.timer.stage("lora"):
+            return epoch, {slot_id: dp.delta(x) if use else None}
 
     def down_proj_get_all(self, slots, layer_idx: int, deltas, out_dim: int):
         raw = self._get_outputs_all(slots, [out_dim])
-        for sid, state in slots.items():
-            r = raw[sid][0]
-            d = deltas.get(sid)
-            if d is not None:
-                r = r + d
-            state.hidden = state.mlp_residual + r
+        with self.timer.stage("lora"):
+            for sid, state in slots.items():
+                r = raw[sid][0]
+                d = deltas.get(sid)
+                if d is not None:
+                    r = r + d
+                state.hidden = state.mlp_residual + r
 
     # -------------------------------------------------------------- LM head
     def lm_head_submit_all(self, slots) -> int:

@@ -305,6 +305,38 @@ def test_matmul_layouts(dev, trans_b):
     assert_close(y, want, what="matmul")
 
 
+@pytest.mark.parametrize("m,k,n,trans_b", [(1, 4096, 48, False), (1, 14336, 16, True), (1, 4096, 16, True),
+                                             (7, 4096, 32, False), (64, 1024, 256, False), (3, 14336, 8, False),
+                                             (2, 16384, 256, True), (1, 520, 40, True)])
+def test_matmul_shrink_shapes(dev, m, k, n, trans_b):
+    """The worker's LoRA shrink shapes (few columns, long rows: one
+    workgroup per row, LDS-staged x) against a float32 evaluation of the
+    same bf16 operands."""
+    ops = _ops()
+    x = randn((m, k), SEED_X)
+    b = randn((n, k) if trans_b else (k, n), SEED_W, std=0.02)
+    y = ops.matmul(x.to(dev), b.to(dev), trans_b=trans_b, alpha=2.0)
+    torch.cuda.synchronize()
+    want = (x.float() @ (b.float().t() if trans_b else b.float())) * 2.0
+    assert_close(y, want, what=f"matmul {m}x{k}x{n} nt={trans_b}")
+
+
+def test_matmul_shrink_unaligned_stride_takes_generic_path(dev):
+    """A row stride that breaks 16-byte alignment is still computed (by the
+    generic kernel) and agrees with the aligned case."""
+    ops = _ops()
+    m, k, n = 2, 4096, 16
+    x = randn((m, k + 3), SEED_X)
+    b = randn((n, k), SEED_W, std=0.02)
+    xd = x.to(dev)
+    y1 = ops.matmul(xd[:, :k], b.to(dev), trans_b=True)
+    y2 = ops.matmul(xd[:, :k].contiguous(), b.to(dev), trans_b=True)
+    torch.cuda.synchronize()
+    want = x[:, :k].float() @ b.float().t()
+    assert_close(y1, want, what="unaligned")
+    assert_close(y2, want, what="aligned")
+
+
 def test_matmul_strided_block_of_fused_B(dev):
     """A column block of a block-diagonal fused_B is read through its row stride."""
     ops = _ops()

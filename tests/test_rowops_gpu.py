@@ -172,3 +172,42 @@ def test_row_ops_reject_bad_rows(dev):
         ops.silu_mul_rows([big[1:129]], [big[:64]], 64)  # misaligned row
     with pytest.raises(ValueError):
         ops.silu_mul_rows([big] * 65, [big] * 65, 64)  # more than 64 rows
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 4096), (1, 150, 512), (2, 70, 64)])
+def test_rms_norm_matrix_matches_row_kernel(dev, shape):
+    """ops.rms_norm (the worker engine's norm) over [b, t, d] in 64-row
+    launches: every row equals the oracle, and rows past the first launch
+    equal what the row kernel gives for them alone."""
+    ops = _ops()
+    d = shape[-1]
+    x = randn(shape, 11)
+    w = (1 + randn((d,), 12, std=0.1).float()).to(BF16)
+    got = ops.rms_norm(x.to(dev), w.to(dev), 1e-5)
+    torch.cuda.synchronize()
+    assert got.shape == x.shape
+    assert_close(got.cpu(), ref.rms_norm(x, w, 1e-5), what="rms_norm")
+    flat = x.reshape(-1, d)
+    n = flat.shape[0]
+    tail = list(range(max(0, n - 3), n))
+    outs = _rows(dev, len(tail), d)
+    ops.rmsnorm_rows(flat[tail].to(dev).contiguous(), w.to(dev), 1e-5, [o[:d] for o in outs])
+    torch.cuda.synchronize()
+    for o, t in zip(outs, tail):
+        assert bits_equal(o[:d], got.reshape(-1, d)[t])
+
+
+@pytest.mark.parametrize("t,inter", [(1, 14336), (130, 96)])
+def test_engine_silu_mul_reads_fused_halves(dev, t, inter):
+    """The worker engine's SiLU*up: g and u as the two halves of one Gate+Up
+    output (read in place, no copy) and as separate tensors (concatenated
+    first) give the same bits, equal to the oracle within tolerance."""
+    from swarmlora_amd.worker.engine import silu_mul
+    gu = randn((1, t, 2 * inter), 13, std=2.0).to(dev)
+    g, u = gu.split([inter, inter], -1)
+    a = silu_mul(g, u)
+    b = silu_mul(g.clone(), u.clone())
+    torch.cuda.synchronize()
+    assert bits_equal(a, b)
+    want = ref.silu_mul(gu[..., :inter].cpu(), gu[..., inter:].cpu())
+    assert_close(a.cpu(), want, what="engine silu*up")

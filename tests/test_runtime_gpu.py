@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import reference_path as ref
-from tests._util import BF16, assert_close, randn
+from tests._util import BF16, assert_close, randn, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -260,9 +260,14 @@ def test_end_to_end_workers_through_ipc(dev, pooled, gpu_ordered):
         assert torch.cat([s.reshape(-1) for s in steps[:2]]).tolist() == prompts[wid]
         want = oracle_steps(Wt, adapter(wid), steps)
         for si, ((_, hid), wv) in enumerate(zip(rec, want)):
-            # two layers of bf16 rounding differences compound; the final
-            # RMSNorm rescales them, so compare at 3e-2 of the largest entry
-            assert_close(hid, wv[:, -hid.shape[1]:, :], tol=3e-2, what=f"worker {wid} step {si}")
+            # two layers of bf16 rounding differences compound (different
+            # summation orders on both sides, bf16 intermediates between the
+            # rounds), then the final RMSNorm rescales them; measured up to
+            # 5.2e-3 with the worker's own LoRA and 1.03e-2 with the pooled
+            # epilogue, so the bar here is 1.5e-2 of the largest entry
+            e = rel_err(hid, wv[:, -hid.shape[1]:, :])
+            print(f"[e2e pooled={pooled} gpu_ordered={gpu_ordered}] worker {wid} step {si}: {e:.3e}")
+            assert e <= 1.5e-2, f"worker {wid} step {si}: normalised max error {e:.3e} > 1.5e-2"
         # greedy tokens follow the oracle's argmax of the same hidden states
         for si, ((_, hid), wv) in enumerate(zip(rec[1:], want[1:]), start=1):
             logits = (wv[:, -1, :].float() @ Wt["lm_head"].float().t())
