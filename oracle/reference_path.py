@@ -211,10 +211,37 @@ class PagedKVCacheRef:
 
 
 # ------------------------------------------------------------- RoPE / attn --
-def rope_inv_freq(head_dim: int, theta: float) -> torch.Tensor:
-    """Plain RoPE inverse frequencies theta^(-2i/d), the default of HF
-    LlamaRotaryEmbedding (model_builder.py:293-296 builds it from the config)."""
-    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+def rope_inv_freq(head_dim: int, theta: float, rope_scaling: dict = None) -> torch.Tensor:
+    """RoPE inverse frequencies of HF LlamaRotaryEmbedding, which
+    model_builder.py:293-296 builds from the model config: theta^(-2i/d), and
+    with rope_scaling {"rope_type": "llama3", "factor", "low_freq_factor",
+    "high_freq_factor", "original_max_position_embeddings"} (Llama 3.1) the
+    published Llama 3.1 frequency remap: wavelengths 2*pi/f longer than
+    L/low_freq_factor are divided by factor, shorter than L/high_freq_factor
+    kept, and in between interpolated linearly in L/wavelength between f/factor
+    and f (L = original_max_position_embeddings)."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+    if not rope_scaling:
+        return inv
+    kind = rope_scaling.get("rope_type", rope_scaling.get("type"))
+    if kind == "default":
+        return inv
+    if kind != "llama3":
+        raise ValueError(f"rope_scaling type {kind!r} is not restated here")
+    factor = float(rope_scaling["factor"])
+    lo, hi = float(rope_scaling["low_freq_factor"]), float(rope_scaling["high_freq_factor"])
+    L = float(rope_scaling["original_max_position_embeddings"])
+    out = []
+    for f in inv.tolist():
+        wavelen = 2 * math.pi / f
+        if wavelen < L / hi:
+            out.append(f)
+        elif wavelen > L / lo:
+            out.append(f / factor)
+        else:
+            smooth = (L / wavelen - lo) / (hi - lo)
+            out.append((1 - smooth) * f / factor + smooth * f)
+    return torch.tensor(out, dtype=torch.float32)
 
 
 def cos_sin_cache(inv_freq: torch.Tensor, max_seq_len: int, dtype=BF16) -> torch.Tensor:

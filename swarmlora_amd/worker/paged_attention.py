@@ -7,7 +7,8 @@ build_vllm_cos_sin_cache :131-142).  Pages use the flash-attn layout
 reads; freed pages are zeroed by a libswl kernel.
 """
 
-from typing import Dict, List
+import math
+from typing import Dict, List, Optional
 
 import torch
 
@@ -97,9 +98,28 @@ def build_vllm_cos_sin_cache(rotary_emb, max_seq_len: int, device, dtype: torch.
 
 
 class RotaryInvFreq:
-    """Minimal stand-in for HF LlamaRotaryEmbedding's `inv_freq`: plain
-    theta^(-2i/d) frequencies (no rope scaling)."""
+    """Stand-in for HF LlamaRotaryEmbedding's `inv_freq` (the rotary that
+    model_builder.py:293-296 builds from the model config): theta^(-2i/d),
+    and with rope_scaling of type "llama3" (Llama 3.1 configs) the Llama 3.1
+    frequency remap: f / factor for wavelengths above
+    original_max_position_embeddings / low_freq_factor, f below
+    original_max_position_embeddings / high_freq_factor, a linear blend in
+    between."""
 
-    def __init__(self, head_dim: int, theta: float, device="cpu"):
-        self.inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64, device=device).float()
-                                         / head_dim))
+    def __init__(self, head_dim: int, theta: float, device="cpu", rope_scaling: Optional[dict] = None):
+        inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64, device=device).float() / head_dim))
+        kind = (rope_scaling or {}).get("rope_type", (rope_scaling or {}).get("type", "default"))
+        if kind == "llama3":
+            factor = float(rope_scaling["factor"])
+            lo = float(rope_scaling["low_freq_factor"])
+            hi = float(rope_scaling["high_freq_factor"])
+            old_len = float(rope_scaling["original_max_position_embeddings"])
+            wavelen = 2 * math.pi / inv
+            scaled = torch.where(wavelen > old_len / lo, inv / factor, inv)
+            smooth = (old_len / wavelen - lo) / (hi - lo)
+            blended = (1 - smooth) * scaled / factor + smooth * scaled
+            medium = (wavelen >= old_len / hi) & (wavelen <= old_len / lo)
+            inv = torch.where(medium, blended, scaled)
+        elif kind != "default":
+            raise ValueError(f"rope_scaling type {kind!r} is not supported")
+        self.inv_freq = inv

@@ -412,3 +412,37 @@ def test_decode_step_partial_layers_and_worker_batching():
     want = ref.rms_norm(wts["embed"][ids], wts["final_norm"], c.eps)
     assert bits_equal(hn0, want)
     assert bits_equal(lg0, ref.base_gemm(want, wts["lm_head"]))
+
+
+def test_rope_inv_freq_llama3_scaling_matches_transformers():
+    """Llama 3.1's rope_scaling (type llama3): the oracle's remap equals
+    transformers' own initializer for that type, which is what the
+    reference's LlamaRotaryEmbedding(config) calls (model_builder.py:293-296);
+    the unscaled band and the factor-divided band are also checked by hand."""
+    from transformers import LlamaConfig
+    from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+    sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, head_dim=128, rope_theta=500000.0,
+                      max_position_embeddings=131072, rope_scaling=dict(sc))
+    want, _ = ROPE_INIT_FUNCTIONS["llama3"](cfg, "cpu")
+    got = ref.rope_inv_freq(128, 500000.0, sc)
+    assert torch.allclose(got, want.float(), rtol=1e-6, atol=0)
+    plain = ref.rope_inv_freq(128, 500000.0)
+    wl = 2 * math.pi / plain
+    hi_band, lo_band = wl < 8192 / 4.0, wl > 8192 / 1.0
+    assert hi_band.any() and lo_band.any() and (~hi_band & ~lo_band).any()
+    assert torch.equal(got[hi_band], plain[hi_band])
+    assert torch.allclose(got[lo_band], plain[lo_band] / 8.0, rtol=1e-7)
+
+
+def test_worker_rotary_inv_freq_llama3_matches_oracle():
+    """The worker's RotaryInvFreq (host-side torch) with the same scaling."""
+    from swarmlora_amd.worker.paged_attention import RotaryInvFreq
+    sc = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+    assert torch.allclose(RotaryInvFreq(128, 500000.0, rope_scaling=sc).inv_freq,
+                          ref.rope_inv_freq(128, 500000.0, sc), rtol=1e-6, atol=0)
+    assert torch.equal(RotaryInvFreq(128, 500000.0).inv_freq, ref.rope_inv_freq(128, 500000.0))
+    with pytest.raises(ValueError):
+        RotaryInvFreq(128, 500000.0, rope_scaling={"rope_type": "yarn", "factor": 4.0})
