@@ -43,8 +43,9 @@ REFERENCE_TOK_S = 314.0
 # HBM bytes per launch of the decode projection's base kernel, measured with
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and scaled by a
 # copy kernel of known size (the summary file gives the commands and factors)
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "split_kernel_decode_config4_pmc.md")
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+TRAFFIC_FILES = {True: os.path.join(PROFILES, "fullk_kernel_decode_config4_pmc.md"),
+                 False: os.path.join(PROFILES, "split_kernel_decode_config4_pmc.md")}
 
 
 def parse():
@@ -61,6 +62,9 @@ def parse():
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--weights", choices=("packed", "row-major"), default="packed",
                     help="decode: projection weights in fragment tiles (default) or row-major")
+    ap.add_argument("--whole-k", choices=("lm", "all", "none"), default="lm",
+                    help="decode: rounds run as whole-K rounds (one launch, no partial sums): the LM head "
+                         "(default), every round with K <= 4096, or none (split + epilogue kernels everywhere)")
     ap.add_argument("--workload", choices=("decode", "prefill", "ipc"), default="decode",
                     help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
                          "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
@@ -77,11 +81,13 @@ def parse():
     return ap.parse_args()
 
 
-def read_traffic():
-    """hbm_bytes_per_launch from the committed counter summary, or None."""
-    if not os.path.exists(TRAFFIC_FILE):
+def read_traffic(whole_k):
+    """hbm_bytes_per_launch of the dominant kernel from the committed counter
+    summary, or None."""
+    path = TRAFFIC_FILES[bool(whole_k)]
+    if not os.path.exists(path):
         return None
-    with open(TRAFFIC_FILE) as f:
+    with open(path) as f:
         for line in f:
             if line.startswith("hbm_bytes_per_launch:"):
                 return int(float(line.split(":", 1)[1]))
@@ -475,7 +481,8 @@ def main():
 
     max_new = 1 + args.warmup + args.steps + args.timer_steps + 1
     dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill,
-                         packed=args.weights == "packed")
+                         packed=args.weights == "packed",
+                         whole_k={"lm": True, "all": "all", "none": False}[args.whole_k])
     del weights, adapters
     torch.cuda.synchronize()
 
@@ -507,8 +514,14 @@ def main():
         torch.cuda._sleep(100_000_000)
         dec.step_eager()
     recs = ops.timer_collect()
-    base_ms = [r["base_ms"] for r in recs]
-    base_bytes = [r["bytes"] for r in recs]
+    # the dominant kernel: the whole-K round (QKV, O, Gate+Up, LM head) when
+    # the step uses it, else the K-sliced base kernel of every round
+    # the K-sliced base kernel of every projection round (the LM head may be
+    # a whole-K round)
+    whole_k = dec.whole_k == "all"
+    dom = [r for r in recs if r["k"] <= 4096] if whole_k else [r for r in recs if r["n"] != s.vocab or not dec.whole_k]
+    base_ms = [r["base_ms"] for r in dom]
+    base_bytes = [r["bytes"] for r in dom]
     mean_ms = statistics.fmean(base_ms)
     mean_bytes = statistics.fmean(base_bytes)
     achieved = mean_bytes / (mean_ms * 1e-3) / 1e9
@@ -525,7 +538,7 @@ def main():
                       "base_GBps": round(statistics.fmean([x["bytes"] for x in v]) /
                                          (statistics.fmean([x["base_ms"] for x in v]) * 1e-3) / 1e9, 1)}
                  for nm, v in per_op.items()}
-    traffic = read_traffic()
+    traffic = read_traffic(whole_k)
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 2
         src = torch.ones(n, dtype=torch.bfloat16, device=dev)
@@ -566,7 +579,12 @@ def main():
                    "rounds": breakdown},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "split_kernel (decode projection base kernel, all 128 rounds + LM head)",
+                     "kernel": ("fullk_kernel (whole-K decode round: QKV, O, Gate+Up rounds and the LM head, "
+                                "epilogue included; Down stays split_kernel + epilogue_kernel)") if whole_k else
+                               ("split_kernel (decode projection base kernel, all 128 projection rounds; the LM "
+                                "head is a whole-K round)" if dec.whole_k else
+                                "split_kernel (decode projection base kernel, all 128 rounds + LM head)"),
+                     "launches": len(dom),
                      "mean_launch_us": round(mean_ms * 1e3, 3), "bytes_per_launch": int(mean_bytes)},
         "cpu_baseline": cpu,
     }

@@ -173,7 +173,13 @@ typedef struct swl_round_fusion {
   const void* cos_sin;
   int64_t max_pos;
   /* w_layout 1: w is in the fragment-tile layout of swl_pack_weight_bf16
-   * (decode-shaped rounds only); 0: row-major [n, k]. */
+   * (decode-shaped rounds only); 0: row-major [n, k].  2: the whole-K round
+   * (one launch, no partial sums; at most 32 token rows, k a multiple of
+   * 256 up to 4096) over w packed by swl_pack_weight_pairs_bf16 with
+   * pair_off n / 2 for out_mode 2, 64 for out_mode 3, 8 otherwise (n a
+   * multiple of 2 * pair_off); out_mode 1 then writes n / 16 partial sums of
+   * squares per row (ss_out_stride >= n / 16).  Whole-K rounds on one GPU
+   * share a set of counters and must be ordered (one stream). */
   int32_t w_layout;
 } swl_round_fusion;
 
@@ -205,6 +211,15 @@ int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg,
  * 347-376); the round results are bit-identical to the row-major ones. */
 int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out,
                          void* stream);
+
+/* swl_pack_weight_bf16 with paired rows: tile rows 0..7 are eight
+ * consecutive rows j.. of a block of 2 * pair_off rows and tile rows 8..15
+ * the rows j + pair_off.., so one tile holds both columns of a SiLU * up pair
+ * (pair_off = inter) or of a RoPE pair (pair_off = 64 in 128-wide heads).
+ * pair_off a multiple of 8 (8: the plain layout), n a multiple of
+ * 2 * pair_off.  No counterpart in the reference (a layout of this build). */
+int swl_pack_weight_pairs_bf16(const void* w, int64_t n, int64_t k,
+                               int64_t pair_off, void* out, void* stream);
 
 /* swl_round_bf16 with fusions (fusion may be NULL; a non-NULL fusion needs
  * at most 64 token rows). */

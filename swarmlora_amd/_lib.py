@@ -99,6 +99,7 @@ _SIGS = {
     "swl_round_ex_noalloc_bf16": (c_int, [c_int, P_i64, P_vp, P_vp, c_vp, c_vp, c_i64, c_i64, P_i32, c_vp, c_vp, c_int,
                                   P_i64, ctypes.POINTER(RoundFusion), c_vp]),
     "swl_pack_weight_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "swl_pack_weight_pairs_bf16": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp]),
     "swl_lora_segmented_bf16": (c_int, [c_vp, c_i64, c_int, P_i64, P_i32, c_vp, c_vp, c_int, P_i64, c_vp, c_i64,
                                         c_int, c_vp]),
     "swl_matmul_bf16": (c_int, [c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,

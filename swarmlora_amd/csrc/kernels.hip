@@ -898,6 +898,352 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   }
 }
 
+// Row of W held by row rr (0..15) of packed tile `tile` when tiles pair the
+// rows j and j + off (off a multiple of 8): tile rows 0..7 are eight
+// consecutive rows of a block of 2 * off, rows 8..15 the rows off further.
+// off = 8 is the plain order (tile rows = W rows tile * 16 ..).
+__host__ __device__ __forceinline__ int64_t paired_row(int64_t tile, int rr, int64_t off) {
+  const int64_t per = off >> 3;  // tiles per block of 2 * off rows
+  return (tile / per) * (2 * off) + (tile % per) * 8 + (rr & 7) + (rr >= 8 ? off : 0);
+}
+
+// ------------------------------------------- decode: whole-K rounds -------
+// Decode-shaped rounds with K <= 4096 (QKV, O, Gate+Up, LM head) in one
+// launch and without partial sums: a persistent workgroup of 8 waves per CU
+// (two per SIMD, 256 registers each) keeps the K range of every token row in
+// registers (wave w holds k-steps w * nsw .. + nsw of both 16-token tiles as
+// MFMA B fragments, 128 registers at K = 4096, RMS-normalised on the way in
+// when the round takes the residual stream), then walks its
+// units: unit u = blockIdx.x, + gridDim.x, ...  A unit is one 16-row tile,
+// first the stacked lora_A tiles of the round's adapters (the LoRA shrink),
+// then the weight's fragment tiles.  Each wave multiplies its k-steps of the
+// tile (the next unit's 16 fragments are requested right after, 128 KiB in
+// flight per CU), the 8 wave partials are summed in LDS, and the workgroup
+// finishes the tile itself:
+// a shrink tile's rows are stored (written through) for its adapter's
+// tokens and counted; a weight tile gets bias, the LoRA expand (waiting once
+// per workgroup, bounded, until every shrink tile is counted), and the
+// out_mode fusion, then is stored.  The weights are packed with paired rows
+// (pack offset `off`): tile rows r and r + 8 are the output columns c and
+// c + off, so SiLU * up (off = inter) and RoPE (off = 64 within a head)
+// find both operands in one tile.  The last workgroup to finish resets the
+// counters for the next launch.
+constexpr int kFkWaves = 8;
+constexpr int kFkMaxSteps = 16;  // k-steps per wave: K <= 8 * 16 * 32
+
+struct FullKArgs {
+  const bf16* w;                // fragment tiles, rows paired by `off`
+  int64_t N, K;
+  int32_t ntok, nsw, total_steps, off;
+  int32_t n_stiles, n_units;    // shrink tiles first, then ceil(N / 16) weight tiles
+  const bf16* x[32];
+  bf16* y[32];
+  // RMSNorm on the way in (gamma != null): x = bf16(bf16(h * r) * gamma)
+  const bf16* gamma;
+  const float* ss;
+  int32_t ss_n, ss_stride;
+  float eps;
+  // LoRA
+  int32_t has_lora, ngroups, u_ld, nblk;
+  const swl_lora_entry* table;
+  int64_t blk_start[SWL_MAX_LORA_BLOCKS + 1];
+  const bf16* g_a[32];          // stacked lora_A [g_arows][K] of adapter group g
+  int32_t g_arows[32];
+  int32_t g_tile0[33];
+  int8_t tok_grp[32];
+  int32_t lora[32];             // table entry per token (-1: none)
+  float* u;                     // [ntok][u_ld] shrink rows
+  int32_t* sync;                // [0] shrink tiles stored, [1] workgroups done, [2] late waits
+  const bf16* bias;
+  // out_mode 1
+  float* ss_out;
+  int32_t ss_out_stride;
+  // out_mode 3
+  bf16* kc;
+  bf16* vc;
+  const int32_t* bt;
+  const int32_t* seqlens;
+  const int64_t* pos;
+  const bf16* cs;
+  int64_t max_blocks, num_blocks, max_pos;
+  int32_t hq, hkv, bs;
+};
+typedef const __attribute__((address_space(4))) FullKArgs* fullk_args_ptr;
+
+// Cache-policy operand of the buffer builtins: sc0 | sc1 (system scope):
+// stores written through to memory, loads of the memory's value.
+constexpr int kSysScope = 1 | 16;
+
+__device__ __forceinline__ int fk_blk(fullk_args_ptr a, int64_t n) {
+  int b = 0;
+#pragma unroll
+  for (int i = 1; i < SWL_MAX_LORA_BLOCKS; ++i)
+    if (i < a->nblk && n >= a->blk_start[i]) b = i;
+  return b;
+}
+
+template <int TT, int MODE>
+__global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args) {
+  fullk_args_ptr a = (fullk_args_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  __shared__ f32x4 red[kFkWaves][TT][64];
+  __shared__ float rsq[32];
+  extern __shared__ float us[];  // [ntok][u_ld] shrink rows, once every shrink tile is stored
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nsw = a->nsw, ntok = a->ntok;
+  const int s0 = wv * nsw;
+  const int64_t K = a->K;
+
+  // fragments of this wave's k-steps of unit `un` (a shrink tile: 16 rows of
+  // an adapter group's stacked A, row-major, k-steps 32 elements apart; a
+  // weight tile: packed, k-steps 512 elements apart).  Steps past nsw reload
+  // the last one (in bounds); their products are masked to zero.
+  u32x4 wf[kFkMaxSteps];
+  auto issue = [&](int un) {
+    if (un >= a->n_units) return;
+    const bf16* p;
+    int64_t stride;
+    if (un >= a->n_stiles) {
+      p = a->w + ((int64_t)(un - a->n_stiles) * a->total_steps + s0) * 512 + 8 * lane;
+      stride = 512;
+    } else {
+      int g = 0;
+      while (g + 1 < a->ngroups && a->g_tile0[g + 1] <= un) ++g;
+      const int q = (un - a->g_tile0[g]) * 16 + (lane & 15);
+      p = a->g_a[g] + (int64_t)min(q, a->g_arows[g] - 1) * K + 32 * s0 + 8 * (lane >> 4);
+      stride = 32;
+    }
+#pragma unroll
+    for (int s = 0; s < kFkMaxSteps; ++s) {
+      wf[s] = ldg16(p);
+      if (s + 1 < nsw) p += stride;
+    }
+  };
+  int unit = blockIdx.x;
+  issue(unit);
+
+  // token rows: B fragments of this wave's k-steps (token 16 t + lane % 16,
+  // k-group lane / 16); rows past ntok read row 0 and are zeroed
+  u32x4 xf[kFkMaxSteps][TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int tk = 16 * t + (lane & 15);
+    const bf16* xr = a->x[tk < ntok ? tk : 0] + 32 * s0 + 8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < kFkMaxSteps; ++s) xf[s][t] = ldg16(xr + 32 * (s < nsw ? s : nsw - 1));
+  }
+  if (a->gamma) {
+    // r = rsqrt(sum of the row's partial sums of squares / K + eps), one
+    // wave per token
+    for (int tk = wv; tk < ntok; tk += kFkWaves) {
+      float sq = 0.f;
+      for (int j = lane; j < a->ss_n; j += 64) sq += a->ss[(int64_t)tk * a->ss_stride + j];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+      if (lane == 0) rsq[tk] = rsqrtf(sq / (float)K + a->eps);
+    }
+    __syncthreads();
+    const bf16* gp = a->gamma + 32 * s0 + 8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < kFkMaxSteps; ++s) {
+      float gv[8];
+      unpack8(ldg16(gp + 32 * (s < nsw ? s : nsw - 1)), gv);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const int tk = 16 * t + (lane & 15);
+        const float r = rsq[tk < ntok ? tk : 0];
+        float hv[8];
+        unpack8(xf[s][t], hv);
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(f2bf(hv[j] * r)) * gv[j]);
+        xf[s][t] = __builtin_bit_cast(u32x4, o);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const bool live_tok = 16 * t + (lane & 15) < ntok;
+#pragma unroll
+    for (int s = 0; s < kFkMaxSteps; ++s)
+      if (!live_tok || s >= nsw) xf[s][t] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  const __amdgpu_buffer_rsrc_t ursrc =
+      __builtin_amdgcn_make_buffer_rsrc(a->u, 0, a->has_lora ? ntok * a->u_ld * 4 : 0, 0x00020000);
+  bool u_ready = !a->has_lora;
+  while (unit < a->n_units) {
+    f32x4 acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kFkMaxSteps; ++s)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) acc[t] = mfma16(wf[s], xf[s][t], acc[t]);
+    const int cur = unit;
+    unit += gridDim.x;
+    issue(unit);  // in flight during this tile's reduction and epilogue
+#pragma unroll
+    for (int t = 0; t < TT; ++t) red[wv][t][lane] = acc[t];
+    __syncthreads();
+    // sum of the wave partials of tile row r, token tk
+    auto total = [&](int r, int tk) {
+      const int l = (r >> 2) * 16 + (tk & 15), t = tk >> 4, e = r & 3;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kFkWaves; ++w) v += red[w][t][l][e];
+      return v;
+    };
+
+    if (cur < a->n_stiles) {
+      // shrink tile: rows q0 .. q0 + 15 of group g's stacked A
+      int g = 0;
+      while (g + 1 < a->ngroups && a->g_tile0[g + 1] <= cur) ++g;
+      const int q0 = (cur - a->g_tile0[g]) * 16;
+      const int e = threadIdx.x;
+      const int tk = e >> 4, r = e & 15;
+      if (tk < ntok && a->tok_grp[tk] == g && q0 + r < a->g_arows[g]) {
+        const float v = total(r, tk);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ursrc,
+                                              (int)(4 * ((int64_t)tk * a->u_ld + q0 + r)), 0, kSysScope);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's u stores are written through
+      __syncthreads();
+      if (threadIdx.x == 0) (void)__hip_atomic_fetch_add(a->sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      continue;  // red is rewritten only after the next barrier
+    }
+
+    if (!u_ready) {
+      // every shrink tile stored: bounded wait (1 s), then the shrink rows to LDS
+      if (threadIdx.x == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__hip_atomic_load(a->sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a->n_stiles) {
+          if (__builtin_amdgcn_s_memrealtime() - t0 > 100000000ull) {
+            (void)__hip_atomic_fetch_add(a->sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < ntok * a->u_ld; i += kFkWaves * 64)
+        us[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ursrc, 4 * i, 0, kSysScope));
+      __syncthreads();
+      u_ready = true;
+    }
+
+    // weight tile: thread (token tk, pair p) finishes tile rows p and p + 8,
+    // output columns c0 and c0 + off
+    const int64_t tile = cur - a->n_stiles;
+    const int e = threadIdx.x;
+    const int tk = e >> 3, p = e & 7;
+    const int64_t c0 = paired_row(tile, p, a->off), c1 = c0 + a->off;
+    const bool live = tk < ntok && c0 < a->N;
+    float v0 = 0.f, v1 = 0.f;
+    if (live) {
+      v0 = total(p, tk);
+      v1 = total(p + 8, tk);
+      if (a->bias) {
+        v0 += bf2f(a->bias[c0]);
+        if (c1 < a->N) v1 += bf2f(a->bias[c1]);
+      }
+      const int li = a->has_lora ? a->lora[tk] : -1;
+      if (li >= 0) {
+        const swl_lora_entry* ep = a->table + li;
+        const int r = ep->rank;
+        const float* ut = us + tk * a->u_ld;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int64_t c = h ? c1 : c0;
+          if (c >= a->N) continue;
+          const int b = fk_blk(a, c);
+          const bf16* brow = reinterpret_cast<const bf16*>(ep->b[b]) + (c - a->blk_start[b]) * r;
+          const float* ub = ut + b * r;
+          float d = 0.f;
+          if ((r & 7) == 0) {
+            for (int q = 0; q < r; q += 8) {
+              float bv[8];
+              unpack8(ld16(brow + q), bv);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) d += ub[q + i] * bv[i];
+            }
+          } else {
+            for (int q = 0; q < r; ++q) d += ub[q] * bf2f(brow[q]);
+          }
+          (h ? v1 : v0) += d * ep->scale;
+        }
+      }
+    }
+
+    if constexpr (MODE == 0) {
+      if (live) {
+        a->y[tk][c0] = f2bf(v0);
+        if (c1 < a->N) a->y[tk][c1] = f2bf(v1);
+      }
+    } else if constexpr (MODE == 1) {
+      // h = bf16(h + out); the tile's sum of squares of the new h per token
+      float sq = 0.f;
+      if (live) {
+        bf16* yr = a->y[tk];
+        const bf16 h0 = f2bf(bf2f(yr[c0]) + bf2f(f2bf(v0)));
+        const bf16 h1 = f2bf(bf2f(yr[c1]) + bf2f(f2bf(v1)));
+        yr[c0] = h0;
+        yr[c1] = h1;
+        sq = bf2f(h0) * bf2f(h0) + bf2f(h1) * bf2f(h1);
+      }
+      sq += __shfl_xor(sq, 1, 64);
+      sq += __shfl_xor(sq, 2, 64);
+      sq += __shfl_xor(sq, 4, 64);
+      if (live && p == 0) a->ss_out[(int64_t)tk * a->ss_out_stride + tile] = sq;
+    } else if constexpr (MODE == 2) {
+      // c0 a gate column, c1 = c0 + inter its up column
+      if (live) {
+        const float g = bf2f(f2bf(v0)), u = bf2f(f2bf(v1));
+        a->y[tk][c0] = f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u);
+      }
+    } else {
+      // c0 = head * 128 + d (d < 64), c1 = c0 + 64: NeoX RoPE pair of q / k
+      // heads; k and v also appended to their KV pages
+      if (live) {
+        const int hh = (int)(c0 >> 7), d = (int)(c0 & 63);
+        const bool is_q = hh < a->hq, is_k = !is_q && hh < a->hq + a->hkv;
+        float x0 = bf2f(f2bf(v0)), x1 = bf2f(f2bf(v1));
+        const int64_t ps = a->pos[tk];
+        if ((is_q || is_k) && ps >= 0 && ps < a->max_pos) {
+          const float rc = bf2f(a->cs[ps * 128 + d]), rs = bf2f(a->cs[ps * 128 + 64 + d]);
+          const float n0 = bf2f(f2bf(x0 * rc - x1 * rs));
+          const float n1 = bf2f(f2bf(x1 * rc + x0 * rs));
+          x0 = n0;
+          x1 = n1;
+        }
+        bf16* yr = a->y[tk];
+        yr[c0] = f2bf(x0);
+        yr[c1] = f2bf(x1);
+        const int64_t slen = a->seqlens[tk];
+        if (!is_q && slen >= 0 && slen / a->bs < a->max_blocks) {
+          const int32_t pb = a->bt[(int64_t)tk * a->max_blocks + slen / a->bs];
+          if (pb >= 0 && pb < a->num_blocks) {
+            const int kvh = is_k ? hh - a->hq : hh - a->hq - a->hkv;
+            const int64_t dst = ((int64_t)pb * a->bs + slen % a->bs) * a->hkv * 128 + kvh * 128 + d;
+            bf16* cache = is_k ? a->kc : a->vc;
+            cache[dst] = f2bf(x0);
+            cache[dst + 64] = f2bf(x1);
+          }
+        }
+      }
+    }
+    __syncthreads();  // red is rewritten by the next unit
+  }
+
+  // the last workgroup to finish resets the counters for the next launch
+  if (threadIdx.x == 0) {
+    if (__hip_atomic_fetch_add(a->sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
+      __hip_atomic_store(a->sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a->sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 // ------------------------------------------------------- tiled (M>64) -----
 // y[m, n] = sum_k x[m, k] w[n, k] for a packed x [M, K]; rows of y go to the
 // segment (slot) the packed row belongs to.  128x128 output tile per
@@ -1770,17 +2116,17 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
 }
 
 // Fragment-tile packing of a row-major W [N][K]: output 16-byte chunk c =
-// ((tile * steps + step) * 64 + lane) holds row tile * 16 + lane % 16,
+// ((tile * steps + step) * 64 + lane) holds row paired_row(tile, lane % 16),
 // columns step * 32 + 8 (lane / 16) .. + 7 (zero past row N).
-__global__ __launch_bounds__(256) void pack_weight_kernel(const bf16* w, int64_t N, int64_t K, u32x4* out,
-                                                         int64_t nchunks) {
+__global__ __launch_bounds__(256) void pack_weight_kernel(const bf16* w, int64_t N, int64_t K, int64_t off,
+                                                         u32x4* out, int64_t nchunks) {
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= nchunks) return;
   const int64_t steps = K >> 5;
   const int lane = (int)(c & 63);
   const int64_t ts = c >> 6;
   const int64_t tile = ts / steps, step = ts - tile * steps;
-  const int64_t r = tile * 16 + (lane & 15);
+  const int64_t r = paired_row(tile, lane & 15, off);
   u32x4 v = u32x4{0u, 0u, 0u, 0u};
   if (r < N) v = ldg16(w + r * K + step * 32 + 8 * (lane >> 4));
   out[c] = v;
@@ -2233,6 +2579,50 @@ void plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const swl_lor
   p.g_tile0[p.ngroups] = p.tiles;
 }
 
+// Counters of the whole-K rounds (fullk_kernel): [0] shrink tiles stored,
+// [1] workgroups finished, [2] bounded waits that ran out.  Zero at module
+// load; every launch leaves them zero again ([2] aside).  One copy per GPU,
+// addressed through hipGetSymbolAddress; rounds on one GPU that use them
+// must be ordered (one stream).
+static __device__ __align__(256) int32_t fullk_sync[64];
+std::mutex g_fk_mu;
+int32_t* g_fk_sync[64] = {};
+
+int fullk_sync_ptr(int32_t** out) {
+  int dev = 0;
+  SWL_HIP(hipGetDevice(&dev));
+  SWL_CHECK(dev >= 0 && dev < 64, SWL_ERR_INVALID, "whole-K round: device index out of range");
+  std::lock_guard<std::mutex> lk(g_fk_mu);
+  if (!g_fk_sync[dev]) {
+    void* p = nullptr;
+    SWL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(fullk_sync)));
+    SWL_CHECK(p != nullptr, SWL_ERR_HIP, "whole-K round: hipGetSymbolAddress returned null");
+    g_fk_sync[dev] = reinterpret_cast<int32_t*>(p);
+  }
+  *out = g_fk_sync[dev];
+  return SWL_OK;
+}
+
+template <int TT, int MODE>
+int launch_fullk_tm(const FullKArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+  static size_t allowed = 0;
+  int rc = allow_lds(fullk_kernel<TT, MODE>, lds + 16 * 1024 * TT + 256, &allowed);
+  if (rc) return rc;
+  launch_maybe_timed(fullk_kernel<TT, MODE>, grid, dim3(kFkWaves * 64), lds, st, e0, e1, a);
+  return SWL_OK;
+}
+
+template <int TT>
+int launch_fullk_t(int mode, const FullKArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0,
+                   hipEvent_t e1) {
+  switch (mode) {
+    case 1: return launch_fullk_tm<TT, 1>(a, grid, lds, st, e0, e1);
+    case 2: return launch_fullk_tm<TT, 2>(a, grid, lds, st, e0, e1);
+    case 3: return launch_fullk_tm<TT, 3>(a, grid, lds, st, e0, e1);
+    default: return launch_fullk_tm<TT, 0>(a, grid, lds, st, e0, e1);
+  }
+}
+
 template <int TT, int W>
 int launch_split_tw(const SplitArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t tb0, hipEvent_t tb1) {
   static size_t allowed = 0;
@@ -2253,6 +2643,127 @@ int launch_split_w(int TT, const SplitArgs& a, dim3 grid, size_t lds, hipStream_
   }
 }
 
+// Whole-K decode round (fullk_kernel): weights packed with paired rows
+// (w_layout 2; pair offset inter for out_mode 2, 64 for out_mode 3, else 8),
+// at most 32 token rows, K a multiple of 256 up to 4096.
+int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok, const bf16* const* xrows,
+                 bf16* const* yrows, const int32_t* tok_lora, const swl_lora_entry* table,
+                 const swl_lora_entry* host_entries, const LoraEpi* Lblk, int nblk, const swl_round_fusion* fz,
+                 hipStream_t st, void* ws, size_t ws_bytes) {
+  const int mode = fz->out_mode;
+  SWL_CHECK(ntok >= 1 && ntok <= 32, SWL_ERR_INVALID, "whole-K round (w_layout 2): at most 32 token rows");
+  SWL_CHECK(K % (32 * kFkWaves) == 0 && K / (32 * kFkWaves) <= kFkMaxSteps, SWL_ERR_INVALID,
+            "whole-K round (w_layout 2): K must be a multiple of 256, at most 4096");
+  const int64_t off = mode == 2 ? N / 2 : mode == 3 ? 64 : 8;
+  SWL_CHECK(off % 8 == 0 && N % (2 * off) == 0, SWL_ERR_INVALID,
+            "whole-K round (w_layout 2): n must be a multiple of 16 (of 2 * inter for out_mode 2, of 128 for "
+            "out_mode 3)");
+  const int TT = (ntok + 15) / 16;
+  FullKArgs a{};
+  a.w = w;
+  a.N = N;
+  a.K = K;
+  a.ntok = ntok;
+  a.nsw = (int)(K / (32 * kFkWaves));
+  a.total_steps = (int)(K / 32);
+  a.off = (int)off;
+  for (int i = 0; i < ntok; ++i) {
+    a.x[i] = xrows[i];
+    a.y[i] = yrows[i];
+  }
+  if (fz->norm_weight) {
+    a.gamma = reinterpret_cast<const bf16*>(fz->norm_weight);
+    a.ss = fz->ss_in;
+    a.ss_n = fz->ss_in_n;
+    a.ss_stride = fz->ss_in_stride;
+    a.eps = fz->eps;
+  }
+  a.bias = bias;
+  bool has_lora = false;
+  if (tok_lora)
+    for (int i = 0; i < ntok; ++i) has_lora |= tok_lora[i] >= 0;
+  ShrinkPlan sp;
+  if (has_lora) {
+    plan_shrink(sp, ntok, tok_lora, host_entries, nblk);
+    int max_r = 0;
+    a.ngroups = sp.ngroups;
+    for (int g = 0; g < sp.ngroups; ++g) {
+      a.g_a[g] = reinterpret_cast<const bf16*>(host_entries[sp.g_entry[g]].a);
+      a.g_arows[g] = sp.g_arows[g];
+      a.g_tile0[g] = sp.g_tile0[g];
+      max_r = std::max(max_r, host_entries[sp.g_entry[g]].rank);
+    }
+    a.g_tile0[sp.ngroups] = sp.g_tile0[sp.ngroups];
+    for (int i = 0; i < ntok; ++i) {
+      a.tok_grp[i] = sp.tok_grp[i];
+      a.lora[i] = tok_lora[i];
+    }
+    a.u_ld = max_r * nblk;
+    SWL_CHECK(a.u_ld <= kMaxURow, SWL_ERR_INVALID, "round: LoRA rank x blocks exceeds 256");
+    a.has_lora = 1;
+    a.n_stiles = sp.tiles;
+    a.nblk = nblk;
+    a.table = table;
+    for (int b = 0; b <= SWL_MAX_LORA_BLOCKS; ++b) a.blk_start[b] = Lblk->blk_start[b];
+  } else {
+    for (int i = 0; i < ntok; ++i) a.lora[i] = -1;
+  }
+  a.n_units = a.n_stiles + (int)(N / 16);
+  if (mode == 1) {
+    a.ss_out = fz->ss_out;
+    a.ss_out_stride = fz->ss_out_stride;
+  }
+  if (mode == 3) {
+    SWL_CHECK(ntok <= 32, SWL_ERR_INVALID, "round fusion: out_mode 3 token rows");
+    a.kc = reinterpret_cast<bf16*>(fz->k_cache);
+    a.vc = reinterpret_cast<bf16*>(fz->v_cache);
+    a.bt = fz->block_table;
+    a.seqlens = fz->cache_seqlens;
+    a.pos = fz->positions;
+    a.cs = reinterpret_cast<const bf16*>(fz->cos_sin);
+    a.max_blocks = fz->max_blocks;
+    a.num_blocks = fz->num_blocks;
+    a.max_pos = fz->max_pos;
+    a.hq = fz->hq;
+    a.hkv = fz->hkv;
+    a.bs = fz->block_size;
+  }
+  int rc = fullk_sync_ptr(&a.sync);
+  if (rc) return rc;
+  const size_t u_bytes = has_lora ? sizeof(float) * (size_t)ntok * a.u_ld : 0;
+  if (has_lora) {
+    void* scr = ws;
+    if (ws) {
+      SWL_CHECK(u_bytes <= ws_bytes, SWL_ERR_INVALID, "whole-K round: shrink rows exceed the allocation-free scratch");
+    } else {
+      rc = scratch_get(u_bytes, st, &scr);
+      if (rc) return rc;
+    }
+    a.u = reinterpret_cast<float*>(scr);
+  }
+  const dim3 grid((unsigned)std::min<int64_t>(a.n_units, cu_count()));
+  const int tslot = timer_slot(st);
+  if (tslot >= 0) {
+    int64_t bytes = 2 * (N * K + (int64_t)ntok * K);
+    for (int g = 0; g < sp.ngroups && has_lora; ++g) bytes += 2 * (int64_t)sp.g_arows[g] * K;
+    g_timer.N[tslot] = N;
+    g_timer.K[tslot] = K;
+    g_timer.ntok[tslot] = ntok;
+    g_timer.bytes[tslot] = bytes;
+  }
+  hipEvent_t e0 = timer_event(tslot, 0), e1 = timer_event(tslot, 1);
+  rc = TT == 1 ? launch_fullk_t<1>(mode, a, grid, u_bytes, st, e0, e1)
+               : launch_fullk_t<2>(mode, a, grid, u_bytes, st, e0, e1);
+  if (rc) return rc;
+  SWL_LAUNCH_CHECK("fullk_kernel launch");
+  if (tslot >= 0) {
+    // no separate epilogue: its events mark an empty interval after the kernel
+    SWL_HIP(hipEventRecord(timer_event(tslot, 2), st));
+    SWL_HIP(hipEventRecord(timer_event(tslot, 3), st));
+  }
+  return SWL_OK;
+}
+
 // Decode-shaped projection of ntok (<= 64) token rows: y[i] = x[i] . W^T
 // (+ bias) (+ LoRA delta of entry tok_lora[i]).  xrows[i] / yrows[i] are the
 // token's input / output rows (slot buffers).
@@ -2267,13 +2778,16 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const int64_t epi_cols = mode == 2 ? N / 2 : N;
   if (fz) {
     SWL_CHECK(mode >= 0 && mode <= 3, SWL_ERR_INVALID, "round fusion: out_mode must be 0..3");
-    SWL_CHECK(fz->w_layout == 0 || fz->w_layout == 1, SWL_ERR_INVALID, "round fusion: w_layout must be 0 or 1");
+    SWL_CHECK(fz->w_layout >= 0 && fz->w_layout <= 2, SWL_ERR_INVALID, "round fusion: w_layout must be 0, 1 or 2");
     if (fz->norm_weight)
       SWL_CHECK(fz->ss_in && fz->ss_in_n >= 1 && fz->ss_in_stride >= fz->ss_in_n, SWL_ERR_INVALID,
                 "round fusion: norm_weight needs ss_in with ss_in_n >= 1 partial sums per row");
-    if (mode == 1)
+    if (mode == 1 && fz->w_layout != 2)
       SWL_CHECK(fz->ss_out && fz->ss_out_stride >= (N + 255) / 256, SWL_ERR_INVALID,
                 "round fusion: out_mode 1 needs ss_out with ss_out_stride >= ceil(n / 256)");
+    if (mode == 1 && fz->w_layout == 2)
+      SWL_CHECK(fz->ss_out && fz->ss_out_stride >= N / 16, SWL_ERR_INVALID,
+                "round fusion: out_mode 1 of a whole-K round needs ss_out with ss_out_stride >= n / 16");
     if (mode == 2) SWL_CHECK(N % 2 == 0, SWL_ERR_INVALID, "round fusion: out_mode 2 needs n = 2 * inter");
     if (mode == 3)
       SWL_CHECK(fz->hq > 0 && fz->hkv > 0 && N == (int64_t)(fz->hq + 2 * fz->hkv) * 128 && fz->k_cache &&
@@ -2281,6 +2795,9 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
                     fz->block_size > 0 && fz->max_blocks > 0 && fz->max_pos > 0,
                 SWL_ERR_INVALID, "round fusion: out_mode 3 needs n = (hq + 2 hkv) * 128 and the KV / RoPE arguments");
   }
+  if (fz && fz->w_layout == 2)
+    return launch_fullk(w, bias, N, K, ntok, xrows, yrows, tok_lora, table, host_entries, Lblk, nblk, fz, st, ws,
+                        ws_bytes);
   const int64_t total_steps = K / 32;
   SplitArgs a{};
   a.w = w;
@@ -2877,17 +3394,23 @@ int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg, const int64_t* 
   return SWL_OK;
 }
 
-int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out, void* stream) {
+int swl_pack_weight_pairs_bf16(const void* w, int64_t n, int64_t k, int64_t pair_off, void* out, void* stream) {
   SWL_CHECK(w && out, SWL_ERR_INVALID, "swl_pack_weight_bf16: null argument");
   SWL_CHECK(n > 0 && k > 0 && k % 32 == 0, SWL_ERR_INVALID, "swl_pack_weight_bf16: k must be a positive multiple of 32");
   SWL_CHECK((reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
             SWL_ERR_INVALID, "swl_pack_weight_bf16: w and out must be 16-byte aligned");
+  SWL_CHECK(pair_off >= 8 && pair_off % 8 == 0 && (pair_off == 8 || n % (2 * pair_off) == 0), SWL_ERR_INVALID,
+            "swl_pack_weight_pairs_bf16: pair_off must be a multiple of 8 and n a multiple of 2 * pair_off");
   const int64_t nchunks = (n + 15) / 16 * 16 * k / 8;
   SWL_CHECK((nchunks + 255) / 256 < ((int64_t)1 << 31), SWL_ERR_INVALID, "swl_pack_weight_bf16: weight too large");
   hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     reinterpret_cast<const bf16*>(w), n, k, reinterpret_cast<u32x4*>(out), nchunks);
+                     reinterpret_cast<const bf16*>(w), n, k, pair_off, reinterpret_cast<u32x4*>(out), nchunks);
   SWL_LAUNCH_CHECK("pack_weight_kernel launch");
   return SWL_OK;
+}
+
+int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out, void* stream) {
+  return swl_pack_weight_pairs_bf16(w, n, k, 8, out, stream);
 }
 
 int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int trans_b, void* y, int64_t ldy,

@@ -120,11 +120,15 @@ class BatchedDecoder:
     Capacity for `max_new` generated tokens is reserved up front.
     packed (fused step only): projection and LM-head weights kept in the
     fragment-tile layout (ops.PackedWeight) instead of row-major.
+    whole_k (packed step only, at most 32 workers): True runs the LM head as
+    a whole-K round (w_layout 2: one launch, no partial sums); "all" also
+    the QKV, O and Gate+Up rounds (and Down when the intermediate size is at
+    most 4096); the other rounds are K-sliced.
     """
 
     def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
                  first_ids: List[int], device, max_new: int = 64, kv_fill=None, fused: bool = True,
-                 packed: bool = True):
+                 packed: bool = True, whole_k: bool = True):
         self.shape = s = shape
         self.device = dev = torch.device(device)
         self.W = W = len(ctx_lens)
@@ -137,6 +141,7 @@ class BatchedDecoder:
         self.graph = None
         self.fused = fused
         self.packed = packed and fused
+        self.whole_k = whole_k if (whole_k and self.packed and W <= 32) else False
         if fused:
             self._init_fused(weights, adapters, ctx_lens, first_ids, kv_fill)
             return
@@ -230,19 +235,40 @@ class BatchedDecoder:
         s, dev, W = self.shape, self.device, self.W
         self.layers_w = []
         self.norms = []
-        keep = ops.pack_weight if self.packed else (lambda t: t)  # noqa: E731
+        # whole-K rounds: K a multiple of 256 up to 4096, n a multiple of 16
+        # (of 128 for the QKV pairs, of 2 * inter for Gate+Up).  By default
+        # only the LM head takes them (measured at 8B widths, 28 workers:
+        # LM head 192 us against 238 for split + epilogue; the rounds with
+        # per-worker adapters are slower whole-K: every CU loads all 28 token
+        # rows, more bytes than its share of the O / QKV weights, and the
+        # adapters' lora_B rows are read behind the next tile's weights);
+        # whole_k="all" runs every round that fits that way
+        fits = lambda k: bool(self.whole_k) and k % 256 == 0 and k <= 4096  # noqa: E731
+        every = self.whole_k == "all"
+        self.wk = {"qkv": every and fits(s.hidden) and s.qkv % 128 == 0,
+                   "o": every and fits(s.heads * s.head_dim) and s.hidden % 16 == 0,
+                   "gu": every and fits(s.hidden) and s.inter % 8 == 0,
+                   "down": every and fits(s.inter) and s.hidden % 16 == 0,
+                   "lm": fits(s.hidden) and s.vocab % 16 == 0}
+        pair = {"qkv": 64, "gu": s.inter}
+
+        def keep(t, g):
+            if not self.packed:
+                return t
+            return ops.pack_weight(t, pair_off=pair.get(g, 8) if self.wk[g] else 8)
+
         for lw in weights["layers"]:
             t = {k: v.to(dev) for k, v in lw.items()}
             self.layers_w.append({
-                "qkv": keep(torch.cat([t["q"], t["k"], t["v"]], 0).contiguous()),
-                "o": keep(t["o"].contiguous()),
-                "gu": keep(torch.cat([t["gate"], t["up"]], 0).contiguous()),
-                "down": keep(t["down"].contiguous()),
+                "qkv": keep(torch.cat([t["q"], t["k"], t["v"]], 0).contiguous(), "qkv"),
+                "o": keep(t["o"].contiguous(), "o"),
+                "gu": keep(torch.cat([t["gate"], t["up"]], 0).contiguous(), "gu"),
+                "down": keep(t["down"].contiguous(), "down"),
             })
             self.norms.append((t["input_norm"].contiguous(), t["post_norm"].contiguous()))
             del t
         self.embed = weights["embed"].to(dev).contiguous()
-        self.lm_head = keep(weights["lm_head"].to(dev).contiguous())
+        self.lm_head = keep(weights["lm_head"].to(dev).contiguous(), "lm")
         self.final_norm = weights["final_norm"].to(dev).contiguous()
 
         # adapters: one table entry per (worker, layer, fused projection)
@@ -263,8 +289,11 @@ class BatchedDecoder:
 
         self._init_kv(ctx_lens, kv_fill)
 
-        # per-step buffers: one row per worker
-        nss = (s.hidden + 255) // 256
+        # per-step buffers: one row per worker; partial sums of squares of the
+        # residual stream: one per 16 columns from a whole-K round, per 256
+        # from a K-sliced one
+        nss_o = s.hidden // 16 if self.wk["o"] else (s.hidden + 255) // 256
+        nss_d = s.hidden // 16 if self.wk["down"] else (s.hidden + 255) // 256
         self.ids = torch.tensor(first_ids, dtype=torch.int64, device=dev).reshape(W, 1)
         self.h = torch.zeros(W, s.hidden, dtype=BF16, device=dev)        # residual stream
         self.x0 = torch.zeros(W, s.hidden, dtype=BF16, device=dev)       # layer 0's normed input
@@ -272,8 +301,8 @@ class BatchedDecoder:
         self.attn = torch.zeros(W, s.heads * s.head_dim, dtype=BF16, device=dev)
         self.act = torch.zeros(W, s.inter, dtype=BF16, device=dev)
         self.logits = torch.zeros(W, s.vocab, dtype=BF16, device=dev)
-        self.ss_o = torch.zeros(W, nss, dtype=torch.float32, device=dev)
-        self.ss_d = torch.zeros(W, nss, dtype=torch.float32, device=dev)
+        self.ss_o = torch.zeros(W, nss_o, dtype=torch.float32, device=dev)
+        self.ss_d = torch.zeros(W, nss_d, dtype=torch.float32, device=dev)
         rows = lambda t: [t[w:w + 1] for w in range(W)]  # noqa: E731
         self.rows_x0 = ops.RowSet([self.x0[w] for w in range(W)], s.hidden)
         self.rows_qkv = ops.RowSet([self.qkv[w] for w in range(W)], s.qkv)
@@ -289,15 +318,17 @@ class BatchedDecoder:
             kv = dict(k_cache=self.kv.key_caches[li], v_cache=self.kv.value_caches[li], hq=s.heads, hkv=s.kv_heads,
                       block_table=self.block_tables, cache_seqlens=self.seqlens, positions=self.positions,
                       cos_sin=self.cos_sin)
-            wl = 1 if self.packed else 0
+            wl = {g: (2 if self.wk[g] else 1) if self.packed else 0 for g in self.wk}
             plan = (
                 ("qkv", rows(self.x0) if li == 0 else rows(self.h), rows(self.qkv),
-                 ops.round_fusion(out_mode=3, w_layout=wl, **kv) if li == 0 else
-                 ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, out_mode=3, w_layout=wl, **kv)),
-                ("o", rows(self.attn), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_o, w_layout=wl)),
+                 ops.round_fusion(out_mode=3, w_layout=wl["qkv"], **kv) if li == 0 else
+                 ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, out_mode=3, w_layout=wl["qkv"],
+                                  **kv)),
+                ("o", rows(self.attn), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_o, w_layout=wl["o"])),
                 ("gu", rows(self.h), rows(self.act),
-                 ops.round_fusion(norm_weight=post_norm, eps=s.eps, ss_in=self.ss_o, out_mode=2, w_layout=wl)),
-                ("down", rows(self.act), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_d, w_layout=wl)),
+                 ops.round_fusion(norm_weight=post_norm, eps=s.eps, ss_in=self.ss_o, out_mode=2, w_layout=wl["gu"])),
+                ("down", rows(self.act), rows(self.h),
+                 ops.round_fusion(out_mode=1, ss_out=self.ss_d, w_layout=wl["down"])),
             )
             layer_calls = []
             for g, xin, yout, fz in plan:
@@ -306,7 +337,8 @@ class BatchedDecoder:
                                        out_div=2 if fz.out_mode == 2 else 1)
                 layer_calls.append((args, fz))
             self._calls.append(layer_calls)
-        lm_fz = ops.round_fusion(norm_weight=self.final_norm, eps=s.eps, ss_in=self.ss_d, w_layout=1 if self.packed else 0)
+        lm_fz = ops.round_fusion(norm_weight=self.final_norm, eps=s.eps, ss_in=self.ss_d,
+                                 w_layout=(2 if self.wk["lm"] else 1) if self.packed else 0)
         self._lm_call = (ops._round_args(rows(self.h), rows(self.logits), one, self.lm_head, None, None, None, None),
                          lm_fz)
         self._scale = 1.0 / (s.head_dim ** 0.5)

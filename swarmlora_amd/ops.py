@@ -164,19 +164,23 @@ class LoraTable:
 
 class PackedWeight:
     """Fragment-tile copy of a row-major weight [n, k] for decode-shaped
-    rounds (swl_pack_weight_bf16): 16-row tiles stored whole, k-step by
-    k-step, each k-step block the MFMA A operand of those rows.  `data` is
-    flat bf16 of ceil(n / 16) * 16 * k elements."""
+    rounds (swl_pack_weight_pairs_bf16): 16-row tiles stored whole, k-step
+    by k-step, each k-step block the MFMA A operand of those rows.  `data` is
+    flat bf16 of ceil(n / 16) * 16 * k elements.  pair_off > 8 pairs the rows
+    j and j + pair_off in each tile (whole-K rounds: inter for the Gate+Up
+    weight, 64 for the fused QKV weight)."""
 
-    def __init__(self, w: torch.Tensor):
+    def __init__(self, w: torch.Tensor, pair_off: int = 8):
         _need(w, "w")
         if w.dim() != 2 or not w.is_contiguous():
             raise ValueError("w must be a contiguous [n, k] matrix")
         self.n, self.k = w.shape
         if self.k % 32:
             raise ValueError("k must be a multiple of 32")
+        self.pair_off = int(pair_off)
         self.data = torch.empty((self.n + 15) // 16 * 16 * self.k, dtype=BF16, device=w.device)
-        _lib.check(_lib.load().swl_pack_weight_bf16(_ptr(w), self.n, self.k, _ptr(self.data), _stream()))
+        _lib.check(_lib.load().swl_pack_weight_pairs_bf16(_ptr(w), self.n, self.k, self.pair_off, _ptr(self.data),
+                                                          _stream()))
 
     @property
     def shape(self):
@@ -190,9 +194,9 @@ class PackedWeight:
         return self.data.data_ptr()
 
 
-def pack_weight(w: torch.Tensor) -> PackedWeight:
+def pack_weight(w: torch.Tensor, pair_off: int = 8) -> PackedWeight:
     """Fragment-tile copy of w [n, k] (see PackedWeight)."""
-    return PackedWeight(w)
+    return PackedWeight(w, pair_off)
 
 
 def _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols, out_div=1):
@@ -254,8 +258,8 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
     producing round); the record keeps the tensors it points to alive."""
     f = RoundFusion()
     keep = []
-    if w_layout not in (0, 1):
-        raise ValueError("w_layout must be 0 (row-major) or 1 (fragment tiles)")
+    if w_layout not in (0, 1, 2):
+        raise ValueError("w_layout must be 0 (row-major), 1 (fragment tiles) or 2 (whole-K round, paired tiles)")
     f.w_layout = w_layout
     if norm_weight is not None:
         _need(norm_weight, "norm_weight")
@@ -303,16 +307,26 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
              blk_cols: Optional[Sequence[int]] = None, fusion: Optional[RoundFusion] = None,
              noalloc: bool = False):
     """round_fused with the decode-step fusions of `fusion` (round_fusion()).
-    A PackedWeight w sets the fusion's w_layout to 1 (decode-shaped rounds
-    only).  noalloc=True calls the allocation-free entry point
+    A PackedWeight w runs the K-sliced decode round (w_layout 1) unless the
+    fusion asks for the whole-K round (w_layout 2, weights packed with the
+    pair offset its out_mode needs: n / 2 for 2, 64 for 3, else 8).
+    noalloc=True calls the allocation-free entry point
     (swl_round_ex_noalloc_bf16: at most 64 token rows, partials in the
     library's fixed 64 MiB device array)."""
     if isinstance(w, PackedWeight):
         if fusion is None:
             fusion = RoundFusion()
-        fusion.w_layout = 1
+        if fusion.w_layout != 2:
+            fusion.w_layout = 1
+            if w.pair_off != 8:
+                raise ValueError("weights packed with paired rows need the whole-K round (w_layout 2)")
+        else:
+            want = w.n // 2 if fusion.out_mode == 2 else 64 if fusion.out_mode == 3 else 8
+            if w.pair_off != want:
+                raise ValueError(f"whole-K round with out_mode {fusion.out_mode} needs pair_off {want}, "
+                                 f"the weight has {w.pair_off}")
     elif fusion is not None and fusion.w_layout != 0:
-        raise ValueError("fusion.w_layout = 1 needs a PackedWeight")
+        raise ValueError("fusion.w_layout 1 or 2 needs a PackedWeight")
     args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols,
                        out_div=2 if fusion is not None and fusion.out_mode == 2 else 1)
     fn = _lib.load().swl_round_ex_noalloc_bf16 if noalloc else _lib.load().swl_round_ex_bf16
