@@ -62,9 +62,10 @@ def parse():
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--weights", choices=("packed", "row-major"), default="packed",
                     help="decode: projection weights in fragment tiles (default) or row-major")
-    ap.add_argument("--whole-k", choices=("lm", "all", "none"), default="lm",
-                    help="decode: rounds run as whole-K rounds (one launch, no partial sums): the LM head "
-                         "(default), every round with K <= 4096, or none (split + epilogue kernels everywhere)")
+    ap.add_argument("--whole-k", default="lm",
+                    help="decode: rounds run as whole-K rounds (no K-slice partials), a comma list of qkv, o, gu, "
+                         "down, lm (those with K <= 4096 take it), 'all' or 'none' (split + epilogue kernels "
+                         "everywhere); default lm")
     ap.add_argument("--workload", choices=("decode", "prefill", "ipc"), default="decode",
                     help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
                          "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
@@ -482,7 +483,7 @@ def main():
     max_new = 1 + args.warmup + args.steps + args.timer_steps + 1
     dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill,
                          packed=args.weights == "packed",
-                         whole_k={"lm": True, "all": "all", "none": False}[args.whole_k])
+                         whole_k="" if args.whole_k == "none" else args.whole_k)
     del weights, adapters
     torch.cuda.synchronize()
 
@@ -516,10 +517,13 @@ def main():
     recs = ops.timer_collect()
     # the dominant kernel: the whole-K round (QKV, O, Gate+Up, LM head) when
     # the step uses it, else the K-sliced base kernel of every round
-    # the K-sliced base kernel of every projection round (the LM head may be
-    # a whole-K round)
-    whole_k = dec.whole_k == "all"
-    dom = [r for r in recs if r["k"] <= 4096] if whole_k else [r for r in recs if r["n"] != s.vocab or not dec.whole_k]
+    # the dominant kernel: the whole-K round when the Gate+Up round (the
+    # largest) takes it (its launches: every whole-K round), else the
+    # K-sliced base kernel of the K-sliced rounds
+    whole_k = bool(dec.wk.get("gu"))
+    wk_n = {n for g, n in (("qkv", s.qkv), ("o", s.hidden), ("gu", 2 * s.inter), ("lm", s.vocab)) if dec.wk.get(g)}
+    wk_rec = lambda r: r["k"] <= 4096 and r["n"] in wk_n  # noqa: E731
+    dom = [r for r in recs if wk_rec(r)] if whole_k else [r for r in recs if not wk_rec(r)]
     base_ms = [r["base_ms"] for r in dom]
     base_bytes = [r["bytes"] for r in dom]
     mean_ms = statistics.fmean(base_ms)
@@ -579,11 +583,11 @@ def main():
                    "rounds": breakdown},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": ("fullk_kernel (whole-K decode round: QKV, O, Gate+Up rounds and the LM head, "
-                                "epilogue included; Down stays split_kernel + epilogue_kernel)") if whole_k else
-                               ("split_kernel (decode projection base kernel, all 128 projection rounds; the LM "
-                                "head is a whole-K round)" if dec.whole_k else
-                                "split_kernel (decode projection base kernel, all 128 rounds + LM head)"),
+                     "kernel": (f"fullk_kernel (whole-K decode round, epilogue included: "
+                                f"{', '.join(g for g in ('qkv', 'o', 'gu', 'lm') if dec.wk.get(g))}; the other "
+                                f"rounds split_kernel + epilogue_kernel)") if whole_k else
+                               (f"split_kernel (K-sliced decode projection base kernel; whole-K rounds: "
+                                f"{', '.join(g for g in dec.wk if dec.wk[g]) or 'none'})"),
                      "launches": len(dom),
                      "mean_launch_us": round(mean_ms * 1e3, 3), "bytes_per_launch": int(mean_bytes)},
         "cpu_baseline": cpu,

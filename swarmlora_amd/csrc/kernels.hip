@@ -907,35 +907,40 @@ __host__ __device__ __forceinline__ int64_t paired_row(int64_t tile, int rr, int
   return (tile / per) * (2 * off) + (tile % per) * 8 + (rr & 7) + (rr >= 8 ? off : 0);
 }
 
+// s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0
+// and 15:14, expcnt and lgkmcnt at their maxima)
+__host__ __device__ constexpr unsigned wait_vm_imm(int n) {
+  return 0x0F70u | (unsigned)(n & 15) | ((unsigned)(n >> 4) << 14);
+}
+
 // ------------------------------------------- decode: whole-K rounds -------
-// Decode-shaped rounds with K <= 4096 (QKV, O, Gate+Up, LM head) in one
-// launch and without partial sums: a persistent workgroup of 8 waves per CU
-// (two per SIMD, 256 registers each) keeps the K range of every token row in
-// registers (wave w holds k-steps w * nsw .. + nsw of both 16-token tiles as
-// MFMA B fragments, 128 registers at K = 4096, RMS-normalised on the way in
-// when the round takes the residual stream), then walks its
-// units: unit u = blockIdx.x, + gridDim.x, ...  A unit is one 16-row tile,
-// first the stacked lora_A tiles of the round's adapters (the LoRA shrink),
-// then the weight's fragment tiles.  Each wave multiplies its k-steps of the
-// tile (the next unit's 16 fragments are requested right after, 128 KiB in
-// flight per CU), the 8 wave partials are summed in LDS, and the workgroup
-// finishes the tile itself:
-// a shrink tile's rows are stored (written through) for its adapter's
-// tokens and counted; a weight tile gets bias, the LoRA expand (waiting once
-// per workgroup, bounded, until every shrink tile is counted), and the
-// out_mode fusion, then is stored.  The weights are packed with paired rows
-// (pack offset `off`): tile rows r and r + 8 are the output columns c and
-// c + off, so SiLU * up (off = inter) and RoPE (off = 64 within a head)
-// find both operands in one tile.  The last workgroup to finish resets the
-// counters for the next launch.
+// Decode-shaped rounds with K <= 4096 (QKV, O, Gate+Up, LM head) without
+// K-slice partials: a persistent workgroup of 8 waves per CU (two per SIMD,
+// 256 registers each) keeps the K range of every token row in registers
+// (wave w holds k-steps w * nsw .. + nsw of both 16-token tiles as MFMA B
+// fragments, 128 registers at K = 4096, RMS-normalised on the way in when
+// the round takes the residual stream), then walks its 16-row weight tiles
+// (blockIdx.x, + gridDim.x, ...).  Each wave multiplies its k-steps of the
+// tile, the next tile's 16 fragments are requested right after (128 KiB in
+// flight per CU), the 8 wave partials are summed in LDS and the workgroup
+// finishes the tile itself: bias, the LoRA expand and the out_mode fusion,
+// then the stores.  The LoRA shrink rows u = x . A^T of the round's adapters
+// come from fullk_shrink_kernel, launched just before (K-slice partials,
+// summed into LDS once per workgroup); with every adapter at rank 16 the
+// lora_B rows a tile needs are moved into LDS by LDS-DMA together with the
+// tile's weights.  The weights are packed with paired rows (pack offset
+// `off`): tile rows r and r + 8 are the output columns c and c + off, so
+// SiLU * up (off = inter) and RoPE (off = 64 within a head) find both
+// operands in one tile.
 constexpr int kFkWaves = 8;
 constexpr int kFkMaxSteps = 16;  // k-steps per wave: K <= 8 * 16 * 32
+constexpr int kFkShrinkKs = 4;   // K-slices of the shrink kernel
 
 struct FullKArgs {
   const bf16* w;                // fragment tiles, rows paired by `off`
   int64_t N, K;
   int32_t ntok, nsw, total_steps, off;
-  int32_t n_stiles, n_units;    // shrink tiles first, then ceil(N / 16) weight tiles
+  int32_t n_tiles;              // ceil(N / 16)
   const bf16* x[32];
   bf16* y[32];
   // RMSNorm on the way in (gamma != null): x = bf16(bf16(h * r) * gamma)
@@ -952,8 +957,8 @@ struct FullKArgs {
   int32_t g_tile0[33];
   int8_t tok_grp[32];
   int32_t lora[32];             // table entry per token (-1: none)
-  float* u;                     // [ntok][u_ld] shrink rows
-  int32_t* sync;                // [0] shrink tiles stored, [1] workgroups done, [2] late waits
+  int32_t bdma;                 // every adapter of the round has rank 16: lora_B rows staged in LDS
+  float* u;                     // [kFkShrinkKs][ntok][u_ld] shrink partials
   const bf16* bias;
   // out_mode 1
   float* ss_out;
@@ -970,10 +975,6 @@ struct FullKArgs {
 };
 typedef const __attribute__((address_space(4))) FullKArgs* fullk_args_ptr;
 
-// Cache-policy operand of the buffer builtins: sc0 | sc1 (system scope):
-// stores written through to memory, loads of the memory's value.
-constexpr int kSysScope = 1 | 16;
-
 __device__ __forceinline__ int fk_blk(fullk_args_ptr a, int64_t n) {
   int b = 0;
 #pragma unroll
@@ -982,97 +983,224 @@ __device__ __forceinline__ int fk_blk(fullk_args_ptr a, int64_t n) {
   return b;
 }
 
+// Workgroup barrier for LDS hand-offs only: this wave's LDS accesses are
+// complete, then s_barrier.  Unlike __syncthreads it does not wait for the
+// wave's outstanding global loads (the next tile's weights stay in flight);
+// the signal fences keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// RMSNorm row factors r = rsqrt(sum of the row's partial sums of squares / K
+// + eps) into rsq[tk], one wave per token.
+__device__ __forceinline__ void fk_row_factors(fullk_args_ptr a, float* rsq, int waves, int wv, int lane) {
+  for (int tk = wv; tk < a->ntok; tk += waves) {
+    float sq = 0.f;
+    for (int j = lane; j < a->ss_n; j += 64) sq += a->ss[(int64_t)tk * a->ss_stride + j];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if (lane == 0) rsq[tk] = rsqrtf(sq / (float)a->K + a->eps);
+  }
+}
+
+// x = bf16(bf16(h * r) * gamma) of one B fragment (token row factor r,
+// gamma of the fragment's 8 dims)
+__device__ __forceinline__ u32x4 fk_norm8(u32x4 h, float r, u32x4 g) {
+  float hv[8], gv[8];
+  unpack8(h, hv);
+  unpack8(g, gv);
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(f2bf(hv[j] * r)) * gv[j]);
+  return __builtin_bit_cast(u32x4, o);
+}
+
+// LoRA shrink of a whole-K round: workgroup (shrink tile t, K-slice ks),
+// 4 waves over the slice's k-steps; tile t is 16 rows of adapter group g's
+// stacked A, multiplied with every token row (its tokens keep the result).
+// u[ks][tk][q0 + r] = partial sum over the slice.
+__global__ __launch_bounds__(256) void fullk_shrink_kernel(FullKArgs args) {
+  fullk_args_ptr a = (fullk_args_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  __shared__ f32x4 red[4][2][64];
+  __shared__ float rsq[32];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.x, ks = blockIdx.y;
+  const int ntok = a->ntok;
+  int g = 0;
+  while (g + 1 < a->ngroups && a->g_tile0[g + 1] <= t) ++g;
+  const int q0 = (t - a->g_tile0[g]) * 16;
+  const int steps = a->total_steps / kFkShrinkKs;  // k-steps of the slice
+  const int st0 = ks * steps;
+  if (a->gamma) {
+    fk_row_factors(a, rsq, 4, wv, lane);
+    __syncthreads();
+  }
+  // wave wv takes the slice's k-steps wv * spw .. + spw (at most 8), every
+  // load requested before the first product
+  const int spw = (steps + 3) / 4;
+  const int sw0 = st0 + wv * spw;
+  const int nj = max(0, min(spw, st0 + steps - sw0));  // this wave's steps
+  const bf16* ap = a->g_a[g] + (int64_t)min(q0 + (lane & 15), a->g_arows[g] - 1) * a->K + 8 * (lane >> 4);
+  u32x4 wa[8], xv[8][2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int s = min(sw0 + j, st0 + steps - 1);
+    wa[j] = ldg16(ap + 32 * s);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int tk = 16 * tt + (lane & 15);
+      const bool mine = j < nj && tk < ntok && a->tok_grp[tk] == g;
+      xv[j][tt] = mine ? ldg16(a->x[tk] + 32 * s + 8 * (lane >> 4)) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (a->gamma && j < nj) {
+      const u32x4 gv = ldg16(a->gamma + 32 * (sw0 + j) + 8 * (lane >> 4));
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int tk = 16 * tt + (lane & 15);
+        xv[j][tt] = fk_norm8(xv[j][tt], rsq[tk < ntok ? tk : 0], gv);
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) acc[tt] = mfma16(wa[j], xv[j][tt], acc[tt]);
+  }
+  red[wv][0][lane] = acc[0];
+  red[wv][1][lane] = acc[1];
+  __syncthreads();
+  const int e = threadIdx.x;  // (token, row): 32 x 16 = 512 > 256 threads: two passes
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int tk = (e >> 4) + 16 * pass, r = e & 15;
+    if (tk < ntok && a->tok_grp[tk] == g && q0 + r < a->g_arows[g]) {
+      const int l = (r >> 2) * 16 + (tk & 15);
+      const float v = (red[0][tk >> 4][l][r & 3] + red[1][tk >> 4][l][r & 3]) +
+                      (red[2][tk >> 4][l][r & 3] + red[3][tk >> 4][l][r & 3]);
+      a->u[((int64_t)ks * ntok + tk) * a->u_ld + q0 + r] = v;
+    }
+  }
+}
+
 template <int TT, int MODE>
 __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args) {
   fullk_args_ptr a = (fullk_args_ptr)__builtin_amdgcn_kernarg_segment_ptr();
   __shared__ f32x4 red[kFkWaves][TT][64];
   __shared__ float rsq[32];
-  extern __shared__ float us[];  // [ntok][u_ld] shrink rows, once every shrink tile is stored
+  // lora_B rows of a weight tile (rank-16 rounds): [token][tile row][16],
+  // two buffers (the next tile's rows land while this tile finishes)
+  __shared__ __attribute__((aligned(16))) bf16 bsm[2][32][16][16];
+  __shared__ const bf16* btab[32][SWL_MAX_LORA_BLOCKS];  // lora_B base of each token and column block
+  // per-token values the epilogue needs, read once here so that no load of
+  // the epilogue waits behind the next tile's weight loads: output row,
+  // adapter entry (-1: none), its rank and scale
+  __shared__ bf16* ytab[32];
+  __shared__ int32_t ltab[32], rtab[32];
+  __shared__ float stab[32];
+  extern __shared__ float us[];  // [ntok][u_ld + 4] shrink rows (padded: tokens fall in different banks)
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nsw = a->nsw, ntok = a->ntok;
   const int s0 = wv * nsw;
-  const int64_t K = a->K;
+  const int u_ld = a->u_ld, us_ld = a->u_ld + 4;
 
-  // fragments of this wave's k-steps of unit `un` (a shrink tile: 16 rows of
-  // an adapter group's stacked A, row-major, k-steps 32 elements apart; a
-  // weight tile: packed, k-steps 512 elements apart).  Steps past nsw reload
-  // the last one (in bounds); their products are masked to zero.
+  // this wave's k-steps of weight tile `tile` (packed, k-steps 512 elements
+  // apart); steps past nsw reload the last one (in bounds), their products
+  // masked to zero by the zeroed token fragments
   u32x4 wf[kFkMaxSteps];
-  auto issue = [&](int un) {
-    if (un >= a->n_units) return;
-    const bf16* p;
-    int64_t stride;
-    if (un >= a->n_stiles) {
-      p = a->w + ((int64_t)(un - a->n_stiles) * a->total_steps + s0) * 512 + 8 * lane;
-      stride = 512;
-    } else {
-      int g = 0;
-      while (g + 1 < a->ngroups && a->g_tile0[g + 1] <= un) ++g;
-      const int q = (un - a->g_tile0[g]) * 16 + (lane & 15);
-      p = a->g_a[g] + (int64_t)min(q, a->g_arows[g] - 1) * K + 32 * s0 + 8 * (lane >> 4);
-      stride = 32;
-    }
+  auto issue = [&](int tile) {
+    if (tile >= a->n_tiles) return;
+    const bf16* p = a->w + ((int64_t)tile * a->total_steps + s0) * 512 + 8 * lane;
 #pragma unroll
     for (int s = 0; s < kFkMaxSteps; ++s) {
       wf[s] = ldg16(p);
-      if (s + 1 < nsw) p += stride;
+      if (s + 1 < nsw) p += 512;
     }
   };
-  int unit = blockIdx.x;
-  issue(unit);
+  // lora_B rows of weight tile `tile` into bsm[buf] with LDS-DMA:
+  // instruction i (2 per wave, the last one repeated where there are fewer)
+  // moves tokens 2 i and 2 i + 1, each the 8 rows of its adapter's B under
+  // tile rows 0..7 (columns c0 ..) and under rows 8..15 (columns c0 + off
+  // ..), 256 bytes a piece.  Tokens without an adapter read harmless bytes
+  // of w.
+  const int n_bins = (ntok + 1) >> 1;
+  auto issue_b = [&](int tile, int buf) {
+    const int64_t c0 = paired_row(tile, 0, a->off), c1 = c0 + a->off;
+    const int b0 = fk_blk(a, c0), b1 = fk_blk(a, c1);
+    const int64_t r0 = (c0 - a->blk_start[b0]) * 16, r1 = (c1 - a->blk_start[b1]) * 16;
+    const int h = (lane >> 4) & 1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ins = min(wv + kFkWaves * j, n_bins - 1);
+      const int tk = 2 * ins + (lane >> 5);
+      const bf16* src = btab[tk < ntok ? tk : 0][h ? b1 : b0] + (h ? r1 : r0) + (lane & 15) * 8;
+      __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(reinterpret_cast<char*>(&bsm[buf][0][0][0]) + ins * 1024),
+                                       16, 0, 0);
+    }
+  };
 
   // token rows: B fragments of this wave's k-steps (token 16 t + lane % 16,
-  // k-group lane / 16); rows past ntok read row 0 and are zeroed
+  // k-group lane / 16), requested first; rows past ntok are zero
   u32x4 xf[kFkMaxSteps][TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) {
     const int tk = 16 * t + (lane & 15);
     const bf16* xr = a->x[tk < ntok ? tk : 0] + 32 * s0 + 8 * (lane >> 4);
 #pragma unroll
-    for (int s = 0; s < kFkMaxSteps; ++s) xf[s][t] = ldg16(xr + 32 * (s < nsw ? s : nsw - 1));
+    for (int s = 0; s < kFkMaxSteps; ++s)
+      xf[s][t] = (tk < ntok && s < nsw) ? ldg16(xr + 32 * s) : u32x4{0u, 0u, 0u, 0u};
   }
-  if (a->gamma) {
-    // r = rsqrt(sum of the row's partial sums of squares / K + eps), one
-    // wave per token
-    for (int tk = wv; tk < ntok; tk += kFkWaves) {
-      float sq = 0.f;
-      for (int j = lane; j < a->ss_n; j += 64) sq += a->ss[(int64_t)tk * a->ss_stride + j];
+  int tile = blockIdx.x;
+  issue(tile);
+  if (threadIdx.x < 32) {
+    const int tk = threadIdx.x;
+    const int li = (tk < ntok && a->has_lora) ? a->lora[tk] : -1;
+    ytab[tk] = tk < ntok ? a->y[tk] : nullptr;
+    ltab[tk] = li;
+    rtab[tk] = li >= 0 ? a->table[li].rank : 0;
+    stab[tk] = li >= 0 ? a->table[li].scale : 0.f;
+  }
+  if (a->has_lora) {
+    // shrink rows: the sum of the shrink kernel's K-slice partials
+    for (int i = threadIdx.x; i < ntok * u_ld; i += kFkWaves * 64) {
+      const int tk = i / u_ld, q = i - tk * u_ld;
+      float v = 0.f;
 #pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
-      if (lane == 0) rsq[tk] = rsqrtf(sq / (float)K + a->eps);
+      for (int ks = 0; ks < kFkShrinkKs; ++ks) v += a->u[((int64_t)ks * ntok + tk) * u_ld + q];
+      us[tk * us_ld + q] = v;
     }
-    __syncthreads();
+  }
+  if (a->bdma) {
+    for (int i = threadIdx.x; i < 32 * SWL_MAX_LORA_BLOCKS; i += kFkWaves * 64) {
+      const int tk = i / SWL_MAX_LORA_BLOCKS, b = i % SWL_MAX_LORA_BLOCKS;
+      const int li = tk < ntok ? a->lora[tk] : -1;
+      btab[tk][b] = (li >= 0 && b < a->nblk) ? reinterpret_cast<const bf16*>(a->table[li].b[b]) : a->w;
+    }
+  }
+  if (a->gamma) fk_row_factors(a, rsq, kFkWaves, wv, lane);
+  lds_barrier();
+  int nb = 0;  // tiles whose lora_B rows were requested (buffer nb % 2 next)
+  if (a->bdma && tile < a->n_tiles) issue_b(tile, nb++ & 1);
+  if (a->gamma) {
     const bf16* gp = a->gamma + 32 * s0 + 8 * (lane >> 4);
 #pragma unroll
     for (int s = 0; s < kFkMaxSteps; ++s) {
-      float gv[8];
-      unpack8(ldg16(gp + 32 * (s < nsw ? s : nsw - 1)), gv);
+      if (s >= nsw) continue;
+      const u32x4 gv = ldg16(gp + 32 * s);
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         const int tk = 16 * t + (lane & 15);
-        const float r = rsq[tk < ntok ? tk : 0];
-        float hv[8];
-        unpack8(xf[s][t], hv);
-        bf16x8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(f2bf(hv[j] * r)) * gv[j]);
-        xf[s][t] = __builtin_bit_cast(u32x4, o);
+        xf[s][t] = fk_norm8(xf[s][t], rsq[tk < ntok ? tk : 0], gv);
       }
     }
   }
-#pragma unroll
-  for (int t = 0; t < TT; ++t) {
-    const bool live_tok = 16 * t + (lane & 15) < ntok;
-#pragma unroll
-    for (int s = 0; s < kFkMaxSteps; ++s)
-      if (!live_tok || s >= nsw) xf[s][t] = u32x4{0u, 0u, 0u, 0u};
-  }
 
-  const __amdgpu_buffer_rsrc_t ursrc =
-      __builtin_amdgcn_make_buffer_rsrc(a->u, 0, a->has_lora ? ntok * a->u_ld * 4 : 0, 0x00020000);
-  bool u_ready = !a->has_lora;
-  while (unit < a->n_units) {
+  while (tile < a->n_tiles) {
     f32x4 acc[TT];
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1080,12 +1208,24 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
     for (int s = 0; s < kFkMaxSteps; ++s)
 #pragma unroll
       for (int t = 0; t < TT; ++t) acc[t] = mfma16(wf[s], xf[s][t], acc[t]);
-    const int cur = unit;
-    unit += gridDim.x;
-    issue(unit);  // in flight during this tile's reduction and epilogue
+    const int cur = tile;
+    const int cur_buf = (nb + 1) & 1;  // the buffer cur's lora_B rows went to
+    tile += gridDim.x;
+    issue(tile);  // in flight during this tile's reduction and epilogue
+    const bool next_b = a->bdma && tile < a->n_tiles;
+    if (next_b) issue_b(tile, nb++ & 1);
 #pragma unroll
     for (int t = 0; t < TT; ++t) red[wv][t][lane] = acc[t];
-    __syncthreads();
+    lds_barrier();
+    if (a->bdma) {
+      // this tile's lora_B rows have landed: at most the next tile's 16
+      // weight loads and 2 DMA are younger
+      if (next_b)
+        __builtin_amdgcn_s_waitcnt(wait_vm_imm(kFkMaxSteps + 2));
+      else
+        __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
+      lds_barrier();
+    }
     // sum of the wave partials of tile row r, token tk
     auto total = [&](int r, int tk) {
       const int l = (r >> 2) * 16 + (tk & 15), t = tk >> 4, e = r & 3;
@@ -1095,49 +1235,11 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
       return v;
     };
 
-    if (cur < a->n_stiles) {
-      // shrink tile: rows q0 .. q0 + 15 of group g's stacked A
-      int g = 0;
-      while (g + 1 < a->ngroups && a->g_tile0[g + 1] <= cur) ++g;
-      const int q0 = (cur - a->g_tile0[g]) * 16;
-      const int e = threadIdx.x;
-      const int tk = e >> 4, r = e & 15;
-      if (tk < ntok && a->tok_grp[tk] == g && q0 + r < a->g_arows[g]) {
-        const float v = total(r, tk);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ursrc,
-                                              (int)(4 * ((int64_t)tk * a->u_ld + q0 + r)), 0, kSysScope);
-      }
-      __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's u stores are written through
-      __syncthreads();
-      if (threadIdx.x == 0) (void)__hip_atomic_fetch_add(a->sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      continue;  // red is rewritten only after the next barrier
-    }
-
-    if (!u_ready) {
-      // every shrink tile stored: bounded wait (1 s), then the shrink rows to LDS
-      if (threadIdx.x == 0) {
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        while (__hip_atomic_load(a->sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a->n_stiles) {
-          if (__builtin_amdgcn_s_memrealtime() - t0 > 100000000ull) {
-            (void)__hip_atomic_fetch_add(a->sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(2);
-        }
-      }
-      __syncthreads();
-      for (int i = threadIdx.x; i < ntok * a->u_ld; i += kFkWaves * 64)
-        us[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ursrc, 4 * i, 0, kSysScope));
-      __syncthreads();
-      u_ready = true;
-    }
-
-    // weight tile: thread (token tk, pair p) finishes tile rows p and p + 8,
-    // output columns c0 and c0 + off
-    const int64_t tile = cur - a->n_stiles;
+    // thread (token tk, pair p) finishes tile rows p and p + 8, output
+    // columns c0 and c0 + off
     const int e = threadIdx.x;
     const int tk = e >> 3, p = e & 7;
-    const int64_t c0 = paired_row(tile, p, a->off), c1 = c0 + a->off;
+    const int64_t c0 = paired_row(cur, p, a->off), c1 = c0 + a->off;
     const bool live = tk < ntok && c0 < a->N;
     float v0 = 0.f, v1 = 0.f;
     if (live) {
@@ -1145,46 +1247,57 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
       v1 = total(p + 8, tk);
       if (a->bias) {
         v0 += bf2f(a->bias[c0]);
-        if (c1 < a->N) v1 += bf2f(a->bias[c1]);
+        v1 += bf2f(a->bias[c1]);
       }
-      const int li = a->has_lora ? a->lora[tk] : -1;
+      const int li = ltab[tk];
       if (li >= 0) {
-        const swl_lora_entry* ep = a->table + li;
-        const int r = ep->rank;
-        const float* ut = us + tk * a->u_ld;
+        const int r = rtab[tk];
+        const float scale = stab[tk];
+        const float* ut = us + tk * us_ld;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int64_t c = h ? c1 : c0;
-          if (c >= a->N) continue;
           const int b = fk_blk(a, c);
-          const bf16* brow = reinterpret_cast<const bf16*>(ep->b[b]) + (c - a->blk_start[b]) * r;
           const float* ub = ut + b * r;
           float d = 0.f;
-          if ((r & 7) == 0) {
-            for (int q = 0; q < r; q += 8) {
+          if (a->bdma) {
+            const bf16* bl = &bsm[cur_buf][tk][8 * h + p][0];
+#pragma unroll
+            for (int q = 0; q < 16; q += 8) {
               float bv[8];
-              unpack8(ld16(brow + q), bv);
+              unpack8(*reinterpret_cast<const u32x4*>(bl + q), bv);
 #pragma unroll
               for (int i = 0; i < 8; ++i) d += ub[q + i] * bv[i];
             }
           } else {
-            for (int q = 0; q < r; ++q) d += ub[q] * bf2f(brow[q]);
+            const bf16* brow =
+                reinterpret_cast<const bf16*>(a->table[li].b[b]) + (c - a->blk_start[b]) * r;
+            if ((r & 7) == 0) {
+              for (int q = 0; q < r; q += 8) {
+                float bv[8];
+                unpack8(ld16(brow + q), bv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) d += ub[q + i] * bv[i];
+              }
+            } else {
+              for (int q = 0; q < r; ++q) d += ub[q] * bf2f(brow[q]);
+            }
           }
-          (h ? v1 : v0) += d * ep->scale;
+          (h ? v1 : v0) += d * scale;
         }
       }
     }
 
     if constexpr (MODE == 0) {
       if (live) {
-        a->y[tk][c0] = f2bf(v0);
-        if (c1 < a->N) a->y[tk][c1] = f2bf(v1);
+        ytab[tk][c0] = f2bf(v0);
+        ytab[tk][c1] = f2bf(v1);
       }
     } else if constexpr (MODE == 1) {
       // h = bf16(h + out); the tile's sum of squares of the new h per token
       float sq = 0.f;
       if (live) {
-        bf16* yr = a->y[tk];
+        bf16* yr = ytab[tk];
         const bf16 h0 = f2bf(bf2f(yr[c0]) + bf2f(f2bf(v0)));
         const bf16 h1 = f2bf(bf2f(yr[c1]) + bf2f(f2bf(v1)));
         yr[c0] = h0;
@@ -1194,12 +1307,12 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
       sq += __shfl_xor(sq, 1, 64);
       sq += __shfl_xor(sq, 2, 64);
       sq += __shfl_xor(sq, 4, 64);
-      if (live && p == 0) a->ss_out[(int64_t)tk * a->ss_out_stride + tile] = sq;
+      if (live && p == 0) a->ss_out[(int64_t)tk * a->ss_out_stride + cur] = sq;
     } else if constexpr (MODE == 2) {
       // c0 a gate column, c1 = c0 + inter its up column
       if (live) {
         const float g = bf2f(f2bf(v0)), u = bf2f(f2bf(v1));
-        a->y[tk][c0] = f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u);
+        ytab[tk][c0] = f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u);
       }
     } else {
       // c0 = head * 128 + d (d < 64), c1 = c0 + 64: NeoX RoPE pair of q / k
@@ -1216,7 +1329,7 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
           x0 = n0;
           x1 = n1;
         }
-        bf16* yr = a->y[tk];
+        bf16* yr = ytab[tk];
         yr[c0] = f2bf(x0);
         yr[c1] = f2bf(x1);
         const int64_t slen = a->seqlens[tk];
@@ -1232,15 +1345,7 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
         }
       }
     }
-    __syncthreads();  // red is rewritten by the next unit
-  }
-
-  // the last workgroup to finish resets the counters for the next launch
-  if (threadIdx.x == 0) {
-    if (__hip_atomic_fetch_add(a->sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
-      __hip_atomic_store(a->sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a->sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    lds_barrier();  // red and bsm[cur_buf] are rewritten after this
   }
 }
 
@@ -1889,10 +1994,6 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_f<0x4E>(v);
   v += dpp_f<0x141>(v);
   return v + dpp_f<0x140>(v);
-}
-
-__host__ __device__ constexpr unsigned wait_vm_imm(int n) {
-  return 0x0F70u | (unsigned)(n & 15) | ((unsigned)(n >> 4) << 14);
 }
 
 template <int G, int S, int W>
@@ -2579,34 +2680,11 @@ void plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const swl_lor
   p.g_tile0[p.ngroups] = p.tiles;
 }
 
-// Counters of the whole-K rounds (fullk_kernel): [0] shrink tiles stored,
-// [1] workgroups finished, [2] bounded waits that ran out.  Zero at module
-// load; every launch leaves them zero again ([2] aside).  One copy per GPU,
-// addressed through hipGetSymbolAddress; rounds on one GPU that use them
-// must be ordered (one stream).
-static __device__ __align__(256) int32_t fullk_sync[64];
-std::mutex g_fk_mu;
-int32_t* g_fk_sync[64] = {};
-
-int fullk_sync_ptr(int32_t** out) {
-  int dev = 0;
-  SWL_HIP(hipGetDevice(&dev));
-  SWL_CHECK(dev >= 0 && dev < 64, SWL_ERR_INVALID, "whole-K round: device index out of range");
-  std::lock_guard<std::mutex> lk(g_fk_mu);
-  if (!g_fk_sync[dev]) {
-    void* p = nullptr;
-    SWL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(fullk_sync)));
-    SWL_CHECK(p != nullptr, SWL_ERR_HIP, "whole-K round: hipGetSymbolAddress returned null");
-    g_fk_sync[dev] = reinterpret_cast<int32_t*>(p);
-  }
-  *out = g_fk_sync[dev];
-  return SWL_OK;
-}
-
 template <int TT, int MODE>
 int launch_fullk_tm(const FullKArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   static size_t allowed = 0;
-  int rc = allow_lds(fullk_kernel<TT, MODE>, lds + 16 * 1024 * TT + 256, &allowed);
+  // static LDS: partial sums (16 KiB per token tile), lora_B buffers (16 KiB), tables
+  int rc = allow_lds(fullk_kernel<TT, MODE>, lds + 16 * 1024 * TT + 16 * 1024 + 2048, &allowed);
   if (rc) return rc;
   launch_maybe_timed(fullk_kernel<TT, MODE>, grid, dim3(kFkWaves * 64), lds, st, e0, e1, a);
   return SWL_OK;
@@ -2643,9 +2721,10 @@ int launch_split_w(int TT, const SplitArgs& a, dim3 grid, size_t lds, hipStream_
   }
 }
 
-// Whole-K decode round (fullk_kernel): weights packed with paired rows
-// (w_layout 2; pair offset inter for out_mode 2, 64 for out_mode 3, else 8),
-// at most 32 token rows, K a multiple of 256 up to 4096.
+// Whole-K decode round (fullk_shrink_kernel when the round has adapters,
+// then fullk_kernel): weights packed with paired rows (w_layout 2; pair
+// offset inter for out_mode 2, 64 for out_mode 3, else 8), at most 32 token
+// rows, K a multiple of 256 up to 4096.
 int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok, const bf16* const* xrows,
                  bf16* const* yrows, const int32_t* tok_lora, const swl_lora_entry* table,
                  const swl_lora_entry* host_entries, const LoraEpi* Lblk, int nblk, const swl_round_fusion* fz,
@@ -2667,6 +2746,7 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
   a.nsw = (int)(K / (32 * kFkWaves));
   a.total_steps = (int)(K / 32);
   a.off = (int)off;
+  a.n_tiles = (int)(N / 16);
   for (int i = 0; i < ntok; ++i) {
     a.x[i] = xrows[i];
     a.y[i] = yrows[i];
@@ -2701,20 +2781,19 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
     a.u_ld = max_r * nblk;
     SWL_CHECK(a.u_ld <= kMaxURow, SWL_ERR_INVALID, "round: LoRA rank x blocks exceeds 256");
     a.has_lora = 1;
-    a.n_stiles = sp.tiles;
+    a.bdma = 1;
+    for (int g = 0; g < sp.ngroups; ++g) a.bdma &= host_entries[sp.g_entry[g]].rank == 16 ? 1 : 0;
     a.nblk = nblk;
     a.table = table;
     for (int b = 0; b <= SWL_MAX_LORA_BLOCKS; ++b) a.blk_start[b] = Lblk->blk_start[b];
   } else {
     for (int i = 0; i < ntok; ++i) a.lora[i] = -1;
   }
-  a.n_units = a.n_stiles + (int)(N / 16);
   if (mode == 1) {
     a.ss_out = fz->ss_out;
     a.ss_out_stride = fz->ss_out_stride;
   }
   if (mode == 3) {
-    SWL_CHECK(ntok <= 32, SWL_ERR_INVALID, "round fusion: out_mode 3 token rows");
     a.kc = reinterpret_cast<bf16*>(fz->k_cache);
     a.vc = reinterpret_cast<bf16*>(fz->v_cache);
     a.bt = fz->block_table;
@@ -2728,21 +2807,27 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
     a.hkv = fz->hkv;
     a.bs = fz->block_size;
   }
-  int rc = fullk_sync_ptr(&a.sync);
-  if (rc) return rc;
-  const size_t u_bytes = has_lora ? sizeof(float) * (size_t)ntok * a.u_ld : 0;
+  // LDS of the shrink rows: [ntok][u_ld + 4] floats
+  const size_t us_bytes = has_lora ? sizeof(float) * (size_t)ntok * (a.u_ld + 4) : 0;
   if (has_lora) {
+    const size_t u_bytes = sizeof(float) * (size_t)kFkShrinkKs * ntok * a.u_ld;
     void* scr = ws;
     if (ws) {
       SWL_CHECK(u_bytes <= ws_bytes, SWL_ERR_INVALID, "whole-K round: shrink rows exceed the allocation-free scratch");
     } else {
-      rc = scratch_get(u_bytes, st, &scr);
+      int rc = scratch_get(u_bytes, st, &scr);
       if (rc) return rc;
     }
     a.u = reinterpret_cast<float*>(scr);
   }
-  const dim3 grid((unsigned)std::min<int64_t>(a.n_units, cu_count()));
+  const dim3 grid((unsigned)std::min<int64_t>(a.n_tiles, cu_count()));
   const int tslot = timer_slot(st);
+  if (has_lora) {
+    // timed in the record's second slot (the K-sliced round's epilogue slot)
+    launch_maybe_timed(fullk_shrink_kernel, dim3((unsigned)sp.tiles, (unsigned)kFkShrinkKs), dim3(256), 0, st,
+                       timer_event(tslot, 2), timer_event(tslot, 3), a);
+    SWL_LAUNCH_CHECK("fullk_shrink_kernel launch");
+  }
   if (tslot >= 0) {
     int64_t bytes = 2 * (N * K + (int64_t)ntok * K);
     for (int g = 0; g < sp.ngroups && has_lora; ++g) bytes += 2 * (int64_t)sp.g_arows[g] * K;
@@ -2752,12 +2837,12 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
     g_timer.bytes[tslot] = bytes;
   }
   hipEvent_t e0 = timer_event(tslot, 0), e1 = timer_event(tslot, 1);
-  rc = TT == 1 ? launch_fullk_t<1>(mode, a, grid, u_bytes, st, e0, e1)
-               : launch_fullk_t<2>(mode, a, grid, u_bytes, st, e0, e1);
+  int rc = TT == 1 ? launch_fullk_t<1>(mode, a, grid, us_bytes, st, e0, e1)
+                   : launch_fullk_t<2>(mode, a, grid, us_bytes, st, e0, e1);
   if (rc) return rc;
   SWL_LAUNCH_CHECK("fullk_kernel launch");
-  if (tslot >= 0) {
-    // no separate epilogue: its events mark an empty interval after the kernel
+  if (tslot >= 0 && !has_lora) {
+    // no shrink kernel: its events mark an empty interval after the round
     SWL_HIP(hipEventRecord(timer_event(tslot, 2), st));
     SWL_HIP(hipEventRecord(timer_event(tslot, 3), st));
   }
@@ -3527,6 +3612,7 @@ int swl_timer_collect(int max_records, float* base_ms, float* epilogue_ms, int64
   g_timer.armed = false;
   const int m = std::min(g_timer.n, max_records);
   for (int i = 0; i < m; ++i) {
+    SWL_HIP(hipEventSynchronize(g_timer.ev[4 * i + 1]));
     SWL_HIP(hipEventSynchronize(g_timer.ev[4 * i + 3]));
     float a = 0.f, b = 0.f;
     SWL_HIP(hipEventElapsedTime(&a, g_timer.ev[4 * i], g_timer.ev[4 * i + 1]));

@@ -120,10 +120,10 @@ class BatchedDecoder:
     Capacity for `max_new` generated tokens is reserved up front.
     packed (fused step only): projection and LM-head weights kept in the
     fragment-tile layout (ops.PackedWeight) instead of row-major.
-    whole_k (packed step only, at most 32 workers): True runs the LM head as
-    a whole-K round (w_layout 2: one launch, no partial sums); "all" also
-    the QKV, O and Gate+Up rounds (and Down when the intermediate size is at
-    most 4096); the other rounds are K-sliced.
+    whole_k (packed step only, at most 32 workers): the rounds run as
+    whole-K rounds (w_layout 2: no K-slice partials) when their K allows
+    (<= 4096): True for the LM head, "all" for every round, or a set /
+    comma list of "qkv", "o", "gu", "down", "lm"; the others are K-sliced.
     """
 
     def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
@@ -141,7 +141,18 @@ class BatchedDecoder:
         self.graph = None
         self.fused = fused
         self.packed = packed and fused
-        self.whole_k = whole_k if (whole_k and self.packed and W <= 32) else False
+        names = ("qkv", "o", "gu", "down", "lm")
+        if whole_k is True:
+            wk = {"lm"}
+        elif whole_k == "all":
+            wk = set(names)
+        elif isinstance(whole_k, str):
+            wk = {g for g in whole_k.split(",") if g}
+        else:
+            wk = set(whole_k or ())
+        if not wk <= set(names):
+            raise ValueError(f"whole_k: rounds must be among {names}")
+        self.whole_k = wk if (self.packed and W <= 32) else set()
         if fused:
             self._init_fused(weights, adapters, ctx_lens, first_ids, kv_fill)
             return
@@ -237,19 +248,17 @@ class BatchedDecoder:
         self.norms = []
         # whole-K rounds: K a multiple of 256 up to 4096, n a multiple of 16
         # (of 128 for the QKV pairs, of 2 * inter for Gate+Up).  By default
-        # only the LM head takes them (measured at 8B widths, 28 workers:
-        # LM head 192 us against 238 for split + epilogue; the rounds with
-        # per-worker adapters are slower whole-K: every CU loads all 28 token
-        # rows, more bytes than its share of the O / QKV weights, and the
-        # adapters' lora_B rows are read behind the next tile's weights);
-        # whole_k="all" runs every round that fits that way
-        fits = lambda k: bool(self.whole_k) and k % 256 == 0 and k <= 4096  # noqa: E731
-        every = self.whole_k == "all"
-        self.wk = {"qkv": every and fits(s.hidden) and s.qkv % 128 == 0,
-                   "o": every and fits(s.heads * s.head_dim) and s.hidden % 16 == 0,
-                   "gu": every and fits(s.hidden) and s.inter % 8 == 0,
-                   "down": every and fits(s.inter) and s.hidden % 16 == 0,
-                   "lm": fits(s.hidden) and s.vocab % 16 == 0}
+        # only the LM head takes them (measured at 8B widths, 28 workers, in
+        # the captured step: LM head 206 us against 248 for split +
+        # epilogue; Gate+Up 81 us against 75: with cold weights one tile per
+        # CU in flight streams at ~3.6 TB/s, and every CU loads all token
+        # rows, more bytes than its share of the O / QKV weights)
+        fits = lambda g, k: g in self.whole_k and k % 256 == 0 and k <= 4096  # noqa: E731
+        self.wk = {"qkv": fits("qkv", s.hidden) and s.qkv % 128 == 0,
+                   "o": fits("o", s.heads * s.head_dim) and s.hidden % 16 == 0,
+                   "gu": fits("gu", s.hidden) and s.inter % 8 == 0,
+                   "down": fits("down", s.inter) and s.hidden % 16 == 0,
+                   "lm": fits("lm", s.hidden) and s.vocab % 16 == 0}
         pair = {"qkv": 64, "gu": s.inter}
 
         def keep(t, g):
