@@ -48,6 +48,7 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -1371,6 +1372,9 @@ struct TiledArgs {
   SegPtrs out;            // per-segment output base pointers (row stride N)
   int32_t seg_lora[kMaxSeg];
   LoraEpi L;              // u rows are packed rows
+  // gemm256_kernel: LoRA delta as MFMA k-steps (every tile inside one column
+  // block, ranks multiples of 8 up to 64) instead of in the epilogue
+  int32_t lora_mfma;
 };
 
 // LDS rows of 64 bf16 (eight 16-byte chunks) with the chunks of row r
@@ -1497,6 +1501,224 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
       epilogue_store4(v, n, a.N, a.bias, a.L, lidx, (int)m, yrow);
     }
     __syncthreads();
+  }
+}
+
+// ------------------------------------------ prefill: 256 x 256 tiles ------
+// y[m, n] = sum_k x[m, k] w[n, k] for the packed prefill batch, one
+// 256 (columns) x 256 (tokens) output tile per workgroup of 4 waves, each
+// wave 128 x 128 as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16 (W rows as the A
+// operand, token rows as B: a lane ends up with 4 consecutive columns of one
+// token, the layout the epilogue stores; 256 fp32 accumulators a lane).  K
+// advances 32 at a time through a ring of 4 LDS stages of 32 KiB (W 256 x
+// 32 and x 256 x 32), filled by LDS-DMA (global_load_lds, 16 bytes a lane,
+// no register round trip) two stages ahead, so one barrier per stage
+// separates the refill of a stage from the last reads of it.  LDS rows are
+// 64 bytes (four 16-byte chunks); chunk c of row r sits at c ^ ((r / 2) % 4)
+// so a 16-lane fragment read (16 rows, one chunk) touches each bank group at
+// most twice.  Workgroups are numbered so that each XCD (workgroup i runs on
+// XCD i % 8) walks a contiguous run of tiles, tokens fastest: the W rows of
+// a tile column are read by the XCD's workgroups together, from its L2.
+constexpr int PG_M = 256, PG_N = 256, PG_K = 32, PG_STAGES = 4;
+constexpr int PG_STAGE_BYTES = (PG_M + PG_N) * PG_K * 2;  // 32 KiB
+constexpr int PG_ELD = 64 + 4;                            // epilogue staging row (fp32)
+constexpr int PG_LDS_BYTES = PG_STAGES * PG_STAGE_BYTES > 4 * 128 * PG_ELD * 4 ? PG_STAGES * PG_STAGE_BYTES
+                                                                                : 4 * 128 * PG_ELD * 4;
+
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_m, int tiles, int per_xcd) {
+  // PG_STAGES x [W 256 x 32 | x 256 x 32]; then the epilogue's 4 x [128][PG_ELD] fp32
+  extern __shared__ __attribute__((aligned(16))) char pg_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wv >> 1, wn = wv & 1;  // wave: tokens wm * 128.., columns wn * 128..
+  const int lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (lin >= tiles) return;  // uniform over the workgroup
+  const int64_t m0 = (int64_t)(lin % tiles_m) * PG_M;
+  const int64_t n0 = (int64_t)(lin / tiles_m) * PG_N;
+  const int nk = (int)(a.K / PG_K);
+
+  // LDS-DMA of stage kt: wave w moves W rows 64 w .. + 64 and x rows
+  // 64 w .. + 64 (4 instructions each, 16 rows of 64 bytes an instruction);
+  // lane l -> row r0 + l / 4, stored chunk l % 4, read from global chunk
+  // (l % 4) ^ ((l / 8) % 4)
+  const int dr = lane >> 2, dc = (lane & 3) ^ ((lane >> 3) & 3);
+  const bf16* wsrc[4];
+  const bf16* xsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = 64 * wv + 16 * i + dr;
+    wsrc[i] = a.w + min(n0 + r, a.N - 1) * a.K + 8 * dc;
+    xsrc[i] = a.x + min(m0 + r, a.M - 1) * a.K + 8 * dc;
+  }
+  auto issue = [&](int kt) {
+    char* st = pg_lds + (kt % PG_STAGES) * PG_STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(wsrc[i] + (int64_t)kt * PG_K),
+                                       (lds_ptr)(st + (64 * wv + 16 * i) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[i] + (int64_t)kt * PG_K),
+                                       (lds_ptr)(st + PG_N * 64 + (64 * wv + 16 * i) * 64), 16, 0, 0);
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // fragment rows of this lane: W row wn * 128 + 32 i + l % 32, x row
+  // wm * 128 + 32 j + l % 32; k chunk 2 kk + l / 32 of the stage
+  const int fr = lane & 31, fh = lane >> 5;
+  auto frags = [&](int kt, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+    const char* st = pg_lds + (kt % PG_STAGES) * PG_STAGE_BYTES;
+    const int c = 2 * kk + fh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rw = wn * 128 + 32 * i + fr, rx = wm * 128 + 32 * i + fr;
+      fa[i] = *reinterpret_cast<const u32x4*>(st + rw * 64 + ((c ^ ((rw >> 1) & 3)) << 4));
+      fb[i] = *reinterpret_cast<const u32x4*>(st + PG_N * 64 + rx * 64 + ((c ^ ((rx >> 1) & 3)) << 4));
+    }
+  };
+  auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+  };
+  // this wave's DMA of stage `kt` has landed (8 instructions a stage, up to
+  // two younger stages still in flight), then every wave's
+  auto stage_ready = [&](int kt) {
+    const int younger = min(2, nk - 1 - kt);
+    if (younger == 2)
+      __builtin_amdgcn_s_waitcnt(wait_vm_imm(16));
+    else if (younger == 1)
+      __builtin_amdgcn_s_waitcnt(wait_vm_imm(8));
+    else
+      __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
+    lds_barrier();
+  };
+
+  // Stages are requested three ahead; the barrier that makes stage kt + 1
+  // readable also certifies that every wave has read stage kt - 1 (its last
+  // fragments are read before that barrier), whose slot the next request
+  // refills.  Fragments are double-buffered in registers: the second k-step
+  // of a stage and the first of the next are read while the MFMAs of the
+  // k-step before run.
+  for (int kt = 0; kt < 3 && kt < nk; ++kt) issue(kt);
+  stage_ready(0);
+  u32x4 f0a[4], f0b[4], f1a[4], f1b[4];
+  frags(0, 0, f0a, f0b);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 3 < nk) issue(kt + 3);
+    frags(kt, 1, f1a, f1b);
+    mma(f0a, f0b);
+    if (kt + 1 < nk) stage_ready(kt + 1);
+    mma(f1a, f1b);
+    if (kt + 1 < nk) frags(kt + 1, 0, f0a, f0b);
+  }
+
+  // LoRA delta as extra k-steps: for every segment of the tile's token rows
+  // that has an adapter, A = the adapter's lora_B rows of the tile's
+  // columns (k = rank), B = the segment's shrink rows u * scale rounded to
+  // bf16 (zero for the other segments' rows), 16 ranks a step
+  if (a.has_lora && a.lora_mfma) {
+    const int b = [&] {
+      int bb = 0;
+#pragma unroll
+      for (int i = 1; i < SWL_MAX_LORA_BLOCKS; ++i)
+        if (i < a.L.nblk && n0 >= a.L.blk_start[i]) bb = i;
+      return bb;
+    }();
+    const int64_t bstart = blk_start_of(a.L, b);
+    for (int sg = find_seg(a.out.off, a.out.n, m0); sg < a.out.n && a.out.off[sg] < m0 + PG_M; ++sg) {
+      const int e = a.seg_lora[sg];
+      if (e < 0) continue;
+      const swl_lora_entry* ep = a.L.table + e;
+      const int r = ep->rank;
+      const float scale = ep->scale;
+      const bf16* bb = reinterpret_cast<const bf16*>(ep->b[b]);
+      const int64_t lo = a.out.off[sg], hi = a.out.off[sg + 1];
+      for (int q0 = 0; q0 < r; q0 += 16) {
+        const int q = q0 + 8 * fh;
+        u32x4 fa[4], fb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t n = n0 + wn * 128 + 32 * i + fr;
+          fa[i] = (n < a.N && q < r) ? ld16(bb + (n - bstart) * r + q) : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t m = m0 + wm * 128 + 32 * j + fr;
+          u32x4 v = u32x4{0u, 0u, 0u, 0u};
+          if (m >= lo && m < hi && q < r) {
+            const float* up = a.L.u + m * a.L.u_ld + b * r + q;
+            const f32x4 u0 = *reinterpret_cast<const f32x4*>(up), u1 = *reinterpret_cast<const f32x4*>(up + 4);
+            bf16x8 o;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              o[t] = f2bf(u0[t] * scale);
+              o[4 + t] = f2bf(u1[t] * scale);
+            }
+            v = __builtin_bit_cast(u32x4, o);
+          }
+          fb[j] = v;
+        }
+        mma(fa, fb);
+      }
+    }
+  }
+
+  // Epilogue through LDS (the stages are free once every wave is past its
+  // last reads), in two halves of the columns so each wave's share fits:
+  // acc[i][j] element e of lane l is column 32 i + 8 (e / 4) + 4 (l / 32) +
+  // e % 4 of the wave's 128, token 32 j + l % 32.  Wave w's half h lands in
+  // region w as [128 tokens][64 columns (+4 pad)] fp32; then thread t takes
+  // quads of four columns, 16 threads a token row, and finishes them
+  // (bias, LoRA expand, one bf16 rounding, the segment's row).
+  constexpr int ELD = PG_ELD;
+  float* reg = reinterpret_cast<float*>(pg_lds) + wv * 128 * ELD;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    lds_barrier();  // the previous half's (or the k-loop's) reads are done
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int tok = 32 * j + fr, col = 32 * ii + 8 * q + 4 * fh;
+          const f32x16& c = acc[2 * h + ii][j];
+          *reinterpret_cast<f32x4*>(reg + tok * ELD + col) = f32x4{c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]};
+        }
+    lds_barrier();
+    // items: wave region w2 (tokens wm2 * 128, columns wn2 * 128 + 64 h),
+    // token row tr, quad cq; 4 x 128 x 16 items, 32 a thread
+    for (int it = threadIdx.x; it < 4 * 128 * 16; it += 256) {
+      const int w2 = it >> 11, tr = (it >> 4) & 127, cq = it & 15;
+      const int64_t m = m0 + (w2 >> 1) * 128 + tr;
+      const int64_t n = n0 + (w2 & 1) * 128 + 64 * h + 4 * cq;
+      if (m >= a.M || n >= a.N) continue;
+      const f32x4 q4 = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * 128 + tr) * ELD + 4 * cq);
+      float v[4] = {q4[0], q4[1], q4[2], q4[3]};
+      bf16* yrow;
+      int lidx = -1;
+      if (a.y) {
+        yrow = a.y + m * a.ldy;
+      } else {
+        const int sg = find_seg(a.out.off, a.out.n, m);
+        yrow = reinterpret_cast<bf16*>(const_cast<void*>(a.out.ptr[sg])) + (m - a.out.off[sg]) * a.N;
+        lidx = (a.has_lora && !a.lora_mfma) ? a.seg_lora[sg] : -1;
+      }
+      epilogue_store4(v, n, a.N, a.bias, a.L, lidx, (int)m, yrow);
+    }
   }
 }
 
@@ -3059,6 +3281,31 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   return SWL_OK;
 }
 
+// Prefill GEMM launch: gemm256_kernel (256 x 256 tiles), or tiled_kernel
+// (128 x 128) with SWL_PREFILL_TILED=1.
+int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
+  static const bool use_tiled = [] {
+    const char* e = getenv("SWL_PREFILL_TILED");
+    return e && atoi(e) != 0;
+  }();
+  if (use_tiled || a.K % PG_K != 0) {
+    const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM));
+    hipLaunchKernelGGL(tiled_kernel, grid, dim3(256), 0, st, a);
+    SWL_LAUNCH_CHECK("tiled_kernel launch");
+    return SWL_OK;
+  }
+  const int tiles_m = (int)((a.M + PG_M - 1) / PG_M), tiles_n = (int)((a.N + PG_N - 1) / PG_N);
+  const int tiles = tiles_m * tiles_n;
+  const int per_xcd = (tiles + 7) / 8;
+  const size_t lds = PG_LDS_BYTES;
+  static size_t allowed = 0;
+  int rc = allow_lds(gemm256_kernel, lds, &allowed);
+  if (rc) return rc;
+  hipLaunchKernelGGL(gemm256_kernel, dim3((unsigned)(8 * per_xcd)), dim3(256), lds, st, a, tiles_m, tiles, per_xcd);
+  SWL_LAUNCH_CHECK("gemm256_kernel launch");
+  return SWL_OK;
+}
+
 // LoRA shrink of the packed prefill batch (one launch for all segments with
 // an adapter): seg_off / seg_rows are packed row offsets and counts; the u
 // rows are packed rows; n_ks K-slices of partials, folded into the first.
@@ -3377,10 +3624,7 @@ int swl_gemm_bf16(const void* x, const void* w, const void* bias, void* y, int64
   a.y = reinterpret_cast<bf16*>(y);
   a.ldy = n;
   a.has_lora = 0;
-  const dim3 grid((unsigned)((n + TN - 1) / TN), (unsigned)((m + TM - 1) / TM));
-  hipLaunchKernelGGL(tiled_kernel, grid, dim3(256), 0, st, a);
-  SWL_LAUNCH_CHECK("tiled_kernel launch");
-  return SWL_OK;
+  return launch_prefill_gemm(a, st);
 }
 
 int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in, void* const* seg_out, const void* w,
@@ -3838,11 +4082,17 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
     a.L.usplit = 1;  // folded into split 0
     a.L.u_ld = u_ld;
     a.L.u_split_stride = (int64_t)T * u_ld;
+    // the 256 x 256 kernel adds the LoRA delta as MFMA k-steps when every
+    // tile lies inside one column block and the ranks are multiples of 8
+    a.lora_mfma = 1;
+    for (int b = 1; b < nblk; ++b) a.lora_mfma &= (L.blk_start[b] % PG_N == 0) ? 1 : 0;
+    for (int i = 0; i < n_seg; ++i)
+      if (a.seg_lora[i] >= 0) {
+        const int r = host_entries[a.seg_lora[i]].rank;
+        a.lora_mfma &= (r % 8 == 0 && r <= 64) ? 1 : 0;
+      }
   }
-  const dim3 grid((unsigned)((N + TN - 1) / TN), (unsigned)((T + TM - 1) / TM));
-  hipLaunchKernelGGL(tiled_kernel, grid, dim3(256), 0, st, a);
-  SWL_LAUNCH_CHECK("tiled_kernel launch");
-  return SWL_OK;
+  return launch_prefill_gemm(a, st);
 }
 
 }  // namespace swl
