@@ -1593,37 +1593,49 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
   };
-  // this wave's DMA of stage `kt` has landed (8 instructions a stage, up to
-  // two younger stages still in flight), then every wave's
-  auto stage_ready = [&](int kt) {
-    const int younger = min(2, nk - 1 - kt);
-    if (younger == 2)
-      __builtin_amdgcn_s_waitcnt(wait_vm_imm(16));
-    else if (younger == 1)
-      __builtin_amdgcn_s_waitcnt(wait_vm_imm(8));
-    else
-      __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
-    lds_barrier();
-  };
-
   // Stages are requested three ahead; the barrier that makes stage kt + 1
   // readable also certifies that every wave has read stage kt - 1 (its last
   // fragments are read before that barrier), whose slot the next request
-  // refills.  Fragments are double-buffered in registers: the second k-step
-  // of a stage and the first of the next are read while the MFMAs of the
-  // k-step before run.
-  for (int kt = 0; kt < 3 && kt < nk; ++kt) issue(kt);
-  stage_ready(0);
+  // refills.  The loop has no branches: past the last stage the requests
+  // re-read stage nk - 1 into slots nobody reads again, so every iteration
+  // waits for the same count (this wave's 8 DMA instructions of stage kt + 1
+  // have landed when at most the 16 of kt + 2 and kt + 3 are outstanding),
+  // and the scheduler can interleave.  Fragments are double-buffered in
+  // registers: the second k-step of a stage is read while the MFMAs of the
+  // first run, and the first k-step of the next stage while those of the
+  // second run; the stage's DMA requests go out between the first MFMAs.
+  for (int kt = 0; kt < 3; ++kt) issue(min(kt, nk - 1));
+  __builtin_amdgcn_s_waitcnt(wait_vm_imm(16));
+  lds_barrier();
   u32x4 f0a[4], f0b[4], f1a[4], f1b[4];
   frags(0, 0, f0a, f0b);
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 3 < nk) issue(kt + 3);
+    issue(min(kt + 3, nk - 1));
     frags(kt, 1, f1a, f1b);
     mma(f0a, f0b);
-    if (kt + 1 < nk) stage_ready(kt + 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM (LDS-DMA)
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier
+    __builtin_amdgcn_s_waitcnt(wait_vm_imm(16));
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    frags(kt + 1, 0, f0a, f0b);
     mma(f1a, f1b);
-    if (kt + 1 < nk) frags(kt + 1, 0, f0a, f0b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  // the requests past the last stage land before the LDS is reused
+  __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
 
   // LoRA delta as extra k-steps: for every segment of the tile's token rows
   // that has an adapter, A = the adapter's lora_B rows of the tile's
@@ -3288,7 +3300,7 @@ int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
     const char* e = getenv("SWL_PREFILL_TILED");
     return e && atoi(e) != 0;
   }();
-  if (use_tiled || a.K % PG_K != 0) {
+  if (use_tiled || a.K % PG_K != 0 || a.K < PG_K) {
     const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM));
     hipLaunchKernelGGL(tiled_kernel, grid, dim3(256), 0, st, a);
     SWL_LAUNCH_CHECK("tiled_kernel launch");
