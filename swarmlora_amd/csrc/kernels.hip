@@ -55,7 +55,16 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kMaxSeg = SWL_MAX_SLOTS;
 constexpr int kSkinnyMaxTok = 64;
 
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// 16-byte load of device memory through a global-address-space pointer
+// (global_load, not flat: a flat load also counts against lgkmcnt)
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const __attribute__((address_space(1))) u32x4*)(p); }
+
+// Stores through global-address-space pointers (global_store, not flat): a
+// flat store also counts against lgkmcnt, so every later wait for an LDS
+// read would wait for the store too.  Every output row is device memory.
+__device__ __forceinline__ void stg(bf16* p, u32x2 v) { *(__attribute__((address_space(1))) u32x2*)(p) = v; }
+__device__ __forceinline__ void stg(bf16* p, bf16 v) { *(__attribute__((address_space(1))) bf16*)(p) = v; }
+__device__ __forceinline__ bf16 ldg(const bf16* p) { return *(const __attribute__((address_space(1))) bf16*)(p); }
 
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
@@ -200,7 +209,7 @@ __device__ __forceinline__ void lora_delta4(const LoraEpi L, const swl_lora_entr
       float uq = 0.f;
       for (int s = 0; s < L.usplit; ++s) uq += up[s * L.u_split_stride + q];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) d[j] += uq * bf2f(b0[(int64_t)j * r + q]);
+      for (int j = 0; j < 4; ++j) d[j] += uq * bf2f(ldg(b0 + (int64_t)j * r + q));
     }
   }
 #pragma unroll
@@ -216,9 +225,23 @@ __device__ __forceinline__ float lora_delta1(const LoraEpi L, const swl_lora_ent
   for (int q = 0; q < r; ++q) {
     float uq = 0.f;
     for (int s = 0; s < L.usplit; ++s) uq += up[s * L.u_split_stride + q];
-    d += uq * bf2f(b0[q]);
+    d += uq * bf2f(ldg(b0 + q));
   }
   return d * ep->scale;
+}
+
+// Store 4 consecutive columns n..n+3 of one row (bf16, one rounding).
+__device__ __forceinline__ void store4_bf16(const float (&v)[4], int64_t n, int64_t N, bf16* yrow) {
+  if (n + 3 < N && ((reinterpret_cast<uintptr_t>(yrow + n) & 7) == 0)) {
+    bf16 o0 = f2bf(v[0]), o1 = f2bf(v[1]), o2 = f2bf(v[2]), o3 = f2bf(v[3]);
+    u32x2 pk;
+    pk[0] = (uint32_t)__builtin_bit_cast(uint16_t, o0) | ((uint32_t)__builtin_bit_cast(uint16_t, o1) << 16);
+    pk[1] = (uint32_t)__builtin_bit_cast(uint16_t, o2) | ((uint32_t)__builtin_bit_cast(uint16_t, o3) << 16);
+    stg(yrow + n, pk);
+  } else {
+    for (int j = 0; j < 4; ++j)
+      if (n + j < N) stg(yrow + n + j, f2bf(v[j]));
+  }
 }
 
 // Finalise 4 consecutive columns n..n+3 of one token and store them (bf16).
@@ -244,16 +267,7 @@ __device__ __forceinline__ void epilogue_store4(float (&v)[4], int64_t n, int64_
         if (n + j < N) v[j] += lora_delta1(L, ep, urow, n + j);
     }
   }
-  if (n + 3 < N && ((reinterpret_cast<uintptr_t>(yrow + n) & 7) == 0)) {
-    bf16 o0 = f2bf(v[0]), o1 = f2bf(v[1]), o2 = f2bf(v[2]), o3 = f2bf(v[3]);
-    u32x2 pk;
-    pk[0] = (uint32_t)__builtin_bit_cast(uint16_t, o0) | ((uint32_t)__builtin_bit_cast(uint16_t, o1) << 16);
-    pk[1] = (uint32_t)__builtin_bit_cast(uint16_t, o2) | ((uint32_t)__builtin_bit_cast(uint16_t, o3) << 16);
-    *reinterpret_cast<u32x2*>(yrow + n) = pk;
-  } else {
-    for (int j = 0; j < 4; ++j)
-      if (n + j < N) yrow[n + j] = f2bf(v[j]);
-  }
+  store4_bf16(v, n, N, yrow);
 }
 
 // ------------------------------------------------------ skinny (M<=64) ----
@@ -1281,7 +1295,7 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
                 for (int i = 0; i < 8; ++i) d += ub[q + i] * bv[i];
               }
             } else {
-              for (int q = 0; q < r; ++q) d += ub[q] * bf2f(brow[q]);
+              for (int q = 0; q < r; ++q) d += ub[q] * bf2f(ldg(brow + q));
             }
           }
           (h ? v1 : v0) += d * scale;
@@ -1291,18 +1305,18 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
 
     if constexpr (MODE == 0) {
       if (live) {
-        ytab[tk][c0] = f2bf(v0);
-        ytab[tk][c1] = f2bf(v1);
+        stg(ytab[tk] + c0, f2bf(v0));
+        stg(ytab[tk] + c1, f2bf(v1));
       }
     } else if constexpr (MODE == 1) {
       // h = bf16(h + out); the tile's sum of squares of the new h per token
       float sq = 0.f;
       if (live) {
         bf16* yr = ytab[tk];
-        const bf16 h0 = f2bf(bf2f(yr[c0]) + bf2f(f2bf(v0)));
-        const bf16 h1 = f2bf(bf2f(yr[c1]) + bf2f(f2bf(v1)));
-        yr[c0] = h0;
-        yr[c1] = h1;
+        const bf16 h0 = f2bf(bf2f(ldg(yr + c0)) + bf2f(f2bf(v0)));
+        const bf16 h1 = f2bf(bf2f(ldg(yr + c1)) + bf2f(f2bf(v1)));
+        stg(yr + c0, h0);
+        stg(yr + c1, h1);
         sq = bf2f(h0) * bf2f(h0) + bf2f(h1) * bf2f(h1);
       }
       sq += __shfl_xor(sq, 1, 64);
@@ -1313,7 +1327,7 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
       // c0 a gate column, c1 = c0 + inter its up column
       if (live) {
         const float g = bf2f(f2bf(v0)), u = bf2f(f2bf(v1));
-        ytab[tk][c0] = f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u);
+        stg(ytab[tk] + c0, f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u));
       }
     } else {
       // c0 = head * 128 + d (d < 64), c1 = c0 + 64: NeoX RoPE pair of q / k
@@ -1331,8 +1345,8 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
           x1 = n1;
         }
         bf16* yr = ytab[tk];
-        yr[c0] = f2bf(x0);
-        yr[c1] = f2bf(x1);
+        stg(yr + c0, f2bf(x0));
+        stg(yr + c1, f2bf(x1));
         const int64_t slen = a->seqlens[tk];
         if (!is_q && slen >= 0 && slen / a->bs < a->max_blocks) {
           const int32_t pb = a->bt[(int64_t)tk * a->max_blocks + slen / a->bs];
@@ -1340,8 +1354,8 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
             const int kvh = is_k ? hh - a->hq : hh - a->hq - a->hkv;
             const int64_t dst = ((int64_t)pb * a->bs + slen % a->bs) * a->hkv * 128 + kvh * 128 + d;
             bf16* cache = is_k ? a->kc : a->vc;
-            cache[dst] = f2bf(x0);
-            cache[dst + 64] = f2bf(x1);
+            stg(cache + dst, f2bf(x0));
+            stg(cache + dst + 64, f2bf(x1));
           }
         }
       }
@@ -1510,20 +1524,26 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 // wave 128 x 128 as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16 (W rows as the A
 // operand, token rows as B: a lane ends up with 4 consecutive columns of one
 // token, the layout the epilogue stores; 256 fp32 accumulators a lane).  K
-// advances 32 at a time through a ring of 4 LDS stages of 32 KiB (W 256 x
-// 32 and x 256 x 32), filled by LDS-DMA (global_load_lds, 16 bytes a lane,
-// no register round trip) two stages ahead, so one barrier per stage
-// separates the refill of a stage from the last reads of it.  LDS rows are
-// 64 bytes (four 16-byte chunks); chunk c of row r sits at c ^ ((r / 2) % 4)
-// so a 16-lane fragment read (16 rows, one chunk) touches each bank group at
-// most twice.  Workgroups are numbered so that each XCD (workgroup i runs on
-// XCD i % 8) walks a contiguous run of tiles, tokens fastest: the W rows of
-// a tile column are read by the XCD's workgroups together, from its L2.
-constexpr int PG_M = 256, PG_N = 256, PG_K = 32, PG_STAGES = 4;
-constexpr int PG_STAGE_BYTES = (PG_M + PG_N) * PG_K * 2;  // 32 KiB
+// advances 64 at a time through 2 LDS slots of 64 KiB (W 256 x 64 and x 256
+// x 64), filled by LDS-DMA (global_load_lds, 16 bytes a lane, no register
+// round trip) one stage ahead; every row a DMA instruction reads is one
+// whole 128-byte line.  One barrier per stage separates the refill of a
+// slot from the last reads of it.  LDS rows are 128 bytes (eight 16-byte
+// chunks); chunk c of row r sits at c ^ (r % 8) ^ ((r / 8) % 2), so a
+// fragment read (32 consecutive rows, one chunk) meets distinct banks in
+// every 8 and every 16 of its lanes.  Workgroups are numbered so that each
+// XCD (workgroup i runs on XCD i % 8) walks a contiguous run of tiles,
+// tokens fastest: the W rows of a tile column are read by the XCD's
+// workgroups together, from its L2.
+constexpr int PG_M = 256, PG_N = 256, PG_K = 64, PG_SLOTS = 2;
+constexpr int PG_ROW = PG_K * 2;                           // bytes of an LDS row
+constexpr int PG_STAGE_BYTES = (PG_M + PG_N) * PG_ROW;  // 64 KiB
 constexpr int PG_ELD = 64 + 4;                            // epilogue staging row (fp32)
-constexpr int PG_LDS_BYTES = PG_STAGES * PG_STAGE_BYTES > 4 * 128 * PG_ELD * 4 ? PG_STAGES * PG_STAGE_BYTES
+constexpr int PG_STAGE_AREA = PG_SLOTS * PG_STAGE_BYTES > 4 * 128 * PG_ELD * 4 ? PG_SLOTS * PG_STAGE_BYTES
                                                                                 : 4 * 128 * PG_ELD * 4;
+// then the tile's row table: output row pointer (8 bytes) and epilogue
+// adapter (4 bytes) of each of its 256 token rows
+constexpr int PG_LDS_BYTES = PG_STAGE_AREA + PG_M * 12;
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
@@ -1531,7 +1551,7 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 }
 
 __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_m, int tiles, int per_xcd) {
-  // PG_STAGES x [W 256 x 32 | x 256 x 32]; then the epilogue's 4 x [128][PG_ELD] fp32
+  // PG_SLOTS x [W 256 x 64 | x 256 x 64]; then the epilogue's 4 x [128][PG_ELD] fp32
   extern __shared__ __attribute__((aligned(16))) char pg_lds[];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1542,27 +1562,29 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
   const int64_t n0 = (int64_t)(lin / tiles_m) * PG_N;
   const int nk = (int)(a.K / PG_K);
 
-  // LDS-DMA of stage kt: wave w moves W rows 64 w .. + 64 and x rows
-  // 64 w .. + 64 (4 instructions each, 16 rows of 64 bytes an instruction);
-  // lane l -> row r0 + l / 4, stored chunk l % 4, read from global chunk
-  // (l % 4) ^ ((l / 8) % 4)
-  const int dr = lane >> 2, dc = (lane & 3) ^ ((lane >> 3) & 3);
-  const bf16* wsrc[4];
-  const bf16* xsrc[4];
+  // LDS-DMA of stage kt into slot s: wave w moves W rows 64 w .. + 64 and x
+  // rows 64 w .. + 64 (8 instructions each, 8 rows of 128 bytes an
+  // instruction); lane l of instruction i -> row 64 w + 8 i + l / 8, stored
+  // chunk l % 8, read from global chunk (l % 8) ^ (l / 8) ^ (i % 2)
+  const int dr = lane >> 3;
+  const bf16* wsrc[8];
+  const bf16* xsrc[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = 64 * wv + 16 * i + dr;
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = 64 * wv + 8 * i + dr;
+    const int dc = (lane & 7) ^ dr ^ (i & 1);
     wsrc[i] = a.w + min(n0 + r, a.N - 1) * a.K + 8 * dc;
     xsrc[i] = a.x + min(m0 + r, a.M - 1) * a.K + 8 * dc;
   }
-  auto issue = [&](int kt) {
-    char* st = pg_lds + (kt % PG_STAGES) * PG_STAGE_BYTES;
+  // half h: instructions 4 h .. 4 h + 3 of W and of x
+  auto issue = [&](int kt, int s, int h) {
+    char* st = pg_lds + s * PG_STAGE_BYTES;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 4 * h; i < 4 * h + 4; ++i) {
       __builtin_amdgcn_global_load_lds((gbl_ptr)(wsrc[i] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + (64 * wv + 16 * i) * 64), 16, 0, 0);
+                                       (lds_ptr)(st + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[i] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + PG_N * 64 + (64 * wv + 16 * i) * 64), 16, 0, 0);
+                                       (lds_ptr)(st + PG_N * PG_ROW + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
     }
   };
 
@@ -1575,16 +1597,16 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   // fragment rows of this lane: W row wn * 128 + 32 i + l % 32, x row
-  // wm * 128 + 32 j + l % 32; k chunk 2 kk + l / 32 of the stage
+  // wm * 128 + 32 j + l % 32 (both = l % 32 modulo 32, so one swizzle);
+  // k chunk 2 kk + l / 32 of the stage
   const int fr = lane & 31, fh = lane >> 5;
-  auto frags = [&](int kt, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
-    const char* st = pg_lds + (kt % PG_STAGES) * PG_STAGE_BYTES;
-    const int c = 2 * kk + fh;
+  const int sw = (fr & 7) ^ ((fr >> 3) & 1);
+  auto frags = [&](int s, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
+    const char* st = pg_lds + s * PG_STAGE_BYTES + fr * PG_ROW + (((2 * kk + fh) ^ sw) << 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rw = wn * 128 + 32 * i + fr, rx = wm * 128 + 32 * i + fr;
-      fa[i] = *reinterpret_cast<const u32x4*>(st + rw * 64 + ((c ^ ((rw >> 1) & 3)) << 4));
-      fb[i] = *reinterpret_cast<const u32x4*>(st + PG_N * 64 + rx * 64 + ((c ^ ((rx >> 1) & 3)) << 4));
+      fa[i] = *reinterpret_cast<const u32x4*>(st + (wn * 128 + 32 * i) * PG_ROW);
+      fb[i] = *reinterpret_cast<const u32x4*>(st + PG_N * PG_ROW + (wm * 128 + 32 * i) * PG_ROW);
     }
   };
   auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
@@ -1593,46 +1615,99 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
   };
-  // Stages are requested three ahead; the barrier that makes stage kt + 1
-  // readable also certifies that every wave has read stage kt - 1 (its last
-  // fragments are read before that barrier), whose slot the next request
-  // refills.  The loop has no branches: past the last stage the requests
-  // re-read stage nk - 1 into slots nobody reads again, so every iteration
-  // waits for the same count (this wave's 8 DMA instructions of stage kt + 1
-  // have landed when at most the 16 of kt + 2 and kt + 3 are outstanding),
-  // and the scheduler can interleave.  Fragments are double-buffered in
-  // registers: the second k-step of a stage is read while the MFMAs of the
-  // first run, and the first k-step of the next stage while those of the
-  // second run; the stage's DMA requests go out between the first MFMAs.
-  for (int kt = 0; kt < 3; ++kt) issue(min(kt, nk - 1));
+  // One instruction group of the main loop: MFMA t of the 32 of half a
+  // stage (k-step t / 16 of the pair, tile (t % 16) / 4, (t % 4)), then at
+  // most one fragment read and one DMA request, then a scheduling fence, so
+  // the order written here is the order issued.  Spreading the requests
+  // keeps the CU's address queue from blocking the wave (a 1 KiB LDS-DMA
+  // request takes the queue about 16 cycles).
+  auto mfma_at = [&](u32x4 (&a0)[4], u32x4 (&b0)[4], u32x4 (&a1)[4], u32x4 (&b1)[4], int t) {
+    const int i = (t & 15) >> 2, j = t & 3;
+    if (t < 16)
+      acc[i][j] = mfma32(a0[i], b0[j], acc[i][j]);
+    else
+      acc[i][j] = mfma32(a1[i], b1[j], acc[i][j]);
+  };
+  auto read_at = [&](int s, int kk, u32x4 (&fa_)[4], u32x4 (&fb_)[4], int idx) {
+    const char* st = pg_lds + s * PG_STAGE_BYTES + fr * PG_ROW + (((2 * kk + fh) ^ sw) << 4);
+    if (idx < 4)
+      fa_[idx] = *reinterpret_cast<const u32x4*>(st + (wn * 128 + 32 * idx) * PG_ROW);
+    else
+      fb_[idx - 4] = *reinterpret_cast<const u32x4*>(st + PG_N * PG_ROW + (wm * 128 + 32 * (idx - 4)) * PG_ROW);
+  };
+  auto request_at = [&](int kt, int s, int q) {  // DMA instruction q of 16 (W 0..7, x 8..15)
+    char* st = pg_lds + s * PG_STAGE_BYTES;
+    const int i = q & 7;
+    if (q < 8)
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(wsrc[i] + (int64_t)kt * PG_K),
+                                       (lds_ptr)(st + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[i] + (int64_t)kt * PG_K),
+                                       (lds_ptr)(st + PG_N * PG_ROW + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
+  };
+
+  // Fragments of the four k-steps of a stage sit in four register sets,
+  // read two k-steps ahead of their MFMAs.  Stage kt + 2 is requested into
+  // slot kt % 2 after the barrier at mid-stage kt that ends every wave's
+  // reads of it (the fragments of k-steps 2 and 3 were read during k-steps
+  // 0 and 1); the same barrier publishes stage kt + 1, whose first two
+  // k-steps are read during the last two of stage kt.  The loop has no
+  // branches: past the last stage the requests re-read stage nk - 1 into
+  // the free slot, which only the discarded reads at the very end look at.
+  u32x4 fa[4][4], fb[4][4];
+  issue(0, 0, 0);
+  issue(0, 0, 1);
+  issue(min(1, nk - 1), 1, 0);
+  issue(min(1, nk - 1), 1, 1);
+  // row table (its loads overlap the first stages' DMA)
+  bf16** rowtab = reinterpret_cast<bf16**>(pg_lds + PG_STAGE_AREA);
+  int* lidxtab = reinterpret_cast<int*>(pg_lds + PG_STAGE_AREA + PG_M * 8);
+  {
+    const int64_t m = m0 + threadIdx.x;
+    bf16* yrow = nullptr;
+    int lidx = -1;
+    if (m < a.M) {
+      if (a.y) {
+        yrow = a.y + m * a.ldy;
+      } else {
+        const int sg = find_seg(a.out.off, a.out.n, m);
+        yrow = reinterpret_cast<bf16*>(const_cast<void*>(a.out.ptr[sg])) + (m - a.out.off[sg]) * a.N;
+        lidx = (a.has_lora && !a.lora_mfma) ? a.seg_lora[sg] : -1;
+      }
+    }
+    rowtab[threadIdx.x] = yrow;
+    lidxtab[threadIdx.x] = lidx;
+  }
   __builtin_amdgcn_s_waitcnt(wait_vm_imm(16));
   lds_barrier();
-  u32x4 f0a[4], f0b[4], f1a[4], f1b[4];
-  frags(0, 0, f0a, f0b);
+  frags(0, 0, fa[0], fb[0]);
+  frags(0, 1, fa[1], fb[1]);
   for (int kt = 0; kt < nk; ++kt) {
-    issue(min(kt + 3, nk - 1));
-    frags(kt, 1, f1a, f1b);
-    mma(f0a, f0b);
+    const int s = kt & 1;
+    // k-steps 0, 1 of stage kt; reads of its k-steps 2, 3 during the first 16
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM (LDS-DMA)
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    for (int t = 0; t < 32; ++t) {
+      mfma_at(fa[0], fb[0], fa[1], fb[1], t);
+      if (t < 8) read_at(s, 2, fa[2], fb[2], t);
+      else if (t < 16) read_at(s, 3, fa[3], fb[3], t - 8);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier
-    __builtin_amdgcn_s_waitcnt(wait_vm_imm(16));
+    // this wave's DMA of stage kt + 1 has landed (it is all that is
+    // outstanding), then every wave's; every wave is past its reads of slot s
+    __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    frags(kt + 1, 0, f0a, f0b);
-    mma(f1a, f1b);
+    // k-steps 2, 3; reads of stage kt + 1's k-steps 0, 1 during the first
+    // 16, a DMA request of stage kt + 2 every second MFMA
+    const int nx = min(kt + 2, nk - 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    for (int t = 0; t < 32; ++t) {
+      mfma_at(fa[2], fb[2], fa[3], fb[3], t);
+      if (t < 8) read_at(s ^ 1, 0, fa[0], fb[0], t);
+      else if (t < 16) read_at(s ^ 1, 1, fa[1], fb[1], t - 8);
+      if ((t & 1) == 0) request_at(nx, s, t >> 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    __builtin_amdgcn_sched_barrier(0);
   }
   // the requests past the last stage land before the LDS is reused
   __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
@@ -1712,24 +1787,57 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
         }
     lds_barrier();
     // items: wave region w2 (tokens wm2 * 128, columns wn2 * 128 + 64 h),
-    // token row tr, quad cq; 4 x 128 x 16 items, 32 a thread
-    for (int it = threadIdx.x; it < 4 * 128 * 16; it += 256) {
-      const int w2 = it >> 11, tr = (it >> 4) & 127, cq = it & 15;
-      const int64_t m = m0 + (w2 >> 1) * 128 + tr;
+    // token row tr, quad cq; 4 x 128 x 16 items, 32 a thread, all of one
+    // thread's in the two column quads cq = t % 16 of the two wn2, whose
+    // bias it loads once
+    const int cq = threadIdx.x & 15;
+    float bq[2][4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int64_t n = n0 + c * 128 + 64 * h + 4 * cq;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bq[c][e] = (a.bias && n + e < a.N) ? bf2f(a.bias[n + e]) : 0.f;
+    }
+    auto item = [&](int k, bool lora) {
+      const int w2 = k >> 3, tr = ((threadIdx.x >> 4) + 16 * k) & 127;
+      const int row = (w2 >> 1) * 128 + tr;
+      const int64_t m = m0 + row;
       const int64_t n = n0 + (w2 & 1) * 128 + 64 * h + 4 * cq;
-      if (m >= a.M || n >= a.N) continue;
+      if (m >= a.M || n >= a.N) return;
       const f32x4 q4 = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * 128 + tr) * ELD + 4 * cq);
-      float v[4] = {q4[0], q4[1], q4[2], q4[3]};
-      bf16* yrow;
-      int lidx = -1;
-      if (a.y) {
-        yrow = a.y + m * a.ldy;
-      } else {
-        const int sg = find_seg(a.out.off, a.out.n, m);
-        yrow = reinterpret_cast<bf16*>(const_cast<void*>(a.out.ptr[sg])) + (m - a.out.off[sg]) * a.N;
-        lidx = (a.has_lora && !a.lora_mfma) ? a.seg_lora[sg] : -1;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = q4[e] + bq[w2 & 1][e];
+      epilogue_store4(v, n, a.N, nullptr, a.L, lora ? lidxtab[row] : -1, (int)m, rowtab[row]);
+    };
+    if (a.has_lora && !a.lora_mfma) {
+      // the LoRA delta in the epilogue (per-quad loads of u and lora_B)
+      for (int k = 0; k < 32; ++k) item(k, true);
+    } else {
+      // k = 8 w2 + kk: the 8 staged quads and row pointers of a region are
+      // read together, then stored
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        f32x4 q[8];
+        bf16* rp[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const int tr = (threadIdx.x >> 4) + 16 * kk;
+          q[kk] = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * 128 + tr) * ELD + 4 * cq);
+          rp[kk] = rowtab[(w2 >> 1) * 128 + tr];
+        }
+        const int64_t n = n0 + (w2 & 1) * 128 + 64 * h + 4 * cq;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const int64_t m = m0 + (w2 >> 1) * 128 + (threadIdx.x >> 4) + 16 * kk;
+          if (m < a.M && n < a.N) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = q[kk][e] + bq[w2 & 1][e];
+            store4_bf16(v, n, a.N, rp[kk]);
+          }
+        }
       }
-      epilogue_store4(v, n, a.N, a.bias, a.L, lidx, (int)m, yrow);
     }
   }
 }
