@@ -66,6 +66,9 @@ def parse():
                     help="decode: rounds run as whole-K rounds (no K-slice partials), a comma list of qkv, o, gu, "
                          "down, lm (those with K <= 4096 take it), 'all' or 'none' (split + epilogue kernels "
                          "everywhere); default lm")
+    ap.add_argument("--chain", action="store_true",
+                    help="decode: each layer's O, Gate+Up and Down rounds and the next layer's QKV round as one "
+                         "persistent launch (swl_chain_*)")
     ap.add_argument("--workload", choices=("decode", "prefill", "ipc"), default="decode",
                     help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
                          "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
@@ -483,7 +486,7 @@ def main():
     max_new = 1 + args.warmup + args.steps + args.timer_steps + 1
     dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill,
                          packed=args.weights == "packed",
-                         whole_k="" if args.whole_k == "none" else args.whole_k)
+                         whole_k="" if args.whole_k == "none" else args.whole_k, chain=args.chain)
     del weights, adapters
     torch.cuda.synchronize()
 

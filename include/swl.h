@@ -355,6 +355,78 @@ int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, 
                                   const int32_t* cache_seqlens, const int64_t* positions, const void* cos_sin,
                                   int64_t max_pos, int rope, float softmax_scale, void* stream);
 
+/* ------------------------------------------- persistent decode chain ----
+ * Several dependent decode-shaped rounds in one persistent launch: the O,
+ * Gate+Up and Down rounds of a layer and the next layer's fused QKV round of
+ * the reference's per-layer op sequence (ext_aggregator.cpp:1095-1199, the
+ * rounds of ext_aggregator.cpp:562-612 with the worker's elementwise steps of
+ * worker_sync.py:1344-1401 between them), each a whole-K round over weights
+ * packed by swl_pack_weight_pairs_bf16 with the round's pair offset (n / 2
+ * for out_mode 2, 64 for out_mode 3, 8 for out_mode 1).  Round r reads token
+ * rows x [ntok, k] (row stride ldx), RMS-normalised on the way in when
+ * norm_weight is set (factors from ss_in, as swl_round_fusion), adds the
+ * LoRA delta of each token's table entry (rank 16, nblk column blocks of
+ * widths blk_cols) and writes y by out_mode: 1 y = bf16(res + out) with one
+ * sum of squares of y per 16 columns into ss_out (stride ss_out_stride
+ * >= n / 16); 2 y [ntok, n / 2] = SiLU(gate) * up; 3 rows with NeoX RoPE on
+ * q and k, k and v appended to the KV pages described by kv (its k_cache ..
+ * max_pos fields).  A round may read what an earlier round of the chain
+ * wrote; no round may write a buffer an earlier round of the chain reads
+ * (the caller rotates the residual buffers).  ntok <= 32, k a multiple of
+ * 256 (up to 4096 with norm_weight), at most SWL_CHAIN_MAX_ROUNDS rounds.
+ * No counterpart in the reference (it launches each round and each
+ * elementwise step separately). */
+#define SWL_CHAIN_MAX_ROUNDS 4
+typedef struct swl_chain_round {
+  const void* w;
+  int64_t n, k;
+  int32_t out_mode;
+  const void* x;
+  int64_t ldx;
+  const void* norm_weight;
+  const float* ss_in;
+  int32_t ss_in_n, ss_in_stride;
+  float eps;
+  void* y;
+  int64_t ldy;
+  const void* res;
+  int64_t ldres;
+  float* ss_out;
+  int32_t ss_out_stride;
+  const int32_t* lora; /* HOST [ntok] table entry per token (-1: none), or NULL */
+  int32_t nblk;
+  int64_t blk_cols[SWL_MAX_LORA_BLOCKS];
+} swl_chain_round;
+
+typedef struct swl_chain_plan swl_chain_plan;
+
+/* Validates the rounds, resolves the LoRA entries (lora_table_host: the host
+ * mirror of the table, n_entries records) and uploads the launch arguments
+ * to device memory (allocates); the plan is then launched any number of
+ * times, also from a captured graph.  kv: the KV fields for out_mode 3 (may
+ * be NULL otherwise). */
+int swl_chain_create(int ntok, int n_rounds, const swl_chain_round* rounds, const swl_lora_entry* lora_table_host,
+                     int n_entries, const swl_round_fusion* kv, swl_chain_plan** plan);
+/* One launch of the plan on `stream` (no allocation; launches of one plan
+ * must not overlap). */
+int swl_chain_launch(swl_chain_plan* plan, void* stream);
+/* Synchronises the device, returns the plan's status word (bit r: a
+ * device-side wait of round r gave up after its time limit, so that launch's
+ * results are not valid) and clears it. */
+int swl_chain_status(swl_chain_plan* plan, uint32_t* timed_out);
+/* Benchmark instrumentation: with trace non-NULL (device memory, grid x
+ * (2 + 3 * SWL_CHAIN_MAX_ROUNDS) uint64), every later launch stores per
+ * workgroup the 100 MHz real-time clock at its start, per round when the
+ * round's wait ended, when its LoRA expand rows were ready and when its
+ * part of the round was stored, and at its exit; NULL turns it off.
+ * swl_chain_grid: workgroups per launch. */
+int swl_chain_trace(swl_chain_plan* plan, uint64_t* trace);
+int swl_chain_grid(const swl_chain_plan* plan);
+/* Algorithmic HBM bytes of one launch (weights, distinct LoRA A and B, token
+ * rows in and out). */
+int64_t swl_chain_bytes(const swl_chain_plan* plan);
+int swl_chain_destroy(swl_chain_plan* plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,32 @@ class RoundFusion(ctypes.Structure):
     ]
 
 
+class ChainRound(ctypes.Structure):
+    """swl_chain_round (include/swl.h)."""
+    _fields_ = [
+        ("w", c_vp),
+        ("n", c_i64),
+        ("k", c_i64),
+        ("out_mode", ctypes.c_int32),
+        ("x", c_vp),
+        ("ldx", c_i64),
+        ("norm_weight", c_vp),
+        ("ss_in", c_vp),
+        ("ss_in_n", ctypes.c_int32),
+        ("ss_in_stride", ctypes.c_int32),
+        ("eps", c_f32),
+        ("y", c_vp),
+        ("ldy", c_i64),
+        ("res", c_vp),
+        ("ldres", c_i64),
+        ("ss_out", c_vp),
+        ("ss_out_stride", ctypes.c_int32),
+        ("lora", c_vp),
+        ("nblk", ctypes.c_int32),
+        ("blk_cols", c_i64 * 4),
+    ]
+
+
 class PoolStatus(ctypes.Structure):
     """Mirror of swl_pool_status (include/swl_runtime.h)."""
     _fields_ = [
@@ -118,6 +144,14 @@ _SIGS = {
     "swl_silu_mul_rows_bf16": (c_int, [P_vp, P_vp, c_i64, c_i64, c_vp]),
     "swl_paged_attention_rows_bf16": (c_int, [P_vp, P_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64,
                                               c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_f32, c_vp]),
+    "swl_chain_create": (c_int, [c_int, c_int, ctypes.POINTER(ChainRound), c_vp, c_int, ctypes.POINTER(RoundFusion),
+                                 ctypes.POINTER(c_vp)]),
+    "swl_chain_launch": (c_int, [c_vp, c_vp]),
+    "swl_chain_status": (c_int, [c_vp, ctypes.POINTER(ctypes.c_uint32)]),
+    "swl_chain_bytes": (c_i64, [c_vp]),
+    "swl_chain_trace": (c_int, [c_vp, c_vp]),
+    "swl_chain_grid": (c_int, [c_vp]),
+    "swl_chain_destroy": (c_int, [c_vp]),
 }
 
 _RUNTIME_SIGS = {}

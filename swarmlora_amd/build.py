@@ -25,6 +25,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 SOURCES = [
     "kernels.hip",
+    "chain.hip",
     "ipc_queue.cpp",
     "aggregator.cpp",
     "worker_slots.cpp",

@@ -124,11 +124,15 @@ class BatchedDecoder:
     whole-K rounds (w_layout 2: no K-slice partials) when their K allows
     (<= 4096): True for the LM head, "all" for every round, or a set /
     comma list of "qkv", "o", "gu", "down", "lm"; the others are K-sliced.
+    chain (packed step, at most 32 workers, rank-16 adapters): each layer's
+    O, Gate+Up and Down rounds and the next layer's QKV round run as one
+    persistent launch (ops.ChainPlan); layer 0's QKV round and the LM head
+    are whole-K rounds.
     """
 
     def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
                  first_ids: List[int], device, max_new: int = 64, kv_fill=None, fused: bool = True,
-                 packed: bool = True, whole_k: bool = True):
+                 packed: bool = True, whole_k: bool = True, chain: bool = False):
         self.shape = s = shape
         self.device = dev = torch.device(device)
         self.W = W = len(ctx_lens)
@@ -153,6 +157,13 @@ class BatchedDecoder:
         if not wk <= set(names):
             raise ValueError(f"whole_k: rounds must be among {names}")
         self.whole_k = wk if (self.packed and W <= 32) else set()
+        self.chain = bool(chain)
+        if self.chain:
+            if not self.packed or W > 32:
+                raise ValueError("chain: the packed fused step with at most 32 workers")
+            if any(ad is not None for ad in adapters) and shape.rank != 16:
+                raise ValueError("chain: adapters must have rank 16")
+            self.whole_k = set(names)
         if fused:
             self._init_fused(weights, adapters, ctx_lens, first_ids, kv_fill)
             return
@@ -351,6 +362,68 @@ class BatchedDecoder:
         self._lm_call = (ops._round_args(rows(self.h), rows(self.logits), one, self.lm_head, None, None, None, None),
                          lm_fz)
         self._scale = 1.0 / (s.head_dim ** 0.5)
+        if self.chain:
+            self._init_chain(has_lora, blk, lm_fz)
+
+    def _init_chain(self, has_lora, blk, lm_fz):
+        """Per layer one ops.ChainPlan: O (residual), Gate+Up (RMSNorm in,
+        SiLU*up), Down (residual, token rows streamed) and the next layer's
+        QKV (RMSNorm in, RoPE + KV append).  The residual stream rotates
+        through three buffers so that no round of a launch writes a buffer an
+        earlier round of it reads: layer l reads h[i], writes the O output to
+        h[i + 1] and the Down output to h[i + 2] (mod 3), and layer l + 1
+        starts from that."""
+        s, dev, W = self.shape, self.device, self.W
+        one = [1] * W
+        self.hbuf = [self.h] + [torch.zeros(W, s.hidden, dtype=BF16, device=dev) for _ in range(2)]
+        self.ss_o = torch.zeros(W, s.hidden // 16, dtype=torch.float32, device=dev)
+        self.ss_d = torch.zeros(W, s.hidden // 16, dtype=torch.float32, device=dev)
+        rows = lambda t: [t[w:w + 1] for w in range(W)]  # noqa: E731
+        tab = self.table if has_lora else None
+        self.chains = []
+        cur = 0
+        for li in range(s.layers):
+            lw, (in_norm, post_norm) = self.layers_w[li], self.norms[li]
+            mid, out = (cur + 1) % 3, (cur + 2) % 3
+            lora = (lambda g, l=li: self.seg_lora[l][g] if has_lora else None)
+            rounds = [
+                dict(w=lw["o"], out_mode=1, x=self.attn, y=self.hbuf[mid], res=self.hbuf[cur], ss_out=self.ss_o,
+                     lora=lora("o"), blk_cols=blk["o"]),
+                dict(w=lw["gu"], out_mode=2, x=self.hbuf[mid], y=self.act, norm_weight=post_norm, ss_in=self.ss_o,
+                     eps=s.eps, lora=lora("gu"), blk_cols=blk["gu"]),
+                dict(w=lw["down"], out_mode=1, x=self.act, y=self.hbuf[out], res=self.hbuf[mid], ss_out=self.ss_d,
+                     lora=lora("down"), blk_cols=blk["down"]),
+            ]
+            kv = None
+            if li + 1 < s.layers:
+                nl = li + 1
+                rounds.append(dict(w=self.layers_w[nl]["qkv"], out_mode=3, x=self.hbuf[out],
+                                   norm_weight=self.norms[nl][0], ss_in=self.ss_d, eps=s.eps, y=self.qkv,
+                                   lora=lora("qkv", nl), blk_cols=blk["qkv"]))
+                kv = ops.round_fusion(out_mode=3, k_cache=self.kv.key_caches[nl], v_cache=self.kv.value_caches[nl],
+                                      hq=s.heads, hkv=s.kv_heads, block_table=self.block_tables,
+                                      cache_seqlens=self.seqlens, positions=self.positions, cos_sin=self.cos_sin)
+            self.chains.append(ops.ChainPlan(W, rounds, table=tab, kv=kv))
+            cur = out
+        self._h_last = cur
+        # the LM head reads the last layer's output and its per-16-column sums
+        lm_fz = ops.round_fusion(norm_weight=self.final_norm, eps=s.eps, ss_in=self.ss_d, w_layout=2)
+        self._lm_call = (ops._round_args(rows(self.hbuf[cur]), rows(self.logits), one, self.lm_head, None, None,
+                                         None, None), lm_fz)
+
+    @property
+    def final_h(self) -> torch.Tensor:
+        """The residual stream after the last layer (what the final norm and
+        the LM head read): [W, hidden]."""
+        return self.hbuf[self._h_last] if self.chain else self.h
+
+    def chain_status(self) -> int:
+        """OR of the chain plans' status words (0: every device-side wait of
+        the launches since the last call completed in time)."""
+        st = 0
+        for c in getattr(self, "chains", []):
+            st |= c.status()
+        return st
 
     def _round_ex(self, call):
         args, fz = call
@@ -364,10 +437,14 @@ class BatchedDecoder:
         ops.rmsnorm_rows(self.h, self.norms[0][0], s.eps, self.rows_x0)
         for li in range(s.layers):
             qkv, o, gu, down = self._calls[li]
-            self._round_ex(qkv)
+            if li == 0 or not self.chain:
+                self._round_ex(qkv)
             ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
                                      self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
                                      self.seqlens, None, None, self._scale, rope=2)
+            if self.chain:
+                self.chains[li].launch()
+                continue
             self._round_ex(o)
             self._round_ex(gu)
             self._round_ex(down)
@@ -441,6 +518,9 @@ class BatchedDecoder:
 
     def close(self):
         self.graph = None
+        for c in getattr(self, "chains", []):
+            c.close()
+        self.chains = []
         if self.fused:
             return
         for sid, wid in zip(self.slot_ids, self.worker_ids):

@@ -333,6 +333,121 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
     _lib.check(fn(*args, ctypes.byref(fusion) if fusion is not None else None, _stream()))
 
 
+def _rows2d(t: torch.Tensor, name: str, ntok: int, width: int, dtype=BF16):
+    """A 2-D view [>= ntok, >= width] with unit column stride: its row stride."""
+    _need(t, name, dtype)
+    if t.dim() != 2 or t.stride(1) != 1 or t.shape[0] < ntok or t.shape[1] < width:
+        raise ValueError(f"{name} must be a 2-D [{ntok}, {width}] view with unit column stride")
+    return t.stride(0)
+
+
+class ChainPlan:
+    """Several dependent decode rounds in one persistent launch
+    (swl_chain_create / swl_chain_launch): e.g. a layer's O, Gate+Up and Down
+    rounds and the next layer's fused QKV round.  rounds: dicts with
+      w (PackedWeight packed with pair offset n / 2 for out_mode 2, 64 for
+      out_mode 3, else 8), out_mode (1, 2 or 3), x [ntok, k] rows,
+      y output rows, res (out_mode 1: y = res + out), ss_out (out_mode 1,
+      fp32 [ntok, n / 16]), norm_weight + ss_in (+ eps) for RMSNorm on the way
+      in, lora (per-token table entries, -1 none) + blk_cols.
+    table: the LoraTable the entries index; kv: a RoundFusion carrying the KV
+    fields for out_mode 3.  The plan keeps every tensor it points to alive."""
+
+    def __init__(self, ntok: int, rounds, table: Optional["LoraTable"] = None, kv: Optional[RoundFusion] = None):
+        lib = _lib.load()
+        n = len(rounds)
+        arr = (_lib.ChainRound * n)()
+        self._keep = [kv, table]
+        host_tab, n_entries = ctypes.c_void_p(0), 0
+        if table is not None:
+            host_tab = ctypes.cast(table.host_table(), ctypes.c_void_p)
+            n_entries = len(table)
+            self._keep.append(table.device_table())
+        for i, r in enumerate(rounds):
+            c = arr[i]
+            w = r["w"]
+            if not isinstance(w, PackedWeight):
+                raise TypeError("chain rounds need a PackedWeight")
+            mode = int(r["out_mode"])
+            want = w.n // 2 if mode == 2 else 64 if mode == 3 else 8
+            if w.pair_off != want:
+                raise ValueError(f"chain round {i}: out_mode {mode} needs pair_off {want}, the weight has {w.pair_off}")
+            c.w, c.n, c.k, c.out_mode = w.data_ptr(), w.n, w.k, mode
+            c.x = r["x"].data_ptr()
+            c.ldx = _rows2d(r["x"], "x", ntok, w.k)
+            c.y = r["y"].data_ptr()
+            c.ldy = _rows2d(r["y"], "y", ntok, w.n // 2 if mode == 2 else w.n)
+            keep = [w, r["x"], r["y"]]
+            if r.get("norm_weight") is not None:
+                _need(r["norm_weight"], "norm_weight")
+                ss = r["ss_in"]
+                c.ss_in_stride = _rows2d(ss, "ss_in", ntok, 1, torch.float32)
+                c.norm_weight, c.ss_in, c.ss_in_n = r["norm_weight"].data_ptr(), ss.data_ptr(), ss.shape[1]
+                c.eps = float(r.get("eps", 1e-5))
+                keep += [r["norm_weight"], ss]
+            if mode == 1:
+                c.res = r["res"].data_ptr()
+                c.ldres = _rows2d(r["res"], "res", ntok, w.n)
+                keep.append(r["res"])
+                if r.get("ss_out") is not None:
+                    c.ss_out_stride = _rows2d(r["ss_out"], "ss_out", ntok, w.n // 16, torch.float32)
+                    c.ss_out = r["ss_out"].data_ptr()
+                    keep.append(r["ss_out"])
+            if r.get("lora") is not None:
+                if table is None:
+                    raise ValueError("LoRA entries need the table")
+                lo = _i32_array(r["lora"])
+                if len(r["lora"]) < ntok:
+                    raise ValueError("one LoRA entry per token")
+                c.lora = ctypes.cast(lo, ctypes.c_void_p)
+                blk = list(r["blk_cols"])
+                c.nblk = len(blk)
+                for b, v in enumerate(blk):
+                    c.blk_cols[b] = int(v)
+                keep.append(lo)
+            self._keep.append(keep)
+        h = ctypes.c_void_p(0)
+        _lib.check(lib.swl_chain_create(int(ntok), n, arr, host_tab, n_entries,
+                                        ctypes.byref(kv) if kv is not None else None, ctypes.byref(h)))
+        self._h = h
+        self.bytes = int(lib.swl_chain_bytes(h))
+
+    def launch(self):
+        _lib.check(_lib.load().swl_chain_launch(self._h, _stream()))
+
+    def trace(self, buf: Optional[torch.Tensor]):
+        """Attach (int64 [grid, 2 + 3 * 4] device tensor) or detach (None) the
+        per-workgroup timeline of later launches (swl_chain_trace)."""
+        if buf is not None:
+            _need(buf, "trace", torch.int64)
+            if buf.numel() < self.grid * 14 or not buf.is_contiguous():
+                raise ValueError("trace needs grid x 14 int64 entries")
+        self._trace = buf
+        _lib.check(_lib.load().swl_chain_trace(self._h, _ptr(buf)))
+
+    @property
+    def grid(self) -> int:
+        return int(_lib.load().swl_chain_grid(self._h))
+
+    def status(self) -> int:
+        """Synchronises; bit r set: a device-side wait of round r gave up (the
+        launch's results are not valid).  Clears the word."""
+        v = ctypes.c_uint32(0)
+        _lib.check(_lib.load().swl_chain_status(self._h, ctypes.byref(v)))
+        return int(v.value)
+
+    def close(self):
+        if self._h:
+            _lib.load().swl_chain_destroy(self._h)
+            self._h = ctypes.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def lora_segmented(x: torch.Tensor, seg_rows: Sequence[int], seg_lora: Sequence[int], table: LoraTable,
                    blk_cols: Sequence[int], y: torch.Tensor, add: bool = False):
     """Segmented LoRA delta of the packed rows x [T, k] (swl_lora_segmented_bf16):

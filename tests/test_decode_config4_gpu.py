@@ -48,7 +48,8 @@ def _contexts():
     return ctx
 
 
-def test_config4_shape_decode_steps_eager_then_graph(dev):
+@pytest.mark.parametrize("chain", [False, True])
+def test_config4_shape_decode_steps_eager_then_graph(dev, chain):
     from swarmlora_amd.decode import BatchedDecoder, DecodeShape, synthetic_adapter, synthetic_weights
     s = DecodeShape(layers=2)
     ctx = _contexts()
@@ -71,7 +72,8 @@ def test_config4_shape_decode_steps_eager_then_graph(dev):
         vc.copy_(torch.randn(vc.shape, generator=kv_gen, device=dev, dtype=torch.bfloat16))
         pages[li] = (kc.cpu(), vc.cpu())
 
-    dec = BatchedDecoder(s, wd, ad_dev, ctx, first, dev, max_new=6, kv_fill=kv_fill, fused=True, packed=True)
+    dec = BatchedDecoder(s, wd, ad_dev, ctx, first, dev, max_new=6, kv_fill=kv_fill, fused=True, packed=True,
+                         chain=chain)
     del wd, ad_dev
     kc = [pages[li][0] for li in range(s.layers)]
     vc = [pages[li][1] for li in range(s.layers)]
@@ -95,7 +97,7 @@ def test_config4_shape_decode_steps_eager_then_graph(dev):
             torch.cuda.synchronize()
             hn, lg = ref.decode_step(s, wts, ads, kc, vc, bt, seq, ids, cs)
             hn32, lg32 = ref.decode_step(s, wts32, ads32, kc32, vc32, bt, seq, ids, cs)
-            got_h = ref.rms_norm(dec.h.cpu(), wts["final_norm"], s.eps)
+            got_h = ref.rms_norm(dec.final_h.cpu(), wts["final_norm"], s.eps)
             got_l = dec.logits.cpu()
             for what, got, want, want32 in (("final hidden", got_h, hn, hn32), ("logits", got_l, lg, lg32)):
                 e_gb, e_gf, e_bf = rel_err(got, want), rel_err(got, want32), rel_err(want, want32)
@@ -109,6 +111,7 @@ def test_config4_shape_decode_steps_eager_then_graph(dev):
                 assert int(nxt[w]) == int(glf[w].argmax()), f"step {step} worker {w}: argmax"
                 assert lg32[w, nxt[w]] >= lg32[w].max() - TOL_BF16 * lg32[w].abs().max(), f"step {step} worker {w}"
             assert dec.seqlens.cpu().tolist() == (seq + 1).tolist()
+        assert dec.chain_status() == 0, "a device-side wait of a chain launch ran out"
         # KV pages: every entry the steps did not append is unchanged (bit for bit); the appended k
         # (roped) and v rows are within 1e-2 in layer 0 (one QKV round from identical inputs) and
         # within the two-evaluation bound in later layers (inputs carry the composed drift)

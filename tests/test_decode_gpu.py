@@ -62,7 +62,7 @@ def _check_step(dec, shape, wts, ads, kc, vc, cs, bt, step):
     torch.cuda.synchronize()
     hn, lg = ref.decode_step(shape, wts, ads, kc, vc, bt, seq, ids, cs)
     if dec.fused:  # the final norm runs inside the LM-head round: check the residual stream through it
-        got_h = ref.rms_norm(dec.h.cpu(), wts["final_norm"], shape.eps)
+        got_h = ref.rms_norm(dec.final_h.cpu(), wts["final_norm"], shape.eps)
     else:
         got_h = dec.lm_in.cpu()
     got_l = dec.logits.cpu()
