@@ -181,6 +181,11 @@ typedef struct swl_round_fusion {
    * squares per row (ss_out_stride >= n / 16).  Whole-K rounds on one GPU
    * share a set of counters and must be ordered (one stream). */
   int32_t w_layout;
+  /* a_layout 1: the stacked lora_A of every adapter entry the round uses is
+   * in the fragment-tile layout of swl_pack_weight_bf16 (its nblk * rank rows
+   * padded to 16 with zeros), streamed like the weight tiles; 0: row-major
+   * [nblk * rank, k].  Decode-shaped rounds with w_layout 0 or 1 only. */
+  int32_t a_layout;
 } swl_round_fusion;
 
 /* Segmented LoRA delta of a packed batch x [T, k] (segment i = rows

@@ -67,6 +67,7 @@ class RoundFusion(ctypes.Structure):
         ("cos_sin", c_vp),
         ("max_pos", c_i64),
         ("w_layout", ctypes.c_int32),
+        ("a_layout", ctypes.c_int32),
     ]
 
 

@@ -56,6 +56,9 @@ constexpr int kStoreSys = 1 | 16;
 __device__ __forceinline__ u32x4 ldg16(const void* p) {
   return *(const __attribute__((address_space(1))) u32x4*)(p);
 }
+__device__ __forceinline__ float ldg_f32(const float* p) {
+  return *(const __attribute__((address_space(1))) float*)(p);
+}
 
 // Row of W held by row rr (0..15) of packed tile `tile` when tiles pair the
 // rows j and j + off (off a multiple of 8): tile rows 0..7 are eight

@@ -263,6 +263,7 @@ struct SplitArgs {
   int64_t N, K;
   int32_t ntok;
   int32_t w_packed;
+  int32_t a_packed;                   // the adapter groups' stacked A are fragment tiles too
   int32_t n_ks, n_workers;            // grid = n_ks x n_workers workgroups
   int32_t total_steps, ks_steps;      // k-steps of 32 in K; max per K-slice
   int32_t n_wtiles, n_tiles;          // W row tiles (ceil(N / 16)); all tiles incl. adapter rows
@@ -463,7 +464,9 @@ __global__ __launch_bounds__(256) void lora_expand_kernel(ExpandArgs a) {
 // Row pointer (this lane's row, at the K-slice start) of row tile `tile`: a
 // tile of W, or a tile of one adapter group's stacked A (rows past the end of
 // either re-read its last row; their results are never stored).  grp: -1 for
-// W, the group for adapter rows.
+// W, the group for adapter rows.  Fragment tiles (W with w_packed, A with
+// a_packed): this lane's 16 bytes of the slice's first k-step block; rows
+// past the end are zero rows of the tile.
 __device__ __forceinline__ const bf16* tile_rows(const SplitArgs& a, int tile, int lane, int64_t kbeg, int& grp,
                                                  int& qrow0) {
   const bf16* row;
@@ -481,8 +484,9 @@ __device__ __forceinline__ const bf16* tile_rows(const SplitArgs& a, int tile, i
     int g = 0;
     while (g + 1 < a.ngroups && a.g_tile0[g + 1] <= lt) ++g;
     qrow0 = (lt - a.g_tile0[g]) * 16;
-    row = a.g_a[g] + (int64_t)min(qrow0 + (lane & 15), a.g_arows[g] - 1) * a.K;
     grp = g;
+    if (a.a_packed) return a.g_a[g] + ((int64_t)(lt - a.g_tile0[g]) * a.total_steps + (kbeg >> 5)) * 512 + 8 * lane;
+    row = a.g_a[g] + (int64_t)min(qrow0 + (lane & 15), a.g_arows[g] - 1) * a.K;
   }
   return row + kbeg + 8 * (lane >> 4);
 }
@@ -505,12 +509,37 @@ __global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(Spli
   const int64_t kbeg = (int64_t)st0 * 32;
   const int tstride = a.n_workers * WAVES;
 
-  int tile = wk * WAVES + wv;
+  // tiles wk + n_workers * (wv + WAVES * m): the slice's tiles dealt over
+  // its workers first, then over each worker's waves
+  int tile = wk + a.n_workers * wv;
   int grp = -1, qrow0 = 0;
   const bf16* wp = nullptr;
   u32x4 w[kKDepth];
   // fragment-tile W: k-steps 512 elements apart (uniform per tile)
-  auto packed = [&](int t) { return a.w_packed && t < a.n_wtiles; };
+  auto packed = [&](int t) { return t < a.n_wtiles ? a.w_packed != 0 : a.a_packed != 0; };
+
+  // RMSNorm inputs first, so they return ahead of the weight stream: the
+  // slice of gamma (512 elements per DMA block, clamped to the slice) into
+  // LDS past the activation blocks, and each token row's partial sums of
+  // squares, thread (token t / 16, partial t % 16 + 16 i) one load each for
+  // up to 16 partials per row
+  char* gs = reinterpret_cast<char*>(xs) + a.ks_steps * TT * 1024;
+  float* rs = reinterpret_cast<float*>(gs + (a.ks_steps * 32 + 511) / 512 * 1024);
+  constexpr int kTokPass = WAVES * 4;                          // tokens per pass (16 threads each)
+  constexpr int kPass = (TT * 16 + kTokPass - 1) / kTokPass;   // passes over the token rows
+  const int tk16 = threadIdx.x >> 4, j16 = threadIdx.x & 15;
+  float ssp[kPass];
+  if (a.gamma) {
+    for (int i = wv; i < (npad * 32 + 511) / 512; i += WAVES) {
+      const int64_t k = min(kbeg + (int64_t)i * 512 + 8 * lane, kbeg + (int64_t)nst * 32 - 8);
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(a.gamma + k), (lds_ptr)(gs + i * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+      const int tk = tk16 + p * kTokPass;
+      ssp[p] = (tk < a.ntok && j16 < a.ss_n) ? ldg_f32(a.ss + (int64_t)tk * a.ss_stride + j16) : 0.f;
+    }
+  }
   if (tile < a.n_tiles) {
     wp = tile_rows(a, tile, lane, kbeg, grp, qrow0);
     if (packed(tile))
@@ -533,28 +562,23 @@ __global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(Spli
   // LDS-DMA loads (global_load_lds_dwordx4), no VGPR round trip
   for (int i = wv; i < nblk; i += WAVES)
     __builtin_amdgcn_global_load_lds((gbl_ptr)xsrc(i), (lds_ptr)(reinterpret_cast<char*>(xs) + i * 1024), 16, 0, 0);
-  // Residual-stream rows are RMS-normalised in place after staging: the
-  // slice of gamma (512 elements per DMA block, clamped to the slice) and
-  // each token row's r = rsqrt(sum of its partial sums of squares / K + eps)
-  // go to LDS past the activation blocks; after the barrier every wave
-  // rescales the blocks it staged: h * r rounded to bf16, times gamma,
-  // rounded again, as LlamaRMSNorm does.
-  char* gs = reinterpret_cast<char*>(xs) + a.ks_steps * TT * 1024;
-  float* rs = reinterpret_cast<float*>(gs + (a.ks_steps * 32 + 511) / 512 * 1024);
+  // Residual-stream rows are RMS-normalised in place after staging: each
+  // token row's r = rsqrt(sum of its partial sums of squares / K + eps) goes
+  // to LDS next to gamma; after the barrier every wave rescales the blocks it
+  // staged: h * r rounded to bf16, times gamma, rounded again, as
+  // LlamaRMSNorm does.  Rows with more than 16 partials add the rest here.
   if (a.gamma) {
-    for (int i = wv; i < (npad * 32 + 511) / 512; i += WAVES) {
-      const int64_t k = min(kbeg + (int64_t)i * 512 + 8 * lane, kbeg + (int64_t)nst * 32 - 8);
-      __builtin_amdgcn_global_load_lds((gbl_ptr)(a.gamma + k), (lds_ptr)(gs + i * 1024), 16, 0, 0);
-    }
-    if (threadIdx.x < 64) {
-      const int tk = threadIdx.x;
-      float r = 0.f;
-      if (tk < a.ntok) {
-        float ss = 0.f;
-        for (int j = 0; j < a.ss_n; ++j) ss += a.ss[(int64_t)tk * a.ss_stride + j];
-        r = rsqrtf(ss / (float)a.K + a.eps);
-      }
-      rs[tk] = r;
+#pragma unroll
+    for (int p = 0; p < kPass; ++p) {
+      const int tk = tk16 + p * kTokPass;
+      float v = ssp[p];
+      if (tk < a.ntok)
+        for (int j = j16 + 16; j < a.ss_n; j += 16) v += ldg_f32(a.ss + (int64_t)tk * a.ss_stride + j);
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      v += __shfl_xor(v, 8, 64);
+      if (j16 == 0 && tk < TT * 16) rs[tk] = tk < a.ntok ? rsqrtf(v / (float)a.K + a.eps) : 0.f;
     }
   }
   __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's LDS-DMA (and W) loads have landed
@@ -3127,6 +3151,8 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   if (fz) {
     SWL_CHECK(mode >= 0 && mode <= 3, SWL_ERR_INVALID, "round fusion: out_mode must be 0..3");
     SWL_CHECK(fz->w_layout >= 0 && fz->w_layout <= 2, SWL_ERR_INVALID, "round fusion: w_layout must be 0, 1 or 2");
+    SWL_CHECK(fz->a_layout == 0 || (fz->a_layout == 1 && fz->w_layout != 2), SWL_ERR_INVALID,
+              "round fusion: a_layout must be 0, or 1 (fragment-tile lora_A) with w_layout 0 or 1");
     if (fz->norm_weight)
       SWL_CHECK(fz->ss_in && fz->ss_in_n >= 1 && fz->ss_in_stride >= fz->ss_in_n, SWL_ERR_INVALID,
                 "round fusion: norm_weight needs ss_in with ss_in_n >= 1 partial sums per row");
@@ -3150,6 +3176,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   SplitArgs a{};
   a.w = w;
   a.w_packed = (fz && fz->w_layout == 1) ? 1 : 0;
+  a.a_packed = (fz && fz->a_layout == 1) ? 1 : 0;
   a.N = N;
   a.K = K;
   a.ntok = ntok;
@@ -3194,11 +3221,12 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const int64_t slots = (int64_t)cu_count() * (TT <= 2 ? tu.wg_per_cu : std::min(tu.wg_per_cu, 16 / waves));
   // K-slices: a power of two (slice starts on aligned byte offsets stream
   // best from HBM), the smallest whose slices hold at most slice_steps
-  // k-steps and whose workers fill at least half the resident workgroup
-  // slots (longer slices write fewer fp32 partials but stage more activation
-  // rows per workgroup and leave fewer workers; 16 steps measured best), then
-  // as many more as the LDS cap on the staged activation slice (padded steps
-  // x TT x 1 KiB) requires.
+  // k-steps (longer slices write fewer fp32 partials but stage more
+  // activation rows per workgroup and leave fewer workgroups per CU; 16
+  // steps measured best at 28 rows: O round 8 slices 19.9 us with its
+  // epilogue, 16 slices 21.5, 4 slices 21.9), then as many more as the LDS
+  // cap on the staged activation slice (padded steps x TT x 1 KiB) requires.
+  // Every slice gets all the workers the resident slots allow.
   // When the row tiles alone outnumber the slots (the LM head), slices of up
   // to long_slice steps, by default the longest the 160 KiB of LDS holds:
   // fewer fp32 partials, and the one workgroup per CU the staged slice
@@ -3217,9 +3245,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   if (tu.nks > 0) {
     n_ks = tu.nks;
   } else {
-    while (n_ks < total_steps &&
-           ((total_steps + n_ks - 1) / n_ks > slice_cap || 2 * n_ks * tile_groups < slots))
-      n_ks *= 2;
+    while (n_ks < total_steps && (total_steps + n_ks - 1) / n_ks > slice_cap) n_ks *= 2;
   }
   while (n_ks < total_steps && lds_of(n_ks) > lds_cap) n_ks *= 2;
   n_ks = std::min<int64_t>(n_ks, total_steps);
@@ -3230,7 +3256,13 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   if (a.gamma) lds += (size_t)(a.ks_steps * 32 + 511) / 512 * 1024 + 64 * sizeof(float);
   SWL_CHECK(lds <= 160 * 1024, SWL_ERR_INVALID, "round: staged activation slice exceeds LDS");
   const int64_t res_slots = std::min<int64_t>(slots, (int64_t)cu_count() * std::max<int64_t>(1, (160 * 1024) / lds));
-  a.n_workers = (int)std::max<int64_t>(1, std::min<int64_t>(tile_groups, res_slots / n_ks));
+  // workers per K-slice: every resident slot (grid = slots per CU x CUs,
+  // the same number of workgroups on every CU), at most one per row tile.
+  // The kernel deals a slice's tiles round-robin over its workers first, so
+  // workgroups differ by at most one tile and every CU streams the same
+  // bytes: a CU's share of HBM bandwidth is what sets how long its
+  // workgroups run (measured per CU: end times follow the CU's bytes)
+  a.n_workers = (int)std::max<int64_t>(1, std::min<int64_t>(a.n_tiles, res_slots / n_ks));
 
   const size_t part_bytes = sizeof(float) * (size_t)a.n_ks * ntok * N;
   SWL_CHECK(part_bytes < ((size_t)1 << 31), SWL_ERR_INVALID, "round: K-slice partials exceed 2 GiB");
@@ -4049,7 +4081,7 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
   if (rc0) return rc0;
 
   const int u_ld = ((max_r * std::max(nblk, 1) + 15) / 16) * 16;  // A rows padded to 16-row tiles
-  const bool fused = fz && (fz->norm_weight || fz->out_mode != 0 || fz->w_layout != 0);
+  const bool fused = fz && (fz->norm_weight || fz->out_mode != 0 || fz->w_layout != 0 || fz->a_layout != 0);
   const int64_t out_cols = (fz && fz->out_mode == 2) ? N / 2 : N;
   if (fz && fz->out_mode == 3)
     for (int i = 0; i < n_seg; ++i)

@@ -291,7 +291,11 @@ class BatchedDecoder:
         self.lm_head = keep(weights["lm_head"].to(dev).contiguous(), "lm")
         self.final_norm = weights["final_norm"].to(dev).contiguous()
 
-        # adapters: one table entry per (worker, layer, fused projection)
+        # adapters: one table entry per (worker, layer, fused projection);
+        # the K-sliced rounds of the packed step stream the stacked lora_A as
+        # fragment tiles like their weights (row-major A rows, 64-byte pieces
+        # of 16 rows per load, were the last waves of the QKV and O rounds)
+        self.a_packed = {g: self.packed and not self.chain and not self.wk[g] for g in ("qkv", "o", "gu", "down")}
         self.table = ops.LoraTable(dev)
         groups = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")), ("down", ("down",)))
         self.seg_lora = [{g: [-1] * W for g, _ in groups} for _ in range(s.layers)]
@@ -302,6 +306,8 @@ class BatchedDecoder:
                 for g, projs in groups:
                     A = torch.cat([ad[li][p][0].to(dev) for p in projs], 0).contiguous()
                     Bs = [ad[li][p][1].to(dev).contiguous() for p in projs]
+                    if self.a_packed[g]:
+                        A = ops.pack_weight(A)
                     self.seg_lora[li][g][w] = self.table.add(A, Bs, s.rank, s.scale)
         has_lora = any(ad is not None for ad in adapters)
         blk = {"qkv": [s.hidden, s.kv_heads * s.head_dim, s.kv_heads * s.head_dim], "o": [s.hidden],
@@ -339,16 +345,19 @@ class BatchedDecoder:
                       block_table=self.block_tables, cache_seqlens=self.seqlens, positions=self.positions,
                       cos_sin=self.cos_sin)
             wl = {g: (2 if self.wk[g] else 1) if self.packed else 0 for g in self.wk}
+            al = {g: 1 if has_lora and self.a_packed[g] else 0 for g in self.a_packed}
             plan = (
                 ("qkv", rows(self.x0) if li == 0 else rows(self.h), rows(self.qkv),
-                 ops.round_fusion(out_mode=3, w_layout=wl["qkv"], **kv) if li == 0 else
+                 ops.round_fusion(out_mode=3, w_layout=wl["qkv"], a_layout=al["qkv"], **kv) if li == 0 else
                  ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, out_mode=3, w_layout=wl["qkv"],
-                                  **kv)),
-                ("o", rows(self.attn), rows(self.h), ops.round_fusion(out_mode=1, ss_out=self.ss_o, w_layout=wl["o"])),
+                                  a_layout=al["qkv"], **kv)),
+                ("o", rows(self.attn), rows(self.h),
+                 ops.round_fusion(out_mode=1, ss_out=self.ss_o, w_layout=wl["o"], a_layout=al["o"])),
                 ("gu", rows(self.h), rows(self.act),
-                 ops.round_fusion(norm_weight=post_norm, eps=s.eps, ss_in=self.ss_o, out_mode=2, w_layout=wl["gu"])),
+                 ops.round_fusion(norm_weight=post_norm, eps=s.eps, ss_in=self.ss_o, out_mode=2, w_layout=wl["gu"],
+                                  a_layout=al["gu"])),
                 ("down", rows(self.act), rows(self.h),
-                 ops.round_fusion(out_mode=1, ss_out=self.ss_d, w_layout=wl["down"])),
+                 ops.round_fusion(out_mode=1, ss_out=self.ss_d, w_layout=wl["down"], a_layout=al["down"])),
             )
             layer_calls = []
             for g, xin, yout, fz in plan:

@@ -118,14 +118,22 @@ class LoraTable:
     def __init__(self, device):
         self.device = torch.device(device)
         self._entries: List[LoraEntry] = []
+        self._packed: List[bool] = []
         self._keep = []
         self._dev = None
 
-    def add(self, a: torch.Tensor, bs: Sequence[torch.Tensor], rank: int, scale: float) -> int:
-        """a: bf16 [nblk*rank, k] (stacked lora_A); bs[j]: bf16 [blk_cols[j], rank]."""
-        _need(a, "lora a")
-        if not a.is_contiguous() or a.shape[0] != rank * len(bs):
-            raise ValueError("lora a must be contiguous [nblk * rank, k]")
+    def add(self, a, bs: Sequence[torch.Tensor], rank: int, scale: float) -> int:
+        """a: bf16 [nblk*rank, k] (stacked lora_A), or its PackedWeight
+        (fragment tiles: the K-sliced decode rounds stream it like the
+        weights, round fusion a_layout 1); bs[j]: bf16 [blk_cols[j], rank]."""
+        packed = isinstance(a, PackedWeight)
+        if packed:
+            if a.pair_off != 8 or a.n != rank * len(bs):
+                raise ValueError("packed lora a must be a plain PackedWeight of [nblk * rank, k]")
+        else:
+            _need(a, "lora a")
+            if not a.is_contiguous() or a.shape[0] != rank * len(bs):
+                raise ValueError("lora a must be contiguous [nblk * rank, k]")
         if len(bs) > SWL_MAX_LORA_BLOCKS:
             raise ValueError("too many column blocks")
         e = LoraEntry()
@@ -138,9 +146,19 @@ class LoraTable:
         e.rank = int(rank)
         e.scale = float(scale)
         self._entries.append(e)
+        self._packed.append(packed)
         self._keep.extend([a, *bs])
         self._dev = None
         return len(self._entries) - 1
+
+    def a_layout(self, ids: Sequence[int]) -> int:
+        """Layout of lora_A over the entries `ids` (negative: none): 1 if
+        they are fragment tiles, 0 if row-major; mixed layouts are refused
+        (a round streams one kind)."""
+        kinds = {self._packed[i] for i in ids if i >= 0}
+        if len(kinds) > 1:
+            raise ValueError("a round's adapters must all have row-major or all fragment-tile lora_A")
+        return 1 if kinds == {True} else 0
 
     def _sync(self):
         if self._dev is None:
@@ -238,7 +256,7 @@ def round_fused(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor],
                 seg_lora: Optional[Sequence[int]] = None, table: Optional[LoraTable] = None,
                 blk_cols: Optional[Sequence[int]] = None):
     """One gather -> GEMM -> (+LoRA) -> scatter round over slot buffers."""
-    if isinstance(w, PackedWeight):
+    if isinstance(w, PackedWeight) or (seg_lora is not None and table is not None and table.a_layout(seg_lora)):
         return round_ex(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols)
     args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols)
     _lib.check(_lib.load().swl_round_bf16(*args, _stream()))
@@ -252,7 +270,7 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
                  k_cache: Optional[torch.Tensor] = None, v_cache: Optional[torch.Tensor] = None, hq: int = 0,
                  hkv: int = 0, block_table: Optional[torch.Tensor] = None,
                  cache_seqlens: Optional[torch.Tensor] = None, positions: Optional[torch.Tensor] = None,
-                 cos_sin: Optional[torch.Tensor] = None, w_layout: int = 0) -> RoundFusion:
+                 cos_sin: Optional[torch.Tensor] = None, w_layout: int = 0, a_layout: int = 0) -> RoundFusion:
     """swl_round_fusion for round_ex (include/swl.h documents each mode).
     ss_in / ss_out: fp32 [ntok, n_partial] (n_partial = ceil(n / 256) of the
     producing round); the record keeps the tensors it points to alive."""
@@ -261,6 +279,9 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
     if w_layout not in (0, 1, 2):
         raise ValueError("w_layout must be 0 (row-major), 1 (fragment tiles) or 2 (whole-K round, paired tiles)")
     f.w_layout = w_layout
+    if a_layout not in (0, 1) or (a_layout == 1 and w_layout == 2):
+        raise ValueError("a_layout must be 0 (row-major lora_A) or 1 (fragment tiles, w_layout 0 or 1)")
+    f.a_layout = a_layout
     if norm_weight is not None:
         _need(norm_weight, "norm_weight")
         _need(ss_in, "ss_in", torch.float32)
@@ -327,6 +348,14 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
                                  f"the weight has {w.pair_off}")
     elif fusion is not None and fusion.w_layout != 0:
         raise ValueError("fusion.w_layout 1 or 2 needs a PackedWeight")
+    if seg_lora is not None and table is not None and table.a_layout(seg_lora) == 1:
+        if fusion is None:
+            fusion = RoundFusion()
+        if fusion.w_layout == 2:
+            raise ValueError("fragment-tile lora_A needs a K-sliced round (w_layout 0 or 1)")
+        fusion.a_layout = 1
+    elif fusion is not None and fusion.a_layout != 0:
+        raise ValueError("fusion.a_layout 1 needs adapters added with a PackedWeight lora_A")
     args = _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols,
                        out_div=2 if fusion is not None and fusion.out_mode == 2 else 1)
     fn = _lib.load().swl_round_ex_noalloc_bf16 if noalloc else _lib.load().swl_round_ex_bf16
@@ -360,6 +389,8 @@ class ChainPlan:
         self._keep = [kv, table]
         host_tab, n_entries = ctypes.c_void_p(0), 0
         if table is not None:
+            if table.a_layout(range(len(table))):
+                raise ValueError("chain rounds read row-major lora_A (add the adapters with a plain tensor)")
             host_tab = ctypes.cast(table.host_table(), ctypes.c_void_p)
             n_entries = len(table)
             self._keep.append(table.device_table())
@@ -464,6 +495,8 @@ def lora_segmented(x: torch.Tensor, seg_rows: Sequence[int], seg_lora: Sequence[
         raise ValueError("x and y need sum(seg_rows) rows")
     if any(i >= len(table) for i in seg_lora):
         raise ValueError("seg_lora index out of range")
+    if table.a_layout(seg_lora):
+        raise ValueError("the segmented LoRA delta reads row-major lora_A")
     _lib.check(_lib.load().swl_lora_segmented_bf16(
         _ptr(x), x.shape[1], len(seg_rows), _i64_array(seg_rows), _i32_array(seg_lora), _ptr(table.device_table()),
         ctypes.cast(table.host_table(), ctypes.c_void_p), len(blk_cols), _i64_array(blk_cols), _ptr(y), y.shape[1],

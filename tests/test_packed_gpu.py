@@ -90,6 +90,85 @@ def test_packed_round_matches_row_major_bitwise(dev, T, in_dim, out_dims, lora):
         assert_close(got_pk[i].cpu(), want[i], what=f"token {i}")
 
 
+def _table_packed_a(dev, in_dim, out_dims, ranks, scale=2.0):
+    """Two tables with the same adapters: row-major lora_A and fragment-tile
+    lora_A (a_layout 1)."""
+    ops = _ops()
+    t_rm, t_pk, ads = ops.LoraTable(dev), ops.LoraTable(dev), []
+    for i, r in enumerate(ranks):
+        blocks = [(randn((r, in_dim), 7000 + 10 * i + 2 * j, std=0.02),
+                   randn((od, r), 7000 + 10 * i + 2 * j + 1, std=0.02)) for j, od in enumerate(out_dims)]
+        A = torch.cat([a for a, _ in blocks], 0).contiguous().to(dev)
+        Bs = [b.contiguous().to(dev) for _, b in blocks]
+        t_rm.add(A, Bs, r, scale)
+        t_pk.add(ops.pack_weight(A), Bs, r, scale)
+        ads.append([(a, b, scale) for a, b in blocks])
+    return t_rm, t_pk, ads
+
+
+@pytest.mark.parametrize("T,in_dim,out_dims,ranks,ids", [
+    (28, 4096, [4096, 1024, 1024], [16] * 28, list(range(28))),     # config-4 QKV: own adapter per token
+    (28, 4096, [4096], [16] * 28, list(range(28))),                 # O
+    (28, 4096, [14336, 14336], [16] * 28, list(range(28))),         # Gate+Up
+    (28, 14336, [4096], [16] * 28, list(range(28))),                # Down (long K)
+    (5, 256, [200], [8, 16], [1, 0, 1, -1, 0]),                     # rank 8 (padded tile), a token without one
+    (64, 512, [96, 96], [16, 8, 16], [i % 3 for i in range(64)]),  # four token tiles, shared adapters
+])
+def test_packed_lora_a_matches_row_major_bitwise(dev, T, in_dim, out_dims, ranks, ids):
+    """Rounds whose adapters' stacked lora_A are fragment tiles (a_layout 1)
+    equal the same rounds over row-major lora_A bit for bit (the same
+    products in the same order), with row-major and with packed weights, and
+    match the oracle."""
+    ops = _ops()
+    n = sum(out_dims)
+    w = randn((n, in_dim), SEED_W + 3, std=0.02)
+    xs = [randn((1, in_dim), SEED_X * 50 + i) for i in range(T)]
+    t_rm, t_pk, ads = _table_packed_a(dev, in_dim, out_dims, ranks)
+    wd = w.to(dev)
+    pw = ops.pack_weight(wd)
+    xd = [x.to(dev) for x in xs]
+    outs = {}
+    for name, wt, tab in (("rm", pw, t_rm), ("pk", pw, t_pk), ("pk_rowmajor_w", wd, t_pk)):
+        y = [torch.zeros(1, n, dtype=BF16, device=dev) for _ in range(T)]
+        ops.round_ex(xd, y, [1] * T, wt, None, seg_lora=ids, table=tab, blk_cols=out_dims)
+        torch.cuda.synchronize()
+        outs[name] = torch.cat([t.cpu() for t in y], 0)
+    assert bits_equal(outs["pk"], outs["rm"])
+    assert bits_equal(outs["pk_rowmajor_w"], outs["rm"])
+    op = {3: ref.OP_QKV_FUSED, 2: ref.OP_GATE_UP_FUSED}.get(len(out_dims), ref.OP_O_PROJ)
+    want = ref.round_with_lora(op, xs, [1] * T, w, [ads[j] if j >= 0 else None for j in ids], out_dims)
+    for i in range(T):
+        assert_close(outs["pk"][i:i + 1], want[i], what=f"token {i}")
+
+
+def test_packed_lora_a_refused_where_unsupported(dev):
+    """Fragment-tile lora_A is read only by the K-sliced decode rounds:
+    mixed layouts in one round, the whole-K round, the prefill regime, the
+    segmented delta and chains refuse it."""
+    ops = _ops()
+    t_rm, t_pk, _ = _table_packed_a(dev, 64, [32], [16, 16])
+    A = torch.zeros(16, 64, dtype=BF16, device=dev)
+    B = torch.zeros(32, 16, dtype=BF16, device=dev)
+    t_pk.add(A, [B], 16, 1.0)  # entry 2: row-major in the packed table
+    w = randn((32, 64), 5).to(dev)
+    x1 = [torch.zeros(1, 64, dtype=BF16, device=dev) for _ in range(3)]
+    y1 = [torch.zeros(1, 32, dtype=BF16, device=dev) for _ in range(3)]
+    with pytest.raises(ValueError, match="all have row-major or all fragment-tile"):
+        ops.round_ex(x1, y1, [1, 1, 1], w, seg_lora=[0, 1, 2], table=t_pk, blk_cols=[32])
+    xs = [torch.zeros(65, 64, dtype=BF16, device=dev)]
+    ys = [torch.zeros(65, 32, dtype=BF16, device=dev)]
+    with pytest.raises(RuntimeError, match="at most 64 token rows"):
+        ops.round_ex(xs, ys, [65], w, seg_lora=[0], table=t_pk, blk_cols=[32])
+    with pytest.raises(ValueError, match="row-major lora_A"):
+        ops.lora_segmented(torch.zeros(2, 64, dtype=BF16, device=dev), [2], [0], t_pk, [32],
+                           torch.zeros(2, 32, dtype=BF16, device=dev))
+    with pytest.raises(ValueError, match="a_layout"):
+        ops.round_fusion(w_layout=2, a_layout=1)
+    with pytest.raises(ValueError, match="a_layout 1 needs"):
+        ops.round_ex(x1[:1], y1[:1], [1], w, seg_lora=[0], table=t_rm, blk_cols=[32],
+                     fusion=ops.round_fusion(a_layout=1))
+
+
 def test_packed_round_with_norm_and_residual_fusions(dev):
     """Fused forms over packed weights equal the same fusions over row-major
     weights bit for bit."""
