@@ -289,7 +289,7 @@ struct SplitArgs {
 // (64-row tile of the segment, 64-row block of its stacked A) pairs, item0 is
 // their prefix over the segments.
 struct ShrinkGemmArgs {
-  const bf16* x;          // packed [T, K]
+  const bf16* xs[kMaxSeg];  // rows of segment j (row stride K), in place or in the packed batch
   float* u;               // [n_ks][T][u_ld]
   int64_t K, u_split_stride;
   int32_t n_seg, n_ks, u_ld, total_steps;
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256) void shrink_gemm_kernel(ShrinkGemmArgs a) {
   const int nst = st1 - st0;
   const int64_t kbeg = (int64_t)st0 * 32 + 8 * (lane >> 4);
   const int tr = rt * 64 + wv * 16 + (lane & 15);  // token row of this lane within the segment
-  const bf16* xp = a.x + (int64_t)(a.row0[s] + min(tr, a.rows[s] - 1)) * a.K + kbeg;
+  const bf16* xp = a.xs[s] + (int64_t)min(tr, a.rows[s] - 1) * a.K + kbeg;
   const bf16* ap[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -1320,7 +1320,8 @@ constexpr int TM = 128, TN = 128, TK = 64;
 constexpr int kTiledBufs = 1;
 
 struct TiledArgs {
-  const bf16* x;          // packed [M, K]
+  const bf16* x;          // packed [M, K], or null: row m of segment g read in place at xin[g] + (m - out.off[g]) * K
+  const bf16* xin[kMaxSeg];
   const bf16* w;          // [N, K]
   const bf16* bias;
   int64_t M, N, K;
@@ -1519,7 +1520,13 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
     const int64_t r = 64 * wv + 8 * i + dr;
     const int dc = (lane & 7) ^ dr ^ (i & 1);
     wsrc[i] = a.w + min(n0 + r, a.N - 1) * a.K + 8 * dc;
-    xsrc[i] = a.x + min(m0 + r, a.M - 1) * a.K + 8 * dc;
+    const int64_t mr = min(m0 + r, a.M - 1);
+    if (a.x) {
+      xsrc[i] = a.x + mr * a.K + 8 * dc;
+    } else {  // the token row in its slot buffer (no packed copy)
+      const int sg = find_seg(a.out.off, a.out.n, mr);
+      xsrc[i] = a.xin[sg] + (mr - a.out.off[sg]) * a.K + 8 * dc;
+    }
   }
   // half h: instructions 4 h .. 4 h + 3 of W and of x
   auto issue = [&](int kt, int s, int h) {
@@ -1656,6 +1663,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
   }
   // the requests past the last stage land before the LDS is reused
   __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
+
 
   // LoRA delta as extra k-steps: for every segment of the tile's token rows
   // that has an adapter, A = the adapter's lora_B rows of the tile's
@@ -3354,14 +3362,18 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   return SWL_OK;
 }
 
-// Prefill GEMM launch: gemm256_kernel (256 x 256 tiles), or tiled_kernel
-// (128 x 128) with SWL_PREFILL_TILED=1.
-int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
+// Prefill GEMM: gemm256_kernel (256 x 256 tiles), or tiled_kernel (128 x
+// 128, over a packed copy of the rows) with SWL_PREFILL_TILED=1.
+bool prefill_uses_tiled(int64_t K) {
   static const bool use_tiled = [] {
     const char* e = getenv("SWL_PREFILL_TILED");
     return e && atoi(e) != 0;
   }();
-  if (use_tiled || a.K % PG_K != 0 || a.K < PG_K) {
+  return use_tiled || K % PG_K != 0 || K < PG_K;
+}
+
+int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
+  if (prefill_uses_tiled(a.K)) {
     const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM));
     hipLaunchKernelGGL(tiled_kernel, grid, dim3(256), 0, st, a);
     SWL_LAUNCH_CHECK("tiled_kernel launch");
@@ -3382,11 +3394,10 @@ int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
 // LoRA shrink of the packed prefill batch (one launch for all segments with
 // an adapter): seg_off / seg_rows are packed row offsets and counts; the u
 // rows are packed rows; n_ks K-slices of partials, folded into the first.
-int launch_shrink_gemm(const bf16* x, int64_t K, int n_seg, const int64_t* seg_off, const int64_t* seg_rows,
-                       const int32_t* seg_lora, const swl_lora_entry* host_entries, int nblk, float* u, int u_ld,
-                       int64_t u_split_stride, int n_ks, hipStream_t st) {
+int launch_shrink_gemm(const bf16* const* seg_x, int64_t K, int n_seg, const int64_t* seg_off,
+                       const int64_t* seg_rows, const int32_t* seg_lora, const swl_lora_entry* host_entries, int nblk,
+                       float* u, int u_ld, int64_t u_split_stride, int n_ks, hipStream_t st) {
   ShrinkGemmArgs a{};
-  a.x = x;
   a.u = u;
   a.K = K;
   a.u_split_stride = u_split_stride;
@@ -3397,6 +3408,7 @@ int launch_shrink_gemm(const bf16* x, int64_t K, int n_seg, const int64_t* seg_o
   for (int i = 0; i < n_seg; ++i) {
     if (seg_lora[i] < 0 || seg_rows[i] == 0) continue;
     const int j = a.n_seg++;
+    a.xs[j] = seg_x[i];
     a.item0[j] = items;
     a.row0[j] = (int32_t)seg_off[i];
     a.rows[j] = (int32_t)seg_rows[i];
@@ -3780,8 +3792,10 @@ int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg, const int64_t* 
     rc = scratch_get(sizeof(float) * (size_t)u_ks * (size_t)T * (size_t)u_ld, st, &scr);
     if (rc) return rc;
     float* u = reinterpret_cast<float*>(scr);
-    rc = launch_shrink_gemm(reinterpret_cast<const bf16*>(x), k, n_seg, e.off, seg_rows, e.seg_lora, lora_table_host,
-                            nblk, u, u_ld, T * u_ld, u_ks, st);
+    const bf16* seg_x[kMaxSeg];
+    for (int i = 0; i < n_seg; ++i) seg_x[i] = reinterpret_cast<const bf16*>(x) + e.off[i] * k;
+    rc = launch_shrink_gemm(seg_x, k, n_seg, e.off, seg_rows, e.seg_lora, lora_table_host, nblk, u, u_ld, T * u_ld,
+                            u_ks, st);
     if (rc) return rc;
     e.L.u = u;
     e.L.usplit = 1;  // folded into split 0
@@ -4108,7 +4122,11 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
 
   // ------------------------------------------------------ prefill regime
   SWL_CHECK(K % TK == 0, SWL_ERR_INVALID, "round: K must be a multiple of 64 for > 64 tokens");
-  const size_t xbytes = sizeof(bf16) * (size_t)T * (size_t)K;
+  // the 256 x 256 GEMM and the shrink read the token rows in place from the
+  // slot buffers (16-byte aligned: checked above); only the 128 x 128
+  // kernel takes a packed copy
+  const bool packed_x = prefill_uses_tiled(K);
+  const size_t xbytes = packed_x ? sizeof(bf16) * (size_t)T * (size_t)K : 0;
   const size_t xbytes_al = (xbytes + 255) & ~(size_t)255;
   // LoRA shrink K-slices: enough (item, slice) workgroups to fill the chip
   int u_ks = 1;
@@ -4125,11 +4143,14 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
   int rc = scratch_get(xbytes_al + ubytes, st, &scr);
   if (rc) return rc;
   bf16* packed = reinterpret_cast<bf16*>(scr);
-  rc = swl_gather_bf16(seg_in, rows, n_seg, K, packed, st);
-  if (rc) return rc;
+  if (packed_x) {
+    rc = swl_gather_bf16(seg_in, rows, n_seg, K, packed, st);
+    if (rc) return rc;
+  }
 
   TiledArgs a{};
-  a.x = packed;
+  a.x = packed_x ? packed : nullptr;
+  for (int i = 0; i < n_seg; ++i) a.xin[i] = reinterpret_cast<const bf16*>(seg_in[i]);
   a.w = reinterpret_cast<const bf16*>(w);
   a.bias = reinterpret_cast<const bf16*>(bias);
   a.M = T;
@@ -4146,7 +4167,9 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
       rws[i] = rows[i];
       a.seg_lora[i] = (seg_lora[i] >= 0 && rows[i] > 0) ? seg_lora[i] : -1;
     }
-    rc = launch_shrink_gemm(packed, K, n_seg, a.out.off, rws, a.seg_lora, host_entries, nblk, u, u_ld,
+    const bf16* seg_x[kMaxSeg];
+    for (int i = 0; i < n_seg; ++i) seg_x[i] = packed_x ? packed + a.out.off[i] * K : a.xin[i];
+    rc = launch_shrink_gemm(seg_x, K, n_seg, a.out.off, rws, a.seg_lora, host_entries, nblk, u, u_ld,
                             (int64_t)T * u_ld, u_ks, st);
     if (rc) return rc;
     a.has_lora = 1;
