@@ -85,6 +85,22 @@ def parse():
     return ap.parse_args()
 
 
+def copy_calibration(args, dev):
+    """--copy-calibration MIB: one copy of a buffer of that size (reads and
+    writes MIB each), the reference dispatch that scales rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    if args.copy_calibration <= 0:
+        return
+    import torch
+    n = args.copy_calibration * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def read_traffic(whole_k):
     """hbm_bytes_per_launch of the dominant kernel from the committed counter
     summary, or None."""
@@ -240,6 +256,7 @@ def prefill(args):
         flops += f
         tot_ms += ms
     tflops = flops / (tot_ms * 1e-3) / 1e12
+    copy_calibration(args, dev)
     line = {
         "metric": "prefill-shape round TFLOP/s (BASELINE config 3)",
         "value": round(tflops, 1),
@@ -546,14 +563,7 @@ def main():
                                          (statistics.fmean([x["base_ms"] for x in v]) * 1e-3) / 1e9, 1)}
                  for nm, v in per_op.items()}
     traffic = read_traffic(whole_k)
-    if args.copy_calibration > 0:
-        n = args.copy_calibration * (1 << 20) // 2
-        src = torch.ones(n, dtype=torch.bfloat16, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    copy_calibration(args, dev)
 
     step_bytes = s.step_bytes(ctx, W)
     cpu = None
