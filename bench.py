@@ -66,6 +66,9 @@ def parse():
                     help="decode: rounds run as whole-K rounds (no K-slice partials), a comma list of qkv, o, gu, "
                          "down, lm (those with K <= 4096 take it), 'all' or 'none' (split + epilogue kernels "
                          "everywhere); default lm")
+    ap.add_argument("--defer-qkv", action="store_true",
+                    help="decode: finish the QKV round in the attention kernel (round fusion out_mode 4, attention "
+                         "rope 3) instead of its epilogue kernel")
     ap.add_argument("--chain", action="store_true",
                     help="decode: each layer's O, Gate+Up and Down rounds and the next layer's QKV round as one "
                          "persistent launch (swl_chain_*)")
@@ -503,7 +506,8 @@ def main():
     max_new = 1 + args.warmup + args.steps + args.timer_steps + 1
     dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill,
                          packed=args.weights == "packed",
-                         whole_k="" if args.whole_k == "none" else args.whole_k, chain=args.chain)
+                         whole_k="" if args.whole_k == "none" else args.whole_k, chain=args.chain,
+                         defer_qkv=args.defer_qkv)
     del weights, adapters
     torch.cuda.synchronize()
 

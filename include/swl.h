@@ -130,6 +130,15 @@ int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
                    const swl_lora_entry* lora_table_host, int nblk,
                    const int64_t* blk_cols, void* stream);
 
+/* Where a QKV round with out_mode 4 left its work for the attention kernel:
+ * its fp32 K-slice partial sums, its LoRA shrink partials and the per-token
+ * adapters (layout private to the library).  Filled by swl_round_ex_bf16,
+ * read by swl_paged_attention_rows_ex_bf16; valid until the next round on
+ * the device reuses the library's scratch. */
+typedef struct swl_qkv_partials {
+  uint64_t opaque[128];
+} swl_qkv_partials;
+
 /* Optional fusions of a decode-shaped round (<= 64 token rows) with the
  * worker-side elementwise work on either side of it, for the in-process
  * batched decode step.  No counterpart in the reference: its worker runs this
@@ -154,7 +163,11 @@ int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
  *      q, the rotated k and the v of token t are written to its page slot
  *      (position cache_seqlens[t]) in k_cache / v_cache [num_blocks,
  *      block_size, hkv, 128] through block_table [ntok, max_blocks]; RoPE
- *      (NeoX halves) at positions[t] from cos_sin [max_pos, 128]. */
+ *      (NeoX halves) at positions[t] from cos_sin [max_pos, 128].
+ *   4  deferred QKV (decode, one token per sequence): only the K-sliced base
+ *      kernel runs; fusion->defer receives its partials and
+ *      swl_paged_attention_rows_ex_bf16 (rope 3) finishes the round (bias,
+ *      LoRA expand, RoPE, KV append) inside the attention kernel. */
 typedef struct swl_round_fusion {
   const void* norm_weight;
   float eps;
@@ -186,6 +199,12 @@ typedef struct swl_round_fusion {
    * padded to 16 with zeros), streamed like the weight tiles; 0: row-major
    * [nblk * rank, k].  Decode-shaped rounds with w_layout 0 or 1 only. */
   int32_t a_layout;
+  /* out_mode 4 (a fused QKV round of one token row per sequence, w_layout 0
+   * or 1): only the K-sliced base kernel runs; bias, the LoRA expand, RoPE
+   * and the KV-page append are left to the attention kernel
+   * (swl_paged_attention_rows_ex_bf16 with rope 3), and *defer receives
+   * where the round's partial sums are.  NULL for the other modes. */
+  swl_qkv_partials* defer;
 } swl_round_fusion;
 
 /* Segmented LoRA delta of a packed batch x [T, k] (segment i = rows
@@ -359,6 +378,23 @@ int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, 
                                   int block_size, const int32_t* block_table, int64_t max_blocks,
                                   const int32_t* cache_seqlens, const int64_t* positions, const void* cos_sin,
                                   int64_t max_pos, int rope, float softmax_scale, void* stream);
+
+/* swl_paged_attention_rows_bf16 that also finishes an out_mode 4 QKV round
+ * (rope = 3, decode rows, pages a multiple of 16 keys): every workgroup of a
+ * (sequence, kv head, part) computes its query heads from the round's
+ * partials (sum over the K-slices, bias, LoRA expand, one bf16 rounding,
+ * NeoX RoPE at positions[seq]), and the part holding the new key also its k
+ * and v, which it appends to the pages (cache_seqlens[seq] is the slot)
+ * before it reads them; qkv_rows are not read.  The reference runs these
+ * steps as the worker's rotary_embedding and flash_attn_with_kvcache after
+ * the QKV round (worker_sync.py:169-205, model_builder.py:193-201).  With
+ * qkv == NULL it is swl_paged_attention_rows_bf16. */
+int swl_paged_attention_rows_ex_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len, int hq,
+                                     int hkv, int d, void* k_cache, void* v_cache, int64_t num_blocks,
+                                     int block_size, const int32_t* block_table, int64_t max_blocks,
+                                     const int32_t* cache_seqlens, const int64_t* positions, const void* cos_sin,
+                                     int64_t max_pos, int rope, float softmax_scale,
+                                     const swl_qkv_partials* qkv, void* stream);
 
 /* ------------------------------------------- persistent decode chain ----
  * Several dependent decode-shaped rounds in one persistent launch: the O,

@@ -43,6 +43,12 @@ class LoraEntry(ctypes.Structure):
     ]
 
 
+class QkvPartials(ctypes.Structure):
+    """swl_qkv_partials (include/swl.h): opaque record an out_mode 4 QKV
+    round fills for the attention kernel."""
+    _fields_ = [("opaque", ctypes.c_uint64 * 128)]
+
+
 class RoundFusion(ctypes.Structure):
     """swl_round_fusion (include/swl.h)."""
     _fields_ = [
@@ -68,6 +74,7 @@ class RoundFusion(ctypes.Structure):
         ("max_pos", c_i64),
         ("w_layout", ctypes.c_int32),
         ("a_layout", ctypes.c_int32),
+        ("defer", c_vp),
     ]
 
 
@@ -145,6 +152,9 @@ _SIGS = {
     "swl_silu_mul_rows_bf16": (c_int, [P_vp, P_vp, c_i64, c_i64, c_vp]),
     "swl_paged_attention_rows_bf16": (c_int, [P_vp, P_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64,
                                               c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_f32, c_vp]),
+    "swl_paged_attention_rows_ex_bf16": (c_int, [P_vp, P_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64,
+                                                 c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_f32,
+                                                 ctypes.POINTER(QkvPartials), c_vp]),
     "swl_chain_create": (c_int, [c_int, c_int, ctypes.POINTER(ChainRound), c_vp, c_int, ctypes.POINTER(RoundFusion),
                                  ctypes.POINTER(c_vp)]),
     "swl_chain_launch": (c_int, [c_vp, c_vp]),

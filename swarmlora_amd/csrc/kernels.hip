@@ -35,6 +35,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -144,6 +145,21 @@ __device__ __forceinline__ int64_t blk_start_of(const LoraEpi L, int b) {
     if (i == b) v = L.blk_start[i];
   return v;
 }
+
+// What an out_mode 4 QKV round leaves for the attention kernel (the layout
+// behind swl_qkv_partials): K-slice partials part[n_ks][ntok][N], the LoRA
+// shrink partials and tables in L (u rows indexed by token), each token's
+// adapter entry (-1: none) and the bias.
+struct QkvPartials {
+  const float* part;
+  const bf16* bias;
+  int64_t N;
+  int32_t n_ks, ntok;
+  int32_t has_lora;
+  LoraEpi L;
+  int32_t lora[kSkinnyMaxTok];
+};
+static_assert(sizeof(QkvPartials) <= sizeof(swl_qkv_partials), "swl_qkv_partials must hold QkvPartials");
 
 // delta for 4 consecutive output columns (all inside block `blk`, first one at
 // in-block row `nin`) of the token whose shrink row is `urow`:
@@ -1915,6 +1931,8 @@ struct AttnArgs {
   int32_t rowmode;
   bf16* qkv_row[kSkinnyMaxTok];
   bf16* out_row[kSkinnyMaxTok];
+  // rope 3: q, k and v from an out_mode 4 round's partials
+  QkvPartials qp;
 };
 
 __device__ __forceinline__ bf16* tok_q(const AttnArgs& a, int64_t t) {
@@ -2291,6 +2309,159 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_f<0x140>(v);
 }
 
+// rope 3: the query heads of (sequence s, kv head h) computed from an out_mode
+// 4 QKV round's partials into qsh [G][128] (bf16), and in the part holding
+// the new key (kv) also the k and v rows of head h: into kvsh (k rotated,
+// both rounded to bf16, as fp32) for that part's own use and, written
+// without waiting, to the new key's page slot for later steps.  Units of 4
+// columns: unit (head c, half hf, quad q) covers dims 64 hf + 4 q .. + 3 of
+// head c (c < G: query head h G + c; c = G: k; c = G + 1: v).  Per column:
+// the K-slice partials summed in slice order, bias, the LoRA expand
+// u . B^T * scale (u: the token's shrink row summed over the K-slices), one
+// bf16 rounding, then NeoX RoPE for q and k (the partner dim through xsh)
+// rounded again, as the QKV round's epilogue does.  qkv_load issues the
+// loads (before the part's first K / V tiles, so they return first);
+// qkv_finish uses them; every thread of the workgroup calls both (barriers).
+constexpr int kQpPre = 8;  // K-slice partials of a unit requested together
+constexpr int kQpUnits = 2;  // units per thread (128 threads, G <= 4 with k and v)
+struct QpRegs {
+  f32x4 p[kQpUnits][kQpPre];
+  u32x4 b[kQpUnits][4][2];   // lora_B rows of the 4 columns (rank <= 16, a multiple of 8)
+  float u[kQpPre];           // this thread's shrink partials (q = threadIdx.x < u_ld)
+};
+
+__device__ __forceinline__ int64_t qp_col(const AttnArgs& a, int G, int h, int un) {
+  const int c = un >> 5, d0 = 64 * ((un >> 4) & 1) + 4 * (un & 15);
+  const int64_t cb = c < G ? (int64_t)(h * G + c) * 128 : c == G ? (int64_t)(a.hq + h) * 128
+                                                                 : (int64_t)(a.hq + a.hkv + h) * 128;
+  return cb + d0;
+}
+
+template <int G, int NT>
+__device__ __forceinline__ void qkv_load(const AttnArgs& a, int s, int h, bool kv, QpRegs& R) {
+  const QkvPartials& Q = a.qp;
+  const int lidx = Q.has_lora ? Q.lora[s] : -1;
+  const int nu = 32 * (G + (kv ? 2 : 0));
+  const swl_lora_entry* ep = lidx >= 0 ? Q.L.table + lidx : nullptr;
+  const bool breg = ep && ep->rank <= 16 && (ep->rank & 7) == 0;
+  const int64_t kst = (int64_t)Q.ntok * Q.N;
+#pragma unroll
+  for (int k = 0; k < kQpUnits; ++k) {
+    const int un = threadIdx.x + k * NT;
+    if (un >= nu) continue;
+    const int64_t col = qp_col(a, G, h, un);
+    const float* pp = Q.part + (int64_t)s * Q.N + col;
+#pragma unroll
+    for (int j = 0; j < kQpPre; ++j)
+      R.p[k][j] = j < Q.n_ks ? *reinterpret_cast<const f32x4*>(pp + j * kst) : f32x4{0.f, 0.f, 0.f, 0.f};
+    if (breg) {
+      const int r = ep->rank, b = find_blk(Q.L, col);
+      const bf16* brow = reinterpret_cast<const bf16*>(ep->b[b]) + (col - blk_start_of(Q.L, b)) * r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        R.b[k][e][0] = ld16(brow + e * r);
+        R.b[k][e][1] = r == 16 ? ld16(brow + e * r + 8) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+  if (lidx >= 0 && (int)threadIdx.x < Q.L.u_ld) {
+    const float* up = Q.L.u + (int64_t)s * Q.L.u_ld + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < kQpPre; ++j) R.u[j] = j < Q.L.usplit ? up[j * Q.L.u_split_stride] : 0.f;
+  }
+}
+
+template <int G, int NT>
+__device__ __forceinline__ void qkv_finish(const AttnArgs& a, int s, int h, bool kv, QpRegs& R, bf16* qsh,
+                                           bf16* xsh, float* ush, bf16* kvsh) {
+  const QkvPartials& Q = a.qp;
+  const int lidx = Q.has_lora ? Q.lora[s] : -1;
+  const swl_lora_entry* ep = lidx >= 0 ? Q.L.table + lidx : nullptr;
+  // the token's shrink row: u[q] = sum over the K-slices
+  if (lidx >= 0) {
+    for (int q = threadIdx.x; q < Q.L.u_ld; q += NT) {
+      float acc = 0.f;
+      if (q == (int)threadIdx.x) {
+#pragma unroll
+        for (int j = 0; j < kQpPre; ++j) acc += R.u[j];
+      }
+      const float* up = Q.L.u + (int64_t)s * Q.L.u_ld + q;
+      for (int j = q == (int)threadIdx.x ? kQpPre : 0; j < Q.L.usplit; ++j) acc += up[j * Q.L.u_split_stride];
+      ush[q] = acc;
+    }
+  }
+  __syncthreads();
+  const int nu = 32 * (G + (kv ? 2 : 0));
+  const int64_t kst = (int64_t)Q.ntok * Q.N;
+#pragma unroll
+  for (int k = 0; k < kQpUnits; ++k) {
+    const int un = threadIdx.x + k * NT;
+    if (un >= nu) continue;
+    const int c = un >> 5, d0 = 64 * ((un >> 4) & 1) + 4 * (un & 15);
+    const int64_t col = qp_col(a, G, h, un);
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kQpPre; ++j) sum += R.p[k][j];
+    for (int j = kQpPre; j < Q.n_ks; ++j) sum += *reinterpret_cast<const f32x4*>(Q.part + (int64_t)s * Q.N + col + j * kst);
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = sum[e] + (Q.bias ? bf2f(Q.bias[col + e]) : 0.f);
+    if (ep) {
+      const int r = ep->rank, b = find_blk(Q.L, col);
+      const float* ub = ush + b * r;
+      const bf16* brow = reinterpret_cast<const bf16*>(ep->b[b]) + (col - blk_start_of(Q.L, b)) * r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float dsum = 0.f;
+        if (r <= 16 && (r & 7) == 0) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            if (8 * hh >= r) break;
+            float bv[8];
+            unpack8(R.b[k][e][hh], bv);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) dsum += ub[8 * hh + t] * bv[t];
+          }
+        } else {
+          for (int i = 0; i < r; ++i) dsum += ub[i] * bf2f(brow[e * r + i]);
+        }
+        x[e] += dsum * ep->scale;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xsh[c * 128 + d0 + e] = f2bf(x[e]);
+  }
+  __syncthreads();
+  // RoPE of q and k; q into qsh, k and v into kvsh and their page slot
+  const int64_t pos = a.pos[s];
+  const bool rot_ok = pos >= 0 && pos < a.max_pos;
+  const int64_t slen = a.seqlens[s];
+  int64_t kvbase = -1;
+  if (kv && slen >= 0) {
+    const int64_t bi = slen / a.bs;
+    if (bi < a.max_blocks) {
+      const int32_t pb = a.bt[(int64_t)s * a.max_blocks + bi];
+      if (pb >= 0 && pb < a.num_blocks) kvbase = (((int64_t)pb * a.bs + slen % a.bs) * a.hkv + h) * 128;
+    }
+  }
+  for (int it = threadIdx.x; it < nu * 4; it += NT) {
+    const int c = it >> 7, d = it & 127;
+    float x = bf2f(xsh[c * 128 + d]);
+    if (c <= G && rot_ok) {
+      const float rc = bf2f(a.cs[pos * 128 + (d & 63)]), rsn = bf2f(a.cs[pos * 128 + 64 + (d & 63)]);
+      const float other = bf2f(xsh[c * 128 + (d < 64 ? d + 64 : d - 64)]);
+      x = bf2f(f2bf(d < 64 ? x * rc - other * rsn : x * rc + other * rsn));
+    }
+    if (c < G) {
+      qsh[c * 128 + d] = f2bf(x);
+    } else {
+      kvsh[(c - G) * 128 + d] = f2bf(x);
+      if (kvbase >= 0) (c == G ? a.kc : a.vc)[kvbase + d] = f2bf(x);
+    }
+  }
+  __syncthreads();
+}
+
 template <int G, int S, int W>
 __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* part, int maxparts, int tpp) {
   constexpr int GL = G < 4 ? G : 4;  // lane groups with a query head
@@ -2300,11 +2471,15 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
   __shared__ __attribute__((aligned(16))) char lds[W * WAVE_LDS];
   const int h = blockIdx.x, p = blockIdx.y, s = blockIdx.z;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t ctx = (int64_t)a.seqlens[s] + 1;
-  const int64_t ntiles = (ctx + kTileKeys - 1) / kTileKeys;
+  const int64_t ctx_all = (int64_t)a.seqlens[s] + 1;
+  const int64_t ntiles = (ctx_all + kTileKeys - 1) / kTileKeys;
   const int64_t tb = (int64_t)p * tpp;  // first tile of the part
   if (tb >= ntiles) return;             // uniform over the workgroup
-  const int nt = (int)min<int64_t>(tpp, ntiles - tb);
+  // rope 3: the part holding the new key (key ctx_all - 1) takes it from LDS
+  // after its page tiles, which end before it
+  const bool kvpart = a.rope == 3 && p == (int)((ntiles - 1) / tpp);
+  const int64_t ctx = kvpart ? ctx_all - 1 : ctx_all;
+  const int nt = (int)max<int64_t>(0, min<int64_t>(tpp, (ctx + kTileKeys - 1) / kTileKeys - tb));
   const int ntw = nt > w ? (nt - w + W - 1) / W : 0;  // this wave's tiles: w + j W
   char* ring = lds + w * WAVE_LDS;
   float* sc = reinterpret_cast<float*>(ring + S * kTileBytes);   // [G][16] scores
@@ -2349,18 +2524,38 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
   };
 
   // q of the G query heads as the MFMA B operand: lane l holds column l % 16
-  // (query head, zero past G), dims 32 * step + 8 (l / 16) .. + 7
+  // (query head, zero past G), dims 32 * step + 8 (l / 16) .. + 7.  rope 3:
+  // q computed from the QKV round's partials while the first tiles stream
+  // in; the part holding the new key appends its k and v first, then
+  // streams (its last tile reads them)
   u32x4 qf[4];
-  {
+  __shared__ __attribute__((aligned(16))) bf16 qsh[G * 128];
+  __shared__ bf16 kvsh[2 * 128];
+  if (a.rope == 3) {
+    __shared__ bf16 xsh[(G + 2) * 128];
+    __shared__ float ush[kMaxURow];
+    QpRegs R;
+    qkv_load<G, 64 * W>(a, s, h, kvpart, R);
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+      if (j < ntw) issue(j);
+    qkv_finish<G, 64 * W>(a, s, h, kvpart, R, qsh, xsh, ush, kvsh);
     const int col = lane & 15;
-    const bf16* qp = tok_q(a, s) + (int64_t)(h * G + (col < G ? col : 0)) * 128 + 8 * (lane >> 4);
 #pragma unroll
-    for (int st = 0; st < 4; ++st) qf[st] = col < G ? ldg16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
+    for (int st = 0; st < 4; ++st)
+      qf[st] = col < G ? *reinterpret_cast<const u32x4*>(qsh + col * 128 + 32 * st + 8 * (lane >> 4))
+                       : u32x4{0u, 0u, 0u, 0u};
+  } else {
+    {
+      const int col = lane & 15;
+      const bf16* qp = tok_q(a, s) + (int64_t)(h * G + (col < G ? col : 0)) * 128 + 8 * (lane >> 4);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) qf[st] = col < G ? ldg16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+      if (j < ntw) issue(j);
   }
-
-#pragma unroll
-  for (int j = 0; j < S; ++j)
-    if (j < ntw) issue(j);
 
   const int gg = lane >> 4;  // lane group: query heads gg * HPG ..
   float m[HPG], l[HPG], acc[HPG][8];
@@ -2471,6 +2666,27 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     if (j + S < ntw) issue(j + S);
+  }
+
+  // rope 3, the part holding the new key: wave 0 adds it (q . k_new, online
+  // softmax, p rounded to bf16 for the P.V product as for the page keys)
+  if (kvpart && w == 0) {
+#pragma unroll
+    for (int e = 0; e < HPG; ++e) {
+      const int g = gg < GL ? gg * HPG + e : 0;
+      float part_s = 0.f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) part_s += bf2f(qsh[g * 128 + 8 * (lane & 15) + t]) * bf2f(kvsh[8 * (lane & 15) + t]);
+      const float sc_new = row16_sum(part_s) * a.scale;
+      const float mn = fmaxf(m[e], sc_new);
+      const float corr = __expf(m[e] - mn);
+      const float pe = __expf(sc_new - mn);
+      l[e] = l[e] * corr + pe;
+      m[e] = mn;
+      const float pr = bf2f(f2bf(pe));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[e][d] = acc[e][d] * corr + pr * bf2f(kvsh[128 + 8 * (lane & 15) + d]);
+    }
   }
 
   // merge the W waves (all their DMA has landed) in LDS over the rings
@@ -2839,6 +3055,36 @@ int scratch_get(size_t need, hipStream_t stream, void** out) {
   return SWL_OK;
 }
 
+// A second scratch area with the contract of scratch_get (the decode
+// attention's part records while an out_mode 4 QKV round's partials occupy
+// the first).
+std::mutex g_scratch2_mu;
+std::vector<Scratch> g_scratch2;
+std::vector<void*> g_scratch2_kept;
+
+int scratch_get2(size_t need, hipStream_t stream, void** out) {
+  int dev = 0;
+  SWL_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_scratch2_mu);
+  if ((int)g_scratch2.size() <= dev) g_scratch2.resize(dev + 1);
+  Scratch& s = g_scratch2[dev];
+  if (s.bytes < need) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (stream) SWL_HIP(hipStreamIsCapturing(stream, &cs));
+    SWL_CHECK(cs == hipStreamCaptureStatusNone, SWL_ERR_STATE,
+              "scratch must grow outside graph capture (run the call once before capturing)");
+    size_t nb = std::max({need, s.bytes + s.bytes / 2, (size_t)1 << 20});
+    nb = (nb + 4095) & ~(size_t)4095;
+    void* p = nullptr;
+    SWL_HIP(hipMalloc(&p, nb));
+    if (s.ptr) g_scratch2_kept.push_back(s.ptr);
+    s.ptr = p;
+    s.bytes = nb;
+  }
+  *out = s.ptr;
+  return SWL_OK;
+}
+
 // ---------------------------------------------------------- launch timer
 // Optional HIP-event timing of the decode projection: when armed, every
 // launch_skinny call (outside graph capture) launches its base kernel and
@@ -3157,7 +3403,9 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const int mode = fz ? fz->out_mode : 0;
   const int64_t epi_cols = mode == 2 ? N / 2 : N;
   if (fz) {
-    SWL_CHECK(mode >= 0 && mode <= 3, SWL_ERR_INVALID, "round fusion: out_mode must be 0..3");
+    SWL_CHECK(mode >= 0 && mode <= 4, SWL_ERR_INVALID, "round fusion: out_mode must be 0..4");
+    SWL_CHECK(mode != 4 || (fz->defer && fz->w_layout != 2), SWL_ERR_INVALID,
+              "round fusion: out_mode 4 needs defer and a K-sliced round (w_layout 0 or 1)");
     SWL_CHECK(fz->w_layout >= 0 && fz->w_layout <= 2, SWL_ERR_INVALID, "round fusion: w_layout must be 0, 1 or 2");
     SWL_CHECK(fz->a_layout == 0 || (fz->a_layout == 1 && fz->w_layout != 2), SWL_ERR_INVALID,
               "round fusion: a_layout must be 0, or 1 (fragment-tile lora_A) with w_layout 0 or 1");
@@ -3311,6 +3559,33 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     if (rc2) return rc2;
   }
   SWL_LAUNCH_CHECK("split_kernel launch");
+
+  if (mode == 4) {
+    // the attention kernel finishes the round: tell it where the partials are
+    QkvPartials d{};
+    d.part = a.part;
+    d.bias = bias;
+    d.N = N;
+    d.n_ks = a.n_ks;
+    d.ntok = ntok;
+    d.has_lora = has_lora ? 1 : 0;
+    if (has_lora) {
+      d.L = *Lblk;
+      d.L.table = table;
+      d.L.u = a.u;
+      d.L.usplit = a.n_ks;
+      d.L.u_ld = a.u_ld;
+      d.L.u_split_stride = a.u_split_stride;
+    }
+    for (int i = 0; i < ntok; ++i) d.lora[i] = (has_lora && tok_lora[i] >= 0) ? tok_lora[i] : -1;
+    std::memset(fz->defer, 0, sizeof(swl_qkv_partials));
+    std::memcpy(fz->defer, &d, sizeof(d));
+    if (tslot >= 0) {  // no epilogue kernel: its events mark an empty interval
+      SWL_HIP(hipEventRecord(timer_event(tslot, 2), st));
+      SWL_HIP(hipEventRecord(timer_event(tslot, 3), st));
+    }
+    return SWL_OK;
+  }
 
   EpiArgs e{};
   e.part = a.part;
@@ -3499,7 +3774,9 @@ int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp) {
   const int maxparts = (int)((max_tiles + tpp - 1) / tpp);
   void* scr = nullptr;
   const size_t need = sizeof(float) * (size_t)a.nseq * a.hkv * maxparts * G * kAttnRec;
-  int rc = scratch_get(need, st, &scr);
+  // rope 3 reads the QKV round's partials from the first scratch area while
+  // parts store their records: those go to the second
+  int rc = a.rope == 3 ? scratch_get2(need, st, &scr) : scratch_get(need, st, &scr);
   if (rc) return rc;
   float* part = reinterpret_cast<float*>(scr);
   hipLaunchKernelGGL((attn_tile_kernel<G, S, W>), dim3((unsigned)a.hkv, (unsigned)maxparts, (unsigned)a.nseq),
@@ -3537,12 +3814,14 @@ bool attn_tile_fits(const AttnArgs& a) {
 }
 
 int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
-  if (a.rope != 2) {  // 2: q rotated and k / v appended by the QKV round's epilogue
+  if (a.rope <= 1) {  // 2: q rotated and k / v appended by the QKV round's epilogue; 3: by the attention kernel
     hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L), (unsigned)(a.hq + 2 * a.hkv)), dim3(64),
                        0, st, a);
     SWL_LAUNCH_CHECK("rope_append_kernel launch");
   }
-  if (a.L == 1 && attn_tile_fits(a)) {
+  SWL_CHECK(a.rope != 3 || (a.L == 1 && a.bs % kTileKeys == 0), SWL_ERR_INVALID,
+            "paged attention: rope 3 needs decode rows and pages of a multiple of 16 keys");
+  if (a.L == 1 && (attn_tile_fits(a) || a.rope == 3)) {
     switch (G) {
       case 1: return launch_attn_tile<1>(a, st);
       case 2: return launch_attn_tile<2>(a, st);
@@ -4097,9 +4376,9 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
   const int u_ld = ((max_r * std::max(nblk, 1) + 15) / 16) * 16;  // A rows padded to 16-row tiles
   const bool fused = fz && (fz->norm_weight || fz->out_mode != 0 || fz->w_layout != 0 || fz->a_layout != 0);
   const int64_t out_cols = (fz && fz->out_mode == 2) ? N / 2 : N;
-  if (fz && fz->out_mode == 3)
+  if (fz && (fz->out_mode == 3 || fz->out_mode == 4))
     for (int i = 0; i < n_seg; ++i)
-      SWL_CHECK(rows[i] == 1, SWL_ERR_INVALID, "round fusion: out_mode 3 takes one token row per sequence");
+      SWL_CHECK(rows[i] == 1, SWL_ERR_INVALID, "round fusion: out_modes 3 and 4 take one token row per sequence");
 
   if (T <= kSkinnyMaxTok) {
     // ---------------------------------------------------- decode regime
@@ -4316,12 +4595,13 @@ extern "C" int swl_silu_mul_rows_bf16(const void* const* in_rows, void* const* o
   return SWL_OK;
 }
 
-extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len,
-                                             int hq, int hkv, int d, void* k_cache, void* v_cache,
-                                             int64_t num_blocks, int block_size, const int32_t* block_table,
-                                             int64_t max_blocks, const int32_t* cache_seqlens,
-                                             const int64_t* positions, const void* cos_sin, int64_t max_pos,
-                                             int rope, float softmax_scale, void* stream) {
+extern "C" int swl_paged_attention_rows_ex_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len,
+                                                int hq, int hkv, int d, void* k_cache, void* v_cache,
+                                                int64_t num_blocks, int block_size, const int32_t* block_table,
+                                                int64_t max_blocks, const int32_t* cache_seqlens,
+                                                const int64_t* positions, const void* cos_sin, int64_t max_pos,
+                                                int rope, float softmax_scale, const swl_qkv_partials* qkv,
+                                                void* stream) {
   SWL_CHECK(qkv_rows && out_rows && k_cache && v_cache && block_table && cache_seqlens, SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: null argument");
   SWL_CHECK(d == 128 && hq > 0 && hkv > 0 && hq % hkv == 0, SWL_ERR_INVALID,
@@ -4333,10 +4613,12 @@ extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const*
             "swl_paged_attention_rows_bf16: at most 64 token rows");
   SWL_CHECK(block_size > 0 && num_blocks > 0 && max_blocks > 0, SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: bad page geometry");
-  SWL_CHECK(rope >= 0 && rope <= 2 && (rope != 2 || q_len == 1), SWL_ERR_INVALID,
-            "swl_paged_attention_rows_bf16: rope must be 0, 1 or 2 (2: decode rows only)");
-  SWL_CHECK(rope != 1 || (cos_sin && positions && max_pos > 0), SWL_ERR_INVALID,
+  SWL_CHECK(rope >= 0 && rope <= 3 && (rope < 2 || q_len == 1), SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: rope must be 0, 1, 2 or 3 (2 and 3: decode rows only)");
+  SWL_CHECK((rope == 1 || rope == 3) ? (cos_sin && positions && max_pos > 0) : true, SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: rope needs positions and cos_sin");
+  SWL_CHECK((rope == 3) == (qkv != nullptr), SWL_ERR_INVALID,
+            "swl_paged_attention_rows_ex_bf16: rope 3 and the QKV round's partials go together");
   if (nseq == 0) return SWL_OK;
   AttnArgs a{};
   a.rowmode = 1;
@@ -4363,5 +4645,23 @@ extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const*
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.rope = rope;
   a.scale = softmax_scale;
+  if (qkv) {
+    std::memcpy(&a.qp, qkv, sizeof(a.qp));
+    SWL_CHECK(a.qp.part && a.qp.N == (int64_t)(hq + 2 * hkv) * 128 && a.qp.ntok == nseq && a.qp.n_ks >= 1,
+              SWL_ERR_INVALID,
+              "swl_paged_attention_rows_ex_bf16: the partials are not those of a QKV round of these sequences");
+  }
   return launch_attention(a, G, (hipStream_t)stream);
+}
+
+extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len,
+                                             int hq, int hkv, int d, void* k_cache, void* v_cache,
+                                             int64_t num_blocks, int block_size, const int32_t* block_table,
+                                             int64_t max_blocks, const int32_t* cache_seqlens,
+                                             const int64_t* positions, const void* cos_sin, int64_t max_pos,
+                                             int rope, float softmax_scale, void* stream) {
+  SWL_CHECK(rope != 3, SWL_ERR_INVALID, "swl_paged_attention_rows_bf16: rope 3 needs swl_paged_attention_rows_ex_bf16");
+  return swl_paged_attention_rows_ex_bf16(qkv_rows, out_rows, nseq, q_len, hq, hkv, d, k_cache, v_cache, num_blocks,
+                                          block_size, block_table, max_blocks, cache_seqlens, positions, cos_sin,
+                                          max_pos, rope, softmax_scale, nullptr, stream);
 }

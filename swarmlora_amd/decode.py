@@ -128,11 +128,18 @@ class BatchedDecoder:
     O, Gate+Up and Down rounds and the next layer's QKV round run as one
     persistent launch (ops.ChainPlan); layer 0's QKV round and the LM head
     are whole-K rounds.
+    defer_qkv (fused step, K-sliced QKV round, pages a multiple of 16 keys):
+    the QKV round leaves its partial sums to the attention kernel, which
+    finishes it (bias, LoRA expand, RoPE, KV append: round fusion out_mode 4
+    and attention rope 3) instead of a separate epilogue kernel.  Off by
+    default: every attention part of a sequence re-reads the round's
+    partials and lora_B rows for its query heads (config 4, ~4 parts per
+    sequence: 6.47 ms per step against 6.37).
     """
 
     def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
                  first_ids: List[int], device, max_new: int = 64, kv_fill=None, fused: bool = True,
-                 packed: bool = True, whole_k: bool = True, chain: bool = False):
+                 packed: bool = True, whole_k: bool = True, chain: bool = False, defer_qkv: bool = False):
         self.shape = s = shape
         self.device = dev = torch.device(device)
         self.W = W = len(ctx_lens)
@@ -158,6 +165,7 @@ class BatchedDecoder:
             raise ValueError(f"whole_k: rounds must be among {names}")
         self.whole_k = wk if (self.packed and W <= 32) else set()
         self.chain = bool(chain)
+        self.defer_qkv_req = bool(defer_qkv)
         if self.chain:
             if not self.packed or W > 32:
                 raise ValueError("chain: the packed fused step with at most 32 workers")
@@ -314,6 +322,10 @@ class BatchedDecoder:
                "gu": [s.inter, s.inter], "down": [s.hidden]}
 
         self._init_kv(ctx_lens, kv_fill)
+        # the QKV round finished inside the attention kernel (K-sliced QKV
+        # rounds over pages of whole 16-key tiles)
+        self.defer_qkv = self.defer_qkv_req and not self.chain and not self.wk["qkv"] and s.block_size % 16 == 0
+        self.qkv_defer = ops.QkvPartials() if self.defer_qkv else None
 
         # per-step buffers: one row per worker; partial sums of squares of the
         # residual stream: one per 16 columns from a whole-K round, per 256
@@ -346,11 +358,12 @@ class BatchedDecoder:
                       cos_sin=self.cos_sin)
             wl = {g: (2 if self.wk[g] else 1) if self.packed else 0 for g in self.wk}
             al = {g: 1 if has_lora and self.a_packed[g] else 0 for g in self.a_packed}
+            qkv_out = dict(out_mode=4, defer=self.qkv_defer) if self.defer_qkv else dict(out_mode=3, **kv)
             plan = (
                 ("qkv", rows(self.x0) if li == 0 else rows(self.h), rows(self.qkv),
-                 ops.round_fusion(out_mode=3, w_layout=wl["qkv"], a_layout=al["qkv"], **kv) if li == 0 else
-                 ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, out_mode=3, w_layout=wl["qkv"],
-                                  a_layout=al["qkv"], **kv)),
+                 ops.round_fusion(w_layout=wl["qkv"], a_layout=al["qkv"], **qkv_out) if li == 0 else
+                 ops.round_fusion(norm_weight=in_norm, eps=s.eps, ss_in=self.ss_d, w_layout=wl["qkv"],
+                                  a_layout=al["qkv"], **qkv_out)),
                 ("o", rows(self.attn), rows(self.h),
                  ops.round_fusion(out_mode=1, ss_out=self.ss_o, w_layout=wl["o"], a_layout=al["o"])),
                 ("gu", rows(self.h), rows(self.act),
@@ -448,9 +461,15 @@ class BatchedDecoder:
             qkv, o, gu, down = self._calls[li]
             if li == 0 or not self.chain:
                 self._round_ex(qkv)
-            ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
-                                     self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
-                                     self.seqlens, None, None, self._scale, rope=2)
+            if self.defer_qkv:
+                ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
+                                         self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
+                                         self.seqlens, self.positions, self.cos_sin, self._scale, rope=3,
+                                         qkv_partials=self.qkv_defer)
+            else:
+                ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
+                                         self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
+                                         self.seqlens, None, None, self._scale, rope=2)
             if self.chain:
                 self.chains[li].launch()
                 continue

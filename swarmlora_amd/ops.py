@@ -270,7 +270,8 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
                  k_cache: Optional[torch.Tensor] = None, v_cache: Optional[torch.Tensor] = None, hq: int = 0,
                  hkv: int = 0, block_table: Optional[torch.Tensor] = None,
                  cache_seqlens: Optional[torch.Tensor] = None, positions: Optional[torch.Tensor] = None,
-                 cos_sin: Optional[torch.Tensor] = None, w_layout: int = 0, a_layout: int = 0) -> RoundFusion:
+                 cos_sin: Optional[torch.Tensor] = None, w_layout: int = 0, a_layout: int = 0,
+                 defer: Optional["QkvPartials"] = None) -> RoundFusion:
     """swl_round_fusion for round_ex (include/swl.h documents each mode).
     ss_in / ss_out: fp32 [ntok, n_partial] (n_partial = ceil(n / 256) of the
     producing round); the record keeps the tensors it points to alive."""
@@ -290,8 +291,13 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
         f.norm_weight, f.eps = norm_weight.data_ptr(), float(eps)
         f.ss_in, f.ss_in_n, f.ss_in_stride = ss_in.data_ptr(), ss_in.shape[1], ss_in.stride(0)
         keep += [norm_weight, ss_in]
-    if out_mode not in (0, 1, 2, 3):
-        raise ValueError("out_mode must be 0..3")
+    if out_mode not in (0, 1, 2, 3, 4):
+        raise ValueError("out_mode must be 0..4")
+    if (out_mode == 4) != (defer is not None):
+        raise ValueError("out_mode 4 (the attention kernel finishes the QKV round) goes with a QkvPartials record")
+    if defer is not None:
+        f.defer = ctypes.cast(ctypes.byref(defer), ctypes.c_void_p)
+        keep.append(defer)
     f.out_mode = out_mode
     if out_mode == 1:
         _need(ss_out, "ss_out", torch.float32)
@@ -745,15 +751,23 @@ def silu_mul(gu: torch.Tensor, inter: int) -> torch.Tensor:
     return out
 
 
+QkvPartials = _lib.QkvPartials
+
+
 def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: int, k_cache: torch.Tensor,
                          v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
                          positions: Optional[torch.Tensor], cos_sin: Optional[torch.Tensor], softmax_scale: float,
-                         rope=True):
+                         rope=True, qkv_partials: Optional[QkvPartials] = None):
     """paged_attention over per-token rows: token t = seq * q_len + i has
     its fused [q | k | v] row at qkv_rows[t] (rotated in place) and gets its
     [hq * d] output at out_rows[t].  rope=2: q already rotated and k / v
-    already appended by an out_mode 3 round (decode rows only)."""
-    rope = 2 if rope == 2 else (1 if rope else 0)
+    already appended by an out_mode 3 round (decode rows only).  rope=3 with
+    qkv_partials: the kernel finishes an out_mode 4 QKV round (bias, LoRA
+    expand, RoPE at positions, the KV append) from its partials; the rows are
+    not read."""
+    rope = rope if rope in (2, 3) else (1 if rope else 0)
+    if (rope == 3) != (qkv_partials is not None):
+        raise ValueError("rope 3 goes with the QKV round's QkvPartials record")
     qkv = _rowset(qkv_rows, (hq + 2 * hkv) * d)
     out = _rowset(out_rows, hq * d)
     if len(qkv) != len(out) or len(qkv) % q_len:
@@ -773,7 +787,7 @@ def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: i
     if cache_seqlens.numel() < nseq:
         raise ValueError("cache_seqlens must have nseq entries")
     max_pos = 0
-    if rope == 1:
+    if rope in (1, 3):
         _need(positions, "positions", torch.int64)
         _need(cos_sin, "cos_sin")
         if positions.numel() != nseq * q_len:
@@ -781,10 +795,12 @@ def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: i
         if cos_sin.shape[-1] != d or not cos_sin.is_contiguous():
             raise ValueError("cos_sin must be contiguous [max_pos, d]")
         max_pos = cos_sin.shape[0]
-    _lib.check(_lib.load().swl_paged_attention_rows_bf16(
+    rp = rope in (1, 3)
+    _lib.check(_lib.load().swl_paged_attention_rows_ex_bf16(
         qkv.array, out.array, nseq, q_len, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs, _ptr(block_table),
-        block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope == 1 else None),
-        _ptr(cos_sin if rope == 1 else None), max_pos, rope, float(softmax_scale), _stream()))
+        block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rp else None),
+        _ptr(cos_sin if rp else None), max_pos, rope, float(softmax_scale),
+        ctypes.byref(qkv_partials) if qkv_partials is not None else None, _stream()))
 
 
 # -------------------------------------------------------------- timing ---

@@ -48,8 +48,8 @@ def _contexts():
     return ctx
 
 
-@pytest.mark.parametrize("chain", [False, True])
-def test_config4_shape_decode_steps_eager_then_graph(dev, chain):
+@pytest.mark.parametrize("chain,defer_qkv", [(False, False), (True, False), (False, True)])
+def test_config4_shape_decode_steps_eager_then_graph(dev, chain, defer_qkv):
     from swarmlora_amd.decode import BatchedDecoder, DecodeShape, synthetic_adapter, synthetic_weights
     s = DecodeShape(layers=2)
     ctx = _contexts()
@@ -73,7 +73,7 @@ def test_config4_shape_decode_steps_eager_then_graph(dev, chain):
         pages[li] = (kc.cpu(), vc.cpu())
 
     dec = BatchedDecoder(s, wd, ad_dev, ctx, first, dev, max_new=6, kv_fill=kv_fill, fused=True, packed=True,
-                         chain=chain)
+                         chain=chain, defer_qkv=defer_qkv)
     del wd, ad_dev
     kc = [pages[li][0] for li in range(s.layers)]
     vc = [pages[li][1] for li in range(s.layers)]
