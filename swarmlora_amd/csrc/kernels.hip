@@ -512,8 +512,11 @@ __device__ __forceinline__ const bf16* tile_rows(const SplitArgs& a, int tile, i
 // ... (W's tiles, then the adapter tiles), issuing the next tile's first W
 // group before storing the current tile's partials so the stores and the
 // loads overlap.  No workgroup waits on another.
-template <int TT, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(SplitArgs a) {
+// Resident waves per SIMD the registers are sized for: 6 for three 8-wave
+// workgroups per CU up to 32 token rows (80 VGPRs), 4 for one 16-wave
+// workgroup per CU or wider accumulators (128 VGPRs).
+template <int TT, int WAVES, int KD = kKDepth>
+__global__ __launch_bounds__(WAVES * 64, (TT <= 2 && WAVES < 16) ? 6 : 4) void split_kernel(SplitArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16 xs[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -521,7 +524,7 @@ __global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(Spli
   const int st0 = (int)((int64_t)a.total_steps * ks / a.n_ks);
   const int st1 = (int)((int64_t)a.total_steps * (ks + 1) / a.n_ks);
   const int nst = st1 - st0;
-  const int npad = (nst + kKDepth - 1) / kKDepth * kKDepth;
+  const int npad = (nst + KD - 1) / KD * KD;
   const int64_t kbeg = (int64_t)st0 * 32;
   const int tstride = a.n_workers * WAVES;
 
@@ -530,7 +533,7 @@ __global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(Spli
   int tile = wk + a.n_workers * wv;
   int grp = -1, qrow0 = 0;
   const bf16* wp = nullptr;
-  u32x4 w[kKDepth];
+  u32x4 w[KD];
   // fragment-tile W: k-steps 512 elements apart (uniform per tile)
   auto packed = [&](int t) { return t < a.n_wtiles ? a.w_packed != 0 : a.a_packed != 0; };
 
@@ -628,9 +631,9 @@ __global__ __launch_bounds__(WAVES * 64, TT <= 2 ? 6 : 4) void split_kernel(Spli
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (packed(tile))
-      kloop_lds<TT, kKDepth, 512>(acc, w, wp, xl, 512, npad, nst);
+      kloop_lds<TT, KD, 512>(acc, w, wp, xl, 512, npad, nst);
     else
-      kloop_lds<TT, kKDepth, 32>(acc, w, wp, xl, 512, npad, nst);
+      kloop_lds<TT, KD, 32>(acc, w, wp, xl, 512, npad, nst);
 
     const int cur = tile, cgrp = grp, cq = qrow0;
     tile += tstride;
@@ -3152,6 +3155,7 @@ struct Tuning {
   bool shape_forced = false;  // SWL_SKINNY_WAVES / SWL_SKINNY_WGCU given: no per-shape choice
   int lds_kb = 96;      // activation-slice LDS per workgroup (16..160 KiB)
   int slice_steps = 16; // K-slices hold at most this many 32-wide k-steps
+  int kd = 8;           // k-steps of W in flight per wave (16: only with 16-wave workgroups)
   int nks = 0;          // forced K-slice count (0: chosen per shape)
   int long_slice = 1 << 20;  // slice cap when the row tiles alone overfill the slots (0: off; default:
                              // the longest slice the LDS holds)
@@ -3169,6 +3173,7 @@ const Tuning& tuning() {
     }
     if (const char* e = getenv("SWL_SKINNY_LDS_KB")) v.lds_kb = std::min(160, std::max(16, atoi(e)));
     if (const char* e = getenv("SWL_SKINNY_NKS")) v.nks = std::max(0, atoi(e));
+    if (const char* e = getenv("SWL_SKINNY_KD")) v.kd = atoi(e) == 16 ? 16 : 8;
     if (const char* e = getenv("SWL_SKINNY_SLICE")) v.slice_steps = std::max(1, atoi(e));
     if (const char* e = getenv("SWL_SKINNY_LONG_SLICE")) v.long_slice = std::max(0, atoi(e));
     return v;
@@ -3249,23 +3254,26 @@ int launch_fullk_t(int mode, const FullKArgs& a, dim3 grid, size_t lds, hipStrea
   }
 }
 
-template <int TT, int W>
+template <int TT, int W, int KD>
 int launch_split_tw(const SplitArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t tb0, hipEvent_t tb1) {
   static size_t allowed = 0;
-  int rc = allow_lds(split_kernel<TT, W>, lds, &allowed);
+  int rc = allow_lds(split_kernel<TT, W, KD>, lds, &allowed);
   if (rc) return rc;
-  launch_maybe_timed(split_kernel<TT, W>, grid, dim3(W * 64), lds, st, tb0, tb1, a);
+  launch_maybe_timed(split_kernel<TT, W, KD>, grid, dim3(W * 64), lds, st, tb0, tb1, a);
   return SWL_OK;
 }
 
 template <int W>
-int launch_split_w(int TT, const SplitArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t tb0,
+int launch_split_w(int TT, int kd, const SplitArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t tb0,
                    hipEvent_t tb1) {
+  if (W == 16 && kd == 16 && TT <= 2)  // 16 k-steps in flight per wave (one 16-wave workgroup per CU)
+    return TT == 1 ? launch_split_tw<1, 16, 16>(a, grid, lds, st, tb0, tb1)
+                   : launch_split_tw<2, 16, 16>(a, grid, lds, st, tb0, tb1);
   switch (TT) {
-    case 1: return launch_split_tw<1, W>(a, grid, lds, st, tb0, tb1);
-    case 2: return launch_split_tw<2, W>(a, grid, lds, st, tb0, tb1);
-    case 3: return launch_split_tw<3, W>(a, grid, lds, st, tb0, tb1);
-    default: return launch_split_tw<4, W>(a, grid, lds, st, tb0, tb1);
+    case 1: return launch_split_tw<1, W, kKDepth>(a, grid, lds, st, tb0, tb1);
+    case 2: return launch_split_tw<2, W, kKDepth>(a, grid, lds, st, tb0, tb1);
+    case 3: return launch_split_tw<3, W, kKDepth>(a, grid, lds, st, tb0, tb1);
+    default: return launch_split_tw<4, W, kKDepth>(a, grid, lds, st, tb0, tb1);
   }
 }
 
@@ -3495,7 +3503,8 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   // fewer fp32 partials, and the one workgroup per CU the staged slice
   // leaves resident still has many tiles (LM head at 28 rows: 2 slices of
   // 64 steps 220 us, 4 of 32 steps 246 us).
-  auto padded = [&](int64_t nk) { return ((total_steps + nk - 1) / nk + kKDepth - 1) / kKDepth * kKDepth; };
+  int kd = (tu.kd == 16 && waves == 16 && TT <= 2) ? 16 : kKDepth;
+  auto padded = [&](int64_t nk) { return ((total_steps + nk - 1) / nk + kd - 1) / kd * kd; };
   const bool long_rows = tu.long_slice > 0 && tile_groups > slots;
   const int slice_cap = long_rows ? tu.long_slice : tu.slice_steps;
   auto lds_of = [&](int64_t nk) {  // staged slice (+ RMSNorm gamma and row factors)
@@ -3512,16 +3521,17 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   }
   while (n_ks < total_steps && lds_of(n_ks) > lds_cap) n_ks *= 2;
   n_ks = std::min<int64_t>(n_ks, total_steps);
-  // Rounds whose waves would carry fewer than two tiles each at three 8-wave
-  // workgroups per CU (28 rows: QKV 0.6, O 0.4, Down 1.5; Gate+Up 2.4) run
-  // one 16-wave workgroup per CU instead: the three workgroups of a CU stage
-  // the same K-slice of the token rows three times, and the extra waves add
-  // no bytes in flight (measured: QKV 18.6 -> 17.1 us, O 14.3 -> 13.2, Down
-  // 30.4 -> 29.7; Gate+Up 57.1 -> 57.7, so it keeps three)
-  if (!tu.shape_forced && !long_rows && TT <= 2 && waves == 8 &&
-      (double)a.n_tiles * n_ks < 2.0 * (double)slots * waves) {
+  // One 16-wave workgroup per CU rather than three 8-wave ones (up to 32
+  // token rows, when the row tiles do not overfill the slots): the three
+  // workgroups of a CU would stage the same K-slice of the token rows three
+  // times.  Waves with three tiles or more (Gate+Up at 28 rows: 3.6) keep 16
+  // k-steps of W in flight instead of 8.  Measured per round (28 rows, us,
+  // three 8-wave workgroups -> one 16-wave, depth 8 -> depth 16): QKV 18.6
+  // -> 16.8, O 14.3 -> 13.0, Down 30.4 -> 29.2, Gate+Up 57.1 -> 57.6 -> 56.7.
+  if (!tu.shape_forced && !long_rows && TT <= 2 && waves == 8) {
     waves = 16;
     slots = cu_count();
+    if ((double)a.n_tiles * n_ks >= 3.0 * (double)slots * waves && (total_steps + n_ks - 1) / n_ks > 8) kd = 16;
   }
   a.n_ks = (int)n_ks;
   a.ks_steps = (int)padded(n_ks);  // the widest slice, padded to whole pipeline iterations
@@ -3570,9 +3580,9 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   {
     int rc2 = SWL_OK;
     switch (waves) {
-      case 4: rc2 = launch_split_w<4>(TT, a, grid, lds, st, tb0, tb1); break;
-      case 16: rc2 = launch_split_w<16>(TT, a, grid, lds, st, tb0, tb1); break;
-      default: rc2 = launch_split_w<8>(TT, a, grid, lds, st, tb0, tb1); break;
+      case 4: rc2 = launch_split_w<4>(TT, kd, a, grid, lds, st, tb0, tb1); break;
+      case 16: rc2 = launch_split_w<16>(TT, kd, a, grid, lds, st, tb0, tb1); break;
+      default: rc2 = launch_split_w<8>(TT, kd, a, grid, lds, st, tb0, tb1); break;
     }
     if (rc2) return rc2;
   }
