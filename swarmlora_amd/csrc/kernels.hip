@@ -3531,7 +3531,13 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   if (!tu.shape_forced && !long_rows && TT <= 2 && waves == 8) {
     waves = 16;
     slots = cu_count();
-    if ((double)a.n_tiles * n_ks >= 3.0 * (double)slots * waves && (total_steps + n_ks - 1) / n_ks > 8) kd = 16;
+    if ((double)a.n_tiles * n_ks >= 3.0 * (double)slots * waves && (total_steps + n_ks - 1) / n_ks > 8) {
+      kd = 16;
+      // and twice as long K-slices where the CU's one workgroup can stage
+      // them (half the fp32 partials; Gate+Up 71.7 -> 70.5 us with its
+      // epilogue at 4 slices of 32 steps)
+      if (tu.nks == 0 && n_ks >= 2 && lds_of(n_ks / 2) <= 160 * 1024) n_ks /= 2;
+    }
   }
   a.n_ks = (int)n_ks;
   a.ks_steps = (int)padded(n_ks);  // the widest slice, padded to whole pipeline iterations
