@@ -2465,15 +2465,60 @@ __device__ __forceinline__ void qkv_finish(const AttnArgs& a, int s, int h, bool
   __syncthreads();
 }
 
+// Size-ordered part numbering for up to 64 sequences: workgroup b (linear
+// over the grid) takes kv head b % hkv of part unit b / hkv, where units are
+// every sequence's full parts (tpp tiles) in sequence order, then the partial
+// last parts from the most tiles to the fewest (ties in sequence order).
+// Workgroups past the last unit find none.  Consecutive workgroups land on
+// different CUs, so each CU gets about the same number of full parts and at
+// most one short one, and no workgroup slot goes to a part past a sequence's
+// end.  Every wave computes it on its own (no LDS, no barrier).
+__device__ __forceinline__ bool attn_unit_of(const AttnArgs& a, int maxparts, int tpp, int lane, int& h, int& p,
+                                             int& s) {
+  const int64_t b = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  h = (int)(b % a.hkv);
+  const int64_t unit = b / a.hkv;
+  // tiles ceil((len + 1) / 16), as the parts see them, capped at the grid's
+  // maxparts parts (the parts the sequence-major numbering covers)
+  const int64_t len1 = lane < a.nseq ? (int64_t)a.seqlens[lane] + 1 : 0;
+  const int nt = (int)min<int64_t>(max<int64_t>(0, (len1 + kTileKeys - 1) / kTileKeys), (int64_t)maxparts * tpp);
+  const int F = nt / tpp, R = nt - F * tpp;
+  int pf = F;  // inclusive prefix of the full parts
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(pf, off);
+    if (lane >= off) pf += y;
+  }
+  const int total_full = __shfl(pf, 63);
+  if (unit < total_full) {
+    const uint64_t m = __ballot(pf > unit);
+    s = __builtin_ctzll(m);
+    p = (int)(unit - (__shfl(pf, s) - __shfl(F, s)));
+    return true;
+  }
+  const int64_t r = unit - total_full;
+  int rank = 0;  // among the partial parts, by tiles descending
+  for (int j = 0; j < a.nseq; ++j) {
+    const int rj = __builtin_amdgcn_readlane(R, j);
+    rank += (rj > R || (rj == R && j < lane)) ? 1 : 0;
+  }
+  const uint64_t m = __ballot(R > 0 && rank == r);
+  if (m == 0) return false;
+  s = __builtin_ctzll(m);
+  p = __shfl(F, s);
+  return true;
+}
+
 template <int G, int S, int W>
-__global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* part, int maxparts, int tpp) {
+__global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* part, int maxparts, int tpp, int order) {
   constexpr int GL = G < 4 ? G : 4;  // lane groups with a query head
   constexpr int HPG = G / GL;        // query heads per lane group
   constexpr int WAVE_LDS = S * kTileBytes + G * kTileKeys * 4 + G * kTileKeys * 2;
   static_assert(W * S * kTileBytes >= W * G * kAttnRec * 4, "merge area must fit in the rings");
   __shared__ __attribute__((aligned(16))) char lds[W * WAVE_LDS];
-  const int h = blockIdx.x, p = blockIdx.y, s = blockIdx.z;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int h = blockIdx.x, p = blockIdx.y, s = blockIdx.z;
+  if (order && !attn_unit_of(a, maxparts, tpp, lane, h, p, s)) return;  // uniform over the workgroup
   const int64_t ctx_all = (int64_t)a.seqlens[s] + 1;
   const int64_t ntiles = (ctx_all + kTileKeys - 1) / kTileKeys;
   const int64_t tb = (int64_t)p * tpp;  // first tile of the part
@@ -3784,7 +3829,7 @@ int launch_attn_decode_u(const AttnArgs& a, hipStream_t st) {
 // (SWL_ATTN_STAGES, 2..4); SWL_ATTN_TILE=0 selects the per-chunk kernel.
 struct AttnTileTuning {
   bool on = true;
-  int waves = 2, tpp = 16, stages = 2;
+  int waves = 2, tpp = 16, stages = 2, order = 1;
 };
 const AttnTileTuning& attn_tile_tuning() {
   static AttnTileTuning t = [] {
@@ -3796,6 +3841,7 @@ const AttnTileTuning& attn_tile_tuning() {
     }
     if (const char* e = getenv("SWL_ATTN_TPP")) v.tpp = std::max(1, std::min(64, atoi(e)));
     if (const char* e = getenv("SWL_ATTN_STAGES")) v.stages = std::max(2, std::min(4, atoi(e)));
+    if (const char* e = getenv("SWL_ATTN_ORDER")) v.order = atoi(e) != 0;
     v.tpp = std::max(v.tpp, v.waves);
     return v;
   }();
@@ -3803,7 +3849,7 @@ const AttnTileTuning& attn_tile_tuning() {
 }
 
 template <int G, int S, int W>
-int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp) {
+int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp, int order) {
   const int64_t max_tiles = (a.max_blocks * a.bs + kTileKeys - 1) / kTileKeys;
   const int maxparts = (int)((max_tiles + tpp - 1) / tpp);
   void* scr = nullptr;
@@ -3814,7 +3860,7 @@ int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp) {
   if (rc) return rc;
   float* part = reinterpret_cast<float*>(scr);
   hipLaunchKernelGGL((attn_tile_kernel<G, S, W>), dim3((unsigned)a.hkv, (unsigned)maxparts, (unsigned)a.nseq),
-                     dim3(64 * W), 0, st, a, part, maxparts, tpp);
+                     dim3(64 * W), 0, st, a, part, maxparts, tpp, order && a.nseq <= 64 ? 1 : 0);
   SWL_LAUNCH_CHECK("attn_tile_kernel launch");
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.hq, (unsigned)a.nseq), dim3(128), 0, st, a,
                      (const float*)part, maxparts, G, kTileKeys * tpp);
@@ -3825,10 +3871,10 @@ int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp) {
 template <int G, int S>
 int launch_attn_tile_s(const AttnArgs& a, hipStream_t st, const AttnTileTuning& t) {
   switch (t.waves) {  // 8 waves only with 2 stages (LDS: 160 KiB per CU)
-    case 2: return launch_attn_tile_sw<G, S, 2>(a, st, t.tpp);
-    case 4: return launch_attn_tile_sw<G, S, 4>(a, st, t.tpp);
-    case 8: return launch_attn_tile_sw<G, S, (S == 2 ? 8 : 4)>(a, st, t.tpp);
-    default: return launch_attn_tile_sw<G, S, 1>(a, st, t.tpp);
+    case 2: return launch_attn_tile_sw<G, S, 2>(a, st, t.tpp, t.order);
+    case 4: return launch_attn_tile_sw<G, S, 4>(a, st, t.tpp, t.order);
+    case 8: return launch_attn_tile_sw<G, S, (S == 2 ? 8 : 4)>(a, st, t.tpp, t.order);
+    default: return launch_attn_tile_sw<G, S, 1>(a, st, t.tpp, t.order);
   }
 }
 
