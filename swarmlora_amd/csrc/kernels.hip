@@ -1502,43 +1502,111 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 // workgroups together, from its L2.
 constexpr int PG_M = 256, PG_N = 256, PG_K = 64, PG_SLOTS = 2;
 constexpr int PG_ROW = PG_K * 2;                           // bytes of an LDS row
-constexpr int PG_STAGE_BYTES = (PG_M + PG_N) * PG_ROW;  // 64 KiB
 constexpr int PG_ELD = 64 + 4;                            // epilogue staging row (fp32)
-constexpr int PG_STAGE_AREA = PG_SLOTS * PG_STAGE_BYTES > 4 * 128 * PG_ELD * 4 ? PG_SLOTS * PG_STAGE_BYTES
-                                                                                : 4 * 128 * PG_ELD * 4;
-// then the tile's row table: output row pointer (8 bytes) and epilogue
-// adapter (4 bytes) of each of its 256 token rows
-constexpr int PG_LDS_BYTES = PG_STAGE_AREA + PG_M * 12;
+// NJ: 32-row MFMA tiles of tokens per wave, so 64 NJ token rows a tile (256
+// or 192; W always 256 columns).  Stage: W 256 rows, then x 64 NJ rows.
+template <int NJ>
+struct PgGeom {
+  static constexpr int MT = 64 * NJ;                        // token rows of a tile
+  static constexpr int STAGE = (PG_N + MT) * PG_ROW;        // 64 or 56 KiB
+  static constexpr int EPI = 4 * 32 * NJ * PG_ELD * 4;      // epilogue staging, 4 waves
+  static constexpr int AREA = PG_SLOTS * STAGE > EPI ? PG_SLOTS * STAGE : EPI;
+  // then the tile's row table: output row pointer (8 bytes) and epilogue
+  // adapter (4 bytes) of each of its token rows
+  static constexpr int LDS = AREA + PG_M * 12;
+};
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                  0, 0, 0);
 }
 
+template <int NJ>
 __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_m, int tiles, int per_xcd) {
-  // PG_SLOTS x [W 256 x 64 | x 256 x 64]; then the epilogue's 4 x [128][PG_ELD] fp32
+  // PG_SLOTS x [W 256 x 64 | x MT x 64]; then the epilogue's 4 x [TPW][PG_ELD] fp32
+  using Geo = PgGeom<NJ>;
+  constexpr int MT = Geo::MT, TPW = 32 * NJ, XR = MT / 4;  // token rows: tile, wave, DMA rows a wave
+  constexpr int MF = 4 * NJ, NR = 4 + NJ;                   // MFMAs and fragment reads per k-step
+  constexpr int NREQ = 8 + XR / 8;                          // DMA instructions a wave per stage
   extern __shared__ __attribute__((aligned(16))) char pg_lds[];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wv >> 1, wn = wv & 1;  // wave: tokens wm * 128.., columns wn * 128..
+  const int wm = wv >> 1, wn = wv & 1;  // wave: tokens wm * TPW.., columns wn * 128..
   const int lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (lin >= tiles) return;  // uniform over the workgroup
-  const int64_t m0 = (int64_t)(lin % tiles_m) * PG_M;
+  const int64_t m0 = (int64_t)(lin % tiles_m) * MT;
   const int64_t n0 = (int64_t)(lin / tiles_m) * PG_N;
   const int nk = (int)(a.K / PG_K);
 
-  // LDS-DMA of stage kt into slot s: wave w moves W rows 64 w .. + 64 and x
-  // rows 64 w .. + 64 (8 instructions each, 8 rows of 128 bytes an
-  // instruction); lane l of instruction i -> row 64 w + 8 i + l / 8, stored
-  // chunk l % 8, read from global chunk (l % 8) ^ (l / 8) ^ (i % 2)
+  f32x16 acc[4][NJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  const int fr = lane & 31, fh = lane >> 5;
+  auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[NJ]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+  };
+  // One instruction group of the main loop: MFMA t of the 2 MF of half a
+  // stage (k-step t / MF of the pair, tile ((t % MF) / NJ, t % NJ)), then at
+  // most one fragment read and one DMA request, then a scheduling fence, so
+  // the order written here is the order issued.  Spreading the requests
+  // keeps the CU's address queue from blocking the wave (a 1 KiB LDS-DMA
+  // request takes the queue about 16 cycles).
+  auto mfma_at = [&](u32x4 (&a0)[4], u32x4 (&b0)[NJ], u32x4 (&a1)[4], u32x4 (&b1)[NJ], int t) {
+    const int i = (t % MF) / NJ, j = t % NJ;
+    if (t < MF)
+      acc[i][j] = mfma32(a0[i], b0[j], acc[i][j]);
+    else
+      acc[i][j] = mfma32(a1[i], b1[j], acc[i][j]);
+  };
+
+  // the tile's row table in LDS, built while the first stages' DMA is in
+  // flight
+  bf16** rowtab = reinterpret_cast<bf16**>(pg_lds + Geo::AREA);
+  int* lidxtab = reinterpret_cast<int*>(pg_lds + Geo::AREA + PG_M * 8);
+  auto build_rowtab = [&]() {
+    {
+      const int64_t m = m0 + threadIdx.x;
+      bf16* yrow = nullptr;
+      int lidx = -1;
+      if (m < a.M) {
+        if (a.y) {
+          yrow = a.y + m * a.ldy;
+        } else {
+          const int sg = find_seg(a.out.off, a.out.n, m);
+          yrow = reinterpret_cast<bf16*>(const_cast<void*>(a.out.ptr[sg])) + (m - a.out.off[sg]) * a.N;
+          lidx = (a.has_lora && !a.lora_mfma) ? a.seg_lora[sg] : -1;
+        }
+      }
+      rowtab[threadIdx.x] = yrow;
+      lidxtab[threadIdx.x] = lidx;
+    }
+  };
+
+  // LDS-DMA of stage kt into slot s: wave w moves W rows 64 w .. + 64 (8
+  // instructions) and x rows XR w .. + XR (XR / 8), 8 rows of 128 bytes an
+  // instruction; lane l of instruction i -> row 8 i + l / 8 of the wave's,
+  // stored chunk l % 8, read from global chunk (l % 8) ^ (l / 8) ^ (i % 2)
+  // (the wave's first row is a multiple of 16)
   const int dr = lane >> 3;
   const bf16* wsrc[8];
-  const bf16* xsrc[8];
+  const bf16* xsrc[XR / 8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int64_t r = 64 * wv + 8 * i + dr;
     const int dc = (lane & 7) ^ dr ^ (i & 1);
     wsrc[i] = a.w + min(n0 + r, a.N - 1) * a.K + 8 * dc;
+  }
+#pragma unroll
+  for (int i = 0; i < XR / 8; ++i) {
+    const int64_t r = XR * wv + 8 * i + dr;
+    const int dc = (lane & 7) ^ dr ^ (i & 1);
     const int64_t mr = min(m0 + r, a.M - 1);
     if (a.x) {
       xsrc[i] = a.x + mr * a.K + 8 * dc;
@@ -1547,74 +1615,36 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       xsrc[i] = a.xin[sg] + (mr - a.out.off[sg]) * a.K + 8 * dc;
     }
   }
-  // half h: instructions 4 h .. 4 h + 3 of W and of x
-  auto issue = [&](int kt, int s, int h) {
-    char* st = pg_lds + s * PG_STAGE_BYTES;
+  // DMA instruction q of a stage (W 0..7, x 8..): into slot s
+  auto request_at = [&](int kt, int s, int q) {
+    char* st = pg_lds + s * Geo::STAGE;
+    if (q < 8)
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(wsrc[q] + (int64_t)kt * PG_K),
+                                       (lds_ptr)(st + (64 * wv + 8 * q) * PG_ROW), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[q - 8] + (int64_t)kt * PG_K),
+                                       (lds_ptr)(st + PG_N * PG_ROW + (XR * wv + 8 * (q - 8)) * PG_ROW), 16, 0, 0);
+  };
+  auto issue = [&](int kt, int s) {
 #pragma unroll
-    for (int i = 4 * h; i < 4 * h + 4; ++i) {
-      __builtin_amdgcn_global_load_lds((gbl_ptr)(wsrc[i] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[i] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + PG_N * PG_ROW + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
-    }
+    for (int q = 0; q < NREQ; ++q) request_at(kt, s, q);
   };
 
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   // fragment rows of this lane: W row wn * 128 + 32 i + l % 32, x row
-  // wm * 128 + 32 j + l % 32 (both = l % 32 modulo 32, so one swizzle);
+  // wm * TPW + 32 j + l % 32 (both = l % 32 modulo 32, so one swizzle);
   // k chunk 2 kk + l / 32 of the stage
-  const int fr = lane & 31, fh = lane >> 5;
   const int sw = (fr & 7) ^ ((fr >> 3) & 1);
-  auto frags = [&](int s, int kk, u32x4 (&fa)[4], u32x4 (&fb)[4]) {
-    const char* st = pg_lds + s * PG_STAGE_BYTES + fr * PG_ROW + (((2 * kk + fh) ^ sw) << 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa[i] = *reinterpret_cast<const u32x4*>(st + (wn * 128 + 32 * i) * PG_ROW);
-      fb[i] = *reinterpret_cast<const u32x4*>(st + PG_N * PG_ROW + (wm * 128 + 32 * i) * PG_ROW);
-    }
-  };
-  auto mma = [&](const u32x4 (&fa)[4], const u32x4 (&fb)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
-  };
-  // One instruction group of the main loop: MFMA t of the 32 of half a
-  // stage (k-step t / 16 of the pair, tile (t % 16) / 4, (t % 4)), then at
-  // most one fragment read and one DMA request, then a scheduling fence, so
-  // the order written here is the order issued.  Spreading the requests
-  // keeps the CU's address queue from blocking the wave (a 1 KiB LDS-DMA
-  // request takes the queue about 16 cycles).
-  auto mfma_at = [&](u32x4 (&a0)[4], u32x4 (&b0)[4], u32x4 (&a1)[4], u32x4 (&b1)[4], int t) {
-    const int i = (t & 15) >> 2, j = t & 3;
-    if (t < 16)
-      acc[i][j] = mfma32(a0[i], b0[j], acc[i][j]);
-    else
-      acc[i][j] = mfma32(a1[i], b1[j], acc[i][j]);
-  };
-  auto read_at = [&](int s, int kk, u32x4 (&fa_)[4], u32x4 (&fb_)[4], int idx) {
-    const char* st = pg_lds + s * PG_STAGE_BYTES + fr * PG_ROW + (((2 * kk + fh) ^ sw) << 4);
+  auto read_at = [&](int s, int kk, u32x4 (&fa_)[4], u32x4 (&fb_)[NJ], int idx) {
+    const char* st = pg_lds + s * Geo::STAGE + fr * PG_ROW + (((2 * kk + fh) ^ sw) << 4);
     if (idx < 4)
       fa_[idx] = *reinterpret_cast<const u32x4*>(st + (wn * 128 + 32 * idx) * PG_ROW);
     else
-      fb_[idx - 4] = *reinterpret_cast<const u32x4*>(st + PG_N * PG_ROW + (wm * 128 + 32 * (idx - 4)) * PG_ROW);
+      fb_[idx - 4] = *reinterpret_cast<const u32x4*>(st + PG_N * PG_ROW + (wm * TPW + 32 * (idx - 4)) * PG_ROW);
   };
-  auto request_at = [&](int kt, int s, int q) {  // DMA instruction q of 16 (W 0..7, x 8..15)
-    char* st = pg_lds + s * PG_STAGE_BYTES;
-    const int i = q & 7;
-    if (q < 8)
-      __builtin_amdgcn_global_load_lds((gbl_ptr)(wsrc[i] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
-    else
-      __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[i] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + PG_N * PG_ROW + (64 * wv + 8 * i) * PG_ROW), 16, 0, 0);
+  auto frags = [&](int s, int kk, u32x4 (&fa)[4], u32x4 (&fb)[NJ]) {
+#pragma unroll
+    for (int idx = 0; idx < NR; ++idx) read_at(s, kk, fa, fb, idx);
   };
 
   // Fragments of the four k-steps of a stage sit in four register sets,
@@ -1625,42 +1655,23 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
   // k-steps are read during the last two of stage kt.  The loop has no
   // branches: past the last stage the requests re-read stage nk - 1 into
   // the free slot, which only the discarded reads at the very end look at.
-  u32x4 fa[4][4], fb[4][4];
-  issue(0, 0, 0);
-  issue(0, 0, 1);
-  issue(min(1, nk - 1), 1, 0);
-  issue(min(1, nk - 1), 1, 1);
-  // row table (its loads overlap the first stages' DMA)
-  bf16** rowtab = reinterpret_cast<bf16**>(pg_lds + PG_STAGE_AREA);
-  int* lidxtab = reinterpret_cast<int*>(pg_lds + PG_STAGE_AREA + PG_M * 8);
-  {
-    const int64_t m = m0 + threadIdx.x;
-    bf16* yrow = nullptr;
-    int lidx = -1;
-    if (m < a.M) {
-      if (a.y) {
-        yrow = a.y + m * a.ldy;
-      } else {
-        const int sg = find_seg(a.out.off, a.out.n, m);
-        yrow = reinterpret_cast<bf16*>(const_cast<void*>(a.out.ptr[sg])) + (m - a.out.off[sg]) * a.N;
-        lidx = (a.has_lora && !a.lora_mfma) ? a.seg_lora[sg] : -1;
-      }
-    }
-    rowtab[threadIdx.x] = yrow;
-    lidxtab[threadIdx.x] = lidx;
-  }
-  __builtin_amdgcn_s_waitcnt(wait_vm_imm(16));
+  u32x4 fa[4][4], fb[4][NJ];
+  issue(0, 0);
+  issue(min(1, nk - 1), 1);
+  build_rowtab();
+  __builtin_amdgcn_s_waitcnt(wait_vm_imm(NREQ));
   lds_barrier();
   frags(0, 0, fa[0], fb[0]);
   frags(0, 1, fa[1], fb[1]);
   for (int kt = 0; kt < nk; ++kt) {
     const int s = kt & 1;
-    // k-steps 0, 1 of stage kt; reads of its k-steps 2, 3 during the first 16
+    // k-steps 0, 1 of stage kt; reads of its k-steps 2, 3 during the first
+    // 2 NR
 #pragma unroll
-    for (int t = 0; t < 32; ++t) {
+    for (int t = 0; t < 2 * MF; ++t) {
       mfma_at(fa[0], fb[0], fa[1], fb[1], t);
-      if (t < 8) read_at(s, 2, fa[2], fb[2], t);
-      else if (t < 16) read_at(s, 3, fa[3], fb[3], t - 8);
+      if (t < NR) read_at(s, 2, fa[2], fb[2], t);
+      else if (t < 2 * NR) read_at(s, 3, fa[3], fb[3], t - NR);
       __builtin_amdgcn_sched_barrier(0);
     }
     // this wave's DMA of stage kt + 1 has landed (it is all that is
@@ -1669,19 +1680,20 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     // k-steps 2, 3; reads of stage kt + 1's k-steps 0, 1 during the first
-    // 16, a DMA request of stage kt + 2 every second MFMA
+    // 2 NR, the NREQ DMA requests of stage kt + 2 spread over the 2 MF MFMAs
     const int nx = min(kt + 2, nk - 1);
 #pragma unroll
-    for (int t = 0; t < 32; ++t) {
+    for (int t = 0; t < 2 * MF; ++t) {
       mfma_at(fa[2], fb[2], fa[3], fb[3], t);
-      if (t < 8) read_at(s ^ 1, 0, fa[0], fb[0], t);
-      else if (t < 16) read_at(s ^ 1, 1, fa[1], fb[1], t - 8);
-      if ((t & 1) == 0) request_at(nx, s, t >> 1);
+      if (t < NR) read_at(s ^ 1, 0, fa[0], fb[0], t);
+      else if (t < 2 * NR) read_at(s ^ 1, 1, fa[1], fb[1], t - NR);
+      if (t == 0 || (t * NREQ) / (2 * MF) != ((t - 1) * NREQ) / (2 * MF)) request_at(nx, s, (t * NREQ) / (2 * MF));
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   // the requests past the last stage land before the LDS is reused
   __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
+
 
 
   // LoRA delta as extra k-steps: for every segment of the tile's token rows
@@ -1697,7 +1709,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       return bb;
     }();
     const int64_t bstart = blk_start_of(a.L, b);
-    for (int sg = find_seg(a.out.off, a.out.n, m0); sg < a.out.n && a.out.off[sg] < m0 + PG_M; ++sg) {
+    for (int sg = find_seg(a.out.off, a.out.n, m0); sg < a.out.n && a.out.off[sg] < m0 + MT; ++sg) {
       const int e = a.seg_lora[sg];
       if (e < 0) continue;
       const swl_lora_entry* ep = a.L.table + e;
@@ -1707,15 +1719,15 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       const int64_t lo = a.out.off[sg], hi = a.out.off[sg + 1];
       for (int q0 = 0; q0 < r; q0 += 16) {
         const int q = q0 + 8 * fh;
-        u32x4 fa[4], fb[4];
+        u32x4 fa[4], fb[NJ];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int64_t n = n0 + wn * 128 + 32 * i + fr;
           fa[i] = (n < a.N && q < r) ? ld16(bb + (n - bstart) * r + q) : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t m = m0 + wm * 128 + 32 * j + fr;
+        for (int j = 0; j < NJ; ++j) {
+          const int64_t m = m0 + wm * TPW + 32 * j + fr;
           u32x4 v = u32x4{0u, 0u, 0u, 0u};
           if (m >= lo && m < hi && q < r) {
             const float* up = a.L.u + m * a.L.u_ld + b * r + q;
@@ -1739,18 +1751,18 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
   // last reads), in two halves of the columns so each wave's share fits:
   // acc[i][j] element e of lane l is column 32 i + 8 (e / 4) + 4 (l / 32) +
   // e % 4 of the wave's 128, token 32 j + l % 32.  Wave w's half h lands in
-  // region w as [128 tokens][64 columns (+4 pad)] fp32; then thread t takes
+  // region w as [TPW tokens][64 columns (+4 pad)] fp32; then thread t takes
   // quads of four columns, 16 threads a token row, and finishes them
   // (bias, LoRA expand, one bf16 rounding, the segment's row).
   constexpr int ELD = PG_ELD;
-  float* reg = reinterpret_cast<float*>(pg_lds) + wv * 128 * ELD;
+  float* reg = reinterpret_cast<float*>(pg_lds) + wv * TPW * ELD;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     lds_barrier();  // the previous half's (or the k-loop's) reads are done
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int tok = 32 * j + fr, col = 32 * ii + 8 * q + 4 * fh;
@@ -1758,8 +1770,8 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
           *reinterpret_cast<f32x4*>(reg + tok * ELD + col) = f32x4{c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]};
         }
     lds_barrier();
-    // items: wave region w2 (tokens wm2 * 128, columns wn2 * 128 + 64 h),
-    // token row tr, quad cq; 4 x 128 x 16 items, 32 a thread, all of one
+    // items: wave region w2 (tokens wm2 * TPW, columns wn2 * 128 + 64 h),
+    // token row tr, quad cq; 4 x TPW x 16 items, 8 NJ a thread, all of one
     // thread's in the two column quads cq = t % 16 of the two wn2, whose
     // bias it loads once
     const int cq = threadIdx.x & 15;
@@ -1771,12 +1783,12 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       for (int e = 0; e < 4; ++e) bq[c][e] = (a.bias && n + e < a.N) ? bf2f(a.bias[n + e]) : 0.f;
     }
     auto item = [&](int k, bool lora) {
-      const int w2 = k >> 3, tr = ((threadIdx.x >> 4) + 16 * k) & 127;
-      const int row = (w2 >> 1) * 128 + tr;
+      const int w2 = k / (2 * NJ), tr = (threadIdx.x >> 4) + 16 * (k % (2 * NJ));
+      const int row = (w2 >> 1) * TPW + tr;
       const int64_t m = m0 + row;
       const int64_t n = n0 + (w2 & 1) * 128 + 64 * h + 4 * cq;
       if (m >= a.M || n >= a.N) return;
-      const f32x4 q4 = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * 128 + tr) * ELD + 4 * cq);
+      const f32x4 q4 = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * TPW + tr) * ELD + 4 * cq);
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = q4[e] + bq[w2 & 1][e];
@@ -1784,24 +1796,24 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
     };
     if (a.has_lora && !a.lora_mfma) {
       // the LoRA delta in the epilogue (per-quad loads of u and lora_B)
-      for (int k = 0; k < 32; ++k) item(k, true);
+      for (int k = 0; k < 8 * NJ; ++k) item(k, true);
     } else {
-      // k = 8 w2 + kk: the 8 staged quads and row pointers of a region are
-      // read together, then stored
+      // k = 2 NJ w2 + kk: the 2 NJ staged quads and row pointers of a
+      // region are read together, then stored
 #pragma unroll
       for (int w2 = 0; w2 < 4; ++w2) {
-        f32x4 q[8];
-        bf16* rp[8];
+        f32x4 q[2 * NJ];
+        bf16* rp[2 * NJ];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
+        for (int kk = 0; kk < 2 * NJ; ++kk) {
           const int tr = (threadIdx.x >> 4) + 16 * kk;
-          q[kk] = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * 128 + tr) * ELD + 4 * cq);
-          rp[kk] = rowtab[(w2 >> 1) * 128 + tr];
+          q[kk] = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * TPW + tr) * ELD + 4 * cq);
+          rp[kk] = rowtab[(w2 >> 1) * TPW + tr];
         }
         const int64_t n = n0 + (w2 & 1) * 128 + 64 * h + 4 * cq;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const int64_t m = m0 + (w2 >> 1) * 128 + (threadIdx.x >> 4) + 16 * kk;
+        for (int kk = 0; kk < 2 * NJ; ++kk) {
+          const int64_t m = m0 + (w2 >> 1) * TPW + (threadIdx.x >> 4) + 16 * kk;
           if (m < a.M && n < a.N) {
             float v[4];
 #pragma unroll
@@ -3726,6 +3738,17 @@ bool prefill_uses_tiled(int64_t K) {
   return use_tiled || K % PG_K != 0 || K < PG_K;
 }
 
+template <int NJ>
+int launch_gemm256(const TiledArgs& a, int tiles_m, int tiles, int per_xcd, hipStream_t st) {
+  constexpr size_t lds = PgGeom<NJ>::LDS;
+  static size_t allowed = 0;
+  int rc = allow_lds(gemm256_kernel<NJ>, lds, &allowed);
+  if (rc) return rc;
+  hipLaunchKernelGGL(gemm256_kernel<NJ>, dim3((unsigned)(8 * per_xcd)), dim3(256), lds, st, a, tiles_m, tiles,
+                     per_xcd);
+  return SWL_OK;
+}
+
 int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
   if (prefill_uses_tiled(a.K)) {
     const dim3 grid((unsigned)((a.N + TN - 1) / TN), (unsigned)((a.M + TM - 1) / TM));
@@ -3733,14 +3756,24 @@ int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
     SWL_LAUNCH_CHECK("tiled_kernel launch");
     return SWL_OK;
   }
-  const int tiles_m = (int)((a.M + PG_M - 1) / PG_M), tiles_n = (int)((a.N + PG_N - 1) / PG_N);
+  // token rows a tile: 256, or 192 where the grid then covers the CUs in
+  // fewer tile times (a 192-row tile measured at ~0.9 of a 256-row one: the
+  // W side streams the same bytes): the O and Down rounds at 2325 rows have
+  // 160 tiles of 256 for 256 CUs, 208 of 192 (146 -> 133 us, 370 -> 335)
+  const int tiles_n = (int)((a.N + PG_N - 1) / PG_N);
+  auto tiles_of = [&](int mt) { return (int)((a.M + mt - 1) / mt) * tiles_n; };
+  const int64_t cus = cu_count();
+  auto cost = [&](int nj) { return (double)((tiles_of(64 * nj) + cus - 1) / cus) * (nj == 3 ? 0.9 : 1.0); };
+  static const int forced = [] {
+    const char* e = getenv("SWL_PREFILL_NJ");
+    return e ? atoi(e) : 0;
+  }();
+  const int nj = (forced == 3 || forced == 4) ? forced : (cost(3) < cost(4) ? 3 : 4);
+  const int tiles_m = (int)((a.M + 64 * nj - 1) / (64 * nj));
   const int tiles = tiles_m * tiles_n;
   const int per_xcd = (tiles + 7) / 8;
-  const size_t lds = PG_LDS_BYTES;
-  static size_t allowed = 0;
-  int rc = allow_lds(gemm256_kernel, lds, &allowed);
+  const int rc = nj == 3 ? launch_gemm256<3>(a, tiles_m, tiles, per_xcd, st) : launch_gemm256<4>(a, tiles_m, tiles, per_xcd, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm256_kernel, dim3((unsigned)(8 * per_xcd)), dim3(256), lds, st, a, tiles_m, tiles, per_xcd);
   SWL_LAUNCH_CHECK("gemm256_kernel launch");
   return SWL_OK;
 }
