@@ -1512,8 +1512,16 @@ struct PgGeom {
   static constexpr int EPI = 4 * 32 * NJ * PG_ELD * 4;      // epilogue staging, 4 waves
   static constexpr int AREA = PG_SLOTS * STAGE > EPI ? PG_SLOTS * STAGE : EPI;
   // then the tile's row table: output row pointer (8 bytes) and epilogue
-  // adapter (4 bytes) of each of its token rows
-  static constexpr int LDS = AREA + PG_M * 12;
+  // adapter (4 bytes) of each of its token rows; then the LoRA entries
+  // (lora_B block pointer, rank, scale) of the segments the tile overlaps
+  static constexpr int LDS = AREA + PG_M * 12 + kMaxSeg * 16;
+};
+
+// LoRA entry of one segment of a prefill tile, as the k-step loop reads it
+struct PgSegLora {
+  const bf16* b;  // the adapter's lora_B rows of the tile's column block
+  int32_t rank;   // 0: no adapter
+  float scale;
 };
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -1656,9 +1664,32 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
   // branches: past the last stage the requests re-read stage nk - 1 into
   // the free slot, which only the discarded reads at the very end look at.
   u32x4 fa[4][4], fb[4][NJ];
+  // LoRA entries of the segments the tile overlaps, requested ahead of the
+  // DMA (so that waiting for them does not wait for it) and put in LDS
+  // after it: thread t takes segment sg0 + t
+  PgSegLora* segl = reinterpret_cast<PgSegLora*>(pg_lds + Geo::AREA + PG_M * 12);
+  const bool lora_k = a.has_lora && a.lora_mfma;
+  int lb = 0, sg0 = 0, nseg = 0;
+  PgSegLora my{nullptr, 0, 0.f};
+  if (lora_k) {
+#pragma unroll
+    for (int i = 1; i < SWL_MAX_LORA_BLOCKS; ++i)
+      if (i < a.L.nblk && n0 >= a.L.blk_start[i]) lb = i;
+    sg0 = find_seg(a.out.off, a.out.n, m0);
+    nseg = find_seg(a.out.off, a.out.n, min<int64_t>(m0 + MT, a.M) - 1) - sg0 + 1;
+    const int e = (int)threadIdx.x < nseg ? a.seg_lora[sg0 + threadIdx.x] : -1;
+    if (e >= 0) {
+      const char* ep = reinterpret_cast<const char*>(a.L.table + e);
+      using bptr = const bf16*;
+      my.b = *(const __attribute__((address_space(1))) bptr*)(ep + offsetof(swl_lora_entry, b) + lb * sizeof(void*));
+      my.rank = *(const __attribute__((address_space(1))) int32_t*)(ep + offsetof(swl_lora_entry, rank));
+      my.scale = *(const __attribute__((address_space(1))) float*)(ep + offsetof(swl_lora_entry, scale));
+    }
+  }
   issue(0, 0);
   issue(min(1, nk - 1), 1);
   build_rowtab();
+  if ((int)threadIdx.x < nseg) segl[threadIdx.x] = my;
   __builtin_amdgcn_s_waitcnt(wait_vm_imm(NREQ));
   lds_barrier();
   frags(0, 0, fa[0], fb[0]);
@@ -1699,51 +1730,76 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
   // LoRA delta as extra k-steps: for every segment of the tile's token rows
   // that has an adapter, A = the adapter's lora_B rows of the tile's
   // columns (k = rank), B = the segment's shrink rows u * scale rounded to
-  // bf16 (zero for the other segments' rows), 16 ranks a step
-  if (a.has_lora && a.lora_mfma) {
-    const int b = [&] {
-      int bb = 0;
-#pragma unroll
-      for (int i = 1; i < SWL_MAX_LORA_BLOCKS; ++i)
-        if (i < a.L.nblk && n0 >= a.L.blk_start[i]) bb = i;
-      return bb;
-    }();
-    const int64_t bstart = blk_start_of(a.L, b);
-    for (int sg = find_seg(a.out.off, a.out.n, m0); sg < a.out.n && a.out.off[sg] < m0 + MT; ++sg) {
-      const int e = a.seg_lora[sg];
-      if (e < 0) continue;
-      const swl_lora_entry* ep = a.L.table + e;
-      const int r = ep->rank;
-      const float scale = ep->scale;
-      const bf16* bb = reinterpret_cast<const bf16*>(ep->b[b]);
-      const int64_t lo = a.out.off[sg], hi = a.out.off[sg + 1];
-      for (int q0 = 0; q0 < r; q0 += 16) {
-        const int q = q0 + 8 * fh;
-        u32x4 fa[4], fb[NJ];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t n = n0 + wn * 128 + 32 * i + fr;
-          fa[i] = (n < a.N && q < r) ? ld16(bb + (n - bstart) * r + q) : u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int64_t m = m0 + wm * TPW + 32 * j + fr;
-          u32x4 v = u32x4{0u, 0u, 0u, 0u};
-          if (m >= lo && m < hi && q < r) {
-            const float* up = a.L.u + m * a.L.u_ld + b * r + q;
-            const f32x4 u0 = *reinterpret_cast<const f32x4*>(up), u1 = *reinterpret_cast<const f32x4*>(up + 4);
-            bf16x8 o;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              o[t] = f2bf(u0[t] * scale);
-              o[4 + t] = f2bf(u1[t] * scale);
-            }
-            v = __builtin_bit_cast(u32x4, o);
-          }
-          fb[j] = v;
-        }
-        mma(fa, fb);
+  // bf16 (zero for the other segments' rows), 16 ranks a step.  The steps
+  // run as one loop over (segment, rank step) with the next step's loads in
+  // flight while the current one's MFMAs issue (two register sets taking
+  // turns), the entries read from the tile's LDS table.
+  if (lora_k) {
+    const int64_t bstart = blk_start_of(a.L, lb);
+    auto first = [&](int i) {  // first segment from i with an adapter
+      while (i < nseg && segl[i].rank <= 0) ++i;
+      return i;
+    };
+    auto advance = [&](int& i, int& q0) {
+      q0 += 16;
+      if (q0 >= segl[i].rank) {
+        q0 = 0;
+        i = first(i + 1);
       }
+    };
+    auto load = [&](int i, int q0, u32x4 (&fa_)[4], u32x4 (&u_)[NJ][2]) {
+      const PgSegLora e = segl[i];
+      const int r = e.rank, q = q0 + 8 * fh;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int64_t n = n0 + wn * 128 + 32 * i4 + fr;
+        fa_[i4] = (n < a.N && q < r) ? ld16(e.b + (n - bstart) * r + q) : u32x4{0u, 0u, 0u, 0u};
+      }
+      const int64_t lo = a.out.off[sg0 + i], hi = a.out.off[sg0 + i + 1];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t m = m0 + wm * TPW + 32 * j + fr;
+        if (m >= lo && m < hi && q < r) {
+          const float* up = a.L.u + m * a.L.u_ld + lb * r + q;
+          u_[j][0] = ld16(up);
+          u_[j][1] = ld16(up + 4);
+        } else {
+          u_[j][0] = u_[j][1] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    };
+    auto use = [&](int i, const u32x4 (&fa_)[4], const u32x4 (&u_)[NJ][2]) {
+      const float scale = segl[i].scale;
+      u32x4 fb_[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const f32x4 u0 = __builtin_bit_cast(f32x4, u_[j][0]), u1 = __builtin_bit_cast(f32x4, u_[j][1]);
+        bf16x8 o;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          o[t] = f2bf(u0[t] * scale);
+          o[4 + t] = f2bf(u1[t] * scale);
+        }
+        fb_[j] = __builtin_bit_cast(u32x4, o);
+      }
+      mma(fa_, fb_);
+    };
+    u32x4 xa[4], xu[NJ][2], ya[4], yu[NJ][2];
+    int ci = first(0), cq = 0;
+    if (ci < nseg) load(ci, cq, xa, xu);
+    while (ci < nseg) {
+      int ni = ci, nq = cq;
+      advance(ni, nq);
+      if (ni < nseg) load(ni, nq, ya, yu);
+      use(ci, xa, xu);
+      ci = ni;
+      cq = nq;
+      if (ci >= nseg) break;
+      advance(ni, nq);
+      if (ni < nseg) load(ni, nq, xa, xu);
+      use(ci, ya, yu);
+      ci = ni;
+      cq = nq;
     }
   }
 
