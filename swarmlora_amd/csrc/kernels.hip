@@ -1503,13 +1503,14 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 constexpr int PG_M = 256, PG_N = 256, PG_K = 64, PG_SLOTS = 2;
 constexpr int PG_ROW = PG_K * 2;                           // bytes of an LDS row
 constexpr int PG_ELD = 64 + 4;                            // epilogue staging row (fp32)
-// NJ: 32-row MFMA tiles of tokens per wave, so 64 NJ token rows a tile (256
-// or 192; W always 256 columns).  Stage: W 256 rows, then x 64 NJ rows.
-template <int NJ>
+// Waves 2 WM: two along the columns (128 each), WM along the token rows; NJ:
+// 32-row MFMA tiles of tokens per wave, so 32 WM NJ token rows a tile (256
+// or 192; W always 256 columns).  Stage: W 256 rows, then x MT rows.
+template <int NJ, int WM>
 struct PgGeom {
-  static constexpr int MT = 64 * NJ;                        // token rows of a tile
+  static constexpr int MT = 32 * WM * NJ;                   // token rows of a tile
   static constexpr int STAGE = (PG_N + MT) * PG_ROW;        // 64 or 56 KiB
-  static constexpr int EPI = 4 * 32 * NJ * PG_ELD * 4;      // epilogue staging, 4 waves
+  static constexpr int EPI = 2 * WM * 32 * NJ * PG_ELD * 4; // epilogue staging, one region a wave
   static constexpr int AREA = PG_SLOTS * STAGE > EPI ? PG_SLOTS * STAGE : EPI;
   // then the tile's row table: output row pointer (8 bytes) and epilogue
   // adapter (4 bytes) of each of its token rows; then the LoRA entries
@@ -1529,13 +1530,16 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                  0, 0, 0);
 }
 
-template <int NJ>
-__global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_m, int tiles, int per_xcd) {
-  // PG_SLOTS x [W 256 x 64 | x MT x 64]; then the epilogue's 4 x [TPW][PG_ELD] fp32
-  using Geo = PgGeom<NJ>;
-  constexpr int MT = Geo::MT, TPW = 32 * NJ, XR = MT / 4;  // token rows: tile, wave, DMA rows a wave
-  constexpr int MF = 4 * NJ, NR = 4 + NJ;                   // MFMAs and fragment reads per k-step
-  constexpr int NREQ = 8 + XR / 8;                          // DMA instructions a wave per stage
+template <int NJ, int WM>
+__global__ __launch_bounds__(128 * WM, 1) void gemm256_kernel(TiledArgs a, int tiles_m, int tiles, int per_xcd) {
+  // PG_SLOTS x [W 256 x 64 | x MT x 64]; then the epilogue's WAVES x [TPW][PG_ELD] fp32
+  using Geo = PgGeom<NJ, WM>;
+  constexpr int WAVES = 2 * WM;
+  constexpr int MT = Geo::MT, TPW = 32 * NJ, XR = MT / WAVES;  // token rows: tile, wave, DMA rows a wave
+  constexpr int WR = PG_N / WAVES;                              // W rows a wave moves per stage
+  constexpr int MF = 4 * NJ, NR = 4 + NJ;                       // MFMAs and fragment reads per k-step
+  constexpr int NREQ = WR / 8 + XR / 8;                         // DMA instructions a wave per stage
+  static_assert(PG_N % (8 * WAVES) == 0 && MT % (8 * WAVES) == 0, "the waves' DMA rows must cover the stage");
   extern __shared__ __attribute__((aligned(16))) char pg_lds[];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1579,7 +1583,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
   bf16** rowtab = reinterpret_cast<bf16**>(pg_lds + Geo::AREA);
   int* lidxtab = reinterpret_cast<int*>(pg_lds + Geo::AREA + PG_M * 8);
   auto build_rowtab = [&]() {
-    {
+    if (threadIdx.x < PG_M) {
       const int64_t m = m0 + threadIdx.x;
       bf16* yrow = nullptr;
       int lidx = -1;
@@ -1597,17 +1601,17 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
     }
   };
 
-  // LDS-DMA of stage kt into slot s: wave w moves W rows 64 w .. + 64 (8
-  // instructions) and x rows XR w .. + XR (XR / 8), 8 rows of 128 bytes an
+  // LDS-DMA of stage kt into slot s: wave w moves W rows WR w .. + WR (WR /
+  // 8 instructions) and x rows XR w .. + XR (XR / 8), 8 rows of 128 bytes an
   // instruction; lane l of instruction i -> row 8 i + l / 8 of the wave's,
   // stored chunk l % 8, read from global chunk (l % 8) ^ (l / 8) ^ (i % 2)
   // (the wave's first row is a multiple of 16)
   const int dr = lane >> 3;
-  const bf16* wsrc[8];
+  const bf16* wsrc[WR / 8];
   const bf16* xsrc[XR / 8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t r = 64 * wv + 8 * i + dr;
+  for (int i = 0; i < WR / 8; ++i) {
+    const int64_t r = WR * wv + 8 * i + dr;
     const int dc = (lane & 7) ^ dr ^ (i & 1);
     wsrc[i] = a.w + min(n0 + r, a.N - 1) * a.K + 8 * dc;
   }
@@ -1623,15 +1627,16 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       xsrc[i] = a.xin[sg] + (mr - a.out.off[sg]) * a.K + 8 * dc;
     }
   }
-  // DMA instruction q of a stage (W 0..7, x 8..): into slot s
+  // DMA instruction q of a stage (W 0 .. WR / 8 - 1, then x): into slot s
   auto request_at = [&](int kt, int s, int q) {
     char* st = pg_lds + s * Geo::STAGE;
-    if (q < 8)
+    constexpr int QW = WR / 8;
+    if (q < QW)
       __builtin_amdgcn_global_load_lds((gbl_ptr)(wsrc[q] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + (64 * wv + 8 * q) * PG_ROW), 16, 0, 0);
+                                       (lds_ptr)(st + (WR * wv + 8 * q) * PG_ROW), 16, 0, 0);
     else
-      __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[q - 8] + (int64_t)kt * PG_K),
-                                       (lds_ptr)(st + PG_N * PG_ROW + (XR * wv + 8 * (q - 8)) * PG_ROW), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_ptr)(xsrc[q - QW] + (int64_t)kt * PG_K),
+                                       (lds_ptr)(st + PG_N * PG_ROW + (XR * wv + 8 * (q - QW)) * PG_ROW), 16, 0, 0);
   };
   auto issue = [&](int kt, int s) {
 #pragma unroll
@@ -1827,10 +1832,12 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
         }
     lds_barrier();
     // items: wave region w2 (tokens wm2 * TPW, columns wn2 * 128 + 64 h),
-    // token row tr, quad cq; 4 x TPW x 16 items, 8 NJ a thread, all of one
+    // token row tr, quad cq; WAVES x TPW x 16 items, 8 NJ a thread (row
+    // group t / 16 of RG, rows rg + RG kk of each region), all of one
     // thread's in the two column quads cq = t % 16 of the two wn2, whose
     // bias it loads once
     const int cq = threadIdx.x & 15;
+    constexpr int RG = 4 * WAVES, KK = TPW / RG;  // row groups; rows of a region a thread takes
     float bq[2][4];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -1839,7 +1846,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       for (int e = 0; e < 4; ++e) bq[c][e] = (a.bias && n + e < a.N) ? bf2f(a.bias[n + e]) : 0.f;
     }
     auto item = [&](int k, bool lora) {
-      const int w2 = k / (2 * NJ), tr = (threadIdx.x >> 4) + 16 * (k % (2 * NJ));
+      const int w2 = k / KK, tr = (threadIdx.x >> 4) + RG * (k % KK);
       const int row = (w2 >> 1) * TPW + tr;
       const int64_t m = m0 + row;
       const int64_t n = n0 + (w2 & 1) * 128 + 64 * h + 4 * cq;
@@ -1854,22 +1861,22 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(TiledArgs a, int tiles_
       // the LoRA delta in the epilogue (per-quad loads of u and lora_B)
       for (int k = 0; k < 8 * NJ; ++k) item(k, true);
     } else {
-      // k = 2 NJ w2 + kk: the 2 NJ staged quads and row pointers of a
-      // region are read together, then stored
+      // k = KK w2 + kk: the KK staged quads and row pointers of a region
+      // are read together, then stored
 #pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) {
-        f32x4 q[2 * NJ];
-        bf16* rp[2 * NJ];
+      for (int w2 = 0; w2 < WAVES; ++w2) {
+        f32x4 q[KK];
+        bf16* rp[KK];
 #pragma unroll
-        for (int kk = 0; kk < 2 * NJ; ++kk) {
-          const int tr = (threadIdx.x >> 4) + 16 * kk;
+        for (int kk = 0; kk < KK; ++kk) {
+          const int tr = (threadIdx.x >> 4) + RG * kk;
           q[kk] = *reinterpret_cast<const f32x4*>(reinterpret_cast<float*>(pg_lds) + (w2 * TPW + tr) * ELD + 4 * cq);
           rp[kk] = rowtab[(w2 >> 1) * TPW + tr];
         }
         const int64_t n = n0 + (w2 & 1) * 128 + 64 * h + 4 * cq;
 #pragma unroll
-        for (int kk = 0; kk < 2 * NJ; ++kk) {
-          const int64_t m = m0 + (w2 >> 1) * TPW + (threadIdx.x >> 4) + 16 * kk;
+        for (int kk = 0; kk < KK; ++kk) {
+          const int64_t m = m0 + (w2 >> 1) * TPW + (threadIdx.x >> 4) + RG * kk;
           if (m < a.M && n < a.N) {
             float v[4];
 #pragma unroll
@@ -3794,14 +3801,14 @@ bool prefill_uses_tiled(int64_t K) {
   return use_tiled || K % PG_K != 0 || K < PG_K;
 }
 
-template <int NJ>
+template <int NJ, int WM>
 int launch_gemm256(const TiledArgs& a, int tiles_m, int tiles, int per_xcd, hipStream_t st) {
-  constexpr size_t lds = PgGeom<NJ>::LDS;
+  constexpr size_t lds = PgGeom<NJ, WM>::LDS;
   static size_t allowed = 0;
-  int rc = allow_lds(gemm256_kernel<NJ>, lds, &allowed);
+  int rc = allow_lds(gemm256_kernel<NJ, WM>, lds, &allowed);
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm256_kernel<NJ>, dim3((unsigned)(8 * per_xcd)), dim3(256), lds, st, a, tiles_m, tiles,
-                     per_xcd);
+  hipLaunchKernelGGL((gemm256_kernel<NJ, WM>), dim3((unsigned)(8 * per_xcd)), dim3(128 * WM), lds, st, a, tiles_m,
+                     tiles, per_xcd);
   return SWL_OK;
 }
 
@@ -3828,7 +3835,15 @@ int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
   const int tiles_m = (int)((a.M + 64 * nj - 1) / (64 * nj));
   const int tiles = tiles_m * tiles_n;
   const int per_xcd = (tiles + 7) / 8;
-  const int rc = nj == 3 ? launch_gemm256<3>(a, tiles_m, tiles, per_xcd, st) : launch_gemm256<4>(a, tiles_m, tiles, per_xcd, st);
+  static const int waves = [] {
+    const char* e = getenv("SWL_PREFILL_WAVES");
+    return e ? atoi(e) : 4;
+  }();
+  int rc;
+  if (waves == 8)  // 8 waves for 256-row tiles (4 x 2 waves of 64 x 128); 192-row tiles keep 4
+    rc = nj == 3 ? launch_gemm256<3, 2>(a, tiles_m, tiles, per_xcd, st) : launch_gemm256<2, 4>(a, tiles_m, tiles, per_xcd, st);
+  else
+    rc = nj == 3 ? launch_gemm256<3, 2>(a, tiles_m, tiles, per_xcd, st) : launch_gemm256<4, 2>(a, tiles_m, tiles, per_xcd, st);
   if (rc) return rc;
   SWL_LAUNCH_CHECK("gemm256_kernel launch");
   return SWL_OK;
