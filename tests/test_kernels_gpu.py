@@ -410,6 +410,22 @@ def test_paged_attention_decode_block_sizes(dev, bs):
     assert bits_equal(got_state[3], ref_state[3]), "v pages must be a bit-exact append"
 
 
+@pytest.mark.parametrize("nseq", [64, 70])
+def test_paged_attention_decode_many_sequences(dev, nseq):
+    """Decode over many ragged contexts: up to 64 sequences take the
+    size-ordered part numbering (full parts first, then the partial last
+    parts by length), more take the sequence-major one.  Contexts include
+    0 keys, exactly one and two full 256-key parts (255 and 511 cached keys:
+    the new key completes the part), one key past a part, and the rest drawn
+    at random up to 700."""
+    g = torch.Generator().manual_seed(77 + nseq)
+    ctx0 = torch.randint(0, 701, (nseq,), generator=g).tolist()
+    ctx0[:5] = [0, 255, 511, 256, 700]
+    out, want, got_state, ref_state = _attn_case(dev, nseq, 1, ctx0, seed=21)
+    assert_close(out, want, what=f"attention over {nseq} sequences")
+    assert bits_equal(got_state[3], ref_state[3]), "v pages must be a bit-exact append"
+
+
 def test_paged_attention_single_key_returns_v(dev):
     """ctx = 1: softmax over one key is 1, so the output is v exactly."""
     out, want, (q_d, k_d, kc_d, vc_d), _ = _attn_case(dev, 2, 1, [0, 0])
