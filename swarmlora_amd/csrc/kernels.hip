@@ -3657,6 +3657,13 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
       // them (half the fp32 partials; Gate+Up 71.7 -> 70.5 us with its
       // epilogue at 4 slices of 32 steps)
       if (tu.nks == 0 && n_ks >= 2 && lds_of(n_ks / 2) <= 160 * 1024) n_ks /= 2;
+    } else if (tu.nks == 0 && n_ks >= 32 && lds_of(n_ks / 2) <= 160 * 1024) {
+      // long-K rounds (Down at 28 rows: 32 slices of 14 steps) take half as
+      // many slices of twice the steps, 16 k-steps in flight: half the fp32
+      // partials (Down 29.2 + 7.3 -> 28.9 + 6.3 us with its epilogue, 6.11 ->
+      // 6.04 ms per config-4 step)
+      kd = 16;
+      n_ks /= 2;
     }
   }
   a.n_ks = (int)n_ks;
