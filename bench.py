@@ -79,12 +79,15 @@ def parse():
                          "print lines of their own")
     ap.add_argument("--ipc-workers", type=int, default=8,
                     help="drop-in leg of the decode line: worker processes (at most 8; with the aggregator's "
-                         "process at most 9 processes use the GPU)")
+                         "process and this one at most 10 processes use the GPU)")
     ap.add_argument("--no-ipc", action="store_true", help="decode: skip the drop-in (multi-process) leg")
-    ap.add_argument("--ipc-layers", type=int, default=4, help="ipc: 8B-shaped layers")
-    ap.add_argument("--ipc-tokens", type=int, default=8, help="ipc: decode tokens per worker (after 2 warm-up)")
-    ap.add_argument("--ipc-pooled", action="store_true",
-                    help="ipc: adapters pooled in the aggregator (delta added in the round) instead of on the worker")
+    ap.add_argument("--ipc-layers", type=int, default=32, help="drop-in leg: 8B-shaped layers")
+    ap.add_argument("--ipc-tokens", type=int, default=6, help="drop-in leg: decode tokens per timed window")
+    ap.add_argument("--ipc-reps", type=int, default=3, help="drop-in leg: timed windows (the median is reported)")
+    ap.add_argument("--ipc-modes", default="host_sync,host_sync_pooled",
+                    help="drop-in leg: comma list of " + ", ".join(IPC_MODES) + " (the decode line's default: the "
+                         "reference's protocol with the worker's own LoRA, then with adapters pooled in the "
+                         "aggregator's rounds)")
     return ap.parse_args()
 
 
@@ -284,9 +287,18 @@ def prefill(args):
     print(json.dumps(line), flush=True)
 
 
-def _ipc_worker(shm_name, claim, wid, layers, n_tok, gpu_ordered, pooled, out):
-    """One worker process of the ipc workload: 8B-shaped layer modules with a
-    rank-16 adapter, decoding n_tok + 2 tokens through the aggregator."""
+IPC_WARM, IPC_COOL = 2, 2
+
+
+def _ipc_worker(shm_name, claim, wid, all_sids, start, layers, n_tok, reps, gpu_ordered, pooled, out):
+    """One worker process of the drop-in path: 8B-shaped layer modules with a
+    rank-16 adapter (on the worker, or pooled in the aggregator), decoding
+    through the aggregator.  All workers join together (barrier `start`), run
+    untimed tokens until every slot of the run is active, then IPC_WARM
+    tokens, `reps` timed windows of n_tok tokens, IPC_COOL tokens and two
+    stage-timed tokens, so that no timed window overlaps another worker's
+    joining, warm-up or stage-synchronised tokens (the rounds run in lock
+    step: one slow worker slows every round)."""
     try:
         from types import SimpleNamespace
         import torch
@@ -296,7 +308,7 @@ def _ipc_worker(shm_name, claim, wid, layers, n_tok, gpu_ordered, pooled, out):
         from swarmlora_amd.worker.batched_ops import BatchedAggregatorOps, SlotState
         from swarmlora_amd.worker.engine import LayerModules, StageTimer, WorkerEngine
         from swarmlora_amd.worker.model_builder import (FastLoRAModule, FusedLoRA, SyncFusedGateUp, SyncFusedQKV,
-                                                        SyncRemoteLoRALinear)
+                                                        SyncRemoteLinear, SyncRemoteLoRALinear)
         from swarmlora_amd.worker.paged_attention import PagedKVCache, RotaryInvFreq, build_vllm_cos_sin_cache
         dev = torch.device("cuda:0")
         torch.cuda.set_device(0)
@@ -307,42 +319,59 @@ def _ipc_worker(shm_name, claim, wid, layers, n_tok, gpu_ordered, pooled, out):
         sid = claim["slot_id"]
         ub.open_slot(sid, claim["input_handle"], claim["output_handle"], claim["input_buffer_size"],
                      claim["output_buffer_size"])
-        ad = synthetic_adapter(s, dev, seed=1000 + wid)
         ones = torch.ones(s.hidden, dtype=torch.bfloat16, device=dev)
         mods = []
-        for li in range(layers):
-            m = {p: FastLoRAModule(a.contiguous(), b.contiguous(), s.scale) for p, (a, b) in ad[li].items()}
-            mods.append(LayerModules(ones, ones,
-                                     SyncFusedQKV(li, [s.hidden, kvd, kvd], FusedLoRA([m["q"], m["k"], m["v"]],
-                                                                                      [s.hidden, kvd, kvd], dev,
-                                                                                      torch.bfloat16)),
-                                     SyncRemoteLoRALinear(3, li, s.hidden, m["o"]),
-                                     SyncFusedGateUp(li, [s.inter, s.inter], FusedLoRA([m["gate"], m["up"]],
-                                                                                       [s.inter, s.inter], dev,
-                                                                                       torch.bfloat16)),
-                                     SyncRemoteLoRALinear(6, li, s.hidden, m["down"])))
-        kv = PagedKVCache(layers, s.kv_heads, s.head_dim, s.block_size, 1, 64, dev, torch.bfloat16)
-        cs = build_vllm_cos_sin_cache(RotaryInvFreq(s.head_dim, s.theta), 64, dev, torch.bfloat16)
+        if pooled:
+            # the aggregator adds the delta in its rounds: plain remote modules
+            for li in range(layers):
+                mods.append(LayerModules(ones, ones, SyncFusedQKV(li, [s.hidden, kvd, kvd], None),
+                                         SyncRemoteLinear(3, li, s.hidden), SyncFusedGateUp(li, [s.inter, s.inter], None),
+                                         SyncRemoteLinear(6, li, s.hidden)))
+        else:
+            ad = synthetic_adapter(s, dev, seed=1000 + wid)
+            for li in range(layers):
+                m = {p: FastLoRAModule(a.contiguous(), b.contiguous(), s.scale) for p, (a, b) in ad[li].items()}
+                mods.append(LayerModules(ones, ones,
+                                         SyncFusedQKV(li, [s.hidden, kvd, kvd], FusedLoRA([m["q"], m["k"], m["v"]],
+                                                                                          [s.hidden, kvd, kvd], dev,
+                                                                                          torch.bfloat16)),
+                                         SyncRemoteLoRALinear(3, li, s.hidden, m["o"]),
+                                         SyncFusedGateUp(li, [s.inter, s.inter], FusedLoRA([m["gate"], m["up"]],
+                                                                                           [s.inter, s.inter], dev,
+                                                                                           torch.bfloat16)),
+                                         SyncRemoteLoRALinear(6, li, s.hidden, m["down"])))
+        max_tok = 64 + IPC_WARM + reps * n_tok + IPC_COOL + 2
+        kv = PagedKVCache(layers, s.kv_heads, s.head_dim, s.block_size, 1, max_tok, dev, torch.bfloat16)
+        cs = build_vllm_cos_sin_cache(RotaryInvFreq(s.head_dim, s.theta), max_tok, dev, torch.bfloat16)
         bops = BatchedAggregatorOps(SimpleNamespace(base_client=SimpleNamespace(hidden_dim=s.hidden)), wid, 15,
                                     pooled_adapter=wid if pooled else None, gpu_ordered=gpu_ordered)
         eng = WorkerEngine(mods, ones, s.eps, s.heads, s.kv_heads, s.head_dim, kv, cs, bops)
+        torch.cuda.synchronize()
+        start.wait(timeout=300)
         extq.slot_signal_join(sid)
         t0 = time.time()
         while not extq.slot_is_active(sid):
             if time.time() - t0 > 120:
                 raise RuntimeError("slot never became active")
-            time.sleep(0.001)
+            time.sleep(0.0005)
         st = SlotState(sid, torch.tensor([[1 + wid]], dtype=torch.int64, device=dev))
         slots = {sid: st}
-        for _ in range(2):
+        pre = 0
+        while not all(extq.slot_is_active(x) for x in all_sids):
             eng.generate_one_token_all(slots)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(n_tok):
+            pre += 1
+            if pre > 60:
+                raise RuntimeError("the other workers never became active")
+        for _ in range(IPC_WARM):
             eng.generate_one_token_all(slots)
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t1
-        # then two tokens through the stage-timed path ([LAYER_PROFILE])
+        windows = []
+        for _ in range(reps):
+            t1 = time.perf_counter()
+            for _ in range(n_tok):
+                eng.generate_one_token_all(slots)  # host-synchronous: reads the sampled token
+            windows.append(time.perf_counter() - t1)
+        for _ in range(IPC_COOL):
+            eng.generate_one_token_all(slots)
         eng.profiler = StageTimer()
         for _ in range(2):
             eng.generate_one_token_all(slots)
@@ -350,33 +379,41 @@ def _ipc_worker(shm_name, claim, wid, layers, n_tok, gpu_ordered, pooled, out):
         eng.profiler = None
         extq.slot_signal_leave(sid)
         ub.close_slot(sid)
-        out.put((wid, (dt, prof), None))
+        out.put((wid, (windows, prof, pre), None))
     except Exception:
         import traceback
         out.put((wid, None, traceback.format_exc()))
 
 
-def ipc_measure(W, L, n_tok, pooled):
+IPC_MODES = {  # name: (GPU-ordered rounds, adapters pooled in the aggregator)
+    "host_sync": (False, False),          # the reference's protocol: worker-side LoRA, host-synchronised rounds
+    "host_sync_pooled": (False, True),    # adapters in the aggregator's pool, delta added inside the round
+    "gpu_ordered": (True, False),
+    "gpu_ordered_pooled": (True, True),
+}
+
+
+def ipc_measure(W, L, n_tok, modes, reps=3):
     """The multi-process serving path: this process is the aggregator (native
     main loop on a thread, 8B-shaped weights for L layers, embed and LM
     head), W worker processes decode one token per step each through the
-    shared-memory ring and IPC-mapped slots.  Runs the same decode twice:
-    host-synchronised rounds (the reference's protocol) and GPU-ordered
-    rounds (sequence words in the slot buffers waited on by the streams).
-    Per mode: tokens/s, step time and µs per round over n_tok timed tokens
-    per worker, then the mean [LAYER_PROFILE] stage split of two stage-timed
-    tokens per worker."""
+    shared-memory ring and IPC-mapped slots, once per mode of IPC_MODES.
+    Per mode: tokens/s, step time and µs per round from `reps` timed windows
+    of n_tok tokens (per window the slowest worker; the median window), then
+    the mean [LAYER_PROFILE] stage split of two stage-timed tokens per
+    worker."""
     import multiprocessing as mp
     import threading
     import torch
     from swarmlora_amd import ext_aggregator as agg
     from swarmlora_amd import ext_ipc_queue as extq
-    from swarmlora_amd.decode import DecodeShape, synthetic_weights
+    from swarmlora_amd.decode import DecodeShape, synthetic_adapter, synthetic_weights
     dev = torch.device("cuda:0")
     s = DecodeShape(layers=L)
     wts = synthetic_weights(s, dev, seed=0)
     res = {}
-    for mode in ("host_sync", "gpu_ordered"):
+    for mode in modes:
+        gpu_ordered, pooled = IPC_MODES[mode]
         q = extq.create_queue(1024, 1024)
         extq.init_batch_control(W)
         agg.init_slot_pool(W, 0, s.hidden, s.inter, s.kv_heads, s.head_dim, 1, 2)
@@ -387,9 +424,8 @@ def ipc_measure(W, L, n_tok, pooled):
         agg.init_aggregator_finalize()
         agg.init_embed_lm_head_weights(wts["embed"], wts["lm_head"])
         agg.init_aggregator_queue(q["shm_name"], 1024)
+        agg.clear_adapters()
         if pooled:
-            from swarmlora_amd.decode import synthetic_adapter
-            agg.clear_adapters()
             for wid in range(W):
                 ad = synthetic_adapter(s, dev, seed=1000 + wid)
                 for li in range(L):
@@ -397,15 +433,19 @@ def ipc_measure(W, L, n_tok, pooled):
                                       (agg.OP_GATE_UP_FUSED, ("gate", "up")), (agg.OP_DOWN_PROJ, ("down",))):
                         agg.register_adapter(wid, li, op, torch.cat([ad[li][p][0] for p in projs], 0).contiguous(),
                                              [ad[li][p][1].contiguous() for p in projs], s.scale)
+                del ad
         claims = {wid: agg.claim_slot(wid) for wid in range(W)}
+        sids = [claims[w]["slot_id"] for w in range(W)]
         loop = threading.Thread(target=agg.aggregator_main_loop_slots, args=(W, 15), daemon=True)
         loop.start()
         ctx = mp.get_context("spawn")
         out = ctx.Queue()
-        procs = [ctx.Process(target=_ipc_worker, args=(q["shm_name"], claims[w], w, L, n_tok,
-                                                       mode == "gpu_ordered", pooled, out))
+        start = ctx.Barrier(W)
+        procs = [ctx.Process(target=_ipc_worker, args=(q["shm_name"], claims[w], w, sids, start, L, n_tok, reps,
+                                                       gpu_ordered, pooled, out))
                  for w in range(W)]
-        times, profs = [], []
+        wins, profs, pre = [], [], []
+        load0 = os.getloadavg()[0]
         try:
             for p in procs:
                 p.start()
@@ -413,8 +453,9 @@ def ipc_measure(W, L, n_tok, pooled):
                 wid, r, err = out.get(timeout=600)
                 if err:
                     raise RuntimeError(f"worker {wid}: {err}")
-                times.append(r[0])
+                wins.append(r[0])
                 profs.extend(r[1])
+                pre.append(r[2])
         finally:
             extq.set_quit(1)
             loop.join(timeout=60)
@@ -431,39 +472,71 @@ def ipc_measure(W, L, n_tok, pooled):
             agg.cleanup_slot_pool()
             extq.close_queue()
         rounds = 2 + 4 * L
-        step_s = max(times) / n_tok
+        per_win = [max(w[i] for w in wins) / n_tok for i in range(reps)]  # slowest worker per window
+        step_s = statistics.median(per_win)
         split = {k: round(statistics.fmean(r[k] for r in profs), 1)
                  for k in ("gather_us", "gemm_us", "scatter_us", "lora_us", "attn_us", "compute_us", "wall_us")}
         split["ipc_pct"] = round(100.0 * (split["gather_us"] + split["scatter_us"]) / split["wall_us"], 1)
         split["round_wait_us"] = round(split["gemm_us"] / rounds, 1)
         res[mode] = {"tok_s": round(W / step_s, 1), "ms_per_step": round(step_s * 1e3, 3),
-                     "us_per_round": round(step_s * 1e6 / rounds, 1), "layer_profile": split}
+                     "us_per_round": round(step_s * 1e6 / rounds, 1),
+                     "us_per_round_windows": [round(x * 1e6 / rounds, 1) for x in per_win],
+                     "untimed_tokens_before_all_active": max(pre), "host_load_1min": round(load0, 2),
+                     "layer_profile": split}
+    return res
+
+
+def _drop_in_child(W, L, n_tok, modes, reps, out):
+    """ipc_measure in a process of its own (a fresh aggregator: nothing of the
+    parent's GPU state, threads or memory carries over)."""
+    try:
+        out.put((ipc_measure(W, L, n_tok, modes, reps), None))
+    except Exception:
+        import traceback
+        out.put((None, traceback.format_exc()))
+
+
+def drop_in_leg(W, L, n_tok, modes, reps=3):
+    """ipc_measure run by a freshly spawned aggregator process."""
+    import multiprocessing as mp
+    ctx = mp.get_context("spawn")
+    out = ctx.Queue()
+    p = ctx.Process(target=_drop_in_child, args=(W, L, n_tok, modes, reps, out))
+    p.start()
+    try:
+        res, err = out.get(timeout=900)
+    finally:
+        p.join(timeout=120)
+        if p.is_alive():
+            p.kill()
+    if err:
+        raise RuntimeError(err)
     return res
 
 
 def ipc(args):
-    """--workload ipc: ipc_measure's line on its own; `value` is tokens/s of
-    the GPU-ordered run."""
+    """--workload ipc: the drop-in path's line on its own; `value` is tokens/s
+    of the first mode."""
     W = min(args.workers, 8)
     L = args.ipc_layers
-    res = ipc_measure(W, L, args.ipc_tokens, args.ipc_pooled)
+    modes = [m for m in args.ipc_modes.split(",") if m]
+    res = drop_in_leg(W, L, args.ipc_tokens, modes, args.ipc_reps)
+    first = res[modes[0]]
     line = {
-        "metric": "multi-process decode tok/s (ipc path, GPU-ordered rounds)",
-        "value": res["gpu_ordered"]["tok_s"],
+        "metric": f"multi-process decode tok/s (drop-in path, {modes[0]})",
+        "value": first["tok_s"],
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.ipc_tokens,
-        "warmup": 2,
-        "ms_per_step": res["gpu_ordered"]["ms_per_step"],
+        "steps": args.ipc_tokens * args.ipc_reps,
+        "warmup": IPC_WARM,
+        "ms_per_step": first["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded random-init weights and adapters)",
         "config": {"workload": f"{W} worker processes x 1 decode token, {L} Llama-3.1-8B-shaped layers, rank-16 "
-                               "adapter per worker " + ("pooled in the aggregator's rounds" if args.ipc_pooled else
-                                                        "applied on the worker") +
-                               ", aggregator main loop in this process",
+                               "adapter per worker, aggregator main loop in a spawned process",
                    "workers": W, "layers": L, "rounds_per_token": 2 + 4 * L, "modes": res},
         "roofline": None,
         "cpu_baseline": None,
@@ -570,6 +643,28 @@ def main():
     copy_calibration(args, dev)
 
     step_bytes = s.step_bytes(ctx, W)
+    dec_wk = dict(dec.wk)
+    dec.close()
+    del dec
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    drop_in = None
+    if not args.no_ipc:
+        # the drop-in path: a freshly spawned aggregator process, real worker
+        # processes, the shared-memory ring and IPC slot buffers, 8B widths
+        W_ipc = max(1, min(args.ipc_workers, 8))
+        modes = [m for m in args.ipc_modes.split(",") if m]
+        try:
+            res = drop_in_leg(W_ipc, args.ipc_layers, args.ipc_tokens, modes, args.ipc_reps)
+            drop_in = {
+                "workload": f"{W_ipc} worker processes + a spawned aggregator process, {args.ipc_layers} 8B-shaped "
+                            f"layers ({2 + 4 * args.ipc_layers} rounds per token), rank-16 adapter per worker; "
+                            "host_sync: applied on the worker (the reference's protocol); host_sync_pooled: pooled "
+                            f"in the aggregator's rounds; {args.ipc_reps} windows of {args.ipc_tokens} tokens once "
+                            "every slot is active, median window",
+                "workers": W_ipc, "layers": args.ipc_layers, "rounds_per_token": 2 + 4 * args.ipc_layers, **res}
+        except Exception as e:  # the headline line is still printed
+            drop_in = {"error": f"{type(e).__name__}: {e}"[:2000]}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(W, args.cpu_seconds)
@@ -601,32 +696,16 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": (f"fullk_kernel (whole-K decode round, epilogue included: "
-                                f"{', '.join(g for g in ('qkv', 'o', 'gu', 'lm') if dec.wk.get(g))}; the other "
+                                f"{', '.join(g for g in ('qkv', 'o', 'gu', 'lm') if dec_wk.get(g))}; the other "
                                 f"rounds split_kernel + epilogue_kernel)") if whole_k else
                                (f"split_kernel (K-sliced decode projection base kernel; whole-K rounds: "
-                                f"{', '.join(g for g in dec.wk if dec.wk[g]) or 'none'})"),
+                                f"{', '.join(g for g in dec_wk if dec_wk[g]) or 'none'})"),
                      "launches": len(dom),
                      "mean_launch_us": round(mean_ms * 1e3, 3), "bytes_per_launch": int(mean_bytes)},
         "cpu_baseline": cpu,
     }
-    dec.close()
-    del dec
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-    if not args.no_ipc:
-        # the drop-in path: real worker processes, the shared-memory ring and
-        # IPC slot buffers, at the same 8B widths (a few layers)
-        W_ipc = max(1, min(args.ipc_workers, 8))
-        try:
-            res = ipc_measure(W_ipc, args.ipc_layers, args.ipc_tokens, pooled=False)
-            line["config"]["drop_in"] = {
-                "workload": f"{W_ipc} worker processes + this aggregator process, {args.ipc_layers} 8B-shaped "
-                            "layers, rank-16 adapter per worker applied on the worker (the reference's protocol), "
-                            f"{args.ipc_tokens} timed tokens per worker",
-                "workers": W_ipc, "layers": args.ipc_layers, "rounds_per_token": 2 + 4 * args.ipc_layers,
-                **res}
-        except Exception as e:  # the headline line is still printed
-            line["config"]["drop_in"] = {"error": f"{type(e).__name__}: {e}"[:2000]}
+    if drop_in is not None:
+        line["config"]["drop_in"] = drop_in
     print(json.dumps(line), flush=True)
 
 

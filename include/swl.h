@@ -286,6 +286,26 @@ int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb,
                     int trans_b, void* y, int64_t ldy, int64_t m, int64_t n,
                     int64_t k, float alpha, void* stream);
 
+/* A worker's LoRA delta of up to 4 token rows in one launch: the two bf16
+ * products of FusedLoRA.forward (u = x . fused_A, then u . fused_B over its
+ * diagonal blocks, model_builder.py:259-262) or of SyncRemoteLoRALinear
+ * (lora_B(lora_A(x)) * scaling, worker_sync.py:305, :375).
+ *   u[m, j] = bf16(sum_k x[m, k] * a[k*a_sk + j*a_sj]),  j < nr (<= 64)
+ *   y[m, c] = bf16(alpha * sum_{rr < rank} u[m, blk*rank + rr] *
+ *                  b[blk][rr*b_srr[blk] + (c - off_blk)*b_sc[blk]])
+ * for the nblk (<= 4) column blocks of blk_cols[blk] columns each, laid out
+ * one after another in y's rows (off_blk = sum of the earlier blocks).
+ * x rows 16-byte aligned, k a multiple of 8.  fused_A [k, n*r] is a_sk = n*r,
+ * a_sj = 1; lora_A [r, k] is a_sk = 1, a_sj = k; a diagonal block of fused_B
+ * [n*r, sum(out)] is b = &fused_B[blk*r, off_blk], b_srr = sum(out), b_sc =
+ * 1; lora_B [out, r] is b_srr = 1, b_sc = r. */
+int swl_lora_rows_bf16(const void* x, int64_t ldx, int64_t m, int64_t k,
+                       const void* a, int64_t a_sk, int64_t a_sj, int64_t nr,
+                       int nblk, int64_t rank, const void* const* b,
+                       const int64_t* b_srr, const int64_t* b_sc,
+                       const int64_t* blk_cols, float alpha, void* y,
+                       int64_t ldy, void* stream);
+
 /* Paged-KV attention for one q_len group, replacing
  * WorkerBatchedOps.batch_flash_attention (worker_sync.py:169-205).  Token t
  * (t = seq * q_len + i) has its query heads at q + t*q_stride ([hq, d]), its

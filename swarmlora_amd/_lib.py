@@ -138,6 +138,8 @@ _SIGS = {
                                         c_int, c_vp]),
     "swl_matmul_bf16": (c_int, [c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
                                 c_vp]),
+    "swl_lora_rows_bf16": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_int, c_i64, P_vp, P_i64,
+                                   P_i64, P_i64, c_f32, c_vp, c_i64, c_vp]),
     "swl_paged_attention_bf16": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_int, c_int,
                                          c_vp, c_vp, c_i64, c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int,
                                          c_f32, c_vp, c_vp]),

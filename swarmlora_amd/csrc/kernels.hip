@@ -1987,6 +1987,106 @@ __global__ __launch_bounds__(1024) void matmul_shrink_kernel(const bf16* __restr
   }
 }
 
+// ---------------------------------------------- worker-side LoRA delta ----
+// One launch per adapter delta of a worker's few token rows: the reference's
+// FusedLoRA.forward ((x . fused_A) . fused_B over the diagonal blocks,
+// model_builder.py:217-262) and SyncRemoteLoRALinear's lora_B(lora_A(x)) *
+// scaling (worker_sync.py:305, :375).  Every workgroup computes the whole
+// shrink u[m, j] = bf16(sum_k x[m, k] A(k, j)), j < nr (A comes from L2 after
+// the first workgroup's misses; K is split over the 256 threads in 8-element
+// chunks, one wave reduction per column); workgroup g then writes its share
+// of the columns c of y[m, c] = bf16(alpha * sum_rr u[m, b*rank + rr] *
+// B_b(rr, c - off_b)), b the block holding c.  A(k, j) = a[k*a_sk + j*a_sj],
+// B_b(rr, c) = b_b[rr*srr_b + c*sc_b].  Two bf16 roundings, as the two bf16
+// matmuls of the reference.
+constexpr int kLoraRowsMaxRows = 4, kLoraRowsMaxNr = 64, kLoraRowsMaxBlk = 4;
+
+struct LoraRowsArgs {
+  const bf16* x;
+  int64_t ldx, K;
+  int m, nr, nblk, rank;
+  const bf16* a;
+  int64_t a_sk, a_sj;
+  int a_mode;  // 0: k-contiguous rows (16-byte loads over k), 1: j-contiguous rows (16-byte loads over j), 2: scalar
+  const bf16* b[kLoraRowsMaxBlk];
+  int64_t srr[kLoraRowsMaxBlk], sc[kLoraRowsMaxBlk], off[kLoraRowsMaxBlk + 1];
+  float alpha;
+  bf16* y;
+  int64_t ldy;
+};
+
+template <int NRMAX>
+__global__ __launch_bounds__(256) void lora_rows_kernel(LoraRowsArgs a) {
+  __shared__ float red[4][NRMAX];
+  __shared__ float us[kLoraRowsMaxRows][NRMAX];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t K8 = a.K >> 3;
+  for (int m = 0; m < a.m; ++m) {
+    const bf16* xr = a.x + m * a.ldx;
+    float acc[NRMAX];
+#pragma unroll
+    for (int j = 0; j < NRMAX; ++j) acc[j] = 0.f;
+    for (int64_t c = tid; c < K8; c += 256) {
+      float xv[8];
+      unpack8(ld16(xr + 8 * c), xv);
+      if (a.a_mode == 0) {
+#pragma unroll
+        for (int j = 0; j < NRMAX; ++j)
+          if (j < a.nr) {
+            float av[8];
+            unpack8(ld16(a.a + j * a.a_sj + 8 * c), av);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) acc[j] += xv[kk] * av[kk];
+          }
+      } else if (a.a_mode == 1) {
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const bf16* ar = a.a + (8 * c + kk) * a.a_sk;
+#pragma unroll
+          for (int jg = 0; jg < NRMAX / 8; ++jg)
+            if (8 * jg < a.nr) {
+              float av[8];
+              unpack8(ld16(ar + 8 * jg), av);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) acc[8 * jg + i] += xv[kk] * av[i];
+            }
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const bf16* ar = a.a + (8 * c + kk) * a.a_sk;
+#pragma unroll
+          for (int j = 0; j < NRMAX; ++j)
+            if (j < a.nr) acc[j] += xv[kk] * bf2f(ar[j * a.a_sj]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NRMAX; ++j)
+      if (j < a.nr) {
+        float v = acc[j];
+        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (lane == 0) red[w][j] = v;
+      }
+    __syncthreads();
+    if (tid < a.nr) us[m][tid] = bf2f(f2bf(red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid]));
+    __syncthreads();
+  }
+  const int64_t N = a.off[a.nblk];
+  for (int64_t c = (int64_t)blockIdx.x * 256 + tid; c < N; c += (int64_t)gridDim.x * 256) {
+    int b = 0;
+    while (b + 1 < a.nblk && c >= a.off[b + 1]) ++b;
+    const bf16* bb = a.b[b] + (c - a.off[b]) * a.sc[b];
+    const int64_t srr = a.srr[b];
+    const int u0 = b * a.rank;
+    for (int m = 0; m < a.m; ++m) {
+      float s = 0.f;
+      for (int rr = 0; rr < a.rank; ++rr) s += us[m][u0 + rr] * bf2f(bb[rr * srr]);
+      a.y[m * a.ldy + c] = f2bf(a.alpha * s);
+    }
+  }
+}
+
 // ------------------------------------------------------ paged attention ---
 struct AttnArgs {
   bf16* q;               // token t at q + t*qs: [hq, 128]
@@ -4330,6 +4430,61 @@ int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int 
                      (hipStream_t)stream, reinterpret_cast<const bf16*>(x), ldx, reinterpret_cast<const bf16*>(b),
                      ldb, trans_b, reinterpret_cast<bf16*>(y), ldy, n, k, alpha);
   SWL_LAUNCH_CHECK("matmul_generic_kernel launch");
+  return SWL_OK;
+}
+
+int swl_lora_rows_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, const void* a, int64_t a_sk, int64_t a_sj,
+                       int64_t nr, int nblk, int64_t rank, const void* const* b, const int64_t* b_srr,
+                       const int64_t* b_sc, const int64_t* blk_cols, float alpha, void* y, int64_t ldy, void* stream) {
+  SWL_CHECK(x && a && b && b_srr && b_sc && blk_cols && y, SWL_ERR_INVALID, "swl_lora_rows_bf16: null argument");
+  SWL_CHECK(m >= 0 && m <= kLoraRowsMaxRows, SWL_ERR_INVALID, "swl_lora_rows_bf16: at most 4 rows");
+  SWL_CHECK(k > 0 && k % 8 == 0 && ldx % 8 == 0 && ldx >= k, SWL_ERR_INVALID,
+            "swl_lora_rows_bf16: k must be a positive multiple of 8 (rows of 16-byte multiples)");
+  SWL_CHECK((reinterpret_cast<uintptr_t>(x) & 15) == 0, SWL_ERR_INVALID, "swl_lora_rows_bf16: x must be 16-byte aligned");
+  SWL_CHECK(nr >= 1 && nr <= kLoraRowsMaxNr, SWL_ERR_INVALID, "swl_lora_rows_bf16: 1..64 shrink columns");
+  SWL_CHECK(nblk >= 1 && nblk <= kLoraRowsMaxBlk && rank >= 1 && nblk * rank <= nr, SWL_ERR_INVALID,
+            "swl_lora_rows_bf16: 1..4 blocks of rank columns within the shrink columns");
+  SWL_CHECK(a_sk > 0 && a_sj > 0, SWL_ERR_INVALID, "swl_lora_rows_bf16: A strides must be positive");
+  if (m == 0) return SWL_OK;
+  LoraRowsArgs r{};
+  r.x = reinterpret_cast<const bf16*>(x);
+  r.ldx = ldx;
+  r.K = k;
+  r.m = (int)m;
+  r.nr = (int)nr;
+  r.nblk = nblk;
+  r.rank = (int)rank;
+  r.a = reinterpret_cast<const bf16*>(a);
+  r.a_sk = a_sk;
+  r.a_sj = a_sj;
+  const bool a_al = (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+  if (a_sk == 1 && a_al && a_sj % 8 == 0)
+    r.a_mode = 0;
+  else if (a_sj == 1 && a_al && a_sk % 8 == 0 && nr % 8 == 0)
+    r.a_mode = 1;
+  else
+    r.a_mode = 2;
+  r.off[0] = 0;
+  for (int i = 0; i < nblk; ++i) {
+    SWL_CHECK(b[i] && blk_cols[i] > 0, SWL_ERR_INVALID, "swl_lora_rows_bf16: empty block");
+    r.b[i] = reinterpret_cast<const bf16*>(b[i]);
+    r.srr[i] = b_srr[i];
+    r.sc[i] = b_sc[i];
+    r.off[i + 1] = r.off[i] + blk_cols[i];
+  }
+  SWL_CHECK(ldy >= r.off[nblk], SWL_ERR_INVALID, "swl_lora_rows_bf16: ldy below the output columns");
+  r.alpha = alpha;
+  r.y = reinterpret_cast<bf16*>(y);
+  r.ldy = ldy;
+  const unsigned grid = (unsigned)std::min<int64_t>(32, std::max<int64_t>(1, (r.off[nblk] + 1023) / 1024));
+  hipStream_t st = (hipStream_t)stream;
+  if (nr <= 16)
+    hipLaunchKernelGGL(lora_rows_kernel<16>, dim3(grid), dim3(256), 0, st, r);
+  else if (nr <= 32)
+    hipLaunchKernelGGL(lora_rows_kernel<32>, dim3(grid), dim3(256), 0, st, r);
+  else
+    hipLaunchKernelGGL(lora_rows_kernel<64>, dim3(grid), dim3(256), 0, st, r);
+  SWL_LAUNCH_CHECK("lora_rows_kernel launch");
   return SWL_OK;
 }
 

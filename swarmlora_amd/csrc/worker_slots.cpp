@@ -91,7 +91,14 @@ int need_slot(const char* fn, int slot_id, SlotCtx** out) {
   if (!g_w.initialized) return swl::fail(SWL_ERR_STATE, std::string(fn) + ": worker slot manager not initialized");
   *out = find_slot(slot_id);
   if (!*out) return swl::fail(SWL_ERR_NOT_FOUND, std::string(fn) + ": slot " + std::to_string(slot_id) + " not found");
-  return check_out_timeout(fn, *out);
+  return SWL_OK;
+}
+
+// need_slot plus the time-out report, for the calls that move data (queries
+// and close_slot do not fail on a pending time-out)
+int need_data_slot(const char* fn, int slot_id, SlotCtx** out) {
+  int rc = need_slot(fn, slot_id, out);
+  return rc ? rc : check_out_timeout(fn, *out);
 }
 
 int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream_t st) {
@@ -184,8 +191,12 @@ int swl_w_close_slot(int slot_id) {
   SlotCtx* c;
   int rc = need_slot("close_slot", slot_id, &c);
   if (rc) return rc;
-  // every stream of this process may still touch the mapping
+  // every stream of this process may still touch the mapping (a pending
+  // GPU-ordered output wait ends by its own limit); a time-out not yet
+  // reported is dropped with the slot
   SWL_HIP(hipDeviceSynchronize());
+  if (g_w.out_timeout && slot_id >= 0 && slot_id < SWL_MAX_SLOTS)
+    reinterpret_cast<volatile uint32_t*>(g_w.out_timeout)[slot_id] = 0;
   if (c->in) {
     const hipError_t e = hipIpcCloseMemHandle(c->in);
     if (e != hipSuccess)
@@ -208,7 +219,7 @@ int swl_w_close_slot(int slot_id) {
 int swl_w_prepare_input(int slot_id, const void* src, int64_t bx, int64_t tx, int64_t dx, size_t elem_size,
                         void* stream) {
   SlotCtx* c;
-  int rc = need_slot("prepare_input_slot", slot_id, &c);
+  int rc = need_data_slot("prepare_input_slot", slot_id, &c);
   if (rc) return rc;
   SWL_CHECK(src && bx > 0 && tx > 0 && dx > 0 && elem_size > 0, SWL_ERR_INVALID, "Input must be 3D [B, T, D]");
   rc = copy_in("prepare_input_slot", c, src, (size_t)bx * tx * dx * elem_size, (hipStream_t)stream);
@@ -240,7 +251,7 @@ int swl_w_slot_sizes(int slot_id, size_t* input_buffer_size, size_t* output_buff
 
 int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream) {
   SlotCtx* c;
-  int rc = need_slot("get_outputs_slot", slot_id, &c);
+  int rc = need_data_slot("get_outputs_slot", slot_id, &c);
   if (rc) return rc;
   SWL_CHECK(dst != nullptr, SWL_ERR_INVALID, "get_outputs_slot: null destination");
   SWL_CHECK(bytes <= c->out_size, SWL_ERR_INVALID,
@@ -255,7 +266,7 @@ int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream) {
 
 int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx, void* stream) {
   SlotCtx* c;
-  int rc = need_slot("prepare_token_ids_slot", slot_id, &c);
+  int rc = need_data_slot("prepare_token_ids_slot", slot_id, &c);
   if (rc) return rc;
   SWL_CHECK(src && bx > 0 && tx > 0, SWL_ERR_INVALID, "token_ids must be 2D [B, T]");
   rc = copy_in("prepare_token_ids_slot", c, src, (size_t)bx * tx * sizeof(int64_t), (hipStream_t)stream);
@@ -269,7 +280,7 @@ int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx
 int swl_w_prepare_hidden_lm(int slot_id, const void* src, int64_t bx, int64_t tx, int64_t dx, size_t elem_size,
                             void* stream) {
   SlotCtx* c;
-  int rc = need_slot("prepare_hidden_for_lm_head_slot", slot_id, &c);
+  int rc = need_data_slot("prepare_hidden_for_lm_head_slot", slot_id, &c);
   if (rc) return rc;
   SWL_CHECK(src && bx > 0 && tx > 0 && dx > 0, SWL_ERR_INVALID, "hidden_states must be 3D [B, T, D]");
   rc = copy_in("prepare_hidden_for_lm_head_slot", c, src, (size_t)bx * tx * dx * elem_size, (hipStream_t)stream);
@@ -282,7 +293,7 @@ int swl_w_prepare_hidden_lm(int slot_id, const void* src, int64_t bx, int64_t tx
 
 int swl_w_get_next_token(int slot_id, int64_t* token, void* stream) {
   SlotCtx* c;
-  int rc = need_slot("get_next_token_slot", slot_id, &c);
+  int rc = need_data_slot("get_next_token_slot", slot_id, &c);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   rc = wait_outputs("get_next_token_slot", c, st);

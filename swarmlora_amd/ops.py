@@ -534,6 +534,49 @@ def matmul(x: torch.Tensor, b: torch.Tensor, trans_b: bool, alpha: float = 1.0,
     return out
 
 
+LORA_ROWS_MAX = 4      # token rows of one lora_rows launch
+LORA_ROWS_MAX_NR = 64  # shrink columns (blocks x rank)
+
+
+def lora_rows(x: torch.Tensor, a: torch.Tensor, a_kmajor: bool, blocks: list, rank: int, alpha: float = 1.0,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """A worker's LoRA delta in one launch (swl_lora_rows_bf16):
+    u = bf16(x @ A) with A = a ([k, nr], a_kmajor) or a.T (a is [nr, k]),
+    then per column block (b, cols, rr_major): bf16(alpha * u[:, blk*rank:
+    (blk+1)*rank] @ B) where B is b [rank, cols] (rr_major, e.g. a diagonal
+    block of fused_B) or b.T (b is [cols, rank], e.g. lora_B).  x is [m, k]
+    with m <= LORA_ROWS_MAX; returns [m, sum(cols)]."""
+    _need(x, "x")
+    _need(a, "a")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("lora_rows: x must be 2-D with unit column stride")
+    m, k = x.shape
+    nr = a.shape[1] if a_kmajor else a.shape[0]
+    if (a.shape[0] if a_kmajor else a.shape[1]) != k:
+        raise ValueError("lora_rows: A does not match x")
+    n = len(blocks)
+    ptrs = (ctypes.c_void_p * n)()
+    srr = (ctypes.c_int64 * n)()
+    sc = (ctypes.c_int64 * n)()
+    cols = (ctypes.c_int64 * n)()
+    for i, (b, c, rr_major) in enumerate(blocks):
+        _need(b, "b")
+        ptrs[i] = b.data_ptr()
+        if rr_major:
+            srr[i], sc[i] = b.stride(0), b.stride(1)
+        else:
+            srr[i], sc[i] = b.stride(1), b.stride(0)
+        cols[i] = int(c)
+    total = int(sum(int(c) for _, c, _ in blocks))
+    if out is None:
+        out = torch.empty(m, total, dtype=BF16, device=x.device)
+    _lib.check(_lib.load().swl_lora_rows_bf16(
+        _ptr(x), x.stride(0), m, k, _ptr(a), a.stride(0) if a_kmajor else a.stride(1),
+        a.stride(1) if a_kmajor else a.stride(0), nr, n, int(rank), ptrs, srr, sc, cols, float(alpha), _ptr(out),
+        out.stride(0), _stream()))
+    return out
+
+
 def _token_rows(t: torch.Tensor, name: str, heads: int, d: int):
     """t is [nseq, L, heads, d] whose heads/dims are contiguous per token and
     whose tokens (nseq*L of them) are evenly strided: returns the stride."""

@@ -49,6 +49,43 @@ class NullTimer:
 NULL_TIMER = NullTimer()
 
 
+def _joined(parts):
+    """The single [.., sum of widths] view that last-dim pieces of one buffer
+    form (adjacent pieces, rows exactly their summed width), or None: lets a
+    fused output and its fused delta be added in one launch."""
+    p0 = parts[0]
+    if p0 is None or p0.stride(-1) != 1:
+        return None
+    es = p0.element_size()
+    total = sum(p.shape[-1] for p in parts if p is not None)
+    off = p0.data_ptr()
+    base = p0.untyped_storage().data_ptr()
+    for p in parts:
+        if (p is None or p.shape[:-1] != p0.shape[:-1] or p.stride() != p0.stride() or p.data_ptr() != off or
+                p.untyped_storage().data_ptr() != base):
+            return None
+        off += p.shape[-1] * es
+    for i in range(p0.dim() - 1):
+        if p0.shape[i] > 1 and p0.stride(i) != total * p0.shape[i + 1:-1].numel():
+            return None
+    return p0.as_strided((*p0.shape[:-1], total), p0.stride())
+
+
+def _add_deltas(raw, deltas):
+    """raw[i] += deltas[i] (bf16, in place on the worker-owned output copy),
+    one launch when both sides are pieces of one buffer each."""
+    if all(d is None for d in deltas):
+        return
+    if all(d is not None for d in deltas):
+        jr, jd = _joined(raw), _joined(deltas)
+        if jr is not None and jd is not None and jr.shape == jd.shape:
+            jr.add_(jd)
+            return
+    for r, d in zip(raw, deltas):
+        if d is not None:
+            r.add_(d)
+
+
 @dataclass
 class SlotState:
     """Per-request state of an active slot (worker_sync.py:100-118)."""
@@ -160,10 +197,9 @@ class BatchedAggregatorOps:
         res = {}
         with self.timer.stage("lora"):
             for sid in slots:
-                q, k, v = raw[sid]
-                dq, dk, dv = deltas.get(sid, (None, None, None))
-                res[sid] = (q + dq if dq is not None else q, k + dk if dk is not None else k,
-                            v + dv if dv is not None else v)
+                # q + dq, k + dk, v + dv (bf16) on the fresh output copy
+                _add_deltas(raw[sid], list(deltas.get(sid, (None, None, None))))
+                res[sid] = tuple(raw[sid])
         return res
 
     # -------------------------------------------------------------------- O
@@ -208,13 +244,8 @@ class BatchedAggregatorOps:
         res = {}
         with self.timer.stage("lora"):
             for sid in slots:
-                g, u = raw[sid]
-                dg, du = deltas.get(sid, (None, None))
-                if dg is not None:
-                    g.add_(dg)
-                if du is not None:
-                    u.add_(du)
-                res[sid] = (g, u)
+                _add_deltas(raw[sid], list(deltas.get(sid, (None, None))))
+                res[sid] = tuple(raw[sid])
         return res
 
     # ----------------------------------------------------------------- Down

@@ -67,6 +67,13 @@ class FastLoRAModule:
         self.lora_dropout = {"default": nn.Identity()}
 
 
+def _rows_fit(x2: torch.Tensor, nr: int) -> bool:
+    """A worker's LoRA delta fits one lora_rows launch: at most 4 token rows
+    of 16-byte multiples, 16-byte aligned, at most 64 shrink columns."""
+    return (0 < x2.shape[0] <= ops.LORA_ROWS_MAX and nr <= ops.LORA_ROWS_MAX_NR and x2.stride(1) == 1 and
+            x2.shape[1] % 8 == 0 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0)
+
+
 class SyncRemoteLinear(nn.Module):
     """Placeholder for a projection the aggregator computes (no adapter)."""
 
@@ -88,10 +95,15 @@ class SyncRemoteLoRALinear(nn.Module):
 
     def delta(self, x: torch.Tensor) -> torch.Tensor:
         """lora_B(lora_A(dropout(x))) * scaling (worker_sync.py:305, :375),
-        with the scaling applied before the single bf16 rounding."""
+        with the scaling applied before the single bf16 rounding; a decode
+        token's few rows take one lora_rows launch."""
         x2 = _as2d(self.dropout(x))
-        u = self.lora_A(x2)
-        y = ops.matmul(u, self.lora_B.weight.data, trans_b=True, alpha=float(self.scaling))
+        A, B = self.lora_A.weight.data, self.lora_B.weight.data
+        if _rows_fit(x2, A.shape[0]):
+            y = ops.lora_rows(x2, A, False, [(B, B.shape[0], False)], A.shape[0], float(self.scaling))
+        else:
+            u = self.lora_A(x2)
+            y = ops.matmul(u, B, trans_b=True, alpha=float(self.scaling))
         return y.reshape(*x.shape[:-1], y.shape[-1])
 
 
@@ -137,13 +149,22 @@ class FusedLoRA(nn.Module):
         if not self.has_lora:
             return [None] * self.num_loras
         x2 = _as2d(self.dropout(x))
-        u = ops.matmul(x2, self.fused_A.data, trans_b=False)            # [m, n*r] bf16
-        delta = torch.empty(x2.shape[0], sum(self.out_dims), dtype=x2.dtype, device=x2.device)
-        r, col = self.rank, 0
-        for i, d in enumerate(self.out_dims):
-            ops.matmul(u[:, i * r:(i + 1) * r], self.fused_B.data[i * r:(i + 1) * r, col:col + d], trans_b=False,
-                       out=delta[:, col:col + d])
-            col += d
+        fA, fB, r = self.fused_A.data, self.fused_B.data, self.rank
+        if _rows_fit(x2, fA.shape[1]) and len(self.out_dims) <= 4:
+            # a decode token's rows: shrink and every block's expand in one launch
+            blocks, col = [], 0
+            for i, d in enumerate(self.out_dims):
+                blocks.append((fB[i * r:(i + 1) * r, col:col + d], d, True))
+                col += d
+            delta = ops.lora_rows(x2, fA, True, blocks, r)
+        else:
+            u = ops.matmul(x2, fA, trans_b=False)            # [m, n*r] bf16
+            delta = torch.empty(x2.shape[0], sum(self.out_dims), dtype=x2.dtype, device=x2.device)
+            col = 0
+            for i, d in enumerate(self.out_dims):
+                ops.matmul(u[:, i * r:(i + 1) * r], fB[i * r:(i + 1) * r, col:col + d], trans_b=False,
+                           out=delta[:, col:col + d])
+                col += d
         delta = delta.reshape(*x.shape[:-1], delta.shape[-1])
         return list(delta.split(self.out_dims, dim=-1))
 

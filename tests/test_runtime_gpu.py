@@ -310,7 +310,17 @@ def _timeout_proc(claim, out):
         # the word was cleared: the slot works again
         ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
         torch.cuda.synchronize()
+        # 3: a slot whose time-out is still unreported closes without raising
+        # (and unmaps its buffers)
+        ub.get_outputs_slot(sid, [H], x)
+        torch.cuda.synchronize()
         ub.close_slot(sid)
+        seen.append("closed")
+        try:
+            ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
+            seen.append("still open")
+        except RuntimeError as e:
+            seen.append(str(e))
         out.put((seen, None))
     except Exception:
         import traceback
@@ -321,7 +331,8 @@ def test_gpu_ordered_output_wait_timeout_is_reported(pool):
     """A GPU-ordered worker whose output sequence word is never written (no
     aggregator runs): the bounded stream wait gives up, and the time-out is
     raised by the next call on the slot (get_outputs_slot path) or by
-    get_next_token_slot itself, instead of stale outputs passing silently."""
+    get_next_token_slot itself, instead of stale outputs passing silently;
+    close_slot on a slot with an unreported time-out still closes it."""
     agg = _agg()
     claim = agg.claim_slot(5)
     ctx = mp.get_context("spawn")
@@ -336,6 +347,8 @@ def test_gpu_ordered_output_wait_timeout_is_reported(pool):
             p.kill()
         agg.release_slot(claim["slot_id"], 5)
     assert err is None, err
-    assert len(seen) == 2
+    assert len(seen) == 4
     assert "prepare_input_slot" in seen[0] and "timed out" in seen[0]
     assert "get_next_token_slot" in seen[1] and "timed out" in seen[1]
+    assert seen[2] == "closed"
+    assert "not found" in seen[3]

@@ -59,6 +59,50 @@ def test_remote_lora_delta_matches_oracle(dev, in_dim):
     assert_close(got, ref.remote_lora_delta(x, A, B, 2.0), what="remote lora")
 
 
+@pytest.mark.parametrize("m,rank,nblk,in_dim,kmajor", [
+    (1, 16, 3, 4096, True),    # FusedLoRA QKV: fused_A [k, 48], 16-byte loads over j
+    (4, 16, 2, 4096, True),    # FusedLoRA Gate+Up shape, four rows
+    (3, 4, 3, 512, True),      # nr = 12: scalar loads of fused_A
+    (2, 32, 2, 4096, True),    # nr = 64
+    (1, 16, 1, 14336, False),  # SyncRemoteLoRALinear Down: lora_A [16, k], lora_B [4096, 16]
+    (4, 8, 1, 4096, False),
+])
+def test_lora_rows_matches_oracle(dev, m, rank, nblk, in_dim, kmajor):
+    """ops.lora_rows (one launch) against the oracle's two bf16 products, for
+    the fused (block-diagonal fused_B) and the per-projection (lora_B) forms."""
+    from swarmlora_amd import ops
+    widths = [4096, 1024, 1024][:nblk] if nblk > 1 else [4096]
+    host = [(randn((rank, in_dim), 50 + i, std=0.02), randn((w, rank), 60 + i, std=0.02)) for i, w in enumerate(widths)]
+    x = randn((m, in_dim), 9)
+    if kmajor:
+        fA, fB = ref.fused_lora_weights([(A, B, 2.0) for A, B in host], widths)
+        blocks, col = [], 0
+        fBd = fB.to(dev)
+        for i, w in enumerate(widths):
+            blocks.append((fBd[i * rank:(i + 1) * rank, col:col + w], w, True))
+            col += w
+        got = ops.lora_rows(x.to(dev), fA.to(dev), True, blocks, rank)
+        want = torch.cat(ref.fused_lora_forward(x, fA, fB, widths), -1)
+    else:
+        A, B = host[0]
+        got = ops.lora_rows(x.to(dev), A.to(dev), False, [(B.to(dev), B.shape[0], False)], rank, 2.0)
+        want = ref.remote_lora_delta(x, A, B, 2.0)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape
+    assert_close(got, want, what="lora_rows")
+
+
+def test_lora_rows_rejects_what_it_cannot_do(dev):
+    from swarmlora_amd import ops
+    x = torch.zeros(5, 512, dtype=BF16, device=dev)
+    A = torch.zeros(16, 512, dtype=BF16, device=dev)
+    B = torch.zeros(64, 16, dtype=BF16, device=dev)
+    with pytest.raises(RuntimeError, match="at most 4 rows"):
+        ops.lora_rows(x, A, False, [(B, 64, False)], 16)
+    with pytest.raises(RuntimeError, match="shrink columns"):
+        ops.lora_rows(x[:1], torch.zeros(80, 512, dtype=BF16, device=dev), False, [(B, 64, False)], 16)
+
+
 def test_paged_kv_cache_allocation_and_zeroing(dev):
     from swarmlora_amd.worker.paged_attention import PagedKVCache
     c = PagedKVCache(2, 8, 128, 16, 2, 64, dev, BF16)
