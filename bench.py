@@ -20,12 +20,20 @@ the CPU oracle's decode_step (torch-CPU bf16, the reference's op order) on a
 bounded sample: the LM head and one layer, scaled to 32 layers, on every
 core the process may use (CPU model and bf16-relevant flags reported).
 
-`config.drop_in` is the drop-in (multi-process) path measured after the
-headline: --ipc-workers worker processes and this process as the
-aggregator, the reference's protocol (worker-side LoRA, host-synchronised
-rounds) and GPU-ordered rounds, with tokens/s, µs per round and the mean
-[LAYER_PROFILE] stage split (gather / round wait / scatter / LoRA / norms
-and attention) of stage-timed tokens.
+`config.per_config` holds BASELINE configs 1, 2, 3 and 5 measured after the
+headline: µs per round (config 1) or per layer of four rounds (configs 2, 3,
+5) from HIP-graph replays (config 3: HIP events around eager rounds), the
+algorithmic bytes (FLOPs for config 3), the achieved rate, its fraction of
+the roofline and the floor; configs 1 and 2 also on the host's CPU cores.
+
+`config.drop_in` is the drop-in (multi-process) path: a spawned aggregator
+process and --ipc-workers worker processes over the shared-memory ring and
+IPC slot buffers, 32 layers (130 rounds per token), host-synchronised rounds
+with the reference's worker-side LoRA and with adapters pooled in the
+aggregator's rounds; tokens/s and µs per round of the median of 3 windows
+timed once every slot is active, and the mean [LAYER_PROFILE] stage split
+(gather / round wait / scatter / LoRA / norms and attention) of
+stage-synchronised tokens.
 """
 
 import argparse
@@ -72,15 +80,17 @@ def parse():
     ap.add_argument("--chain", action="store_true",
                     help="decode: each layer's O, Gate+Up and Down rounds and the next layer's QKV round as one "
                          "persistent launch (swl_chain_*)")
-    ap.add_argument("--workload", choices=("decode", "prefill", "ipc"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "ipc", "configs"), default="decode",
                     help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
                          "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
-                         "shared-memory ring, IPC slots), host-synchronised vs GPU-ordered rounds. The last two "
-                         "print lines of their own")
+                         "shared-memory ring, IPC slots) in the modes of --ipc-modes; configs: the per-config "
+                         "figures of configs 1, 2, 3 and 5. The last three print lines of their own")
     ap.add_argument("--ipc-workers", type=int, default=8,
                     help="drop-in leg of the decode line: worker processes (at most 8; with the aggregator's "
                          "process and this one at most 10 processes use the GPU)")
     ap.add_argument("--no-ipc", action="store_true", help="decode: skip the drop-in (multi-process) leg")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="decode: skip the per-config figures (BASELINE configs 1, 2, 3 and 5)")
     ap.add_argument("--ipc-layers", type=int, default=32, help="drop-in leg: 8B-shaped layers")
     ap.add_argument("--ipc-tokens", type=int, default=6, help="drop-in leg: decode tokens per timed window")
     ap.add_argument("--ipc-reps", type=int, default=3, help="drop-in leg: timed windows (the median is reported)")
@@ -206,14 +216,15 @@ def cpu_baseline(workers, budget_s):
                        f"CPU-seeded weights of the same shapes")}
 
 
-def prefill(args):
+def prefill_measure(steps):
     """one 8B-shaped layer's four rounds (QKV, O,
     Gate+Up, Down) over 16 slots, half of them one token, the rest
     U{32..512} tokens (seeded), each slot with its own adapter of rank drawn
-    from {8, 16, 32, 64}; > 64 token rows, so the rounds take the packed
-    MFMA path (gather, LoRA shrink, tiled_kernel with the expand in its
-    epilogue, scatter).  `value` is the base-GEMM TFLOP/s of the four rounds
-    (2*T*N*K each) over their measured time; `roofline` is bf16 MFMA."""
+    from {8, 16, 32, 64}; > 64 token rows, so the rounds take the prefill
+    path (LoRA shrink, then the 256 x 256 MFMA GEMM reading the slot rows in
+    place, the delta as extra MFMA k-steps, rows written to their slots).
+    Returns per-round ms and TFLOP/s of the base GEMM flops (2*T*N*K) over
+    the measured time of each round (HIP events around `steps` eager calls)."""
     import torch
     from swarmlora_amd import ops
     dev = torch.device("cuda:0")
@@ -252,25 +263,36 @@ def prefill(args):
     for p in plan:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(args.steps):
+        for _ in range(steps):
             run(p)
         e1.record()
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
+        ms = e0.elapsed_time(e1) / steps
         f = 2.0 * T * p[1] * p[2]
         per[p[0]] = {"ms": round(ms, 4), "TFLOPs": round(f / (ms * 1e-3) / 1e12, 1)}
         flops += f
         tot_ms += ms
-    tflops = flops / (tot_ms * 1e-3) / 1e12
-    copy_calibration(args, dev)
+    del plan
+    torch.cuda.empty_cache()
+    return {"T": T, "rows": rows, "ranks": ranks, "rounds": per, "flops": flops, "ms": tot_ms,
+            "tflops": round(flops / (tot_ms * 1e-3) / 1e12, 1)}
+
+
+def prefill(args):
+    """--workload prefill: config 3's line on its own; `roofline` is bf16
+    MFMA."""
+    import torch
+    pf = prefill_measure(args.steps)
+    copy_calibration(args, torch.device("cuda:0"))
+    tflops = pf["tflops"]
     line = {
         "metric": "prefill-shape round TFLOP/s (BASELINE config 3)",
-        "value": round(tflops, 1),
+        "value": tflops,
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": 3,
-        "ms_per_step": round(tot_ms, 4),
+        "ms_per_step": round(pf["ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -278,13 +300,193 @@ def prefill(args):
         "data": "synthetic (seeded random-init weights, adapters and activations)",
         "config": {"workload": "config3: one 8B-shaped layer's QKV, O, Gate+Up and Down rounds over 16 ragged "
                                "slots (8 x 1 token, 8 x U{32..512}), per-slot adapter rank in {8,16,32,64}",
-                   "token_rows": T, "slot_rows": rows, "ranks": ranks, "rounds": per},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                   "token_rows": pf["T"], "slot_rows": pf["rows"], "ranks": pf["ranks"], "rounds": pf["rounds"]},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4), "traffic": None,
-                     "kernel": "round (gather + shrink + tiled_kernel + scatter), base-GEMM flops"},
+                     "kernel": "prefill round (LoRA shrink + gemm256_kernel), base-GEMM flops"},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
+
+
+def _graph_us(fn, iters=20, reps=5):
+    """Mean µs of one fn() call: `iters` calls captured in one HIP graph after
+    3 eager calls (which size the library's scratch and upload adapter
+    tables), the graph replayed `reps` times between HIP events; the kernel
+    boundaries inside the graph are counted, the host's launch time is not."""
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(iters):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * iters)
+    del g
+    return us
+
+
+def _cpu_us(fn, budget_s=3.0, min_reps=20):
+    """Median µs of fn() on the host's cores (3 warm-up calls)."""
+    for _ in range(3):
+        fn()
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < min_reps or (time.perf_counter() - t_start < budget_s and len(ts) < 200):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts) * 1e6
+
+
+def _decode_layer_case(dev, n_slots, adapter_of_slot, n_pool, seed):
+    """One 8B-shaped layer's four projection rounds (fused QKV, O, Gate+Up,
+    Down) over n_slots one-token slots, every weight and adapter bf16
+    ~N(0, 0.02), activations ~N(0, 1); n_pool rank-16 adapters (scale 2.0)
+    on all seven projections, slot i using adapter adapter_of_slot[i].
+    Weights and stacked lora_A in fragment tiles (the decode step's layout).
+    Returns the round closures and their algorithmic bytes."""
+    import torch
+    from swarmlora_amd import ops
+    H, KV, I, r = 4096, 1024, 14336, 16
+    gd = torch.Generator(device=dev).manual_seed(seed)
+
+    def rn(*shape, std=0.02):
+        return (torch.randn(*shape, generator=gd, device=dev) * std).to(torch.bfloat16)
+
+    rounds = [("qkv", H, [H, KV, KV]), ("o", H, [H]), ("gate_up", H, [I, I]), ("down", I, [H])]
+    used = sorted(set(adapter_of_slot))
+    out = []
+    for nm, k, dims in rounds:
+        n = sum(dims)
+        w = ops.pack_weight(rn(n, k))
+        table = ops.LoraTable(dev)
+        for _ in range(n_pool):
+            table.add(ops.pack_weight(rn(r * len(dims), k)), [rn(d, r) for d in dims], r, 2.0)
+        xs = [rn(1, k, std=1.0) for _ in range(n_slots)]
+        ys = [torch.empty(1, n, dtype=torch.bfloat16, device=dev) for _ in range(n_slots)]
+        ids = list(adapter_of_slot)
+        fz = ops.round_fusion(w_layout=1, a_layout=1)
+
+        def run(xs=xs, ys=ys, w=w, table=table, ids=ids, dims=dims, fz=fz):
+            ops.round_ex(xs, ys, [1] * len(xs), w, None, seg_lora=ids, table=table, blk_cols=dims, fusion=fz)
+
+        nbytes = 2 * (n * k + n_slots * (k + n) + len(used) * r * len(dims) * k + len(used) * r * n)
+        out.append((nm, run, nbytes, n, k))
+    return out
+
+
+def per_config_measure(args):
+    """BASELINE configs 1, 2, 3 and 5 on this GPU: µs per round (per layer for
+    the four-round configs) from HIP-graph replays, algorithmic bytes (or
+    FLOPs for config 3) per unit, the achieved rate and its fraction of the
+    roofline, and the BASELINE.md floor; configs 1 and 2 also on the host's
+    CPU cores (the reference's torch path: oracle.execute_round plus the LoRA
+    delta and add, bf16)."""
+    import torch
+    dev = torch.device("cuda:0")
+    res = {}
+    # config 1: fused QKV round, 4 one-token slots, one rank-16 adapter per
+    # slot on the fused output (A [16, 4096], B [6144, 16]), scale 2.0
+    from swarmlora_amd import ops
+    H, QKV, r = 4096, 6144, 16
+    gd = torch.Generator(device=dev).manual_seed(0)
+
+    def rn(*shape, std=0.02):
+        return (torch.randn(*shape, generator=gd, device=dev) * std).to(torch.bfloat16)
+
+    w1 = rn(QKV, H)
+    xs1 = [rn(1, H, std=1.0) for _ in range(4)]
+    ad1 = [(rn(r, H), rn(QKV, r)) for _ in range(4)]
+    wp1 = ops.pack_weight(w1)
+    tab1 = ops.LoraTable(dev)
+    ids1 = [tab1.add(ops.pack_weight(a), [b], r, 2.0) for a, b in ad1]
+    ys1 = [torch.empty(1, QKV, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    fz1 = ops.round_fusion(w_layout=1, a_layout=1)
+    us1 = _graph_us(lambda: ops.round_ex(xs1, ys1, [1] * 4, wp1, None, seg_lora=ids1, table=tab1, blk_cols=[QKV],
+                                         fusion=fz1), iters=50)
+    b1 = 2 * (QKV * H + 4 * (H + QKV) + 4 * r * (H + QKV))
+    # the CPU torch path on the same shapes (gather, x @ W.T, (x @ A.T) @ B.T * s, add, scatter)
+    from oracle import reference_path as ref
+    host = host_cpu_info()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(host["usable_cpus"])
+    w1c, xs1c, ad1c = w1.cpu(), [x.cpu() for x in xs1], [(a.cpu(), b.cpu()) for a, b in ad1]
+
+    def cpu1():
+        base = ref.execute_round(xs1c, [1] * 4, w1c)
+        return [base[i] + ref.remote_lora_delta(xs1c[i], a, b, 2.0) for i, (a, b) in enumerate(ad1c)]
+
+    cpu_us1 = _cpu_us(cpu1)
+    res["config1"] = {"unit": "round", "us": round(us1, 2), "algorithmic_MB": round(b1 / 1e6, 2),
+                      "GBps": round(b1 / us1 / 1e3, 1), "frac_hbm": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 4),
+                      "floor_us": round(b1 / HBM_PEAK_GBS / 1e3, 2),
+                      "cpu_baseline": {"us": round(cpu_us1, 1), "cores": host["usable_cpus"], "kind": "port",
+                                       "sample": "oracle execute_round + remote_lora_delta per slot, torch-CPU bf16, "
+                                                 "median of >= 20"}}
+    del w1, wp1, tab1, xs1, ys1
+    # configs 2 and 5: one layer's four rounds
+    for name, n_slots, n_pool, ids in (
+            ("config2", 28, 28, list(range(28))),
+            ("config5", 64, 500, None)):
+        if ids is None:
+            g = torch.Generator().manual_seed(3)
+            p = torch.tensor([(i + 1) ** -1.1 for i in range(n_pool)])
+            ids = torch.multinomial(p / p.sum(), n_slots, replacement=True, generator=g).tolist()
+        case = _decode_layer_case(dev, n_slots, ids, n_pool, seed=0)
+        rounds = {}
+        tot_us = tot_b = 0.0
+        for nm, run, nb, n, k in case:
+            u = _graph_us(run, iters=20)
+            rounds[nm] = {"us": round(u, 2), "algorithmic_MB": round(nb / 1e6, 2),
+                          "frac_hbm": round(nb / u / 1e3 / HBM_PEAK_GBS, 4)}
+            tot_us += u
+            tot_b += nb
+        res[name] = {"unit": "layer (4 rounds)", "us": round(tot_us, 2), "algorithmic_MB": round(tot_b / 1e6, 2),
+                     "GBps": round(tot_b / tot_us / 1e3, 1), "frac_hbm": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
+                     "floor_us": round(tot_b / HBM_PEAK_GBS / 1e3, 2), "slots": n_slots,
+                     "distinct_adapters": len(set(ids)), "pool": n_pool, "rounds": rounds}
+        del case
+        torch.cuda.empty_cache()
+    # config 2 on the CPU: one layer's four rounds at 28 slots (torch-CPU bf16)
+    gc = torch.Generator().manual_seed(0)
+
+    def rc(*shape, std=0.02):
+        return (torch.randn(*shape, generator=gc) * std).to(torch.bfloat16)
+
+    cpu_rounds = []
+    for k, dims in ((4096, [4096, 1024, 1024]), (4096, [4096]), (4096, [14336, 14336]), (14336, [4096])):
+        n = sum(dims)
+        cpu_rounds.append((rc(n, k), [rc(1, k, std=1.0) for _ in range(28)],
+                           [(rc(r, k), rc(n, r)) for _ in range(28)]))
+
+    def cpu2():
+        for w, xs, ad in cpu_rounds:
+            base = ref.execute_round(xs, [1] * 28, w)
+            [base[i] + ref.remote_lora_delta(xs[i], a, b, 2.0) for i, (a, b) in enumerate(ad)]
+
+    cpu_us2 = _cpu_us(cpu2, budget_s=4.0, min_reps=5)
+    torch.set_num_threads(prev)
+    res["config2"]["cpu_baseline"] = {"us": round(cpu_us2, 1), "cores": host["usable_cpus"], "kind": "port",
+                                      "sample": "oracle execute_round + per-slot LoRA delta for the four rounds, "
+                                                "torch-CPU bf16, median of >= 5"}
+    del cpu_rounds
+    # config 3: the prefill rounds (MFMA bound)
+    pf = prefill_measure(steps=5)
+    res["config3"] = {"unit": "layer (4 rounds)", "us": round(pf["ms"] * 1e3, 1), "TFLOPs": pf["tflops"],
+                      "frac_mfma": round(pf["tflops"] / 2500.0, 4), "token_rows": pf["T"],
+                      "floor_us": round(pf["flops"] / 2.5e15 * 1e6, 1),
+                      "rounds": pf["rounds"]}
+    return res
 
 
 IPC_WARM, IPC_COOL = 2, 2
@@ -560,6 +762,9 @@ def main():
         return prefill(args)
     if args.workload == "ipc":
         return ipc(args)
+    if args.workload == "configs":
+        print(json.dumps({"per_config": per_config_measure(args)}), flush=True)
+        return
     from swarmlora_amd import ops
     from swarmlora_amd.decode import BatchedDecoder, DecodeShape, synthetic_adapter, synthetic_weights
 
@@ -665,6 +870,12 @@ def main():
                 "workers": W_ipc, "layers": args.ipc_layers, "rounds_per_token": 2 + 4 * args.ipc_layers, **res}
         except Exception as e:  # the headline line is still printed
             drop_in = {"error": f"{type(e).__name__}: {e}"[:2000]}
+    per_config = None
+    if not args.no_per_config:
+        try:
+            per_config = per_config_measure(args)
+        except Exception as e:  # the headline line is still printed
+            per_config = {"error": f"{type(e).__name__}: {e}"[:2000]}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(W, args.cpu_seconds)
@@ -704,6 +915,8 @@ def main():
                      "mean_launch_us": round(mean_ms * 1e3, 3), "bytes_per_launch": int(mean_bytes)},
         "cpu_baseline": cpu,
     }
+    if per_config is not None:
+        line["config"]["per_config"] = per_config
     if drop_in is not None:
         line["config"]["drop_in"] = drop_in
     print(json.dumps(line), flush=True)
