@@ -12,10 +12,11 @@ token per worker.  Synthetic random-init weights (seeded), no checkpoint.
 
 `value` is tokens/s over the timed replays of the captured step (inputs and
 weights resident in HBM).  `roofline` is the decode projection's base
-kernel (every projection round and the LM head use it): algorithmic bytes
-per launch over its mean duration, both from HIP events recorded around each
-launch on its stream during eager steps of the same workload (HIP events
-inside a replayed graph carry no timestamps on ROCm).  `cpu_baseline` times
+kernel (split_kernel, the 128 projection rounds of a step; the LM head is a
+whole-K round of its own): algorithmic bytes per launch over its mean
+duration, both from HIP events recorded around each launch on its stream
+during eager steps of the same workload (HIP events inside a replayed graph
+carry no timestamps on ROCm).  `cpu_baseline` times
 the CPU oracle's decode_step (torch-CPU bf16, the reference's op order) on a
 bounded sample: the LM head and one layer, scaled to 32 layers, on every
 core the process may use (CPU model and bf16-relevant flags reported).
@@ -52,8 +53,7 @@ REFERENCE_TOK_S = 314.0
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and scaled by a
 # copy kernel of known size (the summary file gives the commands and factors)
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
-TRAFFIC_FILES = {True: os.path.join(PROFILES, "fullk_kernel_decode_config4_pmc.md"),
-                 False: os.path.join(PROFILES, "split_kernel_decode_config4_pmc.md")}
+TRAFFIC_FILE = os.path.join(PROFILES, "split_kernel_decode_config4_pmc.md")
 
 
 def parse():
@@ -70,16 +70,9 @@ def parse():
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--weights", choices=("packed", "row-major"), default="packed",
                     help="decode: projection weights in fragment tiles (default) or row-major")
-    ap.add_argument("--whole-k", default="lm",
-                    help="decode: rounds run as whole-K rounds (no K-slice partials), a comma list of qkv, o, gu, "
-                         "down, lm (those with K <= 4096 take it), 'all' or 'none' (split + epilogue kernels "
-                         "everywhere); default lm")
-    ap.add_argument("--defer-qkv", action="store_true",
-                    help="decode: finish the QKV round in the attention kernel (round fusion out_mode 4, attention "
-                         "rope 3) instead of its epilogue kernel")
-    ap.add_argument("--chain", action="store_true",
-                    help="decode: each layer's O, Gate+Up and Down rounds and the next layer's QKV round as one "
-                         "persistent launch (swl_chain_*)")
+    ap.add_argument("--whole-k", choices=("lm", "none"), default="lm",
+                    help="decode: the LM head as a whole-K round (one launch, no K-slice partials; default) or "
+                         "K-sliced like the projection rounds")
     ap.add_argument("--workload", choices=("decode", "prefill", "ipc", "configs"), default="decode",
                     help="decode: BASELINE config 4 (the headline line); prefill: config 3's ragged one-layer "
                          "rounds on the MFMA path; ipc: the multi-process serving path (worker processes, "
@@ -117,10 +110,10 @@ def copy_calibration(args, dev):
     del src, dst
 
 
-def read_traffic(whole_k):
-    """hbm_bytes_per_launch of the dominant kernel from the committed counter
-    summary, or None."""
-    path = TRAFFIC_FILES[bool(whole_k)]
+def read_traffic():
+    """hbm_bytes_per_launch of the dominant kernel (split_kernel) from the
+    committed counter summary, or None."""
+    path = TRAFFIC_FILE
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -784,8 +777,7 @@ def main():
     max_new = 1 + args.warmup + args.steps + args.timer_steps + 1
     dec = BatchedDecoder(s, weights, adapters, ctx, first, dev, max_new=max_new, kv_fill=kv_fill,
                          packed=args.weights == "packed",
-                         whole_k="" if args.whole_k == "none" else args.whole_k, chain=args.chain,
-                         defer_qkv=args.defer_qkv)
+                         whole_k=args.whole_k == "lm")
     del weights, adapters
     torch.cuda.synchronize()
 
@@ -817,15 +809,11 @@ def main():
         torch.cuda._sleep(100_000_000)
         dec.step_eager()
     recs = ops.timer_collect()
-    # the dominant kernel: the whole-K round (QKV, O, Gate+Up, LM head) when
-    # the step uses it, else the K-sliced base kernel of every round
-    # the dominant kernel: the whole-K round when the Gate+Up round (the
-    # largest) takes it (its launches: every whole-K round), else the
-    # K-sliced base kernel of the K-sliced rounds
-    whole_k = bool(dec.wk.get("gu"))
-    wk_n = {n for g, n in (("qkv", s.qkv), ("o", s.hidden), ("gu", 2 * s.inter), ("lm", s.vocab)) if dec.wk.get(g)}
-    wk_rec = lambda r: r["k"] <= 4096 and r["n"] in wk_n  # noqa: E731
-    dom = [r for r in recs if wk_rec(r)] if whole_k else [r for r in recs if not wk_rec(r)]
+    # the dominant kernel: the K-sliced base kernel (split_kernel) of the 128
+    # projection rounds; the LM head (a whole-K round by default) is in the
+    # `rounds` breakdown only
+    lm_wk = bool(dec.wk.get("lm"))
+    dom = [r for r in recs if not (lm_wk and r["n"] == s.vocab)]
     base_ms = [r["base_ms"] for r in dom]
     base_bytes = [r["bytes"] for r in dom]
     mean_ms = statistics.fmean(base_ms)
@@ -844,11 +832,10 @@ def main():
                       "base_GBps": round(statistics.fmean([x["bytes"] for x in v]) /
                                          (statistics.fmean([x["base_ms"] for x in v]) * 1e-3) / 1e9, 1)}
                  for nm, v in per_op.items()}
-    traffic = read_traffic(whole_k)
+    traffic = read_traffic()
     copy_calibration(args, dev)
 
     step_bytes = s.step_bytes(ctx, W)
-    dec_wk = dict(dec.wk)
     dec.close()
     del dec
     torch.cuda.synchronize()
@@ -906,11 +893,8 @@ def main():
                    "rounds": breakdown},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": (f"fullk_kernel (whole-K decode round, epilogue included: "
-                                f"{', '.join(g for g in ('qkv', 'o', 'gu', 'lm') if dec_wk.get(g))}; the other "
-                                f"rounds split_kernel + epilogue_kernel)") if whole_k else
-                               (f"split_kernel (K-sliced decode projection base kernel; whole-K rounds: "
-                                f"{', '.join(g for g in dec_wk if dec_wk[g]) or 'none'})"),
+                     "kernel": ("split_kernel (K-sliced decode projection base kernel; the LM head is "
+                                + ("a whole-K round)" if lm_wk else "K-sliced too)")),
                      "launches": len(dom),
                      "mean_launch_us": round(mean_ms * 1e3, 3), "bytes_per_launch": int(mean_bytes)},
         "cpu_baseline": cpu,

@@ -60,7 +60,11 @@ enum {
 
 /* Thread-local text of the last failure on the calling thread. */
 const char* swl_last_error(void);
-/* ABI version of this library (bumped on any signature/layout change). */
+/* ABI version of this library (bumped on any signature/layout change;
+ * 2: swl_round_fusion ends with a_layout, the chain and deferred-QKV entry
+ * points are gone, swl_lora_rows_bf16 added).  A binding checks it against
+ * SWL_ABI_VERSION of the header it was written from. */
+#define SWL_ABI_VERSION 2
 int swl_abi_version(void);
 /* Number of HIP devices visible (0 on a host without a GPU); never faults. */
 int swl_device_count(void);
@@ -130,15 +134,6 @@ int swl_round_bf16(int n_seg, const int64_t* rows, const void* const* seg_in,
                    const swl_lora_entry* lora_table_host, int nblk,
                    const int64_t* blk_cols, void* stream);
 
-/* Where a QKV round with out_mode 4 left its work for the attention kernel:
- * its fp32 K-slice partial sums, its LoRA shrink partials and the per-token
- * adapters (layout private to the library).  Filled by swl_round_ex_bf16,
- * read by swl_paged_attention_rows_ex_bf16; valid until the next round on
- * the device reuses the library's scratch. */
-typedef struct swl_qkv_partials {
-  uint64_t opaque[128];
-} swl_qkv_partials;
-
 /* Optional fusions of a decode-shaped round (<= 64 token rows) with the
  * worker-side elementwise work on either side of it, for the in-process
  * batched decode step.  No counterpart in the reference: its worker runs this
@@ -163,11 +158,7 @@ typedef struct swl_qkv_partials {
  *      q, the rotated k and the v of token t are written to its page slot
  *      (position cache_seqlens[t]) in k_cache / v_cache [num_blocks,
  *      block_size, hkv, 128] through block_table [ntok, max_blocks]; RoPE
- *      (NeoX halves) at positions[t] from cos_sin [max_pos, 128].
- *   4  deferred QKV (decode, one token per sequence): only the K-sliced base
- *      kernel runs; fusion->defer receives its partials and
- *      swl_paged_attention_rows_ex_bf16 (rope 3) finishes the round (bias,
- *      LoRA expand, RoPE, KV append) inside the attention kernel. */
+ *      (NeoX halves) at positions[t] from cos_sin [max_pos, 128]. */
 typedef struct swl_round_fusion {
   const void* norm_weight;
   float eps;
@@ -187,24 +178,18 @@ typedef struct swl_round_fusion {
   int64_t max_pos;
   /* w_layout 1: w is in the fragment-tile layout of swl_pack_weight_bf16
    * (decode-shaped rounds only); 0: row-major [n, k].  2: the whole-K round
-   * (one launch, no partial sums; at most 32 token rows, k a multiple of
-   * 256 up to 4096) over w packed by swl_pack_weight_pairs_bf16 with
-   * pair_off n / 2 for out_mode 2, 64 for out_mode 3, 8 otherwise (n a
-   * multiple of 2 * pair_off); out_mode 1 then writes n / 16 partial sums of
-   * squares per row (ss_out_stride >= n / 16).  Whole-K rounds on one GPU
-   * share a set of counters and must be ordered (one stream). */
+   * over the same fragment tiles (one launch, no partial sums; out_mode 0
+   * with or without norm_weight, at most 32 token rows, k a multiple of 256
+   * up to 4096, n a multiple of 16): the decode step's LM head, where it
+   * beats the K-sliced round (one 1 GB weight); on the projection rounds it
+   * is slower.  The round's LoRA shrink runs as a small kernel just before
+   * it; neither uses cross-workgroup counters. */
   int32_t w_layout;
   /* a_layout 1: the stacked lora_A of every adapter entry the round uses is
    * in the fragment-tile layout of swl_pack_weight_bf16 (its nblk * rank rows
    * padded to 16 with zeros), streamed like the weight tiles; 0: row-major
    * [nblk * rank, k].  Decode-shaped rounds with w_layout 0 or 1 only. */
   int32_t a_layout;
-  /* out_mode 4 (a fused QKV round of one token row per sequence, w_layout 0
-   * or 1): only the K-sliced base kernel runs; bias, the LoRA expand, RoPE
-   * and the KV-page append are left to the attention kernel
-   * (swl_paged_attention_rows_ex_bf16 with rope 3), and *defer receives
-   * where the round's partial sums are.  NULL for the other modes. */
-  swl_qkv_partials* defer;
 } swl_round_fusion;
 
 /* Segmented LoRA delta of a packed batch x [T, k] (segment i = rows
@@ -235,15 +220,6 @@ int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg,
  * 347-376); the round results are bit-identical to the row-major ones. */
 int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out,
                          void* stream);
-
-/* swl_pack_weight_bf16 with paired rows: tile rows 0..7 are eight
- * consecutive rows j.. of a block of 2 * pair_off rows and tile rows 8..15
- * the rows j + pair_off.., so one tile holds both columns of a SiLU * up pair
- * (pair_off = inter) or of a RoPE pair (pair_off = 64 in 128-wide heads).
- * pair_off a multiple of 8 (8: the plain layout), n a multiple of
- * 2 * pair_off.  No counterpart in the reference (a layout of this build). */
-int swl_pack_weight_pairs_bf16(const void* w, int64_t n, int64_t k,
-                               int64_t pair_off, void* out, void* stream);
 
 /* swl_round_bf16 with fusions (fusion may be NULL; a non-NULL fusion needs
  * at most 64 token rows). */
@@ -398,95 +374,6 @@ int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, 
                                   int block_size, const int32_t* block_table, int64_t max_blocks,
                                   const int32_t* cache_seqlens, const int64_t* positions, const void* cos_sin,
                                   int64_t max_pos, int rope, float softmax_scale, void* stream);
-
-/* swl_paged_attention_rows_bf16 that also finishes an out_mode 4 QKV round
- * (rope = 3, decode rows, pages a multiple of 16 keys): every workgroup of a
- * (sequence, kv head, part) computes its query heads from the round's
- * partials (sum over the K-slices, bias, LoRA expand, one bf16 rounding,
- * NeoX RoPE at positions[seq]), and the part holding the new key also its k
- * and v, which it appends to the pages (cache_seqlens[seq] is the slot)
- * before it reads them; qkv_rows are not read.  The reference runs these
- * steps as the worker's rotary_embedding and flash_attn_with_kvcache after
- * the QKV round (worker_sync.py:169-205, model_builder.py:193-201).  With
- * qkv == NULL it is swl_paged_attention_rows_bf16. */
-int swl_paged_attention_rows_ex_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len, int hq,
-                                     int hkv, int d, void* k_cache, void* v_cache, int64_t num_blocks,
-                                     int block_size, const int32_t* block_table, int64_t max_blocks,
-                                     const int32_t* cache_seqlens, const int64_t* positions, const void* cos_sin,
-                                     int64_t max_pos, int rope, float softmax_scale,
-                                     const swl_qkv_partials* qkv, void* stream);
-
-/* ------------------------------------------- persistent decode chain ----
- * Several dependent decode-shaped rounds in one persistent launch: the O,
- * Gate+Up and Down rounds of a layer and the next layer's fused QKV round of
- * the reference's per-layer op sequence (ext_aggregator.cpp:1095-1199, the
- * rounds of ext_aggregator.cpp:562-612 with the worker's elementwise steps of
- * worker_sync.py:1344-1401 between them), each a whole-K round over weights
- * packed by swl_pack_weight_pairs_bf16 with the round's pair offset (n / 2
- * for out_mode 2, 64 for out_mode 3, 8 for out_mode 1).  Round r reads token
- * rows x [ntok, k] (row stride ldx), RMS-normalised on the way in when
- * norm_weight is set (factors from ss_in, as swl_round_fusion), adds the
- * LoRA delta of each token's table entry (rank 16, nblk column blocks of
- * widths blk_cols) and writes y by out_mode: 1 y = bf16(res + out) with one
- * sum of squares of y per 16 columns into ss_out (stride ss_out_stride
- * >= n / 16); 2 y [ntok, n / 2] = SiLU(gate) * up; 3 rows with NeoX RoPE on
- * q and k, k and v appended to the KV pages described by kv (its k_cache ..
- * max_pos fields).  A round may read what an earlier round of the chain
- * wrote; no round may write a buffer an earlier round of the chain reads
- * (the caller rotates the residual buffers).  ntok <= 32, k a multiple of
- * 256 (up to 4096 with norm_weight), at most SWL_CHAIN_MAX_ROUNDS rounds.
- * No counterpart in the reference (it launches each round and each
- * elementwise step separately). */
-#define SWL_CHAIN_MAX_ROUNDS 4
-typedef struct swl_chain_round {
-  const void* w;
-  int64_t n, k;
-  int32_t out_mode;
-  const void* x;
-  int64_t ldx;
-  const void* norm_weight;
-  const float* ss_in;
-  int32_t ss_in_n, ss_in_stride;
-  float eps;
-  void* y;
-  int64_t ldy;
-  const void* res;
-  int64_t ldres;
-  float* ss_out;
-  int32_t ss_out_stride;
-  const int32_t* lora; /* HOST [ntok] table entry per token (-1: none), or NULL */
-  int32_t nblk;
-  int64_t blk_cols[SWL_MAX_LORA_BLOCKS];
-} swl_chain_round;
-
-typedef struct swl_chain_plan swl_chain_plan;
-
-/* Validates the rounds, resolves the LoRA entries (lora_table_host: the host
- * mirror of the table, n_entries records) and uploads the launch arguments
- * to device memory (allocates); the plan is then launched any number of
- * times, also from a captured graph.  kv: the KV fields for out_mode 3 (may
- * be NULL otherwise). */
-int swl_chain_create(int ntok, int n_rounds, const swl_chain_round* rounds, const swl_lora_entry* lora_table_host,
-                     int n_entries, const swl_round_fusion* kv, swl_chain_plan** plan);
-/* One launch of the plan on `stream` (no allocation; launches of one plan
- * must not overlap). */
-int swl_chain_launch(swl_chain_plan* plan, void* stream);
-/* Synchronises the device, returns the plan's status word (bit r: a
- * device-side wait of round r gave up after its time limit, so that launch's
- * results are not valid) and clears it. */
-int swl_chain_status(swl_chain_plan* plan, uint32_t* timed_out);
-/* Benchmark instrumentation: with trace non-NULL (device memory, grid x
- * (2 + 3 * SWL_CHAIN_MAX_ROUNDS) uint64), every later launch stores per
- * workgroup the 100 MHz real-time clock at its start, per round when the
- * round's wait ended, when its LoRA expand rows were ready and when its
- * part of the round was stored, and at its exit; NULL turns it off.
- * swl_chain_grid: workgroups per launch. */
-int swl_chain_trace(swl_chain_plan* plan, uint64_t* trace);
-int swl_chain_grid(const swl_chain_plan* plan);
-/* Algorithmic HBM bytes of one launch (weights, distinct LoRA A and B, token
- * rows in and out). */
-int64_t swl_chain_bytes(const swl_chain_plan* plan);
-int swl_chain_destroy(swl_chain_plan* plan);
 
 #ifdef __cplusplus
 }

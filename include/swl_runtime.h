@@ -157,10 +157,21 @@ int swl_agg_drain_commands(uint64_t active_lo, uint64_t active_hi, int want, int
                            int32_t* ops, int32_t* layers, int64_t* tokens, uint64_t* x_keys, int* got);
 /* Eviction and leave-check periods of the barrier (defaults 500 ms, 10 ms). */
 int swl_agg_set_barrier_timeouts(int evict_ms, int leave_check_ms);
+/* The part of claim_slot that resets a slot's barrier bits for its next
+ * owner (ext_aggregator.cpp:223-227): clears the slot's ready and evicted
+ * bits in the attached queue, which a killed or evicted previous tenant may
+ * have left set.  claim_slot calls it after winning the slot. */
+int swl_agg_scrub_slot(int slot_id);
 /* Slots whose GPU-ordered input did not arrive within the stream wait's
  * limit (2 s) since the last call: writes up to 128 slot ids, returns the
  * count and clears them (such slots are also evicted by the main loop). */
 int swl_agg_take_seq_timeouts(int32_t* slot_ids, int max_ids);
+/* The main loop's token boundary (ext_aggregator.cpp:1053-1084): removes the
+ * slots that signalled leave from the active set *active_lo/_hi, adds the
+ * slots that signalled join (with their pending sampling parameters),
+ * publishes the result as the queue's active set and writes it back with its
+ * size.  The main loop calls it once per token. */
+int swl_agg_token_boundary(uint64_t* active_lo, uint64_t* active_hi, int* count);
 /* aggregator_main_loop_slots (ext_aggregator.cpp:1024-1210): blocks until the
  * quit flag is set.  dtype_code 15 (bfloat16) only. */
 int swl_agg_main_loop(int num_slots, int dtype_code);

@@ -31,6 +31,9 @@ P_vp = ctypes.POINTER(ctypes.c_void_p)
 P_size = ctypes.POINTER(ctypes.c_size_t)
 
 SWL_MAX_LORA_BLOCKS = 4
+# SWL_ABI_VERSION of include/swl.h that the structures and signatures below
+# mirror; load() refuses a library built from another version
+ABI_VERSION = 2
 
 
 class LoraEntry(ctypes.Structure):
@@ -41,12 +44,6 @@ class LoraEntry(ctypes.Structure):
         ("rank", c_i32),
         ("scale", c_f32),
     ]
-
-
-class QkvPartials(ctypes.Structure):
-    """swl_qkv_partials (include/swl.h): opaque record an out_mode 4 QKV
-    round fills for the attention kernel."""
-    _fields_ = [("opaque", ctypes.c_uint64 * 128)]
 
 
 class RoundFusion(ctypes.Structure):
@@ -74,33 +71,6 @@ class RoundFusion(ctypes.Structure):
         ("max_pos", c_i64),
         ("w_layout", ctypes.c_int32),
         ("a_layout", ctypes.c_int32),
-        ("defer", c_vp),
-    ]
-
-
-class ChainRound(ctypes.Structure):
-    """swl_chain_round (include/swl.h)."""
-    _fields_ = [
-        ("w", c_vp),
-        ("n", c_i64),
-        ("k", c_i64),
-        ("out_mode", ctypes.c_int32),
-        ("x", c_vp),
-        ("ldx", c_i64),
-        ("norm_weight", c_vp),
-        ("ss_in", c_vp),
-        ("ss_in_n", ctypes.c_int32),
-        ("ss_in_stride", ctypes.c_int32),
-        ("eps", c_f32),
-        ("y", c_vp),
-        ("ldy", c_i64),
-        ("res", c_vp),
-        ("ldres", c_i64),
-        ("ss_out", c_vp),
-        ("ss_out_stride", ctypes.c_int32),
-        ("lora", c_vp),
-        ("nblk", ctypes.c_int32),
-        ("blk_cols", c_i64 * 4),
     ]
 
 
@@ -133,7 +103,6 @@ _SIGS = {
     "swl_round_ex_noalloc_bf16": (c_int, [c_int, P_i64, P_vp, P_vp, c_vp, c_vp, c_i64, c_i64, P_i32, c_vp, c_vp, c_int,
                                   P_i64, ctypes.POINTER(RoundFusion), c_vp]),
     "swl_pack_weight_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
-    "swl_pack_weight_pairs_bf16": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp]),
     "swl_lora_segmented_bf16": (c_int, [c_vp, c_i64, c_int, P_i64, P_i32, c_vp, c_vp, c_int, P_i64, c_vp, c_i64,
                                         c_int, c_vp]),
     "swl_matmul_bf16": (c_int, [c_vp, c_i64, c_vp, c_i64, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_f32,
@@ -154,17 +123,6 @@ _SIGS = {
     "swl_silu_mul_rows_bf16": (c_int, [P_vp, P_vp, c_i64, c_i64, c_vp]),
     "swl_paged_attention_rows_bf16": (c_int, [P_vp, P_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64,
                                               c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_f32, c_vp]),
-    "swl_paged_attention_rows_ex_bf16": (c_int, [P_vp, P_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, c_i64,
-                                                 c_int, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_f32,
-                                                 ctypes.POINTER(QkvPartials), c_vp]),
-    "swl_chain_create": (c_int, [c_int, c_int, ctypes.POINTER(ChainRound), c_vp, c_int, ctypes.POINTER(RoundFusion),
-                                 ctypes.POINTER(c_vp)]),
-    "swl_chain_launch": (c_int, [c_vp, c_vp]),
-    "swl_chain_status": (c_int, [c_vp, ctypes.POINTER(ctypes.c_uint32)]),
-    "swl_chain_bytes": (c_i64, [c_vp]),
-    "swl_chain_trace": (c_int, [c_vp, c_vp]),
-    "swl_chain_grid": (c_int, [c_vp]),
-    "swl_chain_destroy": (c_int, [c_vp]),
 }
 
 _RUNTIME_SIGS = {}
@@ -196,6 +154,11 @@ def load():
                     f"{LIB_PATH} is missing: build it with `python -m swarmlora_amd.build` "
                     "(the HIP path has no fallback)")
             lib = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+            lib.swl_abi_version.restype = c_int
+            got = lib.swl_abi_version()
+            if got != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has ABI version {got}, this binding expects {ABI_VERSION}: "
+                                   "rebuild it with `python -m swarmlora_amd.build`")
             _declare(lib, _SIGS)
             _declare(lib, _RUNTIME_SIGS)
             _lib = lib

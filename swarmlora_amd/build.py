@@ -25,7 +25,6 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 SOURCES = [
     "kernels.hip",
-    "chain.hip",
     "ipc_queue.cpp",
     "aggregator.cpp",
     "worker_slots.cpp",

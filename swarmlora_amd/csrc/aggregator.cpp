@@ -222,6 +222,17 @@ int swl_agg_init_slot_pool(int num_slots, int device_index, int hidden_dim, int 
   return SWL_OK;
 }
 
+int swl_agg_scrub_slot(int slot_id) {
+  SWL_CHECK(slot_id >= 0 && slot_id < SWL_MAX_SLOTS, SWL_ERR_INVALID, "scrub_slot: invalid slot_id");
+  // A previous tenant may have left a ready bit (signalled, then killed or
+  // evicted) or an evicted bit (went silent): the new owner starts clean.
+  if (g_agg_q.ctrl) {
+    g_agg_q.ctrl->ready.clear_bits(Mask::bit(slot_id));
+    g_agg_q.ctrl->evicted.clear_bits(Mask::bit(slot_id));
+  }
+  return SWL_OK;
+}
+
 int swl_agg_claim_slot(int worker_id, int* slot_id, uint8_t* input_handle, uint8_t* output_handle,
                        size_t* input_buffer_size, size_t* output_buffer_size) {
   SWL_CHECK(g_pool.initialized, SWL_ERR_STATE, "claim_slot: slot pool not initialized");
@@ -239,12 +250,7 @@ int swl_agg_claim_slot(int worker_id, int* slot_id, uint8_t* input_handle, uint8
       continue;
     SlotInfo& s = p.slots[sid];
     s.owner.store(worker_id, std::memory_order_release);
-    // A previous tenant may have left a ready bit (evicted, then signalled) or
-    // an evicted bit (crashed): the new owner starts clean.
-    if (g_agg_q.ctrl) {
-      g_agg_q.ctrl->ready.clear_bits(Mask::bit(sid));
-      g_agg_q.ctrl->evicted.clear_bits(Mask::bit(sid));
-    }
+    (void)swl_agg_scrub_slot(sid);
     *slot_id = sid;
     if (input_handle) std::memcpy(input_handle, &s.in_handle, sizeof(hipIpcMemHandle_t));
     if (output_handle) std::memcpy(output_handle, &s.out_handle, sizeof(hipIpcMemHandle_t));
@@ -763,6 +769,40 @@ int run_op(int op, int layer, int n, const int32_t* sids, const int32_t* wids, c
 
 }  // namespace
 
+extern "C" int swl_agg_token_boundary(uint64_t* active_lo, uint64_t* active_hi, int* count) {
+  SWL_CHECK(g_agg_q.ctrl, SWL_ERR_STATE, "Aggregator queue not initialized");
+  SWL_CHECK(active_lo && active_hi && count, SWL_ERR_INVALID, "token_boundary: null argument");
+  swl::Control* c = g_agg_q.ctrl;
+  Mask active;
+  active.w[0] = *active_lo;
+  active.w[1] = *active_hi;
+  // leaves first, then joins (ext_aggregator.cpp:1053-1084)
+  if (!c->leaves.load().empty()) {
+    const Mask lv = c->leaves.take();
+    active = active & ~lv;
+    std::printf("[Aggregator] Slots LEFT: mask=0x%llx:%llx, active: %d slots\n", (unsigned long long)lv.w[1],
+                (unsigned long long)lv.w[0], active.count());
+    std::fflush(stdout);
+  }
+  if (!c->joins.load().empty()) {
+    const Mask jn = c->joins.take();
+    apply_join_sampling(jn);
+    active = active | jn;
+    std::printf("[Aggregator] Slots JOINED: mask=0x%llx:%llx, active: %d slots\n", (unsigned long long)jn.w[1],
+                (unsigned long long)jn.w[0], active.count());
+    std::fflush(stdout);
+  }
+  const int N = active.count();
+  c->active.store(active);
+  c->active_count.store(N, std::memory_order_release);
+  g_pool.active_mask.store(active);
+  g_pool.active_slot_count.store(N, std::memory_order_release);
+  *active_lo = active.w[0];
+  *active_hi = active.w[1];
+  *count = N;
+  return SWL_OK;
+}
+
 extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
   SWL_CHECK(g_agg_q.ctrl && g_agg_q.ring, SWL_ERR_STATE, "Aggregator queue not initialized");
   SWL_CHECK(g_weights_ready, SWL_ERR_STATE, "Aggregator weights not initialized");
@@ -786,27 +826,9 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
     return reinterpret_cast<uint64_t*>(static_cast<char*>(g_pool.slots[sid].out) + g_pool.out_size + off);
   };
   while (c->quit.load(std::memory_order_acquire) == 0) {
-    // token boundary: leaves first, then joins
-    if (!c->leaves.load().empty()) {
-      const Mask lv = c->leaves.take();
-      active = active & ~lv;
-      std::printf("[Aggregator] Slots LEFT: mask=0x%llx:%llx, active: %d slots\n", (unsigned long long)lv.w[1],
-                  (unsigned long long)lv.w[0], active.count());
-      std::fflush(stdout);
-    }
-    if (!c->joins.load().empty()) {
-      const Mask jn = c->joins.take();
-      apply_join_sampling(jn);
-      active = active | jn;
-      std::printf("[Aggregator] Slots JOINED: mask=0x%llx:%llx, active: %d slots\n", (unsigned long long)jn.w[1],
-                  (unsigned long long)jn.w[0], active.count());
-      std::fflush(stdout);
-    }
-    int N = active.count();
-    c->active.store(active);
-    c->active_count.store(N, std::memory_order_release);
-    g_pool.active_mask.store(active);
-    g_pool.active_slot_count.store(N, std::memory_order_release);
+    int N = 0;
+    rc = swl_agg_token_boundary(&active.w[0], &active.w[1], &N);
+    if (rc) return rc;
     if (N == 0) {
       std::this_thread::sleep_for(std::chrono::milliseconds(1));
       continue;

@@ -1,7 +1,7 @@
 // Device helpers shared by the HIP translation units of libswl (gfx950):
 // bf16 vector types, loads and stores through global-address-space
-// pointers, the 16x16x32 bf16 MFMA, the fragment-tile row pairing of packed
-// weights, s_waitcnt immediates and the LDS-only workgroup barrier.
+// pointers, the 16x16x32 bf16 MFMA, s_waitcnt immediates and the LDS-only
+// workgroup barrier.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -58,15 +58,6 @@ __device__ __forceinline__ u32x4 ldg16(const void* p) {
 }
 __device__ __forceinline__ float ldg_f32(const float* p) {
   return *(const __attribute__((address_space(1))) float*)(p);
-}
-
-// Row of W held by row rr (0..15) of packed tile `tile` when tiles pair the
-// rows j and j + off (off a multiple of 8): tile rows 0..7 are eight
-// consecutive rows of a block of 2 * off, rows 8..15 the rows off further.
-// off = 8 is the plain order (tile rows = W rows tile * 16 ..).
-__host__ __device__ __forceinline__ int64_t paired_row(int64_t tile, int rr, int64_t off) {
-  const int64_t per = off >> 3;  // tiles per block of 2 * off rows
-  return (tile / per) * (2 * off) + (tile % per) * 8 + (rr & 7) + (rr >= 8 ? off : 0);
 }
 
 // s_waitcnt immediate for vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0

@@ -146,21 +146,6 @@ __device__ __forceinline__ int64_t blk_start_of(const LoraEpi L, int b) {
   return v;
 }
 
-// What an out_mode 4 QKV round leaves for the attention kernel (the layout
-// behind swl_qkv_partials): K-slice partials part[n_ks][ntok][N], the LoRA
-// shrink partials and tables in L (u rows indexed by token), each token's
-// adapter entry (-1: none) and the bias.
-struct QkvPartials {
-  const float* part;
-  const bf16* bias;
-  int64_t N;
-  int32_t n_ks, ntok;
-  int32_t has_lora;
-  LoraEpi L;
-  int32_t lora[kSkinnyMaxTok];
-};
-static_assert(sizeof(QkvPartials) <= sizeof(swl_qkv_partials), "swl_qkv_partials must hold QkvPartials");
-
 // delta for 4 consecutive output columns (all inside block `blk`, first one at
 // in-block row `nin`) of the token whose shrink row is `urow`:
 // scale * sum_q u[q] * B[nin + j][q].
@@ -923,23 +908,20 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
 // (blockIdx.x, + gridDim.x, ...).  Each wave multiplies its k-steps of the
 // tile, the next tile's 16 fragments are requested right after (128 KiB in
 // flight per CU), the 8 wave partials are summed in LDS and the workgroup
-// finishes the tile itself: bias, the LoRA expand and the out_mode fusion,
-// then the stores.  The LoRA shrink rows u = x . A^T of the round's adapters
+// finishes the tile itself: bias and the LoRA expand, then the stores.  The LoRA shrink rows u = x . A^T of the round's adapters
 // come from fullk_shrink_kernel, launched just before (K-slice partials,
 // summed into LDS once per workgroup); with every adapter at rank 16 the
 // lora_B rows a tile needs are moved into LDS by LDS-DMA together with the
-// tile's weights.  The weights are packed with paired rows (pack offset
-// `off`): tile rows r and r + 8 are the output columns c and c + off, so
-// SiLU * up (off = inter) and RoPE (off = 64 within a head) find both
-// operands in one tile.
+// tile's weights.  The weights are in the fragment-tile layout of
+// swl_pack_weight_bf16; thread (token, p) finishes tile rows p and p + 8.
 constexpr int kFkWaves = 8;
 constexpr int kFkMaxSteps = 16;  // k-steps per wave: K <= 8 * 16 * 32
 constexpr int kFkShrinkKs = 4;   // K-slices of the shrink kernel
 
 struct FullKArgs {
-  const bf16* w;                // fragment tiles, rows paired by `off`
+  const bf16* w;                // fragment tiles (swl_pack_weight_bf16)
   int64_t N, K;
-  int32_t ntok, nsw, total_steps, off;
+  int32_t ntok, nsw, total_steps;
   int32_t n_tiles;              // ceil(N / 16)
   const bf16* x[32];
   bf16* y[32];
@@ -960,18 +942,6 @@ struct FullKArgs {
   int32_t bdma;                 // every adapter of the round has rank 16: lora_B rows staged in LDS
   float* u;                     // [kFkShrinkKs][ntok][u_ld] shrink partials
   const bf16* bias;
-  // out_mode 1
-  float* ss_out;
-  int32_t ss_out_stride;
-  // out_mode 3
-  bf16* kc;
-  bf16* vc;
-  const int32_t* bt;
-  const int32_t* seqlens;
-  const int64_t* pos;
-  const bf16* cs;
-  int64_t max_blocks, num_blocks, max_pos;
-  int32_t hq, hkv, bs;
 };
 typedef const __attribute__((address_space(4))) FullKArgs* fullk_args_ptr;
 
@@ -1066,7 +1036,7 @@ __global__ __launch_bounds__(256) void fullk_shrink_kernel(FullKArgs args) {
   }
 }
 
-template <int TT, int MODE>
+template <int TT>
 __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args) {
   fullk_args_ptr a = (fullk_args_ptr)__builtin_amdgcn_kernarg_segment_ptr();
   __shared__ f32x4 red[kFkWaves][TT][64];
@@ -1109,7 +1079,7 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
   // of w.
   const int n_bins = (ntok + 1) >> 1;
   auto issue_b = [&](int tile, int buf) {
-    const int64_t c0 = paired_row(tile, 0, a->off), c1 = c0 + a->off;
+    const int64_t c0 = (int64_t)tile * 16, c1 = c0 + 8;
     const int b0 = fk_blk(a, c0), b1 = fk_blk(a, c1);
     const int64_t r0 = (c0 - a->blk_start[b0]) * 16, r1 = (c1 - a->blk_start[b1]) * 16;
     const int h = (lane >> 4) & 1;
@@ -1214,11 +1184,11 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
       return v;
     };
 
-    // thread (token tk, pair p) finishes tile rows p and p + 8, output
-    // columns c0 and c0 + off
+    // thread (token tk, p) finishes tile rows p and p + 8, output columns c0
+    // and c0 + 8
     const int e = threadIdx.x;
     const int tk = e >> 3, p = e & 7;
-    const int64_t c0 = paired_row(cur, p, a->off), c1 = c0 + a->off;
+    const int64_t c0 = (int64_t)cur * 16 + p, c1 = c0 + 8;
     const bool live = tk < ntok && c0 < a->N;
     float v0 = 0.f, v1 = 0.f;
     if (live) {
@@ -1267,62 +1237,9 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
       }
     }
 
-    if constexpr (MODE == 0) {
-      if (live) {
-        stg(ytab[tk] + c0, f2bf(v0));
-        stg(ytab[tk] + c1, f2bf(v1));
-      }
-    } else if constexpr (MODE == 1) {
-      // h = bf16(h + out); the tile's sum of squares of the new h per token
-      float sq = 0.f;
-      if (live) {
-        bf16* yr = ytab[tk];
-        const bf16 h0 = f2bf(bf2f(ldg(yr + c0)) + bf2f(f2bf(v0)));
-        const bf16 h1 = f2bf(bf2f(ldg(yr + c1)) + bf2f(f2bf(v1)));
-        stg(yr + c0, h0);
-        stg(yr + c1, h1);
-        sq = bf2f(h0) * bf2f(h0) + bf2f(h1) * bf2f(h1);
-      }
-      sq += __shfl_xor(sq, 1, 64);
-      sq += __shfl_xor(sq, 2, 64);
-      sq += __shfl_xor(sq, 4, 64);
-      if (live && p == 0) a->ss_out[(int64_t)tk * a->ss_out_stride + cur] = sq;
-    } else if constexpr (MODE == 2) {
-      // c0 a gate column, c1 = c0 + inter its up column
-      if (live) {
-        const float g = bf2f(f2bf(v0)), u = bf2f(f2bf(v1));
-        stg(ytab[tk] + c0, f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u));
-      }
-    } else {
-      // c0 = head * 128 + d (d < 64), c1 = c0 + 64: NeoX RoPE pair of q / k
-      // heads; k and v also appended to their KV pages
-      if (live) {
-        const int hh = (int)(c0 >> 7), d = (int)(c0 & 63);
-        const bool is_q = hh < a->hq, is_k = !is_q && hh < a->hq + a->hkv;
-        float x0 = bf2f(f2bf(v0)), x1 = bf2f(f2bf(v1));
-        const int64_t ps = a->pos[tk];
-        if ((is_q || is_k) && ps >= 0 && ps < a->max_pos) {
-          const float rc = bf2f(a->cs[ps * 128 + d]), rs = bf2f(a->cs[ps * 128 + 64 + d]);
-          const float n0 = bf2f(f2bf(x0 * rc - x1 * rs));
-          const float n1 = bf2f(f2bf(x1 * rc + x0 * rs));
-          x0 = n0;
-          x1 = n1;
-        }
-        bf16* yr = ytab[tk];
-        stg(yr + c0, f2bf(x0));
-        stg(yr + c1, f2bf(x1));
-        const int64_t slen = a->seqlens[tk];
-        if (!is_q && slen >= 0 && slen / a->bs < a->max_blocks) {
-          const int32_t pb = a->bt[(int64_t)tk * a->max_blocks + slen / a->bs];
-          if (pb >= 0 && pb < a->num_blocks) {
-            const int kvh = is_k ? hh - a->hq : hh - a->hq - a->hkv;
-            const int64_t dst = ((int64_t)pb * a->bs + slen % a->bs) * a->hkv * 128 + kvh * 128 + d;
-            bf16* cache = is_k ? a->kc : a->vc;
-            stg(cache + dst, f2bf(x0));
-            stg(cache + dst + 64, f2bf(x1));
-          }
-        }
-      }
+    if (live) {
+      stg(ytab[tk] + c0, f2bf(v0));
+      stg(ytab[tk] + c1, f2bf(v1));
     }
     lds_barrier();  // red and bsm[cur_buf] are rewritten after this
   }
@@ -2109,8 +2026,6 @@ struct AttnArgs {
   int32_t rowmode;
   bf16* qkv_row[kSkinnyMaxTok];
   bf16* out_row[kSkinnyMaxTok];
-  // rope 3: q, k and v from an out_mode 4 round's partials
-  QkvPartials qp;
 };
 
 __device__ __forceinline__ bf16* tok_q(const AttnArgs& a, int64_t t) {
@@ -2487,159 +2402,6 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_f<0x140>(v);
 }
 
-// rope 3: the query heads of (sequence s, kv head h) computed from an out_mode
-// 4 QKV round's partials into qsh [G][128] (bf16), and in the part holding
-// the new key (kv) also the k and v rows of head h: into kvsh (k rotated,
-// both rounded to bf16, as fp32) for that part's own use and, written
-// without waiting, to the new key's page slot for later steps.  Units of 4
-// columns: unit (head c, half hf, quad q) covers dims 64 hf + 4 q .. + 3 of
-// head c (c < G: query head h G + c; c = G: k; c = G + 1: v).  Per column:
-// the K-slice partials summed in slice order, bias, the LoRA expand
-// u . B^T * scale (u: the token's shrink row summed over the K-slices), one
-// bf16 rounding, then NeoX RoPE for q and k (the partner dim through xsh)
-// rounded again, as the QKV round's epilogue does.  qkv_load issues the
-// loads (before the part's first K / V tiles, so they return first);
-// qkv_finish uses them; every thread of the workgroup calls both (barriers).
-constexpr int kQpPre = 8;  // K-slice partials of a unit requested together
-constexpr int kQpUnits = 2;  // units per thread (128 threads, G <= 4 with k and v)
-struct QpRegs {
-  f32x4 p[kQpUnits][kQpPre];
-  u32x4 b[kQpUnits][4][2];   // lora_B rows of the 4 columns (rank <= 16, a multiple of 8)
-  float u[kQpPre];           // this thread's shrink partials (q = threadIdx.x < u_ld)
-};
-
-__device__ __forceinline__ int64_t qp_col(const AttnArgs& a, int G, int h, int un) {
-  const int c = un >> 5, d0 = 64 * ((un >> 4) & 1) + 4 * (un & 15);
-  const int64_t cb = c < G ? (int64_t)(h * G + c) * 128 : c == G ? (int64_t)(a.hq + h) * 128
-                                                                 : (int64_t)(a.hq + a.hkv + h) * 128;
-  return cb + d0;
-}
-
-template <int G, int NT>
-__device__ __forceinline__ void qkv_load(const AttnArgs& a, int s, int h, bool kv, QpRegs& R) {
-  const QkvPartials& Q = a.qp;
-  const int lidx = Q.has_lora ? Q.lora[s] : -1;
-  const int nu = 32 * (G + (kv ? 2 : 0));
-  const swl_lora_entry* ep = lidx >= 0 ? Q.L.table + lidx : nullptr;
-  const bool breg = ep && ep->rank <= 16 && (ep->rank & 7) == 0;
-  const int64_t kst = (int64_t)Q.ntok * Q.N;
-#pragma unroll
-  for (int k = 0; k < kQpUnits; ++k) {
-    const int un = threadIdx.x + k * NT;
-    if (un >= nu) continue;
-    const int64_t col = qp_col(a, G, h, un);
-    const float* pp = Q.part + (int64_t)s * Q.N + col;
-#pragma unroll
-    for (int j = 0; j < kQpPre; ++j)
-      R.p[k][j] = j < Q.n_ks ? *reinterpret_cast<const f32x4*>(pp + j * kst) : f32x4{0.f, 0.f, 0.f, 0.f};
-    if (breg) {
-      const int r = ep->rank, b = find_blk(Q.L, col);
-      const bf16* brow = reinterpret_cast<const bf16*>(ep->b[b]) + (col - blk_start_of(Q.L, b)) * r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        R.b[k][e][0] = ld16(brow + e * r);
-        R.b[k][e][1] = r == 16 ? ld16(brow + e * r + 8) : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  }
-  if (lidx >= 0 && (int)threadIdx.x < Q.L.u_ld) {
-    const float* up = Q.L.u + (int64_t)s * Q.L.u_ld + threadIdx.x;
-#pragma unroll
-    for (int j = 0; j < kQpPre; ++j) R.u[j] = j < Q.L.usplit ? up[j * Q.L.u_split_stride] : 0.f;
-  }
-}
-
-template <int G, int NT>
-__device__ __forceinline__ void qkv_finish(const AttnArgs& a, int s, int h, bool kv, QpRegs& R, bf16* qsh,
-                                           bf16* xsh, float* ush, bf16* kvsh) {
-  const QkvPartials& Q = a.qp;
-  const int lidx = Q.has_lora ? Q.lora[s] : -1;
-  const swl_lora_entry* ep = lidx >= 0 ? Q.L.table + lidx : nullptr;
-  // the token's shrink row: u[q] = sum over the K-slices
-  if (lidx >= 0) {
-    for (int q = threadIdx.x; q < Q.L.u_ld; q += NT) {
-      float acc = 0.f;
-      if (q == (int)threadIdx.x) {
-#pragma unroll
-        for (int j = 0; j < kQpPre; ++j) acc += R.u[j];
-      }
-      const float* up = Q.L.u + (int64_t)s * Q.L.u_ld + q;
-      for (int j = q == (int)threadIdx.x ? kQpPre : 0; j < Q.L.usplit; ++j) acc += up[j * Q.L.u_split_stride];
-      ush[q] = acc;
-    }
-  }
-  __syncthreads();
-  const int nu = 32 * (G + (kv ? 2 : 0));
-  const int64_t kst = (int64_t)Q.ntok * Q.N;
-#pragma unroll
-  for (int k = 0; k < kQpUnits; ++k) {
-    const int un = threadIdx.x + k * NT;
-    if (un >= nu) continue;
-    const int c = un >> 5, d0 = 64 * ((un >> 4) & 1) + 4 * (un & 15);
-    const int64_t col = qp_col(a, G, h, un);
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < kQpPre; ++j) sum += R.p[k][j];
-    for (int j = kQpPre; j < Q.n_ks; ++j) sum += *reinterpret_cast<const f32x4*>(Q.part + (int64_t)s * Q.N + col + j * kst);
-    float x[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = sum[e] + (Q.bias ? bf2f(Q.bias[col + e]) : 0.f);
-    if (ep) {
-      const int r = ep->rank, b = find_blk(Q.L, col);
-      const float* ub = ush + b * r;
-      const bf16* brow = reinterpret_cast<const bf16*>(ep->b[b]) + (col - blk_start_of(Q.L, b)) * r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float dsum = 0.f;
-        if (r <= 16 && (r & 7) == 0) {
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            if (8 * hh >= r) break;
-            float bv[8];
-            unpack8(R.b[k][e][hh], bv);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) dsum += ub[8 * hh + t] * bv[t];
-          }
-        } else {
-          for (int i = 0; i < r; ++i) dsum += ub[i] * bf2f(brow[e * r + i]);
-        }
-        x[e] += dsum * ep->scale;
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) xsh[c * 128 + d0 + e] = f2bf(x[e]);
-  }
-  __syncthreads();
-  // RoPE of q and k; q into qsh, k and v into kvsh and their page slot
-  const int64_t pos = a.pos[s];
-  const bool rot_ok = pos >= 0 && pos < a.max_pos;
-  const int64_t slen = a.seqlens[s];
-  int64_t kvbase = -1;
-  if (kv && slen >= 0) {
-    const int64_t bi = slen / a.bs;
-    if (bi < a.max_blocks) {
-      const int32_t pb = a.bt[(int64_t)s * a.max_blocks + bi];
-      if (pb >= 0 && pb < a.num_blocks) kvbase = (((int64_t)pb * a.bs + slen % a.bs) * a.hkv + h) * 128;
-    }
-  }
-  for (int it = threadIdx.x; it < nu * 4; it += NT) {
-    const int c = it >> 7, d = it & 127;
-    float x = bf2f(xsh[c * 128 + d]);
-    if (c <= G && rot_ok) {
-      const float rc = bf2f(a.cs[pos * 128 + (d & 63)]), rsn = bf2f(a.cs[pos * 128 + 64 + (d & 63)]);
-      const float other = bf2f(xsh[c * 128 + (d < 64 ? d + 64 : d - 64)]);
-      x = bf2f(f2bf(d < 64 ? x * rc - other * rsn : x * rc + other * rsn));
-    }
-    if (c < G) {
-      qsh[c * 128 + d] = f2bf(x);
-    } else {
-      kvsh[(c - G) * 128 + d] = f2bf(x);
-      if (kvbase >= 0) (c == G ? a.kc : a.vc)[kvbase + d] = f2bf(x);
-    }
-  }
-  __syncthreads();
-}
-
 // Size-ordered part numbering for up to 64 sequences: workgroup b (linear
 // over the grid) takes kv head b % hkv of part unit b / hkv, where units are
 // every sequence's full parts (tpp tiles) in sequence order, then the partial
@@ -2694,14 +2456,10 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int h = blockIdx.x, p = blockIdx.y, s = blockIdx.z;
   if (order && !attn_unit_of(a, maxparts, tpp, lane, h, p, s)) return;  // uniform over the workgroup
-  const int64_t ctx_all = (int64_t)a.seqlens[s] + 1;
-  const int64_t ntiles = (ctx_all + kTileKeys - 1) / kTileKeys;
+  const int64_t ctx = (int64_t)a.seqlens[s] + 1;
+  const int64_t ntiles = (ctx + kTileKeys - 1) / kTileKeys;
   const int64_t tb = (int64_t)p * tpp;  // first tile of the part
   if (tb >= ntiles) return;             // uniform over the workgroup
-  // rope 3: the part holding the new key (key ctx_all - 1) takes it from LDS
-  // after its page tiles, which end before it
-  const bool kvpart = a.rope == 3 && p == (int)((ntiles - 1) / tpp);
-  const int64_t ctx = kvpart ? ctx_all - 1 : ctx_all;
   const int nt = (int)max<int64_t>(0, min<int64_t>(tpp, (ctx + kTileKeys - 1) / kTileKeys - tb));
   const int ntw = nt > w ? (nt - w + W - 1) / W : 0;  // this wave's tiles: w + j W
   char* ring = lds + w * WAVE_LDS;
@@ -2747,38 +2505,17 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
   };
 
   // q of the G query heads as the MFMA B operand: lane l holds column l % 16
-  // (query head, zero past G), dims 32 * step + 8 (l / 16) .. + 7.  rope 3:
-  // q computed from the QKV round's partials while the first tiles stream
-  // in; the part holding the new key appends its k and v first, then
-  // streams (its last tile reads them)
+  // (query head, zero past G), dims 32 * step + 8 (l / 16) .. + 7
   u32x4 qf[4];
-  __shared__ __attribute__((aligned(16))) bf16 qsh[G * 128];
-  __shared__ bf16 kvsh[2 * 128];
-  if (a.rope == 3) {
-    __shared__ bf16 xsh[(G + 2) * 128];
-    __shared__ float ush[kMaxURow];
-    QpRegs R;
-    qkv_load<G, 64 * W>(a, s, h, kvpart, R);
-#pragma unroll
-    for (int j = 0; j < S; ++j)
-      if (j < ntw) issue(j);
-    qkv_finish<G, 64 * W>(a, s, h, kvpart, R, qsh, xsh, ush, kvsh);
+  {
     const int col = lane & 15;
+    const bf16* qp = tok_q(a, s) + (int64_t)(h * G + (col < G ? col : 0)) * 128 + 8 * (lane >> 4);
 #pragma unroll
-    for (int st = 0; st < 4; ++st)
-      qf[st] = col < G ? *reinterpret_cast<const u32x4*>(qsh + col * 128 + 32 * st + 8 * (lane >> 4))
-                       : u32x4{0u, 0u, 0u, 0u};
-  } else {
-    {
-      const int col = lane & 15;
-      const bf16* qp = tok_q(a, s) + (int64_t)(h * G + (col < G ? col : 0)) * 128 + 8 * (lane >> 4);
-#pragma unroll
-      for (int st = 0; st < 4; ++st) qf[st] = col < G ? ldg16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int j = 0; j < S; ++j)
-      if (j < ntw) issue(j);
+    for (int st = 0; st < 4; ++st) qf[st] = col < G ? ldg16(qp + 32 * st) : u32x4{0u, 0u, 0u, 0u};
   }
+#pragma unroll
+  for (int j = 0; j < S; ++j)
+    if (j < ntw) issue(j);
 
   const int gg = lane >> 4;  // lane group: query heads gg * HPG ..
   float m[HPG], l[HPG], acc[HPG][8];
@@ -2891,27 +2628,6 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
     if (j + S < ntw) issue(j + S);
   }
 
-  // rope 3, the part holding the new key: wave 0 adds it (q . k_new, online
-  // softmax, p rounded to bf16 for the P.V product as for the page keys)
-  if (kvpart && w == 0) {
-#pragma unroll
-    for (int e = 0; e < HPG; ++e) {
-      const int g = gg < GL ? gg * HPG + e : 0;
-      float part_s = 0.f;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) part_s += bf2f(qsh[g * 128 + 8 * (lane & 15) + t]) * bf2f(kvsh[8 * (lane & 15) + t]);
-      const float sc_new = row16_sum(part_s) * a.scale;
-      const float mn = fmaxf(m[e], sc_new);
-      const float corr = __expf(m[e] - mn);
-      const float pe = __expf(sc_new - mn);
-      l[e] = l[e] * corr + pe;
-      m[e] = mn;
-      const float pr = bf2f(f2bf(pe));
-#pragma unroll
-      for (int d = 0; d < 8; ++d) acc[e][d] = acc[e][d] * corr + pr * bf2f(kvsh[128 + 8 * (lane & 15) + d]);
-    }
-  }
-
   // merge the W waves (all their DMA has landed) in LDS over the rings
   float* mg = reinterpret_cast<float*>(lds);  // [W][G][kAttnRec]
   if (W > 1) __syncthreads();
@@ -2951,17 +2667,17 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
 }
 
 // Fragment-tile packing of a row-major W [N][K]: output 16-byte chunk c =
-// ((tile * steps + step) * 64 + lane) holds row paired_row(tile, lane % 16),
+// ((tile * steps + step) * 64 + lane) holds row 16 tile + lane % 16,
 // columns step * 32 + 8 (lane / 16) .. + 7 (zero past row N).
-__global__ __launch_bounds__(256) void pack_weight_kernel(const bf16* w, int64_t N, int64_t K, int64_t off,
-                                                         u32x4* out, int64_t nchunks) {
+__global__ __launch_bounds__(256) void pack_weight_kernel(const bf16* w, int64_t N, int64_t K, u32x4* out,
+                                                         int64_t nchunks) {
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= nchunks) return;
   const int64_t steps = K >> 5;
   const int lane = (int)(c & 63);
   const int64_t ts = c >> 6;
   const int64_t tile = ts / steps, step = ts - tile * steps;
-  const int64_t r = paired_row(tile, lane & 15, off);
+  const int64_t r = tile * 16 + (lane & 15);
   u32x4 v = u32x4{0u, 0u, 0u, 0u};
   if (r < N) v = ldg16(w + r * K + step * 32 + 8 * (lane >> 4));
   out[c] = v;
@@ -3278,36 +2994,6 @@ int scratch_get(size_t need, hipStream_t stream, void** out) {
   return SWL_OK;
 }
 
-// A second scratch area with the contract of scratch_get (the decode
-// attention's part records while an out_mode 4 QKV round's partials occupy
-// the first).
-std::mutex g_scratch2_mu;
-std::vector<Scratch> g_scratch2;
-std::vector<void*> g_scratch2_kept;
-
-int scratch_get2(size_t need, hipStream_t stream, void** out) {
-  int dev = 0;
-  SWL_HIP(hipGetDevice(&dev));
-  std::lock_guard<std::mutex> lk(g_scratch2_mu);
-  if ((int)g_scratch2.size() <= dev) g_scratch2.resize(dev + 1);
-  Scratch& s = g_scratch2[dev];
-  if (s.bytes < need) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (stream) SWL_HIP(hipStreamIsCapturing(stream, &cs));
-    SWL_CHECK(cs == hipStreamCaptureStatusNone, SWL_ERR_STATE,
-              "scratch must grow outside graph capture (run the call once before capturing)");
-    size_t nb = std::max({need, s.bytes + s.bytes / 2, (size_t)1 << 20});
-    nb = (nb + 4095) & ~(size_t)4095;
-    void* p = nullptr;
-    SWL_HIP(hipMalloc(&p, nb));
-    if (s.ptr) g_scratch2_kept.push_back(s.ptr);
-    s.ptr = p;
-    s.bytes = nb;
-  }
-  *out = s.ptr;
-  return SWL_OK;
-}
-
 // ---------------------------------------------------------- launch timer
 // Optional HIP-event timing of the decode projection: when armed, every
 // launch_skinny call (outside graph capture) launches its base kernel and
@@ -3453,25 +3139,14 @@ void plan_shrink(ShrinkPlan& p, int ntok, const int32_t* tok_lora, const swl_lor
   p.g_tile0[p.ngroups] = p.tiles;
 }
 
-template <int TT, int MODE>
-int launch_fullk_tm(const FullKArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
+template <int TT>
+int launch_fullk_t(const FullKArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   static size_t allowed = 0;
   // static LDS: partial sums (16 KiB per token tile), lora_B buffers (16 KiB), tables
-  int rc = allow_lds(fullk_kernel<TT, MODE>, lds + 16 * 1024 * TT + 16 * 1024 + 2048, &allowed);
+  int rc = allow_lds(fullk_kernel<TT>, lds + 16 * 1024 * TT + 16 * 1024 + 2048, &allowed);
   if (rc) return rc;
-  launch_maybe_timed(fullk_kernel<TT, MODE>, grid, dim3(kFkWaves * 64), lds, st, e0, e1, a);
+  launch_maybe_timed(fullk_kernel<TT>, grid, dim3(kFkWaves * 64), lds, st, e0, e1, a);
   return SWL_OK;
-}
-
-template <int TT>
-int launch_fullk_t(int mode, const FullKArgs& a, dim3 grid, size_t lds, hipStream_t st, hipEvent_t e0,
-                   hipEvent_t e1) {
-  switch (mode) {
-    case 1: return launch_fullk_tm<TT, 1>(a, grid, lds, st, e0, e1);
-    case 2: return launch_fullk_tm<TT, 2>(a, grid, lds, st, e0, e1);
-    case 3: return launch_fullk_tm<TT, 3>(a, grid, lds, st, e0, e1);
-    default: return launch_fullk_tm<TT, 0>(a, grid, lds, st, e0, e1);
-  }
 }
 
 template <int TT, int W, int KD>
@@ -3498,21 +3173,18 @@ int launch_split_w(int TT, int kd, const SplitArgs& a, dim3 grid, size_t lds, hi
 }
 
 // Whole-K decode round (fullk_shrink_kernel when the round has adapters,
-// then fullk_kernel): weights packed with paired rows (w_layout 2; pair
-// offset inter for out_mode 2, 64 for out_mode 3, else 8), at most 32 token
-// rows, K a multiple of 256 up to 4096.
+// then fullk_kernel): fragment-tile weights (w_layout 2), out_mode 0 (with
+// RMSNorm on the way in allowed), at most 32 token rows, K a multiple of 256
+// up to 4096.  The decode step's LM head.
 int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok, const bf16* const* xrows,
                  bf16* const* yrows, const int32_t* tok_lora, const swl_lora_entry* table,
                  const swl_lora_entry* host_entries, const LoraEpi* Lblk, int nblk, const swl_round_fusion* fz,
                  hipStream_t st, void* ws, size_t ws_bytes) {
-  const int mode = fz->out_mode;
+  SWL_CHECK(fz->out_mode == 0, SWL_ERR_INVALID, "whole-K round (w_layout 2): out_mode 0 only");
   SWL_CHECK(ntok >= 1 && ntok <= 32, SWL_ERR_INVALID, "whole-K round (w_layout 2): at most 32 token rows");
   SWL_CHECK(K % (32 * kFkWaves) == 0 && K / (32 * kFkWaves) <= kFkMaxSteps, SWL_ERR_INVALID,
             "whole-K round (w_layout 2): K must be a multiple of 256, at most 4096");
-  const int64_t off = mode == 2 ? N / 2 : mode == 3 ? 64 : 8;
-  SWL_CHECK(off % 8 == 0 && N % (2 * off) == 0, SWL_ERR_INVALID,
-            "whole-K round (w_layout 2): n must be a multiple of 16 (of 2 * inter for out_mode 2, of 128 for "
-            "out_mode 3)");
+  SWL_CHECK(N % 16 == 0, SWL_ERR_INVALID, "whole-K round (w_layout 2): n must be a multiple of 16");
   const int TT = (ntok + 15) / 16;
   FullKArgs a{};
   a.w = w;
@@ -3521,7 +3193,6 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
   a.ntok = ntok;
   a.nsw = (int)(K / (32 * kFkWaves));
   a.total_steps = (int)(K / 32);
-  a.off = (int)off;
   a.n_tiles = (int)(N / 16);
   for (int i = 0; i < ntok; ++i) {
     a.x[i] = xrows[i];
@@ -3565,24 +3236,6 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
   } else {
     for (int i = 0; i < ntok; ++i) a.lora[i] = -1;
   }
-  if (mode == 1) {
-    a.ss_out = fz->ss_out;
-    a.ss_out_stride = fz->ss_out_stride;
-  }
-  if (mode == 3) {
-    a.kc = reinterpret_cast<bf16*>(fz->k_cache);
-    a.vc = reinterpret_cast<bf16*>(fz->v_cache);
-    a.bt = fz->block_table;
-    a.seqlens = fz->cache_seqlens;
-    a.pos = fz->positions;
-    a.cs = reinterpret_cast<const bf16*>(fz->cos_sin);
-    a.max_blocks = fz->max_blocks;
-    a.num_blocks = fz->num_blocks;
-    a.max_pos = fz->max_pos;
-    a.hq = fz->hq;
-    a.hkv = fz->hkv;
-    a.bs = fz->block_size;
-  }
   // LDS of the shrink rows: [ntok][u_ld + 4] floats
   const size_t us_bytes = has_lora ? sizeof(float) * (size_t)ntok * (a.u_ld + 4) : 0;
   if (has_lora) {
@@ -3613,8 +3266,7 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
     g_timer.bytes[tslot] = bytes;
   }
   hipEvent_t e0 = timer_event(tslot, 0), e1 = timer_event(tslot, 1);
-  int rc = TT == 1 ? launch_fullk_t<1>(mode, a, grid, us_bytes, st, e0, e1)
-                   : launch_fullk_t<2>(mode, a, grid, us_bytes, st, e0, e1);
+  int rc = TT == 1 ? launch_fullk_t<1>(a, grid, us_bytes, st, e0, e1) : launch_fullk_t<2>(a, grid, us_bytes, st, e0, e1);
   if (rc) return rc;
   SWL_LAUNCH_CHECK("fullk_kernel launch");
   if (tslot >= 0 && !has_lora) {
@@ -3638,21 +3290,16 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   const int mode = fz ? fz->out_mode : 0;
   const int64_t epi_cols = mode == 2 ? N / 2 : N;
   if (fz) {
-    SWL_CHECK(mode >= 0 && mode <= 4, SWL_ERR_INVALID, "round fusion: out_mode must be 0..4");
-    SWL_CHECK(mode != 4 || (fz->defer && fz->w_layout != 2), SWL_ERR_INVALID,
-              "round fusion: out_mode 4 needs defer and a K-sliced round (w_layout 0 or 1)");
+    SWL_CHECK(mode >= 0 && mode <= 3, SWL_ERR_INVALID, "round fusion: out_mode must be 0..3");
     SWL_CHECK(fz->w_layout >= 0 && fz->w_layout <= 2, SWL_ERR_INVALID, "round fusion: w_layout must be 0, 1 or 2");
     SWL_CHECK(fz->a_layout == 0 || (fz->a_layout == 1 && fz->w_layout != 2), SWL_ERR_INVALID,
               "round fusion: a_layout must be 0, or 1 (fragment-tile lora_A) with w_layout 0 or 1");
     if (fz->norm_weight)
       SWL_CHECK(fz->ss_in && fz->ss_in_n >= 1 && fz->ss_in_stride >= fz->ss_in_n, SWL_ERR_INVALID,
                 "round fusion: norm_weight needs ss_in with ss_in_n >= 1 partial sums per row");
-    if (mode == 1 && fz->w_layout != 2)
+    if (mode == 1)
       SWL_CHECK(fz->ss_out && fz->ss_out_stride >= (N + 255) / 256, SWL_ERR_INVALID,
                 "round fusion: out_mode 1 needs ss_out with ss_out_stride >= ceil(n / 256)");
-    if (mode == 1 && fz->w_layout == 2)
-      SWL_CHECK(fz->ss_out && fz->ss_out_stride >= N / 16, SWL_ERR_INVALID,
-                "round fusion: out_mode 1 of a whole-K round needs ss_out with ss_out_stride >= n / 16");
     if (mode == 2) SWL_CHECK(N % 2 == 0, SWL_ERR_INVALID, "round fusion: out_mode 2 needs n = 2 * inter");
     if (mode == 3)
       SWL_CHECK(fz->hq > 0 && fz->hkv > 0 && N == (int64_t)(fz->hq + 2 * fz->hkv) * 128 && fz->k_cache &&
@@ -3821,32 +3468,6 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   }
   SWL_LAUNCH_CHECK("split_kernel launch");
 
-  if (mode == 4) {
-    // the attention kernel finishes the round: tell it where the partials are
-    QkvPartials d{};
-    d.part = a.part;
-    d.bias = bias;
-    d.N = N;
-    d.n_ks = a.n_ks;
-    d.ntok = ntok;
-    d.has_lora = has_lora ? 1 : 0;
-    if (has_lora) {
-      d.L = *Lblk;
-      d.L.table = table;
-      d.L.u = a.u;
-      d.L.usplit = a.n_ks;
-      d.L.u_ld = a.u_ld;
-      d.L.u_split_stride = a.u_split_stride;
-    }
-    for (int i = 0; i < ntok; ++i) d.lora[i] = (has_lora && tok_lora[i] >= 0) ? tok_lora[i] : -1;
-    std::memset(fz->defer, 0, sizeof(swl_qkv_partials));
-    std::memcpy(fz->defer, &d, sizeof(d));
-    if (tslot >= 0) {  // no epilogue kernel: its events mark an empty interval
-      SWL_HIP(hipEventRecord(timer_event(tslot, 2), st));
-      SWL_HIP(hipEventRecord(timer_event(tslot, 3), st));
-    }
-    return SWL_OK;
-  }
 
   EpiArgs e{};
   e.part = a.part;
@@ -4065,9 +3686,7 @@ int launch_attn_tile_sw(const AttnArgs& a, hipStream_t st, int tpp, int order) {
   const int maxparts = (int)((max_tiles + tpp - 1) / tpp);
   void* scr = nullptr;
   const size_t need = sizeof(float) * (size_t)a.nseq * a.hkv * maxparts * G * kAttnRec;
-  // rope 3 reads the QKV round's partials from the first scratch area while
-  // parts store their records: those go to the second
-  int rc = a.rope == 3 ? scratch_get2(need, st, &scr) : scratch_get(need, st, &scr);
+  int rc = scratch_get(need, st, &scr);
   if (rc) return rc;
   float* part = reinterpret_cast<float*>(scr);
   hipLaunchKernelGGL((attn_tile_kernel<G, S, W>), dim3((unsigned)a.hkv, (unsigned)maxparts, (unsigned)a.nseq),
@@ -4105,14 +3724,12 @@ bool attn_tile_fits(const AttnArgs& a) {
 }
 
 int launch_attention(const AttnArgs& a, int G, hipStream_t st) {
-  if (a.rope <= 1) {  // 2: q rotated and k / v appended by the QKV round's epilogue; 3: by the attention kernel
+  if (a.rope <= 1) {  // 2: q rotated and k / v appended by the QKV round's epilogue
     hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(a.nseq * a.L), (unsigned)(a.hq + 2 * a.hkv)), dim3(64),
                        0, st, a);
     SWL_LAUNCH_CHECK("rope_append_kernel launch");
   }
-  SWL_CHECK(a.rope != 3 || (a.L == 1 && a.bs % kTileKeys == 0), SWL_ERR_INVALID,
-            "paged attention: rope 3 needs decode rows and pages of a multiple of 16 keys");
-  if (a.L == 1 && (attn_tile_fits(a) || a.rope == 3)) {
+  if (a.L == 1 && attn_tile_fits(a)) {
     switch (G) {
       case 1: return launch_attn_tile<1>(a, st);
       case 2: return launch_attn_tile<2>(a, st);
@@ -4212,7 +3829,7 @@ int plan_lora(int n_seg, const int64_t* rows, int64_t N, const int32_t* seg_lora
 extern "C" {
 
 const char* swl_last_error(void) { return swl::last_error().c_str(); }
-int swl_abi_version(void) { return 1; }
+int swl_abi_version(void) { return SWL_ABI_VERSION; }
 int swl_device_count(void) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess) return 0;
@@ -4380,23 +3997,17 @@ int swl_lora_segmented_bf16(const void* x, int64_t k, int n_seg, const int64_t* 
   return SWL_OK;
 }
 
-int swl_pack_weight_pairs_bf16(const void* w, int64_t n, int64_t k, int64_t pair_off, void* out, void* stream) {
+int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out, void* stream) {
   SWL_CHECK(w && out, SWL_ERR_INVALID, "swl_pack_weight_bf16: null argument");
   SWL_CHECK(n > 0 && k > 0 && k % 32 == 0, SWL_ERR_INVALID, "swl_pack_weight_bf16: k must be a positive multiple of 32");
   SWL_CHECK((reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
             SWL_ERR_INVALID, "swl_pack_weight_bf16: w and out must be 16-byte aligned");
-  SWL_CHECK(pair_off >= 8 && pair_off % 8 == 0 && (pair_off == 8 || n % (2 * pair_off) == 0), SWL_ERR_INVALID,
-            "swl_pack_weight_pairs_bf16: pair_off must be a multiple of 8 and n a multiple of 2 * pair_off");
   const int64_t nchunks = (n + 15) / 16 * 16 * k / 8;
   SWL_CHECK((nchunks + 255) / 256 < ((int64_t)1 << 31), SWL_ERR_INVALID, "swl_pack_weight_bf16: weight too large");
   hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((nchunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     reinterpret_cast<const bf16*>(w), n, k, pair_off, reinterpret_cast<u32x4*>(out), nchunks);
+                     reinterpret_cast<const bf16*>(w), n, k, reinterpret_cast<u32x4*>(out), nchunks);
   SWL_LAUNCH_CHECK("pack_weight_kernel launch");
   return SWL_OK;
-}
-
-int swl_pack_weight_bf16(const void* w, int64_t n, int64_t k, void* out, void* stream) {
-  return swl_pack_weight_pairs_bf16(w, n, k, 8, out, stream);
 }
 
 int swl_matmul_bf16(const void* x, int64_t ldx, const void* b, int64_t ldb, int trans_b, void* y, int64_t ldy,
@@ -4722,7 +4333,7 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
   const int u_ld = ((max_r * std::max(nblk, 1) + 15) / 16) * 16;  // A rows padded to 16-row tiles
   const bool fused = fz && (fz->norm_weight || fz->out_mode != 0 || fz->w_layout != 0 || fz->a_layout != 0);
   const int64_t out_cols = (fz && fz->out_mode == 2) ? N / 2 : N;
-  if (fz && (fz->out_mode == 3 || fz->out_mode == 4))
+  if (fz && fz->out_mode == 3)
     for (int i = 0; i < n_seg; ++i)
       SWL_CHECK(rows[i] == 1, SWL_ERR_INVALID, "round fusion: out_modes 3 and 4 take one token row per sequence");
 
@@ -4941,13 +4552,12 @@ extern "C" int swl_silu_mul_rows_bf16(const void* const* in_rows, void* const* o
   return SWL_OK;
 }
 
-extern "C" int swl_paged_attention_rows_ex_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len,
-                                                int hq, int hkv, int d, void* k_cache, void* v_cache,
-                                                int64_t num_blocks, int block_size, const int32_t* block_table,
-                                                int64_t max_blocks, const int32_t* cache_seqlens,
-                                                const int64_t* positions, const void* cos_sin, int64_t max_pos,
-                                                int rope, float softmax_scale, const swl_qkv_partials* qkv,
-                                                void* stream) {
+extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len,
+                                             int hq, int hkv, int d, void* k_cache, void* v_cache,
+                                             int64_t num_blocks, int block_size, const int32_t* block_table,
+                                             int64_t max_blocks, const int32_t* cache_seqlens,
+                                             const int64_t* positions, const void* cos_sin, int64_t max_pos,
+                                             int rope, float softmax_scale, void* stream) {
   SWL_CHECK(qkv_rows && out_rows && k_cache && v_cache && block_table && cache_seqlens, SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: null argument");
   SWL_CHECK(d == 128 && hq > 0 && hkv > 0 && hq % hkv == 0, SWL_ERR_INVALID,
@@ -4959,12 +4569,10 @@ extern "C" int swl_paged_attention_rows_ex_bf16(void* const* qkv_rows, void* con
             "swl_paged_attention_rows_bf16: at most 64 token rows");
   SWL_CHECK(block_size > 0 && num_blocks > 0 && max_blocks > 0, SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: bad page geometry");
-  SWL_CHECK(rope >= 0 && rope <= 3 && (rope < 2 || q_len == 1), SWL_ERR_INVALID,
-            "swl_paged_attention_rows_bf16: rope must be 0, 1, 2 or 3 (2 and 3: decode rows only)");
-  SWL_CHECK((rope == 1 || rope == 3) ? (cos_sin && positions && max_pos > 0) : true, SWL_ERR_INVALID,
+  SWL_CHECK(rope >= 0 && rope <= 2 && (rope < 2 || q_len == 1), SWL_ERR_INVALID,
+            "swl_paged_attention_rows_bf16: rope must be 0, 1 or 2 (2: decode rows only)");
+  SWL_CHECK(rope == 1 ? (cos_sin && positions && max_pos > 0) : true, SWL_ERR_INVALID,
             "swl_paged_attention_rows_bf16: rope needs positions and cos_sin");
-  SWL_CHECK((rope == 3) == (qkv != nullptr), SWL_ERR_INVALID,
-            "swl_paged_attention_rows_ex_bf16: rope 3 and the QKV round's partials go together");
   if (nseq == 0) return SWL_OK;
   AttnArgs a{};
   a.rowmode = 1;
@@ -4991,23 +4599,6 @@ extern "C" int swl_paged_attention_rows_ex_bf16(void* const* qkv_rows, void* con
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.rope = rope;
   a.scale = softmax_scale;
-  if (qkv) {
-    std::memcpy(&a.qp, qkv, sizeof(a.qp));
-    SWL_CHECK(a.qp.part && a.qp.N == (int64_t)(hq + 2 * hkv) * 128 && a.qp.ntok == nseq && a.qp.n_ks >= 1,
-              SWL_ERR_INVALID,
-              "swl_paged_attention_rows_ex_bf16: the partials are not those of a QKV round of these sequences");
-  }
   return launch_attention(a, G, (hipStream_t)stream);
 }
 
-extern "C" int swl_paged_attention_rows_bf16(void* const* qkv_rows, void* const* out_rows, int nseq, int q_len,
-                                             int hq, int hkv, int d, void* k_cache, void* v_cache,
-                                             int64_t num_blocks, int block_size, const int32_t* block_table,
-                                             int64_t max_blocks, const int32_t* cache_seqlens,
-                                             const int64_t* positions, const void* cos_sin, int64_t max_pos,
-                                             int rope, float softmax_scale, void* stream) {
-  SWL_CHECK(rope != 3, SWL_ERR_INVALID, "swl_paged_attention_rows_bf16: rope 3 needs swl_paged_attention_rows_ex_bf16");
-  return swl_paged_attention_rows_ex_bf16(qkv_rows, out_rows, nseq, q_len, hq, hkv, d, k_cache, v_cache, num_blocks,
-                                          block_size, block_table, max_blocks, cache_seqlens, positions, cos_sin,
-                                          max_pos, rope, softmax_scale, nullptr, stream);
-}

@@ -120,26 +120,15 @@ class BatchedDecoder:
     Capacity for `max_new` generated tokens is reserved up front.
     packed (fused step only): projection and LM-head weights kept in the
     fragment-tile layout (ops.PackedWeight) instead of row-major.
-    whole_k (packed step only, at most 32 workers): the rounds run as
-    whole-K rounds (w_layout 2: no K-slice partials) when their K allows
-    (<= 4096): True for the LM head, "all" for every round, or a set /
-    comma list of "qkv", "o", "gu", "down", "lm"; the others are K-sliced.
-    chain (packed step, at most 32 workers, rank-16 adapters): each layer's
-    O, Gate+Up and Down rounds and the next layer's QKV round run as one
-    persistent launch (ops.ChainPlan); layer 0's QKV round and the LM head
-    are whole-K rounds.
-    defer_qkv (fused step, K-sliced QKV round, pages a multiple of 16 keys):
-    the QKV round leaves its partial sums to the attention kernel, which
-    finishes it (bias, LoRA expand, RoPE, KV append: round fusion out_mode 4
-    and attention rope 3) instead of a separate epilogue kernel.  Off by
-    default: every attention part of a sequence re-reads the round's
-    partials and lora_B rows for its query heads (config 4, ~4 parts per
-    sequence: 6.47 ms per step against 6.37).
+    whole_k (packed step only, at most 32 workers): the LM head runs as a
+    whole-K round (w_layout 2: one launch, no K-slice partials; 206 us
+    against 248 for the K-sliced round at 28 workers); the projection rounds
+    are K-sliced (whole-K rounds measured slower for them).
     """
 
     def __init__(self, shape: DecodeShape, weights: dict, adapters: List[Optional[dict]], ctx_lens: List[int],
                  first_ids: List[int], device, max_new: int = 64, kv_fill=None, fused: bool = True,
-                 packed: bool = True, whole_k: bool = True, chain: bool = False, defer_qkv: bool = False):
+                 packed: bool = True, whole_k: bool = True):
         self.shape = s = shape
         self.device = dev = torch.device(device)
         self.W = W = len(ctx_lens)
@@ -152,26 +141,7 @@ class BatchedDecoder:
         self.graph = None
         self.fused = fused
         self.packed = packed and fused
-        names = ("qkv", "o", "gu", "down", "lm")
-        if whole_k is True:
-            wk = {"lm"}
-        elif whole_k == "all":
-            wk = set(names)
-        elif isinstance(whole_k, str):
-            wk = {g for g in whole_k.split(",") if g}
-        else:
-            wk = set(whole_k or ())
-        if not wk <= set(names):
-            raise ValueError(f"whole_k: rounds must be among {names}")
-        self.whole_k = wk if (self.packed and W <= 32) else set()
-        self.chain = bool(chain)
-        self.defer_qkv_req = bool(defer_qkv)
-        if self.chain:
-            if not self.packed or W > 32:
-                raise ValueError("chain: the packed fused step with at most 32 workers")
-            if any(ad is not None for ad in adapters) and shape.rank != 16:
-                raise ValueError("chain: adapters must have rank 16")
-            self.whole_k = set(names)
+        self.whole_k = bool(whole_k) and self.packed and W <= 32
         if fused:
             self._init_fused(weights, adapters, ctx_lens, first_ids, kv_fill)
             return
@@ -265,25 +235,17 @@ class BatchedDecoder:
         s, dev, W = self.shape, self.device, self.W
         self.layers_w = []
         self.norms = []
-        # whole-K rounds: K a multiple of 256 up to 4096, n a multiple of 16
-        # (of 128 for the QKV pairs, of 2 * inter for Gate+Up).  By default
-        # only the LM head takes them (measured at 8B widths, 28 workers, in
-        # the captured step: LM head 206 us against 248 for split +
-        # epilogue; Gate+Up 81 us against 75: with cold weights one tile per
-        # CU in flight streams at ~3.6 TB/s, and every CU loads all token
+        # the whole-K LM head: K a multiple of 256 up to 4096, n a multiple of
+        # 16 (measured at 8B widths, 28 workers, in the captured step: 206 us
+        # against 248 for split + epilogue; the projection rounds are faster
+        # K-sliced at every row count from 1 to 28: with cold weights one
+        # tile per CU in flight streams slower, and every CU loads all token
         # rows, more bytes than its share of the O / QKV weights)
-        fits = lambda g, k: g in self.whole_k and k % 256 == 0 and k <= 4096  # noqa: E731
-        self.wk = {"qkv": fits("qkv", s.hidden) and s.qkv % 128 == 0,
-                   "o": fits("o", s.heads * s.head_dim) and s.hidden % 16 == 0,
-                   "gu": fits("gu", s.hidden) and s.inter % 8 == 0,
-                   "down": fits("down", s.inter) and s.hidden % 16 == 0,
-                   "lm": fits("lm", s.hidden) and s.vocab % 16 == 0}
-        pair = {"qkv": 64, "gu": s.inter}
+        self.wk = {"qkv": False, "o": False, "gu": False, "down": False,
+                   "lm": self.whole_k and s.hidden % 256 == 0 and s.hidden <= 4096 and s.vocab % 16 == 0}
 
         def keep(t, g):
-            if not self.packed:
-                return t
-            return ops.pack_weight(t, pair_off=pair.get(g, 8) if self.wk[g] else 8)
+            return ops.pack_weight(t) if self.packed else t
 
         for lw in weights["layers"]:
             t = {k: v.to(dev) for k, v in lw.items()}
@@ -303,7 +265,7 @@ class BatchedDecoder:
         # the K-sliced rounds of the packed step stream the stacked lora_A as
         # fragment tiles like their weights (row-major A rows, 64-byte pieces
         # of 16 rows per load, were the last waves of the QKV and O rounds)
-        self.a_packed = {g: self.packed and not self.chain and not self.wk[g] for g in ("qkv", "o", "gu", "down")}
+        self.a_packed = {g: self.packed and not self.wk[g] for g in ("qkv", "o", "gu", "down")}
         self.table = ops.LoraTable(dev)
         groups = (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")), ("down", ("down",)))
         self.seg_lora = [{g: [-1] * W for g, _ in groups} for _ in range(s.layers)]
@@ -322,16 +284,11 @@ class BatchedDecoder:
                "gu": [s.inter, s.inter], "down": [s.hidden]}
 
         self._init_kv(ctx_lens, kv_fill)
-        # the QKV round finished inside the attention kernel (K-sliced QKV
-        # rounds over pages of whole 16-key tiles)
-        self.defer_qkv = self.defer_qkv_req and not self.chain and not self.wk["qkv"] and s.block_size % 16 == 0
-        self.qkv_defer = ops.QkvPartials() if self.defer_qkv else None
 
         # per-step buffers: one row per worker; partial sums of squares of the
-        # residual stream: one per 16 columns from a whole-K round, per 256
-        # from a K-sliced one
-        nss_o = s.hidden // 16 if self.wk["o"] else (s.hidden + 255) // 256
-        nss_d = s.hidden // 16 if self.wk["down"] else (s.hidden + 255) // 256
+        # residual stream, one per 256 columns (written by the O and Down
+        # rounds' epilogues)
+        nss_o = nss_d = (s.hidden + 255) // 256
         self.ids = torch.tensor(first_ids, dtype=torch.int64, device=dev).reshape(W, 1)
         self.h = torch.zeros(W, s.hidden, dtype=BF16, device=dev)        # residual stream
         self.x0 = torch.zeros(W, s.hidden, dtype=BF16, device=dev)       # layer 0's normed input
@@ -358,7 +315,7 @@ class BatchedDecoder:
                       cos_sin=self.cos_sin)
             wl = {g: (2 if self.wk[g] else 1) if self.packed else 0 for g in self.wk}
             al = {g: 1 if has_lora and self.a_packed[g] else 0 for g in self.a_packed}
-            qkv_out = dict(out_mode=4, defer=self.qkv_defer) if self.defer_qkv else dict(out_mode=3, **kv)
+            qkv_out = dict(out_mode=3, **kv)
             plan = (
                 ("qkv", rows(self.x0) if li == 0 else rows(self.h), rows(self.qkv),
                  ops.round_fusion(w_layout=wl["qkv"], a_layout=al["qkv"], **qkv_out) if li == 0 else
@@ -384,68 +341,12 @@ class BatchedDecoder:
         self._lm_call = (ops._round_args(rows(self.h), rows(self.logits), one, self.lm_head, None, None, None, None),
                          lm_fz)
         self._scale = 1.0 / (s.head_dim ** 0.5)
-        if self.chain:
-            self._init_chain(has_lora, blk, lm_fz)
-
-    def _init_chain(self, has_lora, blk, lm_fz):
-        """Per layer one ops.ChainPlan: O (residual), Gate+Up (RMSNorm in,
-        SiLU*up), Down (residual, token rows streamed) and the next layer's
-        QKV (RMSNorm in, RoPE + KV append).  The residual stream rotates
-        through three buffers so that no round of a launch writes a buffer an
-        earlier round of it reads: layer l reads h[i], writes the O output to
-        h[i + 1] and the Down output to h[i + 2] (mod 3), and layer l + 1
-        starts from that."""
-        s, dev, W = self.shape, self.device, self.W
-        one = [1] * W
-        self.hbuf = [self.h] + [torch.zeros(W, s.hidden, dtype=BF16, device=dev) for _ in range(2)]
-        self.ss_o = torch.zeros(W, s.hidden // 16, dtype=torch.float32, device=dev)
-        self.ss_d = torch.zeros(W, s.hidden // 16, dtype=torch.float32, device=dev)
-        rows = lambda t: [t[w:w + 1] for w in range(W)]  # noqa: E731
-        tab = self.table if has_lora else None
-        self.chains = []
-        cur = 0
-        for li in range(s.layers):
-            lw, (in_norm, post_norm) = self.layers_w[li], self.norms[li]
-            mid, out = (cur + 1) % 3, (cur + 2) % 3
-            lora = (lambda g, l=li: self.seg_lora[l][g] if has_lora else None)
-            rounds = [
-                dict(w=lw["o"], out_mode=1, x=self.attn, y=self.hbuf[mid], res=self.hbuf[cur], ss_out=self.ss_o,
-                     lora=lora("o"), blk_cols=blk["o"]),
-                dict(w=lw["gu"], out_mode=2, x=self.hbuf[mid], y=self.act, norm_weight=post_norm, ss_in=self.ss_o,
-                     eps=s.eps, lora=lora("gu"), blk_cols=blk["gu"]),
-                dict(w=lw["down"], out_mode=1, x=self.act, y=self.hbuf[out], res=self.hbuf[mid], ss_out=self.ss_d,
-                     lora=lora("down"), blk_cols=blk["down"]),
-            ]
-            kv = None
-            if li + 1 < s.layers:
-                nl = li + 1
-                rounds.append(dict(w=self.layers_w[nl]["qkv"], out_mode=3, x=self.hbuf[out],
-                                   norm_weight=self.norms[nl][0], ss_in=self.ss_d, eps=s.eps, y=self.qkv,
-                                   lora=lora("qkv", nl), blk_cols=blk["qkv"]))
-                kv = ops.round_fusion(out_mode=3, k_cache=self.kv.key_caches[nl], v_cache=self.kv.value_caches[nl],
-                                      hq=s.heads, hkv=s.kv_heads, block_table=self.block_tables,
-                                      cache_seqlens=self.seqlens, positions=self.positions, cos_sin=self.cos_sin)
-            self.chains.append(ops.ChainPlan(W, rounds, table=tab, kv=kv))
-            cur = out
-        self._h_last = cur
-        # the LM head reads the last layer's output and its per-16-column sums
-        lm_fz = ops.round_fusion(norm_weight=self.final_norm, eps=s.eps, ss_in=self.ss_d, w_layout=2)
-        self._lm_call = (ops._round_args(rows(self.hbuf[cur]), rows(self.logits), one, self.lm_head, None, None,
-                                         None, None), lm_fz)
 
     @property
     def final_h(self) -> torch.Tensor:
         """The residual stream after the last layer (what the final norm and
         the LM head read): [W, hidden]."""
-        return self.hbuf[self._h_last] if self.chain else self.h
-
-    def chain_status(self) -> int:
-        """OR of the chain plans' status words (0: every device-side wait of
-        the launches since the last call completed in time)."""
-        st = 0
-        for c in getattr(self, "chains", []):
-            st |= c.status()
-        return st
+        return self.h
 
     def _round_ex(self, call):
         args, fz = call
@@ -459,20 +360,10 @@ class BatchedDecoder:
         ops.rmsnorm_rows(self.h, self.norms[0][0], s.eps, self.rows_x0)
         for li in range(s.layers):
             qkv, o, gu, down = self._calls[li]
-            if li == 0 or not self.chain:
-                self._round_ex(qkv)
-            if self.defer_qkv:
-                ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
-                                         self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
-                                         self.seqlens, self.positions, self.cos_sin, self._scale, rope=3,
-                                         qkv_partials=self.qkv_defer)
-            else:
-                ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
-                                         self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
-                                         self.seqlens, None, None, self._scale, rope=2)
-            if self.chain:
-                self.chains[li].launch()
-                continue
+            self._round_ex(qkv)
+            ops.paged_attention_rows(self.rows_qkv, self.rows_attn, 1, s.heads, s.kv_heads, s.head_dim,
+                                     self.kv.key_caches[li], self.kv.value_caches[li], self.block_tables,
+                                     self.seqlens, None, None, self._scale, rope=2)
             self._round_ex(o)
             self._round_ex(gu)
             self._round_ex(down)
@@ -546,9 +437,6 @@ class BatchedDecoder:
 
     def close(self):
         self.graph = None
-        for c in getattr(self, "chains", []):
-            c.close()
-        self.chains = []
         if self.fused:
             return
         for sid, wid in zip(self.slot_ids, self.worker_ids):

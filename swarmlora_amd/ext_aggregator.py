@@ -49,6 +49,9 @@ _lib.register_signatures({
     "swl_agg_finalize": (c_int, []),
     "swl_agg_set_embed_lm_head": (c_int, [c_vp, c_vp, c_i64, c_i64]),
     "swl_agg_attach_queue": (c_int, [ctypes.c_char_p, c_int]),
+    "swl_agg_scrub_slot": (c_int, [c_int]),
+    "swl_agg_token_boundary": (c_int, [ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                                       ctypes.POINTER(c_int)]),
     "swl_agg_register_adapter": (c_int, [c_int, c_int, c_int, c_vp, ctypes.POINTER(c_vp), c_int, c_int, c_f32]),
     "swl_agg_clear_adapters": (c_int, []),
     "swl_agg_execute_round": (c_int, [c_int, c_int, c_int, P_i32, P_i32, P_i64, P_i32, c_vp]),
@@ -152,6 +155,12 @@ def claim_slot(worker_id):
                                        ctypes.byref(outs)))
     return {"slot_id": sid.value, "worker_id": int(worker_id), "input_handle": hin.raw, "output_handle": hout.raw,
             "input_buffer_size": ins.value, "output_buffer_size": outs.value}
+
+
+def scrub_slot(slot_id):
+    """claim_slot's reset of a slot's ready / evicted bits for its next owner
+    (ext_aggregator.cpp:223-227); claim_slot runs it itself."""
+    _lib.check(_L().swl_agg_scrub_slot(int(slot_id)))
 
 
 def release_slot(slot_id, worker_id):

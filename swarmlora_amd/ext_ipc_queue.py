@@ -9,7 +9,7 @@ protocol runs in libswl.so (swarmlora_amd/csrc/ipc_queue.cpp).
 import ctypes
 
 from . import _lib
-from ._lib import c_f32, c_i64, c_int, c_u64, c_vp
+from ._lib import c_f32, c_i64, c_int, c_u64
 
 _lib.register_signatures({
     "swl_q_create": (c_int, [c_int, c_int, ctypes.c_char_p, c_int]),

@@ -128,8 +128,8 @@ class LoraTable:
         weights, round fusion a_layout 1); bs[j]: bf16 [blk_cols[j], rank]."""
         packed = isinstance(a, PackedWeight)
         if packed:
-            if a.pair_off != 8 or a.n != rank * len(bs):
-                raise ValueError("packed lora a must be a plain PackedWeight of [nblk * rank, k]")
+            if a.n != rank * len(bs):
+                raise ValueError("packed lora a must be a PackedWeight of [nblk * rank, k]")
         else:
             _need(a, "lora a")
             if not a.is_contiguous() or a.shape[0] != rank * len(bs):
@@ -182,23 +182,19 @@ class LoraTable:
 
 class PackedWeight:
     """Fragment-tile copy of a row-major weight [n, k] for decode-shaped
-    rounds (swl_pack_weight_pairs_bf16): 16-row tiles stored whole, k-step
-    by k-step, each k-step block the MFMA A operand of those rows.  `data` is
-    flat bf16 of ceil(n / 16) * 16 * k elements.  pair_off > 8 pairs the rows
-    j and j + pair_off in each tile (whole-K rounds: inter for the Gate+Up
-    weight, 64 for the fused QKV weight)."""
+    rounds (swl_pack_weight_bf16): 16-row tiles stored whole, k-step by
+    k-step, each k-step block the MFMA A operand of those rows.  `data` is
+    flat bf16 of ceil(n / 16) * 16 * k elements."""
 
-    def __init__(self, w: torch.Tensor, pair_off: int = 8):
+    def __init__(self, w: torch.Tensor):
         _need(w, "w")
         if w.dim() != 2 or not w.is_contiguous():
             raise ValueError("w must be a contiguous [n, k] matrix")
         self.n, self.k = w.shape
         if self.k % 32:
             raise ValueError("k must be a multiple of 32")
-        self.pair_off = int(pair_off)
         self.data = torch.empty((self.n + 15) // 16 * 16 * self.k, dtype=BF16, device=w.device)
-        _lib.check(_lib.load().swl_pack_weight_pairs_bf16(_ptr(w), self.n, self.k, self.pair_off, _ptr(self.data),
-                                                          _stream()))
+        _lib.check(_lib.load().swl_pack_weight_bf16(_ptr(w), self.n, self.k, _ptr(self.data), _stream()))
 
     @property
     def shape(self):
@@ -212,9 +208,9 @@ class PackedWeight:
         return self.data.data_ptr()
 
 
-def pack_weight(w: torch.Tensor, pair_off: int = 8) -> PackedWeight:
+def pack_weight(w: torch.Tensor) -> PackedWeight:
     """Fragment-tile copy of w [n, k] (see PackedWeight)."""
-    return PackedWeight(w, pair_off)
+    return PackedWeight(w)
 
 
 def _round_args(seg_in, seg_out, rows, w, bias, seg_lora, table, blk_cols, out_div=1):
@@ -270,15 +266,14 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
                  k_cache: Optional[torch.Tensor] = None, v_cache: Optional[torch.Tensor] = None, hq: int = 0,
                  hkv: int = 0, block_table: Optional[torch.Tensor] = None,
                  cache_seqlens: Optional[torch.Tensor] = None, positions: Optional[torch.Tensor] = None,
-                 cos_sin: Optional[torch.Tensor] = None, w_layout: int = 0, a_layout: int = 0,
-                 defer: Optional["QkvPartials"] = None) -> RoundFusion:
+                 cos_sin: Optional[torch.Tensor] = None, w_layout: int = 0, a_layout: int = 0) -> RoundFusion:
     """swl_round_fusion for round_ex (include/swl.h documents each mode).
     ss_in / ss_out: fp32 [ntok, n_partial] (n_partial = ceil(n / 256) of the
     producing round); the record keeps the tensors it points to alive."""
     f = RoundFusion()
     keep = []
     if w_layout not in (0, 1, 2):
-        raise ValueError("w_layout must be 0 (row-major), 1 (fragment tiles) or 2 (whole-K round, paired tiles)")
+        raise ValueError("w_layout must be 0 (row-major), 1 (fragment tiles) or 2 (whole-K round)")
     f.w_layout = w_layout
     if a_layout not in (0, 1) or (a_layout == 1 and w_layout == 2):
         raise ValueError("a_layout must be 0 (row-major lora_A) or 1 (fragment tiles, w_layout 0 or 1)")
@@ -291,13 +286,8 @@ def round_fusion(norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
         f.norm_weight, f.eps = norm_weight.data_ptr(), float(eps)
         f.ss_in, f.ss_in_n, f.ss_in_stride = ss_in.data_ptr(), ss_in.shape[1], ss_in.stride(0)
         keep += [norm_weight, ss_in]
-    if out_mode not in (0, 1, 2, 3, 4):
-        raise ValueError("out_mode must be 0..4")
-    if (out_mode == 4) != (defer is not None):
-        raise ValueError("out_mode 4 (the attention kernel finishes the QKV round) goes with a QkvPartials record")
-    if defer is not None:
-        f.defer = ctypes.cast(ctypes.byref(defer), ctypes.c_void_p)
-        keep.append(defer)
+    if out_mode not in (0, 1, 2, 3):
+        raise ValueError("out_mode must be 0..3")
     f.out_mode = out_mode
     if out_mode == 1:
         _need(ss_out, "ss_out", torch.float32)
@@ -335,8 +325,8 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
              noalloc: bool = False):
     """round_fused with the decode-step fusions of `fusion` (round_fusion()).
     A PackedWeight w runs the K-sliced decode round (w_layout 1) unless the
-    fusion asks for the whole-K round (w_layout 2, weights packed with the
-    pair offset its out_mode needs: n / 2 for 2, 64 for 3, else 8).
+    fusion asks for the whole-K round (w_layout 2: out_mode 0 only, the
+    decode step's LM head).
     noalloc=True calls the allocation-free entry point
     (swl_round_ex_noalloc_bf16: at most 64 token rows, partials in the
     library's fixed 64 MiB device array)."""
@@ -345,13 +335,8 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
             fusion = RoundFusion()
         if fusion.w_layout != 2:
             fusion.w_layout = 1
-            if w.pair_off != 8:
-                raise ValueError("weights packed with paired rows need the whole-K round (w_layout 2)")
-        else:
-            want = w.n // 2 if fusion.out_mode == 2 else 64 if fusion.out_mode == 3 else 8
-            if w.pair_off != want:
-                raise ValueError(f"whole-K round with out_mode {fusion.out_mode} needs pair_off {want}, "
-                                 f"the weight has {w.pair_off}")
+        elif fusion.out_mode != 0:
+            raise ValueError("the whole-K round (w_layout 2) has out_mode 0 only")
     elif fusion is not None and fusion.w_layout != 0:
         raise ValueError("fusion.w_layout 1 or 2 needs a PackedWeight")
     if seg_lora is not None and table is not None and table.a_layout(seg_lora) == 1:
@@ -366,123 +351,6 @@ def round_ex(seg_in: Sequence[torch.Tensor], seg_out: Sequence[torch.Tensor], ro
                        out_div=2 if fusion is not None and fusion.out_mode == 2 else 1)
     fn = _lib.load().swl_round_ex_noalloc_bf16 if noalloc else _lib.load().swl_round_ex_bf16
     _lib.check(fn(*args, ctypes.byref(fusion) if fusion is not None else None, _stream()))
-
-
-def _rows2d(t: torch.Tensor, name: str, ntok: int, width: int, dtype=BF16):
-    """A 2-D view [>= ntok, >= width] with unit column stride: its row stride."""
-    _need(t, name, dtype)
-    if t.dim() != 2 or t.stride(1) != 1 or t.shape[0] < ntok or t.shape[1] < width:
-        raise ValueError(f"{name} must be a 2-D [{ntok}, {width}] view with unit column stride")
-    return t.stride(0)
-
-
-class ChainPlan:
-    """Several dependent decode rounds in one persistent launch
-    (swl_chain_create / swl_chain_launch): e.g. a layer's O, Gate+Up and Down
-    rounds and the next layer's fused QKV round.  rounds: dicts with
-      w (PackedWeight packed with pair offset n / 2 for out_mode 2, 64 for
-      out_mode 3, else 8), out_mode (1, 2 or 3), x [ntok, k] rows,
-      y output rows, res (out_mode 1: y = res + out), ss_out (out_mode 1,
-      fp32 [ntok, n / 16]), norm_weight + ss_in (+ eps) for RMSNorm on the way
-      in, lora (per-token table entries, -1 none) + blk_cols.
-    table: the LoraTable the entries index; kv: a RoundFusion carrying the KV
-    fields for out_mode 3.  The plan keeps every tensor it points to alive."""
-
-    def __init__(self, ntok: int, rounds, table: Optional["LoraTable"] = None, kv: Optional[RoundFusion] = None):
-        lib = _lib.load()
-        n = len(rounds)
-        arr = (_lib.ChainRound * n)()
-        self._keep = [kv, table]
-        host_tab, n_entries = ctypes.c_void_p(0), 0
-        if table is not None:
-            if table.a_layout(range(len(table))):
-                raise ValueError("chain rounds read row-major lora_A (add the adapters with a plain tensor)")
-            host_tab = ctypes.cast(table.host_table(), ctypes.c_void_p)
-            n_entries = len(table)
-            self._keep.append(table.device_table())
-        for i, r in enumerate(rounds):
-            c = arr[i]
-            w = r["w"]
-            if not isinstance(w, PackedWeight):
-                raise TypeError("chain rounds need a PackedWeight")
-            mode = int(r["out_mode"])
-            want = w.n // 2 if mode == 2 else 64 if mode == 3 else 8
-            if w.pair_off != want:
-                raise ValueError(f"chain round {i}: out_mode {mode} needs pair_off {want}, the weight has {w.pair_off}")
-            c.w, c.n, c.k, c.out_mode = w.data_ptr(), w.n, w.k, mode
-            c.x = r["x"].data_ptr()
-            c.ldx = _rows2d(r["x"], "x", ntok, w.k)
-            c.y = r["y"].data_ptr()
-            c.ldy = _rows2d(r["y"], "y", ntok, w.n // 2 if mode == 2 else w.n)
-            keep = [w, r["x"], r["y"]]
-            if r.get("norm_weight") is not None:
-                _need(r["norm_weight"], "norm_weight")
-                ss = r["ss_in"]
-                c.ss_in_stride = _rows2d(ss, "ss_in", ntok, 1, torch.float32)
-                c.norm_weight, c.ss_in, c.ss_in_n = r["norm_weight"].data_ptr(), ss.data_ptr(), ss.shape[1]
-                c.eps = float(r.get("eps", 1e-5))
-                keep += [r["norm_weight"], ss]
-            if mode == 1:
-                c.res = r["res"].data_ptr()
-                c.ldres = _rows2d(r["res"], "res", ntok, w.n)
-                keep.append(r["res"])
-                if r.get("ss_out") is not None:
-                    c.ss_out_stride = _rows2d(r["ss_out"], "ss_out", ntok, w.n // 16, torch.float32)
-                    c.ss_out = r["ss_out"].data_ptr()
-                    keep.append(r["ss_out"])
-            if r.get("lora") is not None:
-                if table is None:
-                    raise ValueError("LoRA entries need the table")
-                lo = _i32_array(r["lora"])
-                if len(r["lora"]) < ntok:
-                    raise ValueError("one LoRA entry per token")
-                c.lora = ctypes.cast(lo, ctypes.c_void_p)
-                blk = list(r["blk_cols"])
-                c.nblk = len(blk)
-                for b, v in enumerate(blk):
-                    c.blk_cols[b] = int(v)
-                keep.append(lo)
-            self._keep.append(keep)
-        h = ctypes.c_void_p(0)
-        _lib.check(lib.swl_chain_create(int(ntok), n, arr, host_tab, n_entries,
-                                        ctypes.byref(kv) if kv is not None else None, ctypes.byref(h)))
-        self._h = h
-        self.bytes = int(lib.swl_chain_bytes(h))
-
-    def launch(self):
-        _lib.check(_lib.load().swl_chain_launch(self._h, _stream()))
-
-    def trace(self, buf: Optional[torch.Tensor]):
-        """Attach (int64 [grid, 2 + 3 * 4] device tensor) or detach (None) the
-        per-workgroup timeline of later launches (swl_chain_trace)."""
-        if buf is not None:
-            _need(buf, "trace", torch.int64)
-            if buf.numel() < self.grid * 14 or not buf.is_contiguous():
-                raise ValueError("trace needs grid x 14 int64 entries")
-        self._trace = buf
-        _lib.check(_lib.load().swl_chain_trace(self._h, _ptr(buf)))
-
-    @property
-    def grid(self) -> int:
-        return int(_lib.load().swl_chain_grid(self._h))
-
-    def status(self) -> int:
-        """Synchronises; bit r set: a device-side wait of round r gave up (the
-        launch's results are not valid).  Clears the word."""
-        v = ctypes.c_uint32(0)
-        _lib.check(_lib.load().swl_chain_status(self._h, ctypes.byref(v)))
-        return int(v.value)
-
-    def close(self):
-        if self._h:
-            _lib.load().swl_chain_destroy(self._h)
-            self._h = ctypes.c_void_p(0)
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
 
 
 def lora_segmented(x: torch.Tensor, seg_rows: Sequence[int], seg_lora: Sequence[int], table: LoraTable,
@@ -794,23 +662,17 @@ def silu_mul(gu: torch.Tensor, inter: int) -> torch.Tensor:
     return out
 
 
-QkvPartials = _lib.QkvPartials
 
 
 def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: int, k_cache: torch.Tensor,
                          v_cache: torch.Tensor, block_table: torch.Tensor, cache_seqlens: torch.Tensor,
                          positions: Optional[torch.Tensor], cos_sin: Optional[torch.Tensor], softmax_scale: float,
-                         rope=True, qkv_partials: Optional[QkvPartials] = None):
+                         rope=True):
     """paged_attention over per-token rows: token t = seq * q_len + i has
     its fused [q | k | v] row at qkv_rows[t] (rotated in place) and gets its
     [hq * d] output at out_rows[t].  rope=2: q already rotated and k / v
-    already appended by an out_mode 3 round (decode rows only).  rope=3 with
-    qkv_partials: the kernel finishes an out_mode 4 QKV round (bias, LoRA
-    expand, RoPE at positions, the KV append) from its partials; the rows are
-    not read."""
-    rope = rope if rope in (2, 3) else (1 if rope else 0)
-    if (rope == 3) != (qkv_partials is not None):
-        raise ValueError("rope 3 goes with the QKV round's QkvPartials record")
+    already appended by an out_mode 3 round (decode rows only)."""
+    rope = 2 if rope == 2 else (1 if rope else 0)
     qkv = _rowset(qkv_rows, (hq + 2 * hkv) * d)
     out = _rowset(out_rows, hq * d)
     if len(qkv) != len(out) or len(qkv) % q_len:
@@ -830,7 +692,7 @@ def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: i
     if cache_seqlens.numel() < nseq:
         raise ValueError("cache_seqlens must have nseq entries")
     max_pos = 0
-    if rope in (1, 3):
+    if rope == 1:
         _need(positions, "positions", torch.int64)
         _need(cos_sin, "cos_sin")
         if positions.numel() != nseq * q_len:
@@ -838,12 +700,11 @@ def paged_attention_rows(qkv_rows, out_rows, q_len: int, hq: int, hkv: int, d: i
         if cos_sin.shape[-1] != d or not cos_sin.is_contiguous():
             raise ValueError("cos_sin must be contiguous [max_pos, d]")
         max_pos = cos_sin.shape[0]
-    rp = rope in (1, 3)
-    _lib.check(_lib.load().swl_paged_attention_rows_ex_bf16(
+    rp = rope == 1
+    _lib.check(_lib.load().swl_paged_attention_rows_bf16(
         qkv.array, out.array, nseq, q_len, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs, _ptr(block_table),
         block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rp else None),
-        _ptr(cos_sin if rp else None), max_pos, rope, float(softmax_scale),
-        ctypes.byref(qkv_partials) if qkv_partials is not None else None, _stream()))
+        _ptr(cos_sin if rp else None), max_pos, rope, float(softmax_scale), _stream()))
 
 
 # -------------------------------------------------------------- timing ---

@@ -23,7 +23,7 @@ graphs captured before it must be captured again.
 import threading
 import time
 import traceback
-from typing import Dict, Iterator, List, Optional, Sequence, Tuple
+from typing import Dict, Iterator, List, Sequence, Tuple
 
 import torch
 

@@ -10,7 +10,7 @@ libswl (bf16 operands, fp32 accumulation, bf16 results), never torch matmul.
 
 import json
 import os
-from typing import Dict, List, Optional, Sequence
+from typing import Dict, Optional, Sequence
 
 import torch
 import torch.nn as nn

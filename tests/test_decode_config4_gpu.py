@@ -48,8 +48,7 @@ def _contexts():
     return ctx
 
 
-@pytest.mark.parametrize("chain,defer_qkv", [(False, False), (True, False), (False, True)])
-def test_config4_shape_decode_steps_eager_then_graph(dev, chain, defer_qkv):
+def test_config4_shape_decode_steps_eager_then_graph(dev):
     from swarmlora_amd.decode import BatchedDecoder, DecodeShape, synthetic_adapter, synthetic_weights
     s = DecodeShape(layers=2)
     ctx = _contexts()
@@ -72,8 +71,7 @@ def test_config4_shape_decode_steps_eager_then_graph(dev, chain, defer_qkv):
         vc.copy_(torch.randn(vc.shape, generator=kv_gen, device=dev, dtype=torch.bfloat16))
         pages[li] = (kc.cpu(), vc.cpu())
 
-    dec = BatchedDecoder(s, wd, ad_dev, ctx, first, dev, max_new=6, kv_fill=kv_fill, fused=True, packed=True,
-                         chain=chain, defer_qkv=defer_qkv)
+    dec = BatchedDecoder(s, wd, ad_dev, ctx, first, dev, max_new=6, kv_fill=kv_fill, fused=True, packed=True)
     del wd, ad_dev
     kc = [pages[li][0] for li in range(s.layers)]
     vc = [pages[li][1] for li in range(s.layers)]
@@ -111,7 +109,6 @@ def test_config4_shape_decode_steps_eager_then_graph(dev, chain, defer_qkv):
                 assert int(nxt[w]) == int(glf[w].argmax()), f"step {step} worker {w}: argmax"
                 assert lg32[w, nxt[w]] >= lg32[w].max() - TOL_BF16 * lg32[w].abs().max(), f"step {step} worker {w}"
             assert dec.seqlens.cpu().tolist() == (seq + 1).tolist()
-        assert dec.chain_status() == 0, "a device-side wait of a chain launch ran out"
         # KV pages: every entry the steps did not append is unchanged (bit for bit); the appended k
         # (roped) and v rows are within 1e-2 in layer 0 (one QKV round from identical inputs) and
         # within the two-evaluation bound in later layers (inputs carry the composed drift)

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import reference_path as ref
-from tests._util import BF16, rel_err, randn
+from tests._util import rel_err, randn
 
 pytestmark = pytest.mark.gpu
 

@@ -143,8 +143,8 @@ def test_packed_lora_a_matches_row_major_bitwise(dev, T, in_dim, out_dims, ranks
 
 def test_packed_lora_a_refused_where_unsupported(dev):
     """Fragment-tile lora_A is read only by the K-sliced decode rounds:
-    mixed layouts in one round, the whole-K round, the prefill regime, the
-    segmented delta and chains refuse it."""
+    mixed layouts in one round, the whole-K round, the prefill regime and
+    the segmented delta refuse it."""
     ops = _ops()
     t_rm, t_pk, _ = _table_packed_a(dev, 64, [32], [16, 16])
     A = torch.zeros(16, 64, dtype=BF16, device=dev)

@@ -197,3 +197,102 @@ def test_multiprocess_lockstep_rounds(queue):
             p.join(timeout=30)
             if p.is_alive():
                 p.kill()
+
+
+def _boundary(lo=0, hi=0):
+    """The main loop's token boundary over the active set (lo, hi): leaves
+    out, joins in, the result published; returns the active slots."""
+    clo, chi, n = ctypes.c_uint64(lo), ctypes.c_uint64(hi), ctypes.c_int(0)
+    _lib.check(_lib.load().swl_agg_token_boundary(ctypes.byref(clo), ctypes.byref(chi), ctypes.byref(n)))
+    return [s for s in range(128) if ((clo.value if s < 64 else chi.value) >> (s % 64)) & 1]
+
+
+def _tenant_killed_later(shm_name, slot, late_ready, out, cmd):
+    """A worker that joins, runs op 0, goes silent for op 1 (the barrier
+    evicts it), optionally signals ready late, and waits to be killed."""
+    from swarmlora_amd import ext_ipc_queue as q
+    q.open_queue(shm_name, 16, 16)
+    q.slot_signal_join(slot)
+    t0 = time.time()
+    while not q.slot_is_active(slot):
+        if time.time() - t0 > 60:
+            out.put("never active")
+            return
+        time.sleep(0.001)
+    epoch = q.get_barrier_done_epoch()
+    q.submit_slot_command(OP_QKV, 0, slot, 77, 1, 1, 4096, 0, 0, 0, 0, 0)
+    q.slot_signal_ready(slot)
+    q.wait_for_epoch(epoch)
+    out.put("op0")
+    cmd.get(timeout=60)  # op 1 ran without it: evicted
+    if late_ready:
+        q.slot_signal_ready(slot)
+    out.put("parked")
+    time.sleep(600)
+
+
+@pytest.mark.parametrize("late_ready", [False, True])
+def test_worker_killed_with_its_slot_open(queue, late_ready):
+    """Failure case of a worker SIGKILLed while its slot is open
+    (ext_aggregator.cpp:215-227, aggregator.py:484-528): the silent slot is
+    evicted by the barrier, the controller signals its leave and releases it
+    at a token boundary, and the next tenant of the slot starts with clean
+    barrier bits.  The dead tenant leaves an evicted bit (which would make
+    the new tenant abort its request) and, if it signalled ready after the
+    eviction, a ready bit that no signal_done clears any more (the slot is no
+    longer active) and that would let the new tenant's first op run without
+    its input.  The claim's scrub (swl_agg_scrub_slot, what claim_slot runs
+    after winning the slot; the pool itself needs the GPU) clears both: the
+    barrier then waits for the new tenant's own ready."""
+    import os
+    import signal
+    from swarmlora_amd import ext_aggregator as agg
+    ctx = mp.get_context("spawn")
+    out, cmd = ctx.Queue(), ctx.Queue()
+    slot = 3
+    p = ctx.Process(target=_tenant_killed_later, args=(queue["shm_name"], slot, late_ready, out, cmd))
+    p.start()
+    try:
+        active = []
+        t0 = time.time()
+        while slot not in active:
+            assert time.time() - t0 < 120, "the worker never joined"
+            active = _boundary()
+            time.sleep(0.001)
+        cnt, active = _wait([slot])  # op 0
+        assert cnt == 1 and [c[0] for c in _drain([slot], 1)] == [slot]
+        _lib.check(_lib.load().swl_agg_signal_done())
+        assert out.get(timeout=60) == "op0"
+        cnt, active = _wait([slot])  # op 1: the worker stays silent and is evicted
+        assert cnt == 0 and active == [] and extq.is_slot_evicted(slot)
+        _lib.check(_lib.load().swl_agg_signal_done())
+        cmd.put("go")
+        assert out.get(timeout=60) == "parked"
+        os.kill(p.pid, signal.SIGKILL)
+        p.join(timeout=30)
+        assert p.exitcode == -signal.SIGKILL
+        # the controller sees the dead worker: leave, then release at a token boundary
+        extq.slot_signal_leave(slot)
+        assert _boundary(1 << slot) == []
+        if late_ready:
+            # the late ready bit survived: a barrier over the slot would pass at once
+            cnt, active = _wait([slot])
+            assert cnt == 1 and active == [slot]
+        # the next claim of the slot scrubs its bits; the new tenant joins
+        agg.scrub_slot(slot)
+        assert not extq.is_slot_evicted(slot)
+        extq.slot_signal_join(slot)
+        assert _boundary() == [slot]
+        t0 = time.time()
+        cnt, active = _wait([slot])  # no stale ready: the barrier waits for the new tenant (and evicts it here)
+        assert cnt == 0 and time.time() - t0 >= 0.05
+        agg.scrub_slot(slot)
+        extq.slot_signal_ready(slot)  # the new tenant's own ready
+        cnt, active = _wait([slot])
+        assert cnt == 1 and active == [slot] and not extq.is_slot_evicted(slot)
+        _lib.check(_lib.load().swl_agg_signal_done())
+    finally:
+        if p.is_alive():
+            p.kill()
+            p.join(timeout=30)
+        _boundary()  # drop what the test left in the join / leave sets

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import reference_path as ref
-from tests._util import BF16, assert_close, randn, rel_err
+from tests._util import assert_close, randn, rel_err
 
 pytestmark = pytest.mark.gpu
 

@@ -108,17 +108,13 @@ def test_noalloc_round_refuses_what_does_not_fit(dev):
     ys = [torch.zeros(65, 64, dtype=BF16, device=dev)]
     with pytest.raises(RuntimeError, match="at most 64 token rows"):
         ops.round_ex(xs, ys, [65], w, noalloc=True)
-    # partials of 64 rows x 600000 columns (4 K-slices of fp32) do not fit 64 MiB: refused before any
-    # launch (the weight's size is not touched by the check)
-    import ctypes
-    from swarmlora_amd import _lib
-    n = 600000
-    rows = (ctypes.c_int64 * 1)(64)
-    x = torch.zeros(64, 4096, dtype=BF16, device=dev)
-    y = torch.zeros(1, dtype=BF16, device=dev)
-    seg_in = (ctypes.c_void_p * 1)(x.data_ptr())
-    seg_out = (ctypes.c_void_p * 1)(y.data_ptr())
-    rc = _lib.load().swl_round_ex_noalloc_bf16(1, rows, seg_in, seg_out, w.data_ptr(), None, n, 4096, None, None,
-                                               None, 1, None, None, ctypes.c_void_p(
-                                                   torch.cuda.current_stream().cuda_stream))
-    assert rc != 0 and "allocation-free scratch" in _lib.last_error()
+    # partials of 64 rows x 131072 columns (at least 4 K-slices of fp32: 128 MiB) do not fit the
+    # 64 MiB array: refused.  Every buffer is really allocated at its full size (a 1 GiB weight), so
+    # the call stays in bounds whatever order the checks run in.
+    n = 131072
+    w = torch.zeros(n, 4096, dtype=BF16, device=dev)
+    xs = [torch.zeros(64, 4096, dtype=BF16, device=dev)]
+    ys = [torch.zeros(64, n, dtype=BF16, device=dev)]
+    with pytest.raises(RuntimeError, match="allocation-free scratch"):
+        ops.round_ex(xs, ys, [64], w, noalloc=True)
+    del w
