@@ -1,5 +1,8 @@
-"""A small Llama-shaped model (head_dim 128, GQA) built from fixed seeds, plus
-its CPU-oracle forward, for the end-to-end multi-process test."""
+"""Llama-shaped test models built from fixed seeds, plus their CPU-oracle
+forward, for the end-to-end multi-process tests: CFG is small (hidden 512,
+GQA 4/2, two layers); WIDE has Llama-3.1-8B's widths (hidden 4096, 32 query /
+8 kv heads of 128, intermediate 14336, rank-16 adapters) with two layers and
+a 32000-entry vocabulary."""
 
 from types import SimpleNamespace
 
@@ -9,56 +12,84 @@ from tests._util import BF16, randn
 
 CFG = SimpleNamespace(hidden=512, heads=4, kv_heads=2, head_dim=128, inter=1024, vocab=640, layers=2, eps=1e-5,
                       theta=500000.0, rank=8, scale=2.0, block=16, max_seq=256, chunk=16)
+WIDE = SimpleNamespace(hidden=4096, heads=32, kv_heads=8, head_dim=128, inter=14336, vocab=32000, layers=2, eps=1e-5,
+                       theta=500000.0, rank=16, scale=2.0, block=16, max_seq=256, chunk=16)
+CFGS = {"tiny": CFG, "wide": WIDE}
 QKV = CFG.hidden + 2 * CFG.kv_heads * CFG.head_dim
 KVD = CFG.kv_heads * CFG.head_dim
-PROJ = {  # name: (in, out)
-    "self_attn.q_proj": (CFG.hidden, CFG.hidden), "self_attn.k_proj": (CFG.hidden, KVD),
-    "self_attn.v_proj": (CFG.hidden, KVD), "self_attn.o_proj": (CFG.hidden, CFG.hidden),
-    "mlp.gate_proj": (CFG.hidden, CFG.inter), "mlp.up_proj": (CFG.hidden, CFG.inter),
-    "mlp.down_proj": (CFG.inter, CFG.hidden),
-}
 
 
-def base_weights():
+def proj_dims(c=CFG):
+    """name: (in, out) of every projection of config c."""
+    kvd = c.kv_heads * c.head_dim
+    return {"self_attn.q_proj": (c.hidden, c.hidden), "self_attn.k_proj": (c.hidden, kvd),
+            "self_attn.v_proj": (c.hidden, kvd), "self_attn.o_proj": (c.hidden, c.hidden),
+            "mlp.gate_proj": (c.hidden, c.inter), "mlp.up_proj": (c.hidden, c.inter),
+            "mlp.down_proj": (c.inter, c.hidden)}
+
+
+PROJ = proj_dims(CFG)
+
+
+def norm_weights(c=CFG):
+    """The RMSNorm vectors of base_weights(c) alone: [(input, post) per
+    layer], final (the same seeds, without drawing the projections)."""
+    layers = [((1 + randn((c.hidden,), 1000 * (li + 1) + 50, std=0.1).float()).to(BF16),
+               (1 + randn((c.hidden,), 1000 * (li + 1) + 51, std=0.1).float()).to(BF16)) for li in range(c.layers)]
+    return layers, (1 + randn((c.hidden,), 9, std=0.1).float()).to(BF16)
+
+
+def base_weights(c=CFG):
     """CPU bf16 weights: per layer dict of q,k,v,o,gate,up,down and the two
     norm vectors; embed, lm_head and the final norm."""
     layers = []
-    for li in range(CFG.layers):
+    for li in range(c.layers):
         s = 1000 * (li + 1)
-        w = {name.split(".")[1][:-5]: randn((o, i), s + j, std=0.02) for j, (name, (i, o)) in enumerate(PROJ.items())}
-        w["input_norm"] = (1 + randn((CFG.hidden,), s + 50, std=0.1).float()).to(BF16)
-        w["post_norm"] = (1 + randn((CFG.hidden,), s + 51, std=0.1).float()).to(BF16)
+        w = {name.split(".")[1][:-5]: randn((o, i), s + j, std=0.02)
+             for j, (name, (i, o)) in enumerate(proj_dims(c).items())}
+        w["input_norm"] = (1 + randn((c.hidden,), s + 50, std=0.1).float()).to(BF16)
+        w["post_norm"] = (1 + randn((c.hidden,), s + 51, std=0.1).float()).to(BF16)
         layers.append(w)
-    return {"layers": layers, "embed": randn((CFG.vocab, CFG.hidden), 7, std=1.0),
-            "lm_head": randn((CFG.vocab, CFG.hidden), 8, std=0.02),
-            "final_norm": (1 + randn((CFG.hidden,), 9, std=0.1).float()).to(BF16)}
+    return {"layers": layers, "embed": randn((c.vocab, c.hidden), 7, std=1.0),
+            "lm_head": randn((c.vocab, c.hidden), 8, std=0.02),
+            "final_norm": (1 + randn((c.hidden,), 9, std=0.1).float()).to(BF16)}
 
 
-def adapter(worker_id):
+def adapter(worker_id, c=CFG):
     """{layer: {proj_name: (A [r, in], B [out, r])}} for one worker."""
     out = {}
-    for li in range(CFG.layers):
+    for li in range(c.layers):
         out[li] = {}
-        for j, (name, (i, o)) in enumerate(PROJ.items()):
+        for j, (name, (i, o)) in enumerate(proj_dims(c).items()):
             s = 100000 * (worker_id + 1) + 100 * li + 2 * j
-            out[li][name] = (randn((CFG.rank, i), s, std=0.02), randn((o, CFG.rank), s + 1, std=0.02))
+            out[li][name] = (randn((c.rank, i), s, std=0.02), randn((o, c.rank), s + 1, std=0.02))
     return out
 
 
-def oracle_steps(weights, ad, steps):
+def to_float32(weights, ad):
+    """The same weights and adapter in float32 (exact conversions)."""
+    w32 = {"layers": [{k: v.float() for k, v in lw.items()} for lw in weights["layers"]],
+           "embed": weights["embed"].float(), "lm_head": weights["lm_head"].float(),
+           "final_norm": weights["final_norm"].float()}
+    return w32, {li: {n: (a.float(), b.float()) for n, (a, b) in m.items()} for li, m in ad.items()}
+
+
+def oracle_steps(weights, ad, steps, c=CFG):
     """Teacher-forced CPU oracle: steps is the list of [1, t] input id
-    tensors the worker fed; returns the final-norm hidden of each step."""
+    tensors the worker fed; returns the final-norm hidden of each step (in
+    the weights' dtype: bf16, or float32 for the float32 evaluation)."""
     from oracle import reference_path as ref
-    c = CFG
+    dt = weights["embed"].dtype
     inv = ref.rope_inv_freq(c.head_dim, c.theta)
     cs = ref.cos_sin_cache(inv, c.max_seq)
     nblk = c.max_seq // c.block
-    kc = [torch.zeros(nblk, c.block, c.kv_heads, c.head_dim, dtype=BF16) for _ in range(c.layers)]
-    vc = [torch.zeros(nblk, c.block, c.kv_heads, c.head_dim, dtype=BF16) for _ in range(c.layers)]
+    kc = [torch.zeros(nblk, c.block, c.kv_heads, c.head_dim, dtype=dt) for _ in range(c.layers)]
+    vc = [torch.zeros(nblk, c.block, c.kv_heads, c.head_dim, dtype=dt) for _ in range(c.layers)]
     bt = torch.arange(nblk, dtype=torch.int32).reshape(1, nblk)
     seqlen = 0
     outs = []
-    dims_qkv = [c.hidden, KVD, KVD]
+    kvd = c.kv_heads * c.head_dim
+    dims_qkv = [c.hidden, kvd, kvd]
     for ids in steps:
         t = ids.shape[1]
         h = weights["embed"][ids.reshape(-1).clamp(0, c.vocab - 1)].reshape(1, t, c.hidden)
