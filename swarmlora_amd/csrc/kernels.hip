@@ -3388,18 +3388,21 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   }
   while (n_ks < total_steps && lds_of(n_ks) > lds_cap) n_ks *= 2;
   n_ks = std::min<int64_t>(n_ks, total_steps);
-  // One 16-wave workgroup per CU rather than three 8-wave ones (up to 32
-  // token rows, when the row tiles do not overfill the slots): the three
-  // workgroups of a CU would stage the same K-slice of the token rows three
-  // times.  Waves with three tiles or more (Gate+Up at 28 rows: 3.6) keep 16
-  // k-steps of W in flight instead of 8.  Measured per round (28 rows, us,
-  // three 8-wave workgroups -> one 16-wave, depth 8 -> depth 16): QKV 18.6
-  // -> 16.8, O 14.3 -> 13.0, Down 30.4 -> 29.2, Gate+Up 57.1 -> 57.6 -> 56.7.
-  if (!tu.shape_forced && !long_rows && TT <= 2 && waves == 8) {
+  // One 16-wave workgroup per CU rather than several 8-wave ones (when the
+  // row tiles do not overfill the slots): the workgroups of a CU would stage
+  // the same K-slice of the token rows several times.  Waves with three
+  // tiles or more (Gate+Up at 28 rows: 3.6) keep 16 k-steps of W in flight
+  // instead of 8 (up to 32 token rows; the 16-deep variant is not built for
+  // wider token tiles).  Measured per round (28 rows, us, three 8-wave
+  // workgroups -> one 16-wave, depth 8 -> depth 16): QKV 18.6 -> 16.8, O 14.3
+  // -> 13.0, Down 30.4 -> 29.2, Gate+Up 57.1 -> 57.6 -> 56.7; at 64 rows (two
+  // 8-wave workgroups -> one 16-wave, round with its epilogue): QKV 26.7 ->
+  // 25.1, O 20.4 -> 18.6, Gate+Up 97.1 -> 89.7, Down 49.5 -> 42.0.
+  if (!tu.shape_forced && !long_rows && TT <= 4 && waves == 8) {
     waves = 16;
     slots = cu_count();
     if ((double)a.n_tiles * n_ks >= 3.0 * (double)slots * waves && (total_steps + n_ks - 1) / n_ks > 8) {
-      kd = 16;
+      if (TT <= 2) kd = 16;
       // and twice as long K-slices where the CU's one workgroup can stage
       // them (half the fp32 partials; Gate+Up 71.7 -> 70.5 us with its
       // epilogue at 4 slices of 32 steps)
@@ -3409,7 +3412,7 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
       // many slices of twice the steps, 16 k-steps in flight: half the fp32
       // partials (Down 29.2 + 7.3 -> 28.9 + 6.3 us with its epilogue, 6.11 ->
       // 6.04 ms per config-4 step)
-      kd = 16;
+      if (TT <= 2) kd = 16;
       n_ks /= 2;
     }
   }
