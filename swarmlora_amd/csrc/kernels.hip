@@ -3,26 +3,38 @@
 // Kernels
 //   gather_rows_kernel      slot rows -> packed batch (128-bit copies)
 //   scatter_rows_kernel     packed rows (+ delta) -> slot rows
-//   split_kernel<TT,WAVES>  M <= 64 "decode" projection, part 1: workgroups
-//                           of 8 waves own 128 W rows x one K-slice; the
-//                           K-slice of every token's activation (read through
-//                           per-token row pointers: the gather is fused) is
-//                           staged once in LDS and shared by the waves, W is
-//                           streamed from HBM straight into MFMA A-fragments,
-//                           fp32 partials go to scratch.  Lower workgroups run
-//                           the LoRA shrink u = x . A^T for groups of tokens
-//                           sharing an adapter (each adapter's A read once).
+//   split_kernel<TT,WAVES>  M <= 64 "decode" projection, part 1: one K-slice
+//                           per workgroup (16 waves, one workgroup per CU, up
+//                           to 64 token rows); the K-slice of every token's
+//                           activation (read through per-token row pointers:
+//                           the gather is fused) is staged once in LDS and
+//                           shared by the waves, 16-row W tiles dealt over the
+//                           slice's workgroups are streamed from HBM straight
+//                           into MFMA A-fragments, fp32 partials go to
+//                           scratch.  The stacked lora_A of each adapter of
+//                           the round are extra row tiles: the LoRA shrink
+//                           u = x . A^T rides the same stream.
 //   epilogue_kernel         part 2: sums the K-slice partials, adds bias and
 //                           the LoRA expand u . B^T * scale, rounds once and
 //                           stores each token's row into its slot buffer (the
 //                           scatter is fused).
-//   tiled_kernel            M > 64 "prefill" projection: 128x128x64 LDS-staged
-//                           MFMA tiles, fp32 accumulation, same epilogue.
+//   gemm256_kernel          M > 64 "prefill" projection: 256x256 (or 256x192)
+//                           MFMA tiles fed by LDS-DMA, rows read in place from
+//                           the slot buffers, the LoRA delta as extra k-steps.
+//   tiled_kernel            the prefill projection for K not a multiple of 64:
+//                           128x128x64 LDS-staged MFMA tiles over a gathered
+//                           copy, fp32 accumulation, same epilogue.
+//   fullk_kernel            the whole-K decode round (the decode step's LM
+//                           head): no K-slice partials, no epilogue launch.
+//   lora_rows_kernel        a worker's LoRA delta of a few token rows.
 //   matmul_generic_kernel   small row-major products with arbitrary strides
 //                           (worker-side LoRA modules).
-//   rope_append_kernel / attention_kernel   paged-KV decode attention.
+//   rope_append_kernel, attn_tile_kernel + attn_combine_kernel (decode),
+//   attn_chunk_kernel, attention_kernel     paged-KV attention.
 //
-// MFMA used: v_mfma_f32_16x16x32_bf16.  Operand layout (wave64): lane l feeds
+// MFMA used: v_mfma_f32_16x16x32_bf16 (decode rounds, attention, shrink) and
+// v_mfma_f32_32x32x16_bf16 (gemm256_kernel).  16x16x32 operand layout
+// (wave64): lane l feeds
 // row (l % 16) of A and column (l % 16) of B with the 8 consecutive k values of
 // k-group (l / 16); the 16x16 fp32 result lands in lane l as rows
 // 4*(l/16)+j, j=0..3, of column (l % 16).  The k-group -> k assignment is the
@@ -3524,13 +3536,9 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
 
 // Prefill GEMM: gemm256_kernel (256 x 256 tiles), or tiled_kernel (128 x
 // 128, over a packed copy of the rows) with SWL_PREFILL_TILED=1.
-bool prefill_uses_tiled(int64_t K) {
-  static const bool use_tiled = [] {
-    const char* e = getenv("SWL_PREFILL_TILED");
-    return e && atoi(e) != 0;
-  }();
-  return use_tiled || K % PG_K != 0 || K < PG_K;
-}
+// The 128 x 128 kernel over a gathered copy takes the rounds whose K is not a
+// multiple of the 256 x 256 kernel's 64-wide stages.
+bool prefill_uses_tiled(int64_t K) { return K % PG_K != 0 || K < PG_K; }
 
 template <int NJ, int WM>
 int launch_gemm256(const TiledArgs& a, int tiles_m, int tiles, int per_xcd, hipStream_t st) {
