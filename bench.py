@@ -583,8 +583,10 @@ def _ipc_worker(shm_name, claim, wid, all_sids, start, layers, n_tok, reps, gpu_
 IPC_MODES = {  # name: (GPU-ordered rounds, adapters pooled in the aggregator)
     "host_sync": (False, False),          # the reference's protocol: worker-side LoRA, host-synchronised rounds
     "host_sync_pooled": (False, True),    # adapters in the aggregator's pool, delta added inside the round
-    "gpu_ordered": (True, False),
+    "gpu_ordered": (True, False),         # input copies and output reads ordered on the GPU
     "gpu_ordered_pooled": (True, True),
+    "gpu_ordered_inputs": ("inputs", False),  # input copies ordered on the GPU, outputs read after the round
+    "gpu_ordered_inputs_pooled": ("inputs", True),
 }
 
 

@@ -73,6 +73,14 @@ int swl_q_submit(int op_type, int layer_idx, int slot_id, int worker_id, int64_t
 int swl_q_submit_seq(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
                      uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id,
                      uint64_t in_seq);
+/* swl_q_submit_seq with out_host (no counterpart in the reference): 1 when
+ * the worker reads this round's outputs as soon as done is signalled, with
+ * no wait on its stream (swl_w_set_gpu_ordered mode 2); the aggregator then
+ * synchronises its stream before signalling done, as for a host-ordered
+ * command.  Ignored when in_seq is 0. */
+int swl_q_submit_seq_ex(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
+                        uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id,
+                        uint64_t in_seq, int out_host);
 /* Layout sizes of the shared segment (for tests). */
 size_t swl_q_control_bytes(void);
 size_t swl_q_command_bytes(void);
@@ -210,10 +218,13 @@ int swl_w_cleanup(void);
 /* Buffer sizes of an open slot (for shape checks in the Python shim). */
 int swl_w_slot_sizes(int slot_id, size_t* input_buffer_size, size_t* output_buffer_size);
 /* GPU-ordered mode for every slot of this worker (no counterpart in the
- * reference): prepare_* no longer wait on the host; they write the slot's
- * next input sequence value on the stream after the copy.  Output reads
- * (copy_output, get_next_token) first wait on the stream for the
- * aggregator's output sequence word to reach the last input value. */
+ * reference).  enable 1 or 2: prepare_* no longer wait on the host; they
+ * write the slot's next input sequence value on the stream after the copy.
+ * 1: output reads (copy_output, get_next_token) first wait on the stream for
+ * the aggregator's output sequence word to reach the last input value.
+ * 2: output reads do not wait (the commands carry out_host, so the
+ * aggregator signals done only after its stream has finished the round).
+ * 0: the reference's host waits. */
 int swl_w_set_gpu_ordered(int enable);
 /* The input sequence value of the slot's last prepare_* (0 before any). */
 int swl_w_input_seq(int slot_id, uint64_t* seq);

@@ -163,7 +163,7 @@ int upload_adapters() {
 
 namespace {
 int drain_impl(uint64_t active_lo, uint64_t active_hi, int want, int32_t* slot_ids, int32_t* worker_ids, int32_t* ops,
-               int32_t* layers, int64_t* tokens, uint64_t* x_keys, uint64_t* in_seqs, int* got);
+               int32_t* layers, int64_t* tokens, uint64_t* x_keys, uint64_t* in_seqs, int32_t* out_host, int* got);
 }  // namespace
 
 extern "C" {
@@ -628,7 +628,8 @@ int swl_agg_signal_done(void) {
 
 int swl_agg_drain_commands(uint64_t active_lo, uint64_t active_hi, int want, int32_t* slot_ids, int32_t* worker_ids,
                            int32_t* ops, int32_t* layers, int64_t* tokens, uint64_t* x_keys, int* got) {
-  return drain_impl(active_lo, active_hi, want, slot_ids, worker_ids, ops, layers, tokens, x_keys, nullptr, got);
+  return drain_impl(active_lo, active_hi, want, slot_ids, worker_ids, ops, layers, tokens, x_keys, nullptr, nullptr,
+                    got);
 }
 
 int swl_agg_take_seq_timeouts(int32_t* slot_ids, int max_ids) {
@@ -646,7 +647,7 @@ int swl_agg_take_seq_timeouts(int32_t* slot_ids, int max_ids) {
 
 namespace {
 int drain_impl(uint64_t active_lo, uint64_t active_hi, int want, int32_t* slot_ids, int32_t* worker_ids, int32_t* ops,
-               int32_t* layers, int64_t* tokens, uint64_t* x_keys, uint64_t* in_seqs, int* got) {
+               int32_t* layers, int64_t* tokens, uint64_t* x_keys, uint64_t* in_seqs, int32_t* out_host, int* got) {
   SWL_CHECK(g_agg_q.ctrl && g_agg_q.ring, SWL_ERR_STATE, "Aggregator queue not initialized");
   swl::Control* c = g_agg_q.ctrl;
   const Mask active{{active_lo, active_hi}};
@@ -681,6 +682,7 @@ int drain_impl(uint64_t active_lo, uint64_t active_hi, int want, int32_t* slot_i
       tokens[n] = cmd.bx * cmd.tx;
       x_keys[n] = cmd.x_key;
       if (in_seqs) in_seqs[n] = cmd.in_seq;
+      if (out_host) out_host[n] = cmd.out_host;
       if (cmd.op_type == SWL_OP_SET_SAMPLING) {
         swl::SamplingParams p;
         p.do_sample = (cmd.x_key & 1) ? 1 : 0;
@@ -822,6 +824,7 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
   int32_t sids[SWL_MAX_SLOTS], wids[SWL_MAX_SLOTS], ops[SWL_MAX_SLOTS], layers[SWL_MAX_SLOTS];
   int64_t toks[SWL_MAX_SLOTS];
   uint64_t keys[SWL_MAX_SLOTS], seqs[SWL_MAX_SLOTS];
+  int32_t outh[SWL_MAX_SLOTS];
   auto seq_word = [](int sid, size_t off) {
     return reinterpret_cast<uint64_t*>(static_cast<char*>(g_pool.slots[sid].out) + g_pool.out_size + off);
   };
@@ -849,7 +852,7 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
       N = cnt;
       if (c->quit.load(std::memory_order_acquire) != 0) break;
       int got = 0;
-      rc = drain_impl(active.w[0], active.w[1], N, sids, wids, ops, layers, toks, keys, seqs, &got);
+      rc = drain_impl(active.w[0], active.w[1], N, sids, wids, ops, layers, toks, keys, seqs, outh, &got);
       if (rc) return rc;
       if (got == 0 || c->quit.load(std::memory_order_acquire) != 0) {
         if (c->quit.load(std::memory_order_acquire) != 0) swl_agg_signal_done();
@@ -863,6 +866,7 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
         for (int i = 0; i < got; ++i) {
           if (ops[i] == op && layers[i] == layers[0]) {
             sids[m] = sids[i]; wids[m] = wids[i]; toks[m] = toks[i]; keys[m] = keys[i]; seqs[m] = seqs[i];
+            outh[m] = outh[i];
             ++m;
           } else {
             c->evicted.set_bit(sids[i]);
@@ -890,8 +894,19 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
         // ... and each ordered slot's output sequence word follows the round
         // on the stream (written even if the round failed, so no worker waits
         // out its limit on an evicted slot)
-        for (int i = 0; i < m; ++i)
-          if (seqs[i] > 0) SWL_HIP(hipStreamWriteValue64(st, seq_word(sids[i], swl::kOutSeqOffset), seqs[i], 0));
+        {
+          uint64_t* oflag[SWL_MAX_SLOTS];
+          uint64_t oval[SWL_MAX_SLOTS];
+          int nw = 0;
+          for (int i = 0; i < m; ++i)
+            if (seqs[i] > 0) {
+              oflag[nw] = seq_word(sids[i], swl::kOutSeqOffset);
+              oval[nw] = seqs[i];
+              ++nw;
+            }
+          const int wrc = swl::seq_write_launch(nw, oflag, oval, st);
+          if (wrc && !rc) rc = wrc;
+        }
         if (rc) {
           // a malformed command must not take every co-tenant down: evict the
           // slots of this round and keep serving the others
@@ -904,8 +919,11 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
           }
           c->active.store(active);
         }
-        // rounds of GPU-ordered commands only are not waited for on the host
-        if (nord < m) SWL_HIP(hipStreamSynchronize(st));
+        // the host waits for the round unless every command is GPU-ordered
+        // on both sides (its worker waits for the outputs on its stream)
+        bool sync = nord < m;
+        for (int i = 0; i < m; ++i) sync = sync || outh[i] != 0;
+        if (sync) SWL_HIP(hipStreamSynchronize(st));
         int32_t late[SWL_MAX_SLOTS];
         const int nlate = swl_agg_take_seq_timeouts(late, SWL_MAX_SLOTS);
         for (int i = 0; i < nlate && i < SWL_MAX_SLOTS; ++i) {

@@ -86,6 +86,10 @@ struct alignas(64) Command {
   int64_t bx, tx, dx;
   uint64_t x_key, y0_key, y1_key, y2_key;
   uint64_t in_seq;  // > 0: GPU-ordered command (the slot's input sequence word reaches this value)
+  // 1 (GPU-ordered command only): the worker reads the round's outputs once
+  // done is signalled, without a GPU wait, so the aggregator synchronises its
+  // stream before signalling
+  int32_t out_host;
 };
 
 // Control block at offset 0 of the segment; the ring follows it.  Producer

@@ -245,9 +245,9 @@ int64_t swl_q_get_epoch(void) {
   return g_queue.ctrl->epoch.load(std::memory_order_acquire);
 }
 
-int swl_q_submit_seq(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
-                     uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id,
-                     uint64_t in_seq) {
+int swl_q_submit_seq_ex(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
+                        uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id,
+                        uint64_t in_seq, int out_host) {
   SWL_CHECK(g_queue.ctrl && g_queue.ring, SWL_ERR_STATE, "submit_slot_command: queue not initialized");
   // Validate everything before reserving an entry: a reserved entry whose
   // ready flag is never set would stall the aggregator's drain.
@@ -280,14 +280,22 @@ int swl_q_submit_seq(int op_type, int layer_idx, int slot_id, int worker_id, int
   cmd.y1_key = y1_key;
   cmd.y2_key = y2_key;
   cmd.in_seq = in_seq;
+  cmd.out_host = (in_seq > 0 && out_host) ? 1 : 0;
   cmd.ready.store(1, std::memory_order_release);
   return SWL_OK;
 }
 
+int swl_q_submit_seq(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
+                     uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id,
+                     uint64_t in_seq) {
+  return swl_q_submit_seq_ex(op_type, layer_idx, slot_id, worker_id, bx, tx, dx, x_key, y0_key, y1_key, y2_key,
+                             ticket_id, in_seq, 0);
+}
+
 int swl_q_submit(int op_type, int layer_idx, int slot_id, int worker_id, int64_t bx, int64_t tx, int64_t dx,
                  uint64_t x_key, uint64_t y0_key, uint64_t y1_key, uint64_t y2_key, int ticket_id) {
-  return swl_q_submit_seq(op_type, layer_idx, slot_id, worker_id, bx, tx, dx, x_key, y0_key, y1_key, y2_key,
-                          ticket_id, 0);
+  return swl_q_submit_seq_ex(op_type, layer_idx, slot_id, worker_id, bx, tx, dx, x_key, y0_key, y1_key, y2_key,
+                             ticket_id, 0, 0);
 }
 
 size_t swl_q_control_bytes(void) { return sizeof(swl::Control); }

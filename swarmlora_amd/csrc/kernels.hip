@@ -46,6 +46,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -1584,10 +1585,6 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm256_kernel(TiledArgs a, int t
     else
       fb_[idx - 4] = *reinterpret_cast<const u32x4*>(st + PG_N * PG_ROW + (wm * TPW + 32 * (idx - 4)) * PG_ROW);
   };
-  auto frags = [&](int s, int kk, u32x4 (&fa)[4], u32x4 (&fb)[NJ]) {
-#pragma unroll
-    for (int idx = 0; idx < NR; ++idx) read_at(s, kk, fa, fb, idx);
-  };
 
   // Fragments of the four k-steps of a stage sit in four register sets,
   // read two k-steps ahead of their MFMAs.  Stage kt + 2 is requested into
@@ -1626,36 +1623,60 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm256_kernel(TiledArgs a, int t
   if ((int)threadIdx.x < nseg) segl[threadIdx.x] = my;
   __builtin_amdgcn_s_waitcnt(wait_vm_imm(NREQ));
   lds_barrier();
-  frags(0, 0, fa[0], fb[0]);
-  frags(0, 1, fa[1], fb[1]);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int s = kt & 1;
-    // k-steps 0, 1 of stage kt; reads of its k-steps 2, 3 during the first
-    // 2 NR
+  // The main loop over a predicate live(j): whether the wave's 32-row block
+  // j of token rows holds a row of the batch.  Every block does, except in
+  // the batch's last row tile: there the MFMAs and fragment reads of the
+  // empty blocks are skipped (a wave with none reads nothing), so that tile
+  // costs a fraction of a full one; the DMA requests and barriers stay the
+  // same in every wave.
+  auto main_loop = [&](auto live) {
+    auto read_live = [&](int idx) { return idx < 4 ? live(0) : live(idx - 4); };
 #pragma unroll
-    for (int t = 0; t < 2 * MF; ++t) {
-      mfma_at(fa[0], fb[0], fa[1], fb[1], t);
-      if (t < NR) read_at(s, 2, fa[2], fb[2], t);
-      else if (t < 2 * NR) read_at(s, 3, fa[3], fb[3], t - NR);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // this wave's DMA of stage kt + 1 has landed (it is all that is
-    // outstanding), then every wave's; every wave is past its reads of slot s
-    __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
-    lds_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    // k-steps 2, 3; reads of stage kt + 1's k-steps 0, 1 during the first
-    // 2 NR, the NREQ DMA requests of stage kt + 2 spread over the 2 MF MFMAs
-    const int nx = min(kt + 2, nk - 1);
+    for (int idx = 0; idx < NR; ++idx)
+      if (read_live(idx)) read_at(0, 0, fa[0], fb[0], idx);
 #pragma unroll
-    for (int t = 0; t < 2 * MF; ++t) {
-      mfma_at(fa[2], fb[2], fa[3], fb[3], t);
-      if (t < NR) read_at(s ^ 1, 0, fa[0], fb[0], t);
-      else if (t < 2 * NR) read_at(s ^ 1, 1, fa[1], fb[1], t - NR);
-      if (t == 0 || (t * NREQ) / (2 * MF) != ((t - 1) * NREQ) / (2 * MF)) request_at(nx, s, (t * NREQ) / (2 * MF));
+    for (int idx = 0; idx < NR; ++idx)
+      if (read_live(idx)) read_at(0, 1, fa[1], fb[1], idx);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int s = kt & 1;
+      // k-steps 0, 1 of stage kt; reads of its k-steps 2, 3 during the first
+      // 2 NR
+#pragma unroll
+      for (int t = 0; t < 2 * MF; ++t) {
+        if (live(t % NJ)) mfma_at(fa[0], fb[0], fa[1], fb[1], t);
+        if (t < NR) {
+          if (read_live(t)) read_at(s, 2, fa[2], fb[2], t);
+        } else if (t < 2 * NR) {
+          if (read_live(t - NR)) read_at(s, 3, fa[3], fb[3], t - NR);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // this wave's DMA of stage kt + 1 has landed (it is all that is
+      // outstanding), then every wave's; every wave is past its reads of slot s
+      __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
+      lds_barrier();
       __builtin_amdgcn_sched_barrier(0);
+      // k-steps 2, 3; reads of stage kt + 1's k-steps 0, 1 during the first
+      // 2 NR, the NREQ DMA requests of stage kt + 2 spread over the 2 MF MFMAs
+      const int nx = min(kt + 2, nk - 1);
+#pragma unroll
+      for (int t = 0; t < 2 * MF; ++t) {
+        if (live(t % NJ)) mfma_at(fa[2], fb[2], fa[3], fb[3], t);
+        if (t < NR) {
+          if (read_live(t)) read_at(s ^ 1, 0, fa[0], fb[0], t);
+        } else if (t < 2 * NR) {
+          if (read_live(t - NR)) read_at(s ^ 1, 1, fa[1], fb[1], t - NR);
+        }
+        if (t == 0 || (t * NREQ) / (2 * MF) != ((t - 1) * NREQ) / (2 * MF)) request_at(nx, s, (t * NREQ) / (2 * MF));
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-  }
+  };
+  const int jl = (int)min<int64_t>(NJ, max<int64_t>(0, (a.M - m0 - wm * TPW + 31) / 32));
+  if (jl == NJ)
+    main_loop([](int) { return true; });
+  else
+    main_loop([jl](int j) { return j < jl; });
   // the requests past the last stage land before the LDS is reused
   __builtin_amdgcn_s_waitcnt(wait_vm_imm(0));
 
@@ -1981,12 +2002,18 @@ __global__ __launch_bounds__(256) void lora_rows_kernel(LoraRowsArgs a) {
             }
         }
       } else {
-#pragma unroll
+        // scalar reads of A (any strides), one k of the chunk at a time: with
+        // the 8 k unrolled, the 8 NRMAX reads and their 64-bit addresses
+        // were all live at once and spilled
+#pragma unroll 1
         for (int kk = 0; kk < 8; ++kk) {
+          float xk = xv[0];
+#pragma unroll
+          for (int i = 1; i < 8; ++i) xk = kk == i ? xv[i] : xk;
           const bf16* ar = a.a + (8 * c + kk) * a.a_sk;
 #pragma unroll
           for (int j = 0; j < NRMAX; ++j)
-            if (j < a.nr) acc[j] += xv[kk] * bf2f(ar[j * a.a_sj]);
+            if (j < a.nr) acc[j] += xk * bf2f(ar[j * a.a_sj]);
         }
       }
     }
@@ -3534,9 +3561,8 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
   return SWL_OK;
 }
 
-// Prefill GEMM: gemm256_kernel (256 x 256 tiles), or tiled_kernel (128 x
-// 128, over a packed copy of the rows) with SWL_PREFILL_TILED=1.
-// The 128 x 128 kernel over a gathered copy takes the rounds whose K is not a
+// Prefill GEMM: gemm256_kernel (256 x 256 or 256 x 192 tiles); the 128 x
+// 128 tiled_kernel over a gathered copy takes the rounds whose K is not a
 // multiple of the 256 x 256 kernel's 64-wide stages.
 bool prefill_uses_tiled(int64_t K) { return K % PG_K != 0 || K < PG_K; }
 
@@ -3561,11 +3587,21 @@ int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
   // token rows a tile: 256, or 192 where the grid then covers the CUs in
   // fewer tile times (a 192-row tile measured at ~0.9 of a 256-row one: the
   // W side streams the same bytes): the O and Down rounds at 2325 rows have
-  // 160 tiles of 256 for 256 CUs, 208 of 192 (146 -> 133 us, 370 -> 335)
+  // 160 tiles of 256 for 256 CUs, 208 of 192 (146 -> 133 us, 370 -> 335).
+  // A tile of the last row tile costs the share of its first row wave's
+  // 32-row blocks that hold rows, at least 0.4 of a full tile (its stages
+  // still wait for their DMA); such tiles first fill the CUs the last wave
+  // of full tiles leaves idle.
   const int tiles_n = (int)((a.N + PG_N - 1) / PG_N);
-  auto tiles_of = [&](int mt) { return (int)((a.M + mt - 1) / mt) * tiles_n; };
   const int64_t cus = cu_count();
-  auto cost = [&](int nj) { return (double)((tiles_of(64 * nj) + cus - 1) / cus) * (nj == 3 ? 0.9 : 1.0); };
+  auto cost = [&](int nj) {
+    const int64_t mt = 64 * nj, full = (a.M / mt) * tiles_n, rem = a.M % mt;
+    const double pc = rem ? std::max(0.4, (double)std::min<int64_t>(nj, (rem + 31) / 32) / nj) : 0.0;
+    const int64_t waves = (full + cus - 1) / cus;
+    const double spill = (rem ? pc * tiles_n : 0.0) - (double)(waves * cus - full);
+    const double t = (double)waves + (spill > 0 ? std::ceil(spill / ((double)cus * pc)) * pc : 0.0);
+    return t * (nj == 3 ? 0.9 : 1.0);
+  };
   static const int forced = [] {
     const char* e = getenv("SWL_PREFILL_NJ");
     return e ? atoi(e) : 0;
@@ -4247,9 +4283,38 @@ __global__ __launch_bounds__(SWL_MAX_SLOTS) void seq_wait_kernel(SeqWaitArgs a) 
     __builtin_amdgcn_s_sleep(32);
   }
 }
+
+struct SeqWriteArgs {
+  int32_t n;
+  uint64_t* flag[SWL_MAX_SLOTS];
+  uint64_t value[SWL_MAX_SLOTS];
+};
+
+// One lane per flag: the value is stored with system-scope release order
+// (vector stores; the kernel starts after the stream's earlier kernels have
+// completed and released their writes).
+__global__ __launch_bounds__(SWL_MAX_SLOTS) void seq_write_kernel(SeqWriteArgs a) {
+  const int i = threadIdx.x;
+  if (i < a.n) __hip_atomic_store(a.flag[i], a.value[i], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 }  // namespace
 
 namespace swl {
+int seq_write_launch(int n, uint64_t* const* flag, const uint64_t* value, hipStream_t stream) {
+  SWL_CHECK(n >= 0 && n <= SWL_MAX_SLOTS, SWL_ERR_INVALID, "seq_write: at most 128 flags");
+  if (n == 0) return SWL_OK;
+  SeqWriteArgs a{};
+  a.n = n;
+  for (int i = 0; i < n; ++i) {
+    SWL_CHECK(flag[i] != nullptr, SWL_ERR_INVALID, "seq_write: null flag");
+    a.flag[i] = flag[i];
+    a.value[i] = value[i];
+  }
+  hipLaunchKernelGGL(seq_write_kernel, dim3(1), dim3(SWL_MAX_SLOTS), 0, stream, a);
+  SWL_LAUNCH_CHECK("seq_write_kernel launch");
+  return SWL_OK;
+}
+
 int seq_wait_launch(int n, const uint64_t* const* flag, const uint64_t* want, const int32_t* tag, uint32_t* timed_out,
                     uint32_t limit_us, hipStream_t stream) {
   SWL_CHECK(n >= 0 && n <= SWL_MAX_SLOTS, SWL_ERR_INVALID, "seq_wait: at most 128 flags");

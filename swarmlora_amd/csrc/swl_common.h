@@ -35,6 +35,12 @@ constexpr size_t kInSeqOffset = 0, kOutSeqOffset = 128;
 int seq_wait_launch(int n, const uint64_t* const* flag, const uint64_t* want, const int32_t* tag, uint32_t* timed_out,
                     uint32_t limit_us, hipStream_t stream);
 
+// Writes *flag[i] = value[i] for every i < n on `stream`, in one kernel
+// launch, after the stream's earlier work (system-scope release stores, one
+// lane per flag).  Stands in for n hipStreamWriteValue64 calls, each of which
+// is a kernel launch of its own that costs the host ~10-30 us.
+int seq_write_launch(int n, uint64_t* const* flag, const uint64_t* value, hipStream_t stream);
+
 }  // namespace swl
 
 #define SWL_HIP(call)                                   \

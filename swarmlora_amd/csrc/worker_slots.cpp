@@ -48,7 +48,10 @@ struct Manager {
   SlotCtx slots[kMaxSlotsPerWorker];
   int nopen = 0;
   bool initialized = false;
-  bool gpu_ordered = false;
+  // GPU ordering: 0 none (host waits), 1 inputs and outputs, 2 inputs only
+  // (outputs are read once the aggregator has signalled done, which it does
+  // after its stream has finished the round)
+  int gpu_ordered = 0;
   uint32_t* out_timeout = nullptr;  // host-visible words, one per slot id
 } g_w;
 
@@ -59,7 +62,7 @@ uint64_t* seq_word(SlotCtx* c, size_t off) {
 // GPU-ordered mode: the stream waits until the aggregator has written this
 // slot's output sequence word for the last submitted input.
 int wait_outputs(const char* fn, SlotCtx* c, hipStream_t st) {
-  if (!g_w.gpu_ordered || c->seq == 0) return SWL_OK;
+  if (g_w.gpu_ordered != 1 || c->seq == 0) return SWL_OK;
   const uint64_t* flag = seq_word(c, swl::kOutSeqOffset);
   const int32_t tag = c->slot_id;
   int rc = swl::seq_wait_launch(1, &flag, &c->seq, &tag, g_w.out_timeout, out_wait_limit_us(), st);
@@ -110,8 +113,8 @@ int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream
   if (g_w.gpu_ordered) {
     // the aggregator's stream waits for this value before reading the buffer
     ++c->seq;
-    SWL_HIP(hipStreamWriteValue64(st, seq_word(c, swl::kInSeqOffset), c->seq, 0));
-    return SWL_OK;
+    uint64_t* flag = seq_word(c, swl::kInSeqOffset);
+    return swl::seq_write_launch(1, &flag, &c->seq, st);
   }
   // the aggregator reads the buffer from another process once this worker
   // signals ready: the copy must be complete, not just ordered
@@ -134,7 +137,7 @@ int swl_w_init(int worker_id, int worker_device, int aggregator_device, int hidd
   g_w.qkv = qkv_dim;
   for (auto& s : g_w.slots) s = SlotCtx();
   g_w.nopen = 0;
-  g_w.gpu_ordered = false;
+  g_w.gpu_ordered = 0;
   g_w.initialized = true;
   std::printf("[Worker-%d] Slot manager initialized (worker_device=%d, aggregator_device=%d)\n", worker_id,
               worker_device, aggregator_device);
@@ -308,11 +311,12 @@ int swl_w_get_next_token(int slot_id, int64_t* token, void* stream) {
 
 int swl_w_set_gpu_ordered(int enable) {
   SWL_CHECK(g_w.initialized, SWL_ERR_STATE, "set_gpu_ordered: worker slot manager not initialized");
+  SWL_CHECK(enable >= 0 && enable <= 2, SWL_ERR_INVALID, "set_gpu_ordered: mode must be 0, 1 or 2");
   if (enable && !g_w.out_timeout) {
     SWL_HIP(hipHostMalloc((void**)&g_w.out_timeout, SWL_MAX_SLOTS * sizeof(uint32_t), hipHostMallocDefault));
     std::memset(g_w.out_timeout, 0, SWL_MAX_SLOTS * sizeof(uint32_t));
   }
-  g_w.gpu_ordered = enable != 0;
+  g_w.gpu_ordered = enable;
   return SWL_OK;
 }
 
@@ -336,7 +340,7 @@ int swl_w_cleanup(void) {
   }
   g_w.nopen = 0;
   g_w.initialized = false;
-  g_w.gpu_ordered = false;
+  g_w.gpu_ordered = 0;
   if (g_w.out_timeout) (void)hipHostFree(g_w.out_timeout);
   g_w.out_timeout = nullptr;
   return SWL_OK;

@@ -29,6 +29,8 @@ _lib.register_signatures({
     "swl_q_submit": (c_int, [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_u64, c_u64, c_u64, c_u64, c_int]),
     "swl_q_submit_seq": (c_int, [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_u64, c_u64, c_u64, c_u64, c_int,
                                  c_u64]),
+    "swl_q_submit_seq_ex": (c_int, [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_u64, c_u64, c_u64, c_u64,
+                                    c_int, c_u64, c_int]),
     "swl_q_control_bytes": (ctypes.c_size_t, []),
     "swl_q_command_bytes": (ctypes.c_size_t, []),
 })
@@ -102,14 +104,17 @@ def clear_evicted_slot(slot_id):
 
 
 def submit_slot_command(op_type, layer_idx, slot_id, worker_id, bx, tx, dx, x_key, y0_key, y1_key, y2_key,
-                        ticket_id, in_seq=0):
+                        ticket_id, in_seq=0, out_host=False):
     """in_seq > 0 (an addition): the command is GPU-ordered -- the
     aggregator's stream waits for the slot's input sequence word to reach
-    in_seq (ext_unified_barrier.input_seq after a GPU-ordered prepare)."""
+    in_seq (ext_unified_barrier.input_seq after a GPU-ordered prepare).
+    out_host (with in_seq): the worker reads the outputs once done is
+    signalled, without a wait on its stream, so the aggregator finishes the
+    round on its stream before signalling."""
     if in_seq:
-        _lib.check(_L().swl_q_submit_seq(int(op_type), int(layer_idx), int(slot_id), int(worker_id), int(bx),
-                                         int(tx), int(dx), int(x_key), int(y0_key), int(y1_key), int(y2_key),
-                                         int(ticket_id), int(in_seq)))
+        _lib.check(_L().swl_q_submit_seq_ex(int(op_type), int(layer_idx), int(slot_id), int(worker_id), int(bx),
+                                            int(tx), int(dx), int(x_key), int(y0_key), int(y1_key), int(y2_key),
+                                            int(ticket_id), int(in_seq), 1 if out_host else 0))
         return
     _lib.check(_L().swl_q_submit(int(op_type), int(layer_idx), int(slot_id), int(worker_id), int(bx), int(tx),
                                  int(dx), int(x_key), int(y0_key), int(y1_key), int(y2_key), int(ticket_id)))

@@ -136,12 +136,15 @@ def cleanup_worker_slots():
 
 
 # ------------------------------------------------ additions (no reference counterpart)
-def set_gpu_ordered(enable=True):
+def set_gpu_ordered(enable=True, wait_outputs=True):
     """GPU-ordered slots: prepare_* stop waiting for their copy on the host
     and write the slot's next input sequence value on the stream instead;
-    output reads first wait on the stream for the aggregator's output
-    sequence word.  Commands must then carry input_seq(slot_id)."""
-    _lib.check(_L().swl_w_set_gpu_ordered(1 if enable else 0))
+    commands must then carry input_seq(slot_id).  wait_outputs: output reads
+    first wait on the stream for the aggregator's output sequence word;
+    without it they read the outputs at once, and the commands must carry
+    out_host=True (the aggregator then finishes each round before
+    signalling done)."""
+    _lib.check(_L().swl_w_set_gpu_ordered(0 if not enable else (1 if wait_outputs else 2)))
 
 
 def input_seq(slot_id):

@@ -127,16 +127,21 @@ class BatchedAggregatorOps:
     """submit -> signal_ready -> (local LoRA delta) -> wait epoch -> read."""
 
     def __init__(self, slot_manager, worker_id: int, dtype_code: int, pooled_adapter: Optional[int] = None,
-                 gpu_ordered: bool = False):
+                 gpu_ordered=False):
         self.slot_manager = slot_manager
         self.worker_id = worker_id
         # gpu_ordered (an addition): slot copies are ordered against the
         # aggregator's rounds on the GPU (sequence words in the slot buffer)
-        # instead of by host waits; barrier_sync then returns once the round
-        # is launched, not finished
+        # instead of by host waits.  True: inputs and outputs, barrier_sync
+        # then returns once the round is launched, not finished; "inputs":
+        # the input copy only (no host wait before the submit), the outputs
+        # read once the round has finished, as in the reference
+        if gpu_ordered not in (False, True, "inputs"):
+            raise ValueError("gpu_ordered must be False, True or 'inputs'")
         self.gpu_ordered = gpu_ordered
+        self._out_host = gpu_ordered == "inputs"
         if gpu_ordered:
-            ub.set_gpu_ordered(True)
+            ub.set_gpu_ordered(True, wait_outputs=not self._out_host)
         self.dtype_code = dtype_code
         self.dtype = torch.bfloat16 if dtype_code == 15 else torch.float16
         self.hidden_dim = slot_manager.base_client.hidden_dim
@@ -161,7 +166,7 @@ class BatchedAggregatorOps:
         with self.timer.stage("gather"):
             ub.prepare_input_slot(slot_id, op, x)
             extq.submit_slot_command(op, layer_idx, slot_id, self.worker_id, b, t, d, self._x_key, 0, 0, 0, 0,
-                                     in_seq=self._seq(slot_id))
+                                     in_seq=self._seq(slot_id), out_host=self._out_host)
             extq.slot_signal_ready(slot_id)
 
     # ---------------------------------------------------------------- embed
@@ -171,7 +176,7 @@ class BatchedAggregatorOps:
         ub.prepare_token_ids_slot(slot_id, state.input_ids)
         b, t = state.input_ids.shape
         extq.submit_slot_command(OP_EMBED, 0, slot_id, self.worker_id, b, t, self.hidden_dim, 0, 0, 0, 0, 0,
-                                 in_seq=self._seq(slot_id))
+                                 in_seq=self._seq(slot_id), out_host=self._out_host)
         extq.slot_signal_ready(slot_id)
         return epoch
 
@@ -276,7 +281,7 @@ class BatchedAggregatorOps:
         ub.prepare_hidden_for_lm_head_slot(slot_id, state.hidden)
         b, t, d = state.hidden.shape
         extq.submit_slot_command(OP_LM_HEAD, 0, slot_id, self.worker_id, b, t, d, 0, 0, 0, 0, 0,
-                                 in_seq=self._seq(slot_id))
+                                 in_seq=self._seq(slot_id), out_host=self._out_host)
         extq.slot_signal_ready(slot_id)
         return epoch
 

@@ -41,6 +41,7 @@ int round_launch(int, const int64_t*, const void* const*, void* const*, const vo
 int seq_wait_launch(int, const uint64_t* const*, const uint64_t*, const int32_t*, uint32_t*, uint32_t, hipStream_t) {
   no_gpu("seq_wait_launch");
 }
+int seq_write_launch(int, uint64_t* const*, const uint64_t*, hipStream_t) { no_gpu("seq_write_launch"); }
 }  // namespace swl
 
 extern "C" const char* swl_last_error(void) { return swl::last_error().c_str(); }
