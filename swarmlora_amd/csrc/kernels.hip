@@ -381,10 +381,15 @@ __device__ __forceinline__ void kloop_lds(f32x4 (&acc)[TT], u32x4 (&w)[D], const
 
 // One workgroup per (item, K-slice): 4 waves, each 16 token rows x the 64
 // A rows of the item's block (4 MFMA tiles, A rows as the A-operand so the
-// fp32 results land as 4 consecutive q per lane), 4 k-steps of loads in
-// flight; A is shared by the 4 waves through the L1.
+// fp32 results land as 4 consecutive q per lane).  The K-slice runs in
+// groups of 8 k-steps: every thread issues its 8 loads of the group at once
+// (one 16-byte piece of the A block, one of its wave's token rows), the A
+// block is shared through LDS in fragment order (a wave's fragment read is
+// one contiguous 1 KiB), then the 32 MFMAs of the group.
 __global__ __launch_bounds__(256) void shrink_gemm_kernel(ShrinkGemmArgs a) {
-  constexpr int D = 4;
+  constexpr int D = 8;
+  // [k-step][A tile j][lane] fragments of the group's A block
+  __shared__ __attribute__((aligned(16))) u32x4 als[D][4][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int ks = blockIdx.x % a.n_ks, item = blockIdx.x / a.n_ks;
   int lo = 0, hi = a.n_seg - 1;
@@ -399,32 +404,33 @@ __global__ __launch_bounds__(256) void shrink_gemm_kernel(ShrinkGemmArgs a) {
   const int st0 = (int)((int64_t)a.total_steps * ks / a.n_ks);
   const int st1 = (int)((int64_t)a.total_steps * (ks + 1) / a.n_ks);
   const int nst = st1 - st0;
-  const int64_t kbeg = (int64_t)st0 * 32 + 8 * (lane >> 4);
   const int tr = rt * 64 + wv * 16 + (lane & 15);  // token row of this lane within the segment
-  const bf16* xp = a.xs[s] + (int64_t)min(tr, a.rows[s] - 1) * a.K + kbeg;
-  const bf16* ap[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int q = ab * 64 + 16 * j + (lane & 15);
-    ap[j] = a.a[s] + (int64_t)min(q, a.arows[s] - 1) * a.K + kbeg;
-  }
+  const bf16* xp = a.xs[s] + (int64_t)min(tr, a.rows[s] - 1) * a.K + (int64_t)st0 * 32 + 8 * (lane >> 4);
+  // A loader: thread t takes A row t / 4 of the block, 16-byte chunk t % 4
+  // of each k-step, stored as lane (row % 16) + 16 chunk of tile row / 16
+  const int ar = threadIdx.x >> 2, ac = threadIdx.x & 3;
+  const bf16* ag = a.a[s] + (int64_t)min(ab * 64 + ar, a.arows[s] - 1) * a.K + (int64_t)st0 * 32 + 8 * ac;
+  const int aj = ar >> 4, al = (ar & 15) + 16 * ac;
   f32x4 acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < nst; i += D) {
-    u32x4 xv[D], av[D][4];
+  for (int g = 0; g < nst; g += D) {
+    u32x4 av[D], xv[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      const int st = 32 * (i + d < nst ? i + d : nst - 1);
+      const int st = 32 * (g + d < nst ? g + d : nst - 1);
+      av[d] = ldg16(ag + st);
       xv[d] = ldg16(xp + st);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) av[d][j] = ldg16(ap[j] + st);
     }
+    if (g > 0) __syncthreads();  // every wave is past its reads of the previous group
+#pragma unroll
+    for (int d = 0; d < D; ++d) als[d][aj][al] = av[d];
+    __syncthreads();
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      if (i + d >= nst) break;
+      if (g + d >= nst) break;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = mfma16(av[d][j], xv[d], acc[j]);
+      for (int j = 0; j < 4; ++j) acc[j] = mfma16(als[d][j][lane], xv[d], acc[j]);
     }
   }
   if (tr >= a.rows[s]) return;
