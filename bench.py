@@ -87,10 +87,11 @@ def parse():
     ap.add_argument("--ipc-layers", type=int, default=32, help="drop-in leg: 8B-shaped layers")
     ap.add_argument("--ipc-tokens", type=int, default=6, help="drop-in leg: decode tokens per timed window")
     ap.add_argument("--ipc-reps", type=int, default=3, help="drop-in leg: timed windows (the median is reported)")
-    ap.add_argument("--ipc-modes", default="host_sync,host_sync_pooled",
+    ap.add_argument("--ipc-modes", default="host_sync,gpu_ordered_inputs,gpu_ordered,host_sync_pooled",
                     help="drop-in leg: comma list of " + ", ".join(IPC_MODES) + " (the decode line's default: the "
-                         "reference's protocol with the worker's own LoRA, then with adapters pooled in the "
-                         "aggregator's rounds)")
+                         "reference's protocol with the worker's own LoRA, host-synchronised, then with its input "
+                         "copies and then also its output reads ordered on the GPU, then host-synchronised with "
+                         "adapters pooled in the aggregator's rounds)")
     return ap.parse_args()
 
 

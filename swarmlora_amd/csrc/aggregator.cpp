@@ -899,7 +899,7 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
           uint64_t oval[SWL_MAX_SLOTS];
           int nw = 0;
           for (int i = 0; i < m; ++i)
-            if (seqs[i] > 0) {
+            if (seqs[i] > 0 && !outh[i]) {  // out_host workers read after done: no word to wait on
               oflag[nw] = seq_word(sids[i], swl::kOutSeqOffset);
               oval[nw] = seqs[i];
               ++nw;

@@ -4303,6 +4303,19 @@ __global__ __launch_bounds__(SWL_MAX_SLOTS) void seq_write_kernel(SeqWriteArgs a
   const int i = threadIdx.x;
   if (i < a.n) __hip_atomic_store(a.flag[i], a.value[i], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+
+// One workgroup copies n16 16-byte pieces and `tail` more bytes, then every
+// thread releases its stores at agent scope (written back from the XCD's L2),
+// and after the barrier one lane stores the flag with system-scope release.
+__global__ __launch_bounds__(1024) void copy_signal_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src,
+                                                           int64_t n16, int tail, uint64_t* flag, uint64_t value) {
+  for (int64_t i = threadIdx.x; i < n16; i += 1024) dst[i] = src[i];
+  if ((int)threadIdx.x < tail)
+    reinterpret_cast<unsigned char*>(dst + n16)[threadIdx.x] = reinterpret_cast<const unsigned char*>(src + n16)[threadIdx.x];
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 }  // namespace
 
 namespace swl {
@@ -4318,6 +4331,19 @@ int seq_write_launch(int n, uint64_t* const* flag, const uint64_t* value, hipStr
   }
   hipLaunchKernelGGL(seq_write_kernel, dim3(1), dim3(SWL_MAX_SLOTS), 0, stream, a);
   SWL_LAUNCH_CHECK("seq_write_kernel launch");
+  return SWL_OK;
+}
+
+int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag, uint64_t value, hipStream_t stream) {
+  SWL_CHECK(flag != nullptr, SWL_ERR_INVALID, "copy_signal: null flag");
+  const bool fused = bytes <= kCopySignalMax && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0;
+  if (!fused) {
+    if (bytes) SWL_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream));
+    return seq_write_launch(1, &flag, &value, stream);
+  }
+  hipLaunchKernelGGL(copy_signal_kernel, dim3(1), dim3(1024), 0, stream, reinterpret_cast<u32x4*>(dst),
+                     reinterpret_cast<const u32x4*>(src), (int64_t)(bytes / 16), (int)(bytes % 16), flag, value);
+  SWL_LAUNCH_CHECK("copy_signal_kernel launch");
   return SWL_OK;
 }
 

@@ -41,6 +41,14 @@ int seq_wait_launch(int n, const uint64_t* const* flag, const uint64_t* want, co
 // is a kernel launch of its own that costs the host ~10-30 us.
 int seq_write_launch(int n, uint64_t* const* flag, const uint64_t* value, hipStream_t stream);
 
+// Copies `bytes` from src to dst on `stream` and then writes *flag = value
+// (system-scope release after every thread's stores are written back), in
+// one kernel launch of one workgroup: the GPU-ordered input copy of a worker
+// without a second dependent launch.  For copies up to kCopySignalMax bytes
+// with 16-byte aligned pointers; otherwise hipMemcpyAsync + seq_write_launch.
+constexpr size_t kCopySignalMax = 256 * 1024;
+int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag, uint64_t value, hipStream_t stream);
+
 }  // namespace swl
 
 #define SWL_HIP(call)                                   \

@@ -109,13 +109,13 @@ int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream
     return swl::fail(SWL_ERR_INVALID, std::string(fn) + ": input tensor (" + std::to_string(bytes) +
                                           " bytes) exceeds slot buffer size (" + std::to_string(c->in_size) +
                                           " bytes)");
-  SWL_HIP(hipMemcpyAsync(c->in, src, bytes, hipMemcpyDeviceToDevice, st));
   if (g_w.gpu_ordered) {
-    // the aggregator's stream waits for this value before reading the buffer
+    // the copy, then the value the aggregator's stream waits for before it
+    // reads the buffer (one launch for small copies)
     ++c->seq;
-    uint64_t* flag = seq_word(c, swl::kInSeqOffset);
-    return swl::seq_write_launch(1, &flag, &c->seq, st);
+    return swl::copy_signal_launch(c->in, src, bytes, seq_word(c, swl::kInSeqOffset), c->seq, st);
   }
+  SWL_HIP(hipMemcpyAsync(c->in, src, bytes, hipMemcpyDeviceToDevice, st));
   // the aggregator reads the buffer from another process once this worker
   // signals ready: the copy must be complete, not just ordered
   SWL_HIP(hipStreamSynchronize(st));
