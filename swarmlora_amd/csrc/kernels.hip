@@ -4316,6 +4316,42 @@ __global__ __launch_bounds__(1024) void copy_signal_kernel(u32x4* __restrict__ d
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+
+struct WaitCopyArgs {
+  const uint64_t* flag;
+  uint64_t want;
+  uint32_t* timed_out;
+  int32_t tag;
+  uint32_t limit_ticks;  // s_memrealtime runs at 100 MHz
+  u32x4* dst;
+  const u32x4* src;
+  int64_t n16;
+  int32_t tail;
+};
+
+// Lane 0 polls the flag (system-scope loads and a sleep, bounded like
+// seq_wait_kernel); after the barrier every thread takes an agent-scope
+// fence (the XCD's caches drop lines older than the producer's writes), then
+// the workgroup copies.  A wait that ran out of time reports its tag and the
+// copy still runs (the caller learns of it from timed_out).
+__global__ __launch_bounds__(1024) void wait_copy_kernel(WaitCopyArgs a) {
+  if (threadIdx.x == 0) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(a.flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < a.want) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > a.limit_ticks) {
+        __hip_atomic_store(a.timed_out + a.tag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(32);
+    }
+  }
+  __syncthreads();
+  __threadfence();
+  for (int64_t i = threadIdx.x; i < a.n16; i += 1024) a.dst[i] = a.src[i];
+  if ((int)threadIdx.x < a.tail)
+    reinterpret_cast<unsigned char*>(a.dst + a.n16)[threadIdx.x] =
+        reinterpret_cast<const unsigned char*>(a.src + a.n16)[threadIdx.x];
+}
 }  // namespace
 
 namespace swl {
@@ -4344,6 +4380,32 @@ int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag,
   hipLaunchKernelGGL(copy_signal_kernel, dim3(1), dim3(1024), 0, stream, reinterpret_cast<u32x4*>(dst),
                      reinterpret_cast<const u32x4*>(src), (int64_t)(bytes / 16), (int)(bytes % 16), flag, value);
   SWL_LAUNCH_CHECK("copy_signal_kernel launch");
+  return SWL_OK;
+}
+
+int wait_copy_launch(const uint64_t* flag, uint64_t want, int32_t tag, uint32_t* timed_out, uint32_t limit_us,
+                     void* dst, const void* src, size_t bytes, hipStream_t stream) {
+  SWL_CHECK(flag != nullptr && timed_out != nullptr && tag >= 0 && tag < SWL_MAX_SLOTS, SWL_ERR_INVALID,
+            "wait_copy: bad flag");
+  const bool fused = bytes <= kCopySignalMax && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0;
+  if (!fused) {
+    int rc = seq_wait_launch(1, &flag, &want, &tag, timed_out, limit_us, stream);
+    if (rc) return rc;
+    if (bytes) SWL_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream));
+    return SWL_OK;
+  }
+  WaitCopyArgs a{};
+  a.flag = flag;
+  a.want = want;
+  a.timed_out = timed_out;
+  a.tag = tag;
+  a.limit_ticks = (uint32_t)std::min<uint64_t>((uint64_t)limit_us * 100, 0xFFFFFFFFull);
+  a.dst = reinterpret_cast<u32x4*>(dst);
+  a.src = reinterpret_cast<const u32x4*>(src);
+  a.n16 = (int64_t)(bytes / 16);
+  a.tail = (int)(bytes % 16);
+  hipLaunchKernelGGL(wait_copy_kernel, dim3(1), dim3(1024), 0, stream, a);
+  SWL_LAUNCH_CHECK("wait_copy_kernel launch");
   return SWL_OK;
 }
 

@@ -49,6 +49,14 @@ int seq_write_launch(int n, uint64_t* const* flag, const uint64_t* value, hipStr
 constexpr size_t kCopySignalMax = 256 * 1024;
 int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag, uint64_t value, hipStream_t stream);
 
+// The converse: waits on `stream` until *flag >= want (as seq_wait_launch,
+// with its time-out report into timed_out[tag]), then copies `bytes` from
+// src to dst, in one launch of one workgroup for copies up to
+// kCopySignalMax bytes with 16-byte aligned pointers; otherwise
+// seq_wait_launch + hipMemcpyAsync.
+int wait_copy_launch(const uint64_t* flag, uint64_t want, int32_t tag, uint32_t* timed_out, uint32_t limit_us,
+                     void* dst, const void* src, size_t bytes, hipStream_t stream);
+
 }  // namespace swl
 
 #define SWL_HIP(call)                                   \

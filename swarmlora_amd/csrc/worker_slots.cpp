@@ -260,8 +260,14 @@ int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream) {
   SWL_CHECK(bytes <= c->out_size, SWL_ERR_INVALID,
             "get_outputs_slot: output (" + std::to_string(bytes) + " bytes) exceeds slot output buffer (" +
                 std::to_string(c->out_size) + " bytes)");
-  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
-  if (rc) return rc;
+  if (g_w.gpu_ordered == 1 && c->seq > 0) {
+    // the wait for the aggregator's output word and the copy, in one launch
+    // for small outputs
+    rc = swl::wait_copy_launch(seq_word(c, swl::kOutSeqOffset), c->seq, c->slot_id, g_w.out_timeout,
+                               out_wait_limit_us(), dst, c->out, bytes, (hipStream_t)stream);
+    if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+    return SWL_OK;
+  }
   // stream-ordered; consumers of dst on the same stream see the copy
   SWL_HIP(hipMemcpyAsync(dst, c->out, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
   return SWL_OK;
