@@ -854,9 +854,11 @@ def main():
             drop_in = {
                 "workload": f"{W_ipc} worker processes + a spawned aggregator process, {args.ipc_layers} 8B-shaped "
                             f"layers ({2 + 4 * args.ipc_layers} rounds per token), rank-16 adapter per worker; "
-                            "host_sync: applied on the worker (the reference's protocol); host_sync_pooled: pooled "
-                            f"in the aggregator's rounds; {args.ipc_reps} windows of {args.ipc_tokens} tokens once "
-                            "every slot is active, median window",
+                            "host_sync: adapter applied on the worker, host-synchronised rounds (the reference's "
+                            "protocol); gpu_ordered_inputs: the same with the input copies ordered on the GPU; "
+                            "gpu_ordered: input copies and output reads ordered on the GPU; host_sync_pooled: "
+                            f"adapters pooled in the aggregator's rounds; {args.ipc_reps} windows of "
+                            f"{args.ipc_tokens} tokens once every slot is active, median window",
                 "workers": W_ipc, "layers": args.ipc_layers, "rounds_per_token": 2 + 4 * args.ipc_layers, **res}
         except Exception as e:  # the headline line is still printed
             drop_in = {"error": f"{type(e).__name__}: {e}"[:2000]}
