@@ -193,7 +193,7 @@ MARGIN_MEAN = 1.25  # ... and on the mean over a worker's steps
 @pytest.mark.parametrize("model,pooled,gpu_ordered", [
     ("tiny", False, False), ("tiny", True, False), ("tiny", False, True), ("tiny", True, True),
     ("tiny", False, "inputs"), ("tiny", True, "inputs"), ("wide", False, False), ("wide", True, False),
-    ("wide", False, "inputs")])
+    ("wide", False, "inputs"), ("wide", False, True)])
 def test_end_to_end_workers_through_ipc(dev, model, pooled, gpu_ordered):
     """Worker processes (two on the small model, three at Llama-3.1-8B
     widths; one 20-token prompt in two prefill chunks + 3 decode tokens
@@ -211,7 +211,11 @@ def test_end_to_end_workers_through_ipc(dev, model, pooled, gpu_ordered):
     within 2e-2 of the bf16 oracle.  pooled=True moves the LoRA delta into the aggregator's round
     epilogue; gpu_ordered=True orders the slot copies against the rounds
     with sequence words waited on by the streams instead of host waits,
-    "inputs" only the input copies (the outputs are read after the round)."""
+    "inputs" only the input copies (the outputs are read after the round).
+    At 8B widths the first prefill chunk's Down input (448 KiB) and Gate+Up
+    output (896 KiB) take the two-launch copy paths of the GPU-ordered
+    modes, the second chunk's and the decode rows their one-launch
+    copy-and-signal and wait-and-copy kernels."""
     from swarmlora_amd import ext_ipc_queue as extq
     from tests._tiny_model import CFGS, adapter, base_weights, oracle_steps, to_float32
     c = CFGS[model]
