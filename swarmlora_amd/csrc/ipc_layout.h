@@ -11,7 +11,10 @@
 namespace swl {
 
 constexpr uint32_t kQueueMagic = 0x53574C51u;  // "SWLQ"
-constexpr uint32_t kQueueLayoutVersion = 2;
+// 3: commands carry out_host (a process of an earlier layout would ignore
+// it, so a worker reading its outputs without a GPU wait could meet an
+// aggregator that does not finish the round first); attaching checks it
+constexpr uint32_t kQueueLayoutVersion = 3;
 constexpr int kSlotWords = SWL_MAX_SLOTS / 64;
 
 // 128-bit slot set held in registers.

@@ -3616,15 +3616,8 @@ int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
   const int tiles_m = (int)((a.M + 64 * nj - 1) / (64 * nj));
   const int tiles = tiles_m * tiles_n;
   const int per_xcd = (tiles + 7) / 8;
-  static const int waves = [] {
-    const char* e = getenv("SWL_PREFILL_WAVES");
-    return e ? atoi(e) : 4;
-  }();
-  int rc;
-  if (waves == 8)  // 8 waves for 256-row tiles (4 x 2 waves of 64 x 128); 192-row tiles keep 4
-    rc = nj == 3 ? launch_gemm256<3, 2>(a, tiles_m, tiles, per_xcd, st) : launch_gemm256<2, 4>(a, tiles_m, tiles, per_xcd, st);
-  else
-    rc = nj == 3 ? launch_gemm256<3, 2>(a, tiles_m, tiles, per_xcd, st) : launch_gemm256<4, 2>(a, tiles_m, tiles, per_xcd, st);
+  const int rc = nj == 3 ? launch_gemm256<3, 2>(a, tiles_m, tiles, per_xcd, st)
+                          : launch_gemm256<4, 2>(a, tiles_m, tiles, per_xcd, st);
   if (rc) return rc;
   SWL_LAUNCH_CHECK("gemm256_kernel launch");
   return SWL_OK;
