@@ -1745,22 +1745,32 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm256_kernel(TiledArgs a, int t
       }
       mma(fa_, fb_);
     };
-    u32x4 xa[4], xu[NJ][2], ya[4], yu[NJ][2];
-    int ci = first(0), cq = 0;
-    if (ci < nseg) load(ci, cq, xa, xu);
-    while (ci < nseg) {
-      int ni = ci, nq = cq;
-      advance(ni, nq);
-      if (ni < nseg) load(ni, nq, ya, yu);
-      use(ci, xa, xu);
-      ci = ni;
-      cq = nq;
-      if (ci >= nseg) break;
-      advance(ni, nq);
-      if (ni < nseg) load(ni, nq, xa, xu);
-      use(ci, ya, yu);
-      ci = ni;
-      cq = nq;
+    // PD register sets taken in turn: while a step's MFMAs issue, the loads
+    // of the next PD - 1 steps are in flight (a tile over many small
+    // segments runs ~20 latency-bound steps)
+    constexpr int PD = 3;
+    u32x4 ra[PD][4], ru[PD][NJ][2];
+    int di[PD];
+    int li = first(0), lq = 0;  // the next step to load
+#pragma unroll
+    for (int p = 0; p < PD; ++p) {
+      di[p] = li;
+      if (li < nseg) {
+        load(li, lq, ra[p], ru[p]);
+        advance(li, lq);
+      }
+    }
+    while (di[0] < nseg) {
+#pragma unroll
+      for (int p = 0; p < PD; ++p) {
+        if (di[p] >= nseg) break;  // uniform: steps fill the sets in order
+        use(di[p], ra[p], ru[p]);
+        di[p] = li;
+        if (li < nseg) {
+          load(li, lq, ra[p], ru[p]);
+          advance(li, lq);
+        }
+      }
     }
   }
 
