@@ -1467,7 +1467,8 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 }
 
 template <int NJ, int WM>
-__global__ __launch_bounds__(128 * WM, 1) void gemm256_kernel(TiledArgs a, int tiles_m, int tiles, int per_xcd) {
+__global__ __launch_bounds__(128 * WM, 1) void gemm256_kernel(TiledArgs a, int tiles_m, int tiles, int per_xcd,
+                                                               int gm) {
   // PG_SLOTS x [W 256 x 64 | x MT x 64]; then the epilogue's WAVES x [TPW][PG_ELD] fp32
   using Geo = PgGeom<NJ, WM>;
   constexpr int WAVES = 2 * WM;
@@ -1482,8 +1483,13 @@ __global__ __launch_bounds__(128 * WM, 1) void gemm256_kernel(TiledArgs a, int t
   const int wm = wv >> 1, wn = wv & 1;  // wave: tokens wm * TPW.., columns wn * 128..
   const int lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   if (lin >= tiles) return;  // uniform over the workgroup
-  const int64_t m0 = (int64_t)(lin % tiles_m) * MT;
-  const int64_t n0 = (int64_t)(lin / tiles_m) * PG_N;
+  // linear tile lin: groups of gm row tiles, each group walking its column
+  // tiles with the rows fastest (gm = tiles_m: one group)
+  const int gsz = gm * (tiles / tiles_m);
+  const int grp = lin / gsz, gl = lin - grp * gsz;
+  const int gr = min(gm, tiles_m - grp * gm);  // row tiles in this group
+  const int64_t m0 = (int64_t)(grp * gm + gl % gr) * MT;
+  const int64_t n0 = (int64_t)(gl / gr) * PG_N;
   const int nk = (int)(a.K / PG_K);
 
   f32x16 acc[4][NJ];
@@ -3583,13 +3589,13 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
 bool prefill_uses_tiled(int64_t K) { return K % PG_K != 0 || K < PG_K; }
 
 template <int NJ, int WM>
-int launch_gemm256(const TiledArgs& a, int tiles_m, int tiles, int per_xcd, hipStream_t st) {
+int launch_gemm256(const TiledArgs& a, int tiles_m, int tiles, int per_xcd, int gm, hipStream_t st) {
   constexpr size_t lds = PgGeom<NJ, WM>::LDS;
   static size_t allowed = 0;
   int rc = allow_lds(gemm256_kernel<NJ, WM>, lds, &allowed);
   if (rc) return rc;
   hipLaunchKernelGGL((gemm256_kernel<NJ, WM>), dim3((unsigned)(8 * per_xcd)), dim3(128 * WM), lds, st, a, tiles_m,
-                     tiles, per_xcd);
+                     tiles, per_xcd, gm);
   return SWL_OK;
 }
 
@@ -3626,8 +3632,16 @@ int launch_prefill_gemm(const TiledArgs& a, hipStream_t st) {
   const int tiles_m = (int)((a.M + 64 * nj - 1) / (64 * nj));
   const int tiles = tiles_m * tiles_n;
   const int per_xcd = (tiles + 7) / 8;
-  const int rc = nj == 3 ? launch_gemm256<3, 2>(a, tiles_m, tiles, per_xcd, st)
-                          : launch_gemm256<4, 2>(a, tiles_m, tiles, per_xcd, st);
+  // Tile order.  Every XCD (workgroup i on XCD i % 8) walks a contiguous run
+  // of per_xcd linear tiles.  When all tiles run at once (no more tiles than
+  // CUs), the run covers a near-square block of row x column tiles (groups
+  // of gm ~ sqrt(per_xcd) row tiles): at each k-stage the XCD then reads
+  // fewer distinct W and row slices than with all row tiles of a column
+  // fastest.  Rounds of several waves keep the rows fastest (one group).
+  int gm = tiles_m;
+  if (tiles <= cus) gm = std::max(1, std::min(tiles_m, (int)std::lround(std::sqrt((double)per_xcd))));
+  const int rc = nj == 3 ? launch_gemm256<3, 2>(a, tiles_m, tiles, per_xcd, gm, st)
+                          : launch_gemm256<4, 2>(a, tiles_m, tiles, per_xcd, gm, st);
   if (rc) return rc;
   SWL_LAUNCH_CHECK("gemm256_kernel launch");
   return SWL_OK;
