@@ -444,11 +444,20 @@ __global__ __launch_bounds__(256) void shrink_gemm_kernel(ShrinkGemmArgs a) {
 
 // u[0] += u[1] + ... + u[n_ks - 1] over [nvec] float4 (the shrink partials
 // folded once, so the tiled epilogue's expand reads a single split).
+// Every split's load is issued before the first add (n_ks <= kFoldMax),
+// then the sum runs in split order.
+constexpr int kFoldMax = 16;
 __global__ __launch_bounds__(256) void u_fold_kernel(float* u, int64_t split_stride, int n_ks, int64_t nvec) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= nvec) return;
-  f32x4 s = reinterpret_cast<const f32x4*>(u)[i];
-  for (int k = 1; k < n_ks; ++k) s += reinterpret_cast<const f32x4*>(u + k * split_stride)[i];
+  f32x4 v[kFoldMax];
+#pragma unroll
+  for (int k = 0; k < kFoldMax; ++k)
+    if (k < n_ks) v[k] = reinterpret_cast<const f32x4*>(u + k * split_stride)[i];
+  f32x4 s = v[0];
+#pragma unroll
+  for (int k = 1; k < kFoldMax; ++k)
+    if (k < n_ks) s += v[k];
   reinterpret_cast<f32x4*>(u)[i] = s;
 }
 
@@ -3677,6 +3686,7 @@ int launch_shrink_gemm(const bf16* const* seg_x, int64_t K, int n_seg, const int
   hipLaunchKernelGGL(shrink_gemm_kernel, dim3((unsigned)(items * n_ks)), dim3(256), 0, st, a);
   SWL_LAUNCH_CHECK("shrink_gemm_kernel launch");
   if (n_ks > 1) {
+    SWL_CHECK(n_ks <= kFoldMax, SWL_ERR_INVALID, "shrink: at most 16 K-slices");
     const int64_t nvec = u_split_stride / 4;  // u_ld is a multiple of 16
     hipLaunchKernelGGL(u_fold_kernel, dim3((unsigned)((nvec + 255) / 256)), dim3(256), 0, st, u, u_split_stride,
                        n_ks, nvec);
