@@ -51,8 +51,12 @@ def _L():
     return _lib.load()
 
 
-def _stream():
-    return c_vp(torch.cuda.current_stream(_state["device"]).cuda_stream)
+if hasattr(torch._C, "_cuda_getCurrentRawStream"):
+    def _stream():  # the raw handle, without building a Stream object
+        return c_vp(torch._C._cuda_getCurrentRawStream(_state["device"]))
+else:
+    def _stream():
+        return c_vp(torch.cuda.current_stream(_state["device"]).cuda_stream)
 
 
 def _shape(slot_id):
