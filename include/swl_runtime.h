@@ -206,6 +206,13 @@ int swl_w_slot_shape(int slot_id, int64_t* bx, int64_t* tx, int64_t* dx);
  * 276-347, 396-440): `bytes` from the slot output buffer into dst (device),
  * stream-ordered, no host sync. */
 int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream);
+/* get_outputs_slot followed by the worker's adds of its *_get_all methods
+ * (worker_sync.py:314-319, :383-389: out + lora delta, then residual + that,
+ * each rounded to bf16) in one launch: dst = residual + (out + delta) over
+ * the first n bf16 elements of the slot output; delta and residual may be
+ * null.  Stream-ordered; in GPU-ordered mode 1 it first waits for the
+ * output word as swl_w_copy_output does. */
+int swl_w_read_output(int slot_id, void* dst, int64_t n, const void* delta, const void* residual, void* stream);
 /* prepare_token_ids_slot (ext_unified_barrier.cpp:350-393): int64 ids. */
 int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx, void* stream);
 /* prepare_hidden_for_lm_head_slot (ext_unified_barrier.cpp:443-486). */

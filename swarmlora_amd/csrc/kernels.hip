@@ -4344,6 +4344,42 @@ __global__ __launch_bounds__(1024) void copy_signal_kernel(u32x4* __restrict__ d
   if (threadIdx.x == 0) __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+struct CombineArgs {
+  bf16* dst;
+  const bf16* src;
+  const bf16* delta;  // or null
+  const bf16* res;    // or null
+  int64_t n;
+  int32_t vec;        // every pointer 16-byte aligned
+};
+
+// A worker's read of its round output: out (+ its LoRA delta) (+ the
+// residual), each add rounded to bf16 as torch's bf16 adds are; 8 elements
+// a thread.
+__global__ __launch_bounds__(256) void combine_rows_kernel(CombineArgs a) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i0 >= a.n) return;
+  auto one = [&](float s, float d, float r) {
+    float v = s;
+    if (a.delta) v = bf2f(f2bf(v + d));
+    if (a.res) v = r + v;
+    return f2bf(v);
+  };
+  if (a.vec && i0 + 8 <= a.n) {
+    float s[8], d[8], r[8];
+    unpack8(ld16(a.src + i0), s);
+    if (a.delta) unpack8(ld16(a.delta + i0), d);
+    if (a.res) unpack8(ld16(a.res + i0), r);
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = one(s[e], a.delta ? d[e] : 0.f, a.res ? r[e] : 0.f);
+    *reinterpret_cast<u32x4*>(a.dst + i0) = __builtin_bit_cast(u32x4, o);
+    return;
+  }
+  for (int64_t i = i0; i < a.n && i < i0 + 8; ++i)
+    a.dst[i] = one(bf2f(a.src[i]), a.delta ? bf2f(a.delta[i]) : 0.f, a.res ? bf2f(a.res[i]) : 0.f);
+}
+
 struct WaitCopyArgs {
   const uint64_t* flag;
   uint64_t want;
@@ -4407,6 +4443,24 @@ int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag,
   hipLaunchKernelGGL(copy_signal_kernel, dim3(1), dim3(1024), 0, stream, reinterpret_cast<u32x4*>(dst),
                      reinterpret_cast<const u32x4*>(src), (int64_t)(bytes / 16), (int)(bytes % 16), flag, value);
   SWL_LAUNCH_CHECK("copy_signal_kernel launch");
+  return SWL_OK;
+}
+
+int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta, const void* res,
+                        hipStream_t stream) {
+  SWL_CHECK(dst && src && n >= 0, SWL_ERR_INVALID, "combine_rows: bad arguments");
+  if (n == 0) return SWL_OK;
+  CombineArgs a{};
+  a.dst = reinterpret_cast<bf16*>(dst);
+  a.src = reinterpret_cast<const bf16*>(src);
+  a.delta = reinterpret_cast<const bf16*>(delta);
+  a.res = reinterpret_cast<const bf16*>(res);
+  a.n = n;
+  auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
+  a.vec = (al(dst) && al(src) && al(delta) && al(res)) ? 1 : 0;
+  const int64_t threads = (n + 7) / 8;
+  hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
+  SWL_LAUNCH_CHECK("combine_rows_kernel launch");
   return SWL_OK;
 }
 

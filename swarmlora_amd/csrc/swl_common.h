@@ -54,6 +54,12 @@ int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag,
 // src to dst, in one launch of one workgroup for copies up to
 // kCopySignalMax bytes with 16-byte aligned pointers; otherwise
 // seq_wait_launch + hipMemcpyAsync.
+// dst[i] = bf16(res[i] + bf16(src[i] + delta[i])) for i < n bf16 elements
+// (delta and res optional: the same bf16 roundings as the two separate adds
+// out + delta and residual + that), one launch.
+int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta, const void* res,
+                        hipStream_t stream);
+
 int wait_copy_launch(const uint64_t* flag, uint64_t want, int32_t tag, uint32_t* timed_out, uint32_t limit_us,
                      void* dst, const void* src, size_t bytes, hipStream_t stream);
 

@@ -273,6 +273,21 @@ int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream) {
   return SWL_OK;
 }
 
+int swl_w_read_output(int slot_id, void* dst, int64_t n, const void* delta, const void* residual, void* stream) {
+  SlotCtx* c;
+  int rc = need_data_slot("get_outputs_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(dst != nullptr && n >= 0, SWL_ERR_INVALID, "get_outputs_slot: bad destination");
+  SWL_CHECK((size_t)n * sizeof(uint16_t) <= c->out_size, SWL_ERR_INVALID,
+            "get_outputs_slot: output (" + std::to_string(n * 2) + " bytes) exceeds slot output buffer (" +
+                std::to_string(c->out_size) + " bytes)");
+  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
+  if (rc) return rc;
+  rc = swl::combine_rows_launch(dst, c->out, n, delta, residual, (hipStream_t)stream);
+  if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+  return SWL_OK;
+}
+
 int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx, void* stream) {
   SlotCtx* c;
   int rc = need_data_slot("prepare_token_ids_slot", slot_id, &c);

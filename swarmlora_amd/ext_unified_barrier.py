@@ -36,6 +36,7 @@ _lib.register_signatures({
     "swl_w_slot_shape": (c_int, [c_int, _P_i64, _P_i64, _P_i64]),
     "swl_w_slot_sizes": (c_int, [c_int, _P_size, _P_size]),
     "swl_w_copy_output": (c_int, [c_int, c_vp, ctypes.c_size_t, c_vp]),
+    "swl_w_read_output": (c_int, [c_int, c_vp, c_i64, c_vp, c_vp, c_vp]),
     "swl_w_prepare_token_ids": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp]),
     "swl_w_prepare_hidden_lm": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, ctypes.c_size_t, c_vp]),
     "swl_w_get_next_token": (c_int, [c_int, _P_i64, c_vp]),
@@ -101,6 +102,30 @@ def get_outputs_slot(slot_id, out_dims: Sequence[int], input_template) -> List[t
     total = sum(dims)
     out = torch.empty(bx, tx, total, dtype=input_template.dtype, device=input_template.device)
     _lib.check(_L().swl_w_copy_output(int(slot_id), out.data_ptr(), out.numel() * out.element_size(), _stream()))
+    if len(dims) > 1:
+        return list(out.split(dims, dim=-1))
+    return [out]
+
+
+def read_outputs_slot(slot_id, out_dims: Sequence[int], input_template, delta=None, residual=None):
+    """get_outputs_slot with the adds its caller makes next, in one launch:
+    residual + (output + delta), bf16 roundings as torch's two adds; delta
+    and residual are [B, T, sum(out_dims)] bf16 or None (an addition: the
+    reference copies, then adds with torch).  Returns the same split views."""
+    bx, tx, _ = _shape(slot_id)
+    dims = [int(d) for d in out_dims]
+    total = sum(dims)
+    out = torch.empty(bx, tx, total, dtype=input_template.dtype, device=input_template.device)
+    ptrs = []
+    for name, t in (("delta", delta), ("residual", residual)):
+        if t is None:
+            ptrs.append(None)
+            continue
+        if (t.dtype != torch.bfloat16 or out.dtype != torch.bfloat16 or tuple(t.shape) != tuple(out.shape)
+                or not t.is_contiguous()):
+            raise RuntimeError(f"read_outputs_slot: {name} must be a contiguous bf16 [B, T, {total}] tensor")
+        ptrs.append(t.data_ptr())
+    _lib.check(_L().swl_w_read_output(int(slot_id), out.data_ptr(), out.numel(), ptrs[0], ptrs[1], _stream()))
     if len(dims) > 1:
         return list(out.split(dims, dim=-1))
     return [out]

@@ -158,6 +158,37 @@ class BatchedAggregatorOps:
         with self.timer.stage("scatter"):
             return {slot_id: ub.get_outputs_slot(slot_id, dims, state.hidden)}
 
+    def _fused_read(self, slots, dims, delta=None, residual=None):
+        """The slot's output with the caller's adds in the same launch
+        (ub.read_outputs_slot), or None where the operands do not fit it
+        (then the caller copies and adds on its own)."""
+        slot_id, state = next(iter(slots.items()))
+        tmpl = state.hidden
+        if tmpl is None or tmpl.dtype != torch.bfloat16 or len(slots) != 1:
+            return None
+        for t in (delta, residual):
+            if t is not None and (t.dtype != torch.bfloat16 or not t.is_contiguous() or t.shape[-1] != sum(dims)
+                                  or t.dim() != 3):
+                return None
+        with self.timer.stage("scatter"):
+            return ub.read_outputs_slot(slot_id, dims, tmpl, delta, residual)
+
+    def _fused_join(self, slots, deltas, dims, n):
+        """qkv / gate_up read: the fused output plus its fused delta in one
+        launch when the per-block deltas are pieces of one buffer."""
+        sid = next(iter(slots))
+        d = list(deltas.get(sid, (None,) * n))
+        if all(x is None for x in d):
+            jd = None
+        elif any(x is None for x in d):
+            return None
+        else:
+            jd = _joined(d)
+            if jd is None:
+                return None
+        got = self._fused_read(slots, dims, jd, None)
+        return None if got is None else {sid: tuple(got)}
+
     def _seq(self, slot_id):
         return ub.input_seq(slot_id) if self.gpu_ordered else 0
 
@@ -198,6 +229,9 @@ class BatchedAggregatorOps:
         return epoch, deltas
 
     def qkv_get_all(self, slots, layer_idx: int, deltas, dims: List[int]):
+        fused = self._fused_join(slots, deltas, dims, 3)
+        if fused is not None:
+            return fused
         raw = self._get_outputs_all(slots, dims)
         res = {}
         with self.timer.stage("lora"):
@@ -219,6 +253,11 @@ class BatchedAggregatorOps:
             return epoch, {slot_id: o.delta(x) if use else None}
 
     def o_proj_get_all(self, slots, layer_idx: int, deltas, out_dim: int):
+        sid, state = next(iter(slots.items()))
+        got = self._fused_read(slots, [out_dim], deltas.get(sid), state.residual)
+        if got is not None:  # residual + (o + delta), one launch
+            state.hidden = got[0]
+            return
         raw = self._get_outputs_all(slots, [out_dim])
         with self.timer.stage("lora"):
             for sid, state in slots.items():
@@ -245,6 +284,9 @@ class BatchedAggregatorOps:
         # g and u are the two halves of the freshly copied output; the deltas
         # are added in place (the values of g + dg, u + du) so the pair stays
         # one [.., 2 * inter] buffer that the SiLU*up kernel reads directly
+        fused = self._fused_join(slots, deltas, dims, 2)
+        if fused is not None:
+            return fused
         raw = self._get_outputs_all(slots, dims)
         res = {}
         with self.timer.stage("lora"):
@@ -265,6 +307,11 @@ class BatchedAggregatorOps:
             return epoch, {slot_id: dp.delta(x) if use else None}
 
     def down_proj_get_all(self, slots, layer_idx: int, deltas, out_dim: int):
+        sid, state = next(iter(slots.items()))
+        got = self._fused_read(slots, [out_dim], deltas.get(sid), state.mlp_residual)
+        if got is not None:  # mlp_residual + (down + delta), one launch
+            state.hidden = got[0]
+            return
         raw = self._get_outputs_all(slots, [out_dim])
         with self.timer.stage("lora"):
             for sid, state in slots.items():

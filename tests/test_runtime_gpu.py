@@ -306,6 +306,78 @@ def test_end_to_end_workers_through_ipc(dev, model, pooled, gpu_ordered):
                 assert toks[si - 1] == int(logits.argmax())
 
 
+def _read_proc(claim, out):
+    """Worker side of test_read_outputs_matches_copy_and_adds: every case of
+    the fused read against get_outputs_slot + the torch adds it replaces."""
+    try:
+        import torch
+        from swarmlora_amd import ext_unified_barrier as ub
+        torch.cuda.set_device(0)
+        dev = torch.device("cuda:0")
+        ub.init_worker_slot_manager(6, 0, 0, H, I, QKV)
+        sid = claim["slot_id"]
+        ub.open_slot(sid, claim["input_handle"], claim["output_handle"], claim["input_buffer_size"],
+                     claim["output_buffer_size"])
+        g = torch.Generator(device=dev).manual_seed(11)
+        results = []
+        # (tokens, dims, delta, residual, misaligned operands)
+        cases = [(1, [H], True, True, False), (3, [H], True, True, False), (2, [H, 256, 256], True, False, False),
+                 (1, [2 * I], False, False, False), (3, [100], True, True, True), (1, [H], False, True, False)]
+        for t, dims, with_d, with_r, skew in cases:
+            total = sum(dims)
+            x = torch.zeros(1, t, 64, dtype=torch.bfloat16, device=dev)
+            ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)  # records the slot's [1, t] shape
+            def operand():
+                n = t * total
+                buf = torch.randn(n + 1, generator=g, device=dev).to(torch.bfloat16)
+                return (buf[1:] if skew else buf[:n]).view(1, t, total)
+            d = operand() if with_d else None
+            r = operand() if with_r else None
+            ref = ub.get_outputs_slot(sid, [total], x)[0]
+            if d is not None:
+                ref = ref + d
+            if r is not None:
+                ref = r + ref
+            got = ub.read_outputs_slot(sid, dims, x, d, r)
+            got = torch.cat(got, -1) if len(got) > 1 else got[0]
+            torch.cuda.synchronize()
+            results.append(bool(torch.equal(got.view(torch.int16), ref.view(torch.int16))))
+        ub.close_slot(sid)
+        out.put((results, None))
+    except Exception:
+        import traceback
+        out.put((None, traceback.format_exc()))
+
+
+def test_read_outputs_matches_copy_and_adds(pool):
+    """ub.read_outputs_slot (one launch: residual + (output + delta)) is bit
+    for bit the copy of get_outputs_slot followed by the torch bf16 adds of
+    the *_get_all methods it replaces, for deltas and residuals present or
+    not, 1-3 token rows, fused multi-block outputs, and an element count that
+    is not a multiple of 8 with operands off 16-byte alignment (the scalar
+    path).  The slot output holds random bf16 values written by this
+    process (the aggregator side)."""
+    agg = _agg()
+    claim = agg.claim_slot(6)
+    _, sout = agg.slot_tensors(claim["slot_id"])
+    sout.copy_(torch.randn(sout.numel(), generator=torch.Generator(device=sout.device).manual_seed(5),
+                           device=sout.device).to(torch.bfloat16))
+    torch.cuda.synchronize()
+    ctx = mp.get_context("spawn")
+    out = ctx.Queue()
+    p = ctx.Process(target=_read_proc, args=(claim, out))
+    try:
+        p.start()
+        results, err = out.get(timeout=180)
+    finally:
+        p.join(timeout=30)
+        if p.is_alive():
+            p.kill()
+        agg.release_slot(claim["slot_id"], 6)
+    assert err is None, err
+    assert results == [True] * 6, results
+
+
 def _timeout_proc(claim, out):
     try:
         import os
