@@ -4380,6 +4380,98 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(CombineArgs a) {
     a.dst[i] = one(bf2f(a.src[i]), a.delta ? bf2f(a.delta[i]) : 0.f, a.res ? bf2f(a.res[i]) : 0.f);
 }
 
+// The read of an O or Down round's output followed by the next norm, one
+// workgroup of 256 threads per token row: h = bf16(res + bf16(out + delta))
+// is written to dst_h, then LlamaRMSNorm of h to dst_n with the same
+// per-thread sums and reduction as rmsnorm_rows_kernel, so both match the
+// separate read and norm bit for bit.  d a multiple of 8, every pointer
+// 16-byte aligned (the caller checks).
+struct CombineNormArgs {
+  bf16* dst_h;
+  bf16* dst_n;
+  const bf16* src;
+  const bf16* delta;  // or null
+  const bf16* res;    // or null
+  const bf16* w;
+  int64_t d;
+  float eps;
+};
+
+__global__ __launch_bounds__(256) void combine_norm_rows_kernel(CombineNormArgs a) {
+  __shared__ float sh[4];
+  const int64_t off = (int64_t)blockIdx.x * a.d;
+  const int64_t nv = a.d >> 3;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+    float s[8], dl[8], r[8];
+    unpack8(ld16(a.src + off + 8 * i), s);
+    if (a.delta) unpack8(ld16(a.delta + off + 8 * i), dl);
+    if (a.res) unpack8(ld16(a.res + off + 8 * i), r);
+    bf16x8 o;
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float v = s[j];
+      if (a.delta) v = bf2f(f2bf(v + dl[j]));
+      if (a.res) v = r[j] + v;
+      o[j] = f2bf(v);
+      x[j] = bf2f(o[j]);
+    }
+    *reinterpret_cast<u32x4*>(a.dst_h + off + 8 * i) = __builtin_bit_cast(u32x4, o);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+  }
+  ss = block_reduce<float>(ss, [](float x, float y) { return x + y; }, sh);
+  const float rs = rsqrtf(ss / (float)a.d + a.eps);
+  for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+    float x[8], g[8];
+    unpack8(ld16(a.dst_h + off + 8 * i), x);
+    unpack8(ld16(a.w + 8 * i), g);
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(f2bf(x[j] * rs)) * g[j]);
+    *reinterpret_cast<u32x4*>(a.dst_n + off + 8 * i) = __builtin_bit_cast(u32x4, o);
+  }
+}
+
+// The read of a Gate+Up round's output followed by SiLU*up: g = bf16(gate +
+// dgate), u = bf16(up + dup), act = bf16(bf16(silu(g)) * u) as
+// silu_mul_rows_kernel computes it; rows of 2 inter (gate | up) in, inter
+// out.  inter a multiple of 8, pointers 16-byte aligned.
+struct CombineSiluArgs {
+  bf16* dst;
+  const bf16* src;
+  const bf16* delta;  // [rows][2 inter] or null
+  int64_t inter;
+};
+
+__global__ __launch_bounds__(256) void combine_silu_rows_kernel(CombineSiluArgs a) {
+  const int t = blockIdx.y;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (a.inter >> 3)) return;
+  const int64_t ri = (int64_t)t * 2 * a.inter + 8 * i;
+  float g[8], u[8];
+  unpack8(ld16(a.src + ri), g);
+  unpack8(ld16(a.src + ri + a.inter), u);
+  if (a.delta) {
+    float dg[8], du[8];
+    unpack8(ld16(a.delta + ri), dg);
+    unpack8(ld16(a.delta + ri + a.inter), du);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g[j] = bf2f(f2bf(g[j] + dg[j]));
+      u[j] = bf2f(f2bf(u[j] + du[j]));
+    }
+  }
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sg = bf2f(f2bf(g[j] / (1.0f + __expf(-g[j]))));
+    o[j] = f2bf(sg * u[j]);
+  }
+  *reinterpret_cast<u32x4*>(a.dst + (int64_t)t * a.inter + 8 * i) = __builtin_bit_cast(u32x4, o);
+}
+
 struct WaitCopyArgs {
   const uint64_t* flag;
   uint64_t want;
@@ -4461,6 +4553,47 @@ int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta
   const int64_t threads = (n + 7) / 8;
   hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
   SWL_LAUNCH_CHECK("combine_rows_kernel launch");
+  return SWL_OK;
+}
+
+int combine_norm_rows_launch(void* dst_h, void* dst_n, const void* src, int64_t rows, int64_t d, const void* delta,
+                             const void* res, const void* w, float eps, hipStream_t stream) {
+  auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
+  SWL_CHECK(dst_h && dst_n && src && w && rows >= 0 && d > 0 && d % 8 == 0, SWL_ERR_INVALID,
+            "combine_norm_rows: bad arguments (d must be a multiple of 8)");
+  SWL_CHECK(al(dst_h) && al(dst_n) && al(src) && al(delta) && al(res) && al(w), SWL_ERR_INVALID,
+            "combine_norm_rows: pointers must be 16-byte aligned");
+  if (rows == 0) return SWL_OK;
+  CombineNormArgs a{};
+  a.dst_h = reinterpret_cast<bf16*>(dst_h);
+  a.dst_n = reinterpret_cast<bf16*>(dst_n);
+  a.src = reinterpret_cast<const bf16*>(src);
+  a.delta = reinterpret_cast<const bf16*>(delta);
+  a.res = reinterpret_cast<const bf16*>(res);
+  a.w = reinterpret_cast<const bf16*>(w);
+  a.d = d;
+  a.eps = eps;
+  hipLaunchKernelGGL(combine_norm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, stream, a);
+  SWL_LAUNCH_CHECK("combine_norm_rows_kernel launch");
+  return SWL_OK;
+}
+
+int combine_silu_rows_launch(void* dst, const void* src, int64_t rows, int64_t inter, const void* delta,
+                             hipStream_t stream) {
+  auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
+  SWL_CHECK(dst && src && rows >= 0 && inter > 0 && inter % 8 == 0, SWL_ERR_INVALID,
+            "combine_silu_rows: bad arguments (inter must be a multiple of 8)");
+  SWL_CHECK(rows <= 65535, SWL_ERR_INVALID, "combine_silu_rows: at most 65535 rows");
+  SWL_CHECK(al(dst) && al(src) && al(delta), SWL_ERR_INVALID, "combine_silu_rows: pointers must be 16-byte aligned");
+  if (rows == 0) return SWL_OK;
+  CombineSiluArgs a{};
+  a.dst = reinterpret_cast<bf16*>(dst);
+  a.src = reinterpret_cast<const bf16*>(src);
+  a.delta = reinterpret_cast<const bf16*>(delta);
+  a.inter = inter;
+  const dim3 grid((unsigned)(((inter >> 3) + 255) / 256), (unsigned)rows);
+  hipLaunchKernelGGL(combine_silu_rows_kernel, grid, dim3(256), 0, stream, a);
+  SWL_LAUNCH_CHECK("combine_silu_rows_kernel launch");
   return SWL_OK;
 }
 

@@ -288,6 +288,34 @@ int swl_w_read_output(int slot_id, void* dst, int64_t n, const void* delta, cons
   return SWL_OK;
 }
 
+int swl_w_read_output_norm(int slot_id, void* dst_h, void* dst_norm, int64_t rows, int64_t d, const void* delta,
+                           const void* residual, const void* weight, float eps, void* stream) {
+  SlotCtx* c;
+  int rc = need_data_slot("get_outputs_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(rows >= 0 && d > 0 && (size_t)(rows * d) * sizeof(uint16_t) <= c->out_size, SWL_ERR_INVALID,
+            "get_outputs_slot: output rows exceed the slot output buffer");
+  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
+  if (rc) return rc;
+  rc = swl::combine_norm_rows_launch(dst_h, dst_norm, c->out, rows, d, delta, residual, weight, eps,
+                                     (hipStream_t)stream);
+  if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+  return SWL_OK;
+}
+
+int swl_w_read_output_silu(int slot_id, void* dst, int64_t rows, int64_t inter, const void* delta, void* stream) {
+  SlotCtx* c;
+  int rc = need_data_slot("get_outputs_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(rows >= 0 && inter > 0 && (size_t)(rows * 2 * inter) * sizeof(uint16_t) <= c->out_size, SWL_ERR_INVALID,
+            "get_outputs_slot: output rows exceed the slot output buffer");
+  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
+  if (rc) return rc;
+  rc = swl::combine_silu_rows_launch(dst, c->out, rows, inter, delta, (hipStream_t)stream);
+  if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+  return SWL_OK;
+}
+
 int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx, void* stream) {
   SlotCtx* c;
   int rc = need_data_slot("prepare_token_ids_slot", slot_id, &c);

@@ -37,6 +37,8 @@ _lib.register_signatures({
     "swl_w_slot_sizes": (c_int, [c_int, _P_size, _P_size]),
     "swl_w_copy_output": (c_int, [c_int, c_vp, ctypes.c_size_t, c_vp]),
     "swl_w_read_output": (c_int, [c_int, c_vp, c_i64, c_vp, c_vp, c_vp]),
+    "swl_w_read_output_norm": (c_int, [c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
+    "swl_w_read_output_silu": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "swl_w_prepare_token_ids": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp]),
     "swl_w_prepare_hidden_lm": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, ctypes.c_size_t, c_vp]),
     "swl_w_get_next_token": (c_int, [c_int, _P_i64, c_vp]),
@@ -129,6 +131,44 @@ def read_outputs_slot(slot_id, out_dims: Sequence[int], input_template, delta=No
     if len(dims) > 1:
         return list(out.split(dims, dim=-1))
     return [out]
+
+
+def _bf16_operand(t, shape, name):
+    if t is None:
+        return None
+    if t.dtype != torch.bfloat16 or tuple(t.shape) != tuple(shape) or not t.is_contiguous() or t.data_ptr() % 16:
+        raise RuntimeError(f"read_outputs: {name} must be a contiguous, 16-byte aligned bf16 {list(shape)} tensor")
+    return t.data_ptr()
+
+
+def read_outputs_norm_slot(slot_id, out_dim, input_template, delta, residual, weight, eps):
+    """An O or Down round's output read with the worker's adds and the next
+    LlamaRMSNorm in one launch (an addition): returns (h, norm(h) * weight),
+    h = residual + (output + delta), [B, T, out_dim] each; out_dim a
+    multiple of 8."""
+    bx, tx, _ = _shape(slot_id)
+    d = int(out_dim)
+    shape = (bx, tx, d)
+    h = torch.empty(shape, dtype=torch.bfloat16, device=input_template.device)
+    n = torch.empty_like(h)
+    if weight.dtype != torch.bfloat16 or weight.numel() != d or not weight.is_contiguous() or weight.data_ptr() % 16:
+        raise RuntimeError("read_outputs_norm_slot: weight must be a contiguous, aligned bf16 [out_dim] tensor")
+    _lib.check(_L().swl_w_read_output_norm(int(slot_id), h.data_ptr(), n.data_ptr(), bx * tx, d,
+                                           _bf16_operand(delta, shape, "delta"),
+                                           _bf16_operand(residual, shape, "residual"), weight.data_ptr(),
+                                           float(eps), _stream()))
+    return h, n
+
+
+def read_outputs_silu_slot(slot_id, inter, input_template, delta=None):
+    """A Gate+Up round's output read (gate | up, plus the fused delta) and
+    F.silu(gate) * up in one launch (an addition): [B, T, inter]."""
+    bx, tx, _ = _shape(slot_id)
+    i = int(inter)
+    act = torch.empty(bx, tx, i, dtype=torch.bfloat16, device=input_template.device)
+    _lib.check(_L().swl_w_read_output_silu(int(slot_id), act.data_ptr(), bx * tx, i,
+                                           _bf16_operand(delta, (bx, tx, 2 * i), "delta"), _stream()))
+    return act
 
 
 def prepare_token_ids_slot(slot_id, token_ids):

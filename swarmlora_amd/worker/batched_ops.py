@@ -173,6 +173,74 @@ class BatchedAggregatorOps:
         with self.timer.stage("scatter"):
             return ub.read_outputs_slot(slot_id, dims, tmpl, delta, residual)
 
+    def _one_bf16_slot(self, slots):
+        """The (slot, state) of a single-slot worker whose rows are bf16, or
+        None (the fused reads below serve that case)."""
+        if len(slots) != 1:
+            return None
+        sid, state = next(iter(slots.items()))
+        if state.hidden is None or state.hidden.dtype != torch.bfloat16:
+            return None
+        return sid, state
+
+    @staticmethod
+    def _fits(t, d):
+        return t is None or (t.dtype == torch.bfloat16 and t.is_contiguous() and t.dim() == 3 and t.shape[-1] == d
+                             and t.data_ptr() % 16 == 0)
+
+    def o_proj_get_norm_all(self, slots, layer_idx: int, deltas, out_dim: int, weight, eps: float) -> bool:
+        """o_proj_get_all and the post-attention norm the caller runs next, in
+        one launch (an addition): state.mlp_residual = residual + (o + delta),
+        state.hidden = its RMSNorm; False (nothing done) when the operands do
+        not fit, then the caller takes the separate steps."""
+        one = self._one_bf16_slot(slots)
+        if one is None or out_dim % 8:
+            return False
+        sid, state = one
+        d = deltas.get(sid)
+        if not (self._fits(d, out_dim) and self._fits(state.residual, out_dim)):
+            return False
+        with self.timer.stage("scatter"):
+            state.mlp_residual, state.hidden = ub.read_outputs_norm_slot(sid, out_dim, state.hidden, d,
+                                                                         state.residual, weight, eps)
+        return True
+
+    def down_proj_get_norm_all(self, slots, layer_idx: int, deltas, out_dim: int, weight, eps: float) -> bool:
+        """down_proj_get_all and the next norm (the next layer's input norm or
+        the final norm) in one launch (an addition): state.residual =
+        mlp_residual + (down + delta), state.hidden = its RMSNorm."""
+        one = self._one_bf16_slot(slots)
+        if one is None or out_dim % 8:
+            return False
+        sid, state = one
+        d = deltas.get(sid)
+        if not (self._fits(d, out_dim) and self._fits(state.mlp_residual, out_dim)):
+            return False
+        with self.timer.stage("scatter"):
+            state.residual, state.hidden = ub.read_outputs_norm_slot(sid, out_dim, state.hidden, d,
+                                                                     state.mlp_residual, weight, eps)
+        return True
+
+    def gate_up_get_act_all(self, slots, layer_idx: int, deltas, dims: List[int]):
+        """gate_up_get_all and the SiLU*up the caller runs next, in one launch
+        (an addition): {slot: act [B, T, inter]}, or None when the operands
+        do not fit (then the caller takes the separate steps)."""
+        one = self._one_bf16_slot(slots)
+        if one is None or len(dims) != 2 or dims[0] != dims[1] or dims[0] % 8:
+            return None
+        sid, state = one
+        d = list(deltas.get(sid, (None, None)))
+        if all(x is None for x in d):
+            jd = None
+        elif any(x is None for x in d):
+            return None
+        else:
+            jd = _joined(d)
+            if jd is None or not self._fits(jd, 2 * dims[0]):
+                return None
+        with self.timer.stage("scatter"):
+            return {sid: ub.read_outputs_silu_slot(sid, dims[0], state.hidden, jd)}
+
     def _fused_join(self, slots, deltas, dims, n):
         """qkv / gate_up read: the fused output plus its fused delta in one
         launch when the per-block deltas are pieces of one buffer."""

@@ -176,11 +176,17 @@ class WorkerEngine:
         o_mods = [l.o_proj for l in self.layers]
         gu_mods = [l.fused_gate_up for l in self.layers]
         dn_mods = [l.down_proj for l in self.layers]
+        # The O and Down outputs are read together with the norm that follows
+        # each (and the Gate+Up output with SiLU*up) where the operands allow,
+        # one launch instead of three; `normed` says the Down read already
+        # produced the next layer's normalised input (or the final norm).
+        normed = False
         for li, layer in enumerate(self.layers):
             with tm.stage("attn"):
-                for st in slots.values():
-                    st.residual = st.hidden
-                    st.hidden = rms_norm(st.hidden, layer.input_norm, self.eps)
+                if not normed:
+                    for st in slots.values():
+                        st.residual = st.hidden
+                        st.hidden = rms_norm(st.hidden, layer.input_norm, self.eps)
             epoch, deltas = ops.qkv_submit_all(slots, li, qkv_mods)
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)
@@ -194,26 +200,33 @@ class WorkerEngine:
             epoch, deltas = ops.o_proj_submit_all(slots, li, attn, o_mods)
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)
-            ops.o_proj_get_all(slots, li, deltas, self.hidden)
-            with tm.stage("attn"):
-                for st in slots.values():
-                    st.mlp_residual = st.hidden
-                    st.hidden = rms_norm(st.hidden, layer.post_norm, self.eps)
+            if not ops.o_proj_get_norm_all(slots, li, deltas, self.hidden, layer.post_norm, self.eps):
+                ops.o_proj_get_all(slots, li, deltas, self.hidden)
+                with tm.stage("attn"):
+                    for st in slots.values():
+                        st.mlp_residual = st.hidden
+                        st.hidden = rms_norm(st.hidden, layer.post_norm, self.eps)
             epoch, deltas = ops.gate_up_submit_all(slots, li, gu_mods)
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)
-            gu = ops.gate_up_get_all(slots, li, deltas, layer.fused_gate_up.dims)
-            with tm.stage("attn"):
-                mlp = {sid: silu_mul(g, u) for sid, (g, u) in gu.items()}
+            mlp = ops.gate_up_get_act_all(slots, li, deltas, layer.fused_gate_up.dims)
+            if mlp is None:
+                gu = ops.gate_up_get_all(slots, li, deltas, layer.fused_gate_up.dims)
+                with tm.stage("attn"):
+                    mlp = {sid: silu_mul(g, u) for sid, (g, u) in gu.items()}
             epoch, deltas = ops.down_proj_submit_all(slots, li, mlp, dn_mods)
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)
-            ops.down_proj_get_all(slots, li, deltas, self.hidden)
+            nxt = self.layers[li + 1].input_norm if li + 1 < len(self.layers) else self.final_norm
+            normed = ops.down_proj_get_norm_all(slots, li, deltas, self.hidden, nxt, self.eps)
+            if not normed:
+                ops.down_proj_get_all(slots, li, deltas, self.hidden)
         sids = list(slots)
         self.kv.advance_seq_lens_by(sids, [slots[s].input_ids.size(1) for s in sids])
         with tm.stage("attn"):
             for st in slots.values():
-                st.hidden = rms_norm(st.hidden, self.final_norm, self.eps)
+                if not normed:
+                    st.hidden = rms_norm(st.hidden, self.final_norm, self.eps)
                 if st.prefill_chunks:
                     st.hidden = st.hidden[:, -1:, :]
         if record is not None:

@@ -342,6 +342,35 @@ def _read_proc(claim, out):
             got = torch.cat(got, -1) if len(got) > 1 else got[0]
             torch.cuda.synchronize()
             results.append(bool(torch.equal(got.view(torch.int16), ref.view(torch.int16))))
+        from swarmlora_amd import ops
+        w = (torch.randn(H, generator=g, device=dev) * 0.5 + 1).to(torch.bfloat16)
+        same = lambda a, b: bool(torch.equal(a.view(torch.int16), b.view(torch.int16)))  # noqa: E731
+        # the read + the next RMSNorm, against the read, the adds and ops.rms_norm
+        for t, with_d in ((1, True), (3, False)):
+            x = torch.zeros(1, t, 64, dtype=torch.bfloat16, device=dev)
+            ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
+            d = torch.randn(1, t, H, generator=g, device=dev).to(torch.bfloat16) if with_d else None
+            r = torch.randn(1, t, H, generator=g, device=dev).to(torch.bfloat16)
+            ref = ub.get_outputs_slot(sid, [H], x)[0]
+            if d is not None:
+                ref = ref + d
+            ref = r + ref
+            ref_n = ops.rms_norm(ref, w, 1e-5)
+            h, n = ub.read_outputs_norm_slot(sid, H, x, d, r, w, 1e-5)
+            torch.cuda.synchronize()
+            results.append(same(h, ref) and same(n, ref_n))
+        # the Gate+Up read + SiLU*up, against the read, the add and ops.silu_mul
+        for t, with_d in ((1, True), (2, False)):
+            x = torch.zeros(1, t, 64, dtype=torch.bfloat16, device=dev)
+            ub.prepare_input_slot(sid, ub.OP_GATE_UP_FUSED, x)
+            d = torch.randn(1, t, 2 * I, generator=g, device=dev).to(torch.bfloat16) if with_d else None
+            ref = ub.get_outputs_slot(sid, [2 * I], x)[0]
+            if d is not None:
+                ref = ref + d
+            ref_a = ops.silu_mul(ref, I)
+            a = ub.read_outputs_silu_slot(sid, I, x, d)
+            torch.cuda.synchronize()
+            results.append(same(a, ref_a))
         ub.close_slot(sid)
         out.put((results, None))
     except Exception:
@@ -355,8 +384,10 @@ def test_read_outputs_matches_copy_and_adds(pool):
     the *_get_all methods it replaces, for deltas and residuals present or
     not, 1-3 token rows, fused multi-block outputs, and an element count that
     is not a multiple of 8 with operands off 16-byte alignment (the scalar
-    path).  The slot output holds random bf16 values written by this
-    process (the aggregator side)."""
+    path); and the reads fused with the next RMSNorm and with SiLU*up are bit
+    for bit the read, the adds and ops.rms_norm / ops.silu_mul.  The slot
+    output holds random bf16 values written by this process (the aggregator
+    side)."""
     agg = _agg()
     claim = agg.claim_slot(6)
     _, sout = agg.slot_tensors(claim["slot_id"])
@@ -375,7 +406,7 @@ def test_read_outputs_matches_copy_and_adds(pool):
             p.kill()
         agg.release_slot(claim["slot_id"], 6)
     assert err is None, err
-    assert results == [True] * 6, results
+    assert results == [True] * 10, results
 
 
 def _timeout_proc(claim, out):
