@@ -213,17 +213,28 @@ int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream);
  * null.  Stream-ordered; in GPU-ordered mode 1 it first waits for the
  * output word as swl_w_copy_output does. */
 int swl_w_read_output(int slot_id, void* dst, int64_t n, const void* delta, const void* residual, void* stream);
-/* swl_w_read_output of rows x d elements followed by the worker's next
+/* swl_w_read_output of [bx, tx, d] followed by the worker's next
  * LlamaRMSNorm (worker_sync.py:1344-1350: the post-attention norm after the
  * O round, the next layer's input norm or the final norm after Down):
  * dst_h = residual + (out + delta), dst_norm = RMSNorm(dst_h) * weight, bit
- * for bit the separate read and norm.  d % 8 == 0, 16-byte aligned. */
-int swl_w_read_output_norm(int slot_id, void* dst_h, void* dst_norm, int64_t rows, int64_t d, const void* delta,
-                           const void* residual, const void* weight, float eps, void* stream);
+ * for bit the separate read and norm.  d % 8 == 0, 16-byte aligned.
+ * stage_input: the normalised rows are also written into the slot's input
+ * buffer as the next round's input (swl_w_submit_staged_input then stands
+ * in for that round's prepare_input_slot copy). */
+int swl_w_read_output_norm(int slot_id, void* dst_h, void* dst_norm, int64_t bx, int64_t tx, int64_t d,
+                           const void* delta, const void* residual, const void* weight, float eps, int stage_input,
+                           void* stream);
 /* The Gate+Up read (rows of gate | up, 2 inter wide, plus the fused delta)
  * followed by F.silu(gate) * up (worker_sync.py:158, :1397) into rows of
- * inter, bit for bit the separate read and SiLU*up. */
-int swl_w_read_output_silu(int slot_id, void* dst, int64_t rows, int64_t inter, const void* delta, void* stream);
+ * inter, bit for bit the separate read and SiLU*up; stage_input as above
+ * (the Down round's input). */
+int swl_w_read_output_silu(int slot_id, void* dst, int64_t bx, int64_t tx, int64_t inter, const void* delta,
+                           int stage_input, void* stream);
+/* prepare_input_slot (ext_unified_barrier.cpp:225-273) for rows a fused read
+ * already staged in the input buffer: checks the shape against the staged
+ * one, records it, and completes as prepare_input_slot does (host sync, or
+ * the input sequence word in GPU-ordered mode). */
+int swl_w_submit_staged_input(int slot_id, int64_t bx, int64_t tx, int64_t dx, void* stream);
 /* prepare_token_ids_slot (ext_unified_barrier.cpp:350-393): int64 ids. */
 int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx, void* stream);
 /* prepare_hidden_for_lm_head_slot (ext_unified_barrier.cpp:443-486). */

@@ -4389,6 +4389,7 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(CombineArgs a) {
 struct CombineNormArgs {
   bf16* dst_h;
   bf16* dst_n;
+  bf16* dst_n2;       // a second copy of the normalised rows, or null
   const bf16* src;
   const bf16* delta;  // or null
   const bf16* res;    // or null
@@ -4431,6 +4432,7 @@ __global__ __launch_bounds__(256) void combine_norm_rows_kernel(CombineNormArgs 
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(f2bf(x[j] * rs)) * g[j]);
     *reinterpret_cast<u32x4*>(a.dst_n + off + 8 * i) = __builtin_bit_cast(u32x4, o);
+    if (a.dst_n2) *reinterpret_cast<u32x4*>(a.dst_n2 + off + 8 * i) = __builtin_bit_cast(u32x4, o);
   }
 }
 
@@ -4440,6 +4442,7 @@ __global__ __launch_bounds__(256) void combine_norm_rows_kernel(CombineNormArgs 
 // out.  inter a multiple of 8, pointers 16-byte aligned.
 struct CombineSiluArgs {
   bf16* dst;
+  bf16* dst2;         // a second copy, or null
   const bf16* src;
   const bf16* delta;  // [rows][2 inter] or null
   int64_t inter;
@@ -4470,6 +4473,7 @@ __global__ __launch_bounds__(256) void combine_silu_rows_kernel(CombineSiluArgs 
     o[j] = f2bf(sg * u[j]);
   }
   *reinterpret_cast<u32x4*>(a.dst + (int64_t)t * a.inter + 8 * i) = __builtin_bit_cast(u32x4, o);
+  if (a.dst2) *reinterpret_cast<u32x4*>(a.dst2 + (int64_t)t * a.inter + 8 * i) = __builtin_bit_cast(u32x4, o);
 }
 
 struct WaitCopyArgs {
@@ -4556,17 +4560,18 @@ int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta
   return SWL_OK;
 }
 
-int combine_norm_rows_launch(void* dst_h, void* dst_n, const void* src, int64_t rows, int64_t d, const void* delta,
-                             const void* res, const void* w, float eps, hipStream_t stream) {
+int combine_norm_rows_launch(void* dst_h, void* dst_n, void* dst_n2, const void* src, int64_t rows, int64_t d,
+                             const void* delta, const void* res, const void* w, float eps, hipStream_t stream) {
   auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
   SWL_CHECK(dst_h && dst_n && src && w && rows >= 0 && d > 0 && d % 8 == 0, SWL_ERR_INVALID,
             "combine_norm_rows: bad arguments (d must be a multiple of 8)");
-  SWL_CHECK(al(dst_h) && al(dst_n) && al(src) && al(delta) && al(res) && al(w), SWL_ERR_INVALID,
+  SWL_CHECK(al(dst_h) && al(dst_n) && al(dst_n2) && al(src) && al(delta) && al(res) && al(w), SWL_ERR_INVALID,
             "combine_norm_rows: pointers must be 16-byte aligned");
   if (rows == 0) return SWL_OK;
   CombineNormArgs a{};
   a.dst_h = reinterpret_cast<bf16*>(dst_h);
   a.dst_n = reinterpret_cast<bf16*>(dst_n);
+  a.dst_n2 = reinterpret_cast<bf16*>(dst_n2);
   a.src = reinterpret_cast<const bf16*>(src);
   a.delta = reinterpret_cast<const bf16*>(delta);
   a.res = reinterpret_cast<const bf16*>(res);
@@ -4578,16 +4583,18 @@ int combine_norm_rows_launch(void* dst_h, void* dst_n, const void* src, int64_t 
   return SWL_OK;
 }
 
-int combine_silu_rows_launch(void* dst, const void* src, int64_t rows, int64_t inter, const void* delta,
+int combine_silu_rows_launch(void* dst, void* dst2, const void* src, int64_t rows, int64_t inter, const void* delta,
                              hipStream_t stream) {
   auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
   SWL_CHECK(dst && src && rows >= 0 && inter > 0 && inter % 8 == 0, SWL_ERR_INVALID,
             "combine_silu_rows: bad arguments (inter must be a multiple of 8)");
   SWL_CHECK(rows <= 65535, SWL_ERR_INVALID, "combine_silu_rows: at most 65535 rows");
-  SWL_CHECK(al(dst) && al(src) && al(delta), SWL_ERR_INVALID, "combine_silu_rows: pointers must be 16-byte aligned");
+  SWL_CHECK(al(dst) && al(dst2) && al(src) && al(delta), SWL_ERR_INVALID,
+            "combine_silu_rows: pointers must be 16-byte aligned");
   if (rows == 0) return SWL_OK;
   CombineSiluArgs a{};
   a.dst = reinterpret_cast<bf16*>(dst);
+  a.dst2 = reinterpret_cast<bf16*>(dst2);
   a.src = reinterpret_cast<const bf16*>(src);
   a.delta = reinterpret_cast<const bf16*>(delta);
   a.inter = inter;

@@ -61,13 +61,15 @@ int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta
                         hipStream_t stream);
 
 // The same read followed by LlamaRMSNorm of every row (rows x d): dst_h =
-// h, dst_n = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w), bit for bit the
-// separate read and rmsnorm_rows_kernel.  d % 8 == 0, 16-byte aligned.
-int combine_norm_rows_launch(void* dst_h, void* dst_n, const void* src, int64_t rows, int64_t d, const void* delta,
-                             const void* res, const void* w, float eps, hipStream_t stream);
+// h, dst_n (and dst_n2 when not null) = bf16(bf16(h * rsqrt(mean(h^2) +
+// eps)) * w), bit for bit the separate read and rmsnorm_rows_kernel.
+// d % 8 == 0, 16-byte aligned.
+int combine_norm_rows_launch(void* dst_h, void* dst_n, void* dst_n2, const void* src, int64_t rows, int64_t d,
+                             const void* delta, const void* res, const void* w, float eps, hipStream_t stream);
 // A Gate+Up read (rows of 2 inter, optional delta) followed by SiLU*up into
-// rows of inter, bit for bit the separate read and silu_mul_rows_kernel.
-int combine_silu_rows_launch(void* dst, const void* src, int64_t rows, int64_t inter, const void* delta,
+// rows of inter (dst, and dst2 when not null), bit for bit the separate read
+// and silu_mul_rows_kernel.
+int combine_silu_rows_launch(void* dst, void* dst2, const void* src, int64_t rows, int64_t inter, const void* delta,
                              hipStream_t stream);
 
 int wait_copy_launch(const uint64_t* flag, uint64_t want, int32_t tag, uint32_t* timed_out, uint32_t limit_us,

@@ -24,6 +24,11 @@ struct SlotCtx {
   size_t in_size = 0, out_size = 0;
   int64_t bx = 0, tx = 0, dx = 0;
   uint64_t seq = 0;  // GPU-ordered mode: input sequence value of the last prepare_*
+  // the next round's input already written into the input buffer by a fused
+  // output read (swl_w_read_output_norm / _silu with stage_input), shape
+  // [sbx, stx, sdx], waiting for swl_w_submit_staged_input
+  bool staged = false;
+  int64_t sbx = 0, stx = 0, sdx = 0;
 };
 
 // Limit of this worker's stream wait for a round's outputs (the aggregator's
@@ -225,6 +230,7 @@ int swl_w_prepare_input(int slot_id, const void* src, int64_t bx, int64_t tx, in
   int rc = need_data_slot("prepare_input_slot", slot_id, &c);
   if (rc) return rc;
   SWL_CHECK(src && bx > 0 && tx > 0 && dx > 0 && elem_size > 0, SWL_ERR_INVALID, "Input must be 3D [B, T, D]");
+  c->staged = false;
   rc = copy_in("prepare_input_slot", c, src, (size_t)bx * tx * dx * elem_size, (hipStream_t)stream);
   if (rc) return rc;
   c->bx = bx;
@@ -288,31 +294,83 @@ int swl_w_read_output(int slot_id, void* dst, int64_t n, const void* delta, cons
   return SWL_OK;
 }
 
-int swl_w_read_output_norm(int slot_id, void* dst_h, void* dst_norm, int64_t rows, int64_t d, const void* delta,
-                           const void* residual, const void* weight, float eps, void* stream) {
-  SlotCtx* c;
-  int rc = need_data_slot("get_outputs_slot", slot_id, &c);
-  if (rc) return rc;
-  SWL_CHECK(rows >= 0 && d > 0 && (size_t)(rows * d) * sizeof(uint16_t) <= c->out_size, SWL_ERR_INVALID,
-            "get_outputs_slot: output rows exceed the slot output buffer");
-  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
-  if (rc) return rc;
-  rc = swl::combine_norm_rows_launch(dst_h, dst_norm, c->out, rows, d, delta, residual, weight, eps,
-                                     (hipStream_t)stream);
-  if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+// Checks and records a fused read's staging of the next round's input
+// ([bx, tx, d] bf16 rows into the slot's input buffer); null when not asked.
+int stage_target(const char* fn, SlotCtx* c, int stage_input, int64_t bx, int64_t tx, int64_t d, void** dst) {
+  *dst = nullptr;
+  if (!stage_input) return SWL_OK;
+  SWL_CHECK((size_t)(bx * tx * d) * sizeof(uint16_t) <= c->in_size, SWL_ERR_INVALID,
+            std::string(fn) + ": staged input exceeds the slot input buffer");
+  *dst = c->in;
+  c->staged = true;
+  c->sbx = bx;
+  c->stx = tx;
+  c->sdx = d;
   return SWL_OK;
 }
 
-int swl_w_read_output_silu(int slot_id, void* dst, int64_t rows, int64_t inter, const void* delta, void* stream) {
+int swl_w_read_output_norm(int slot_id, void* dst_h, void* dst_norm, int64_t bx, int64_t tx, int64_t d,
+                           const void* delta, const void* residual, const void* weight, float eps, int stage_input,
+                           void* stream) {
   SlotCtx* c;
   int rc = need_data_slot("get_outputs_slot", slot_id, &c);
   if (rc) return rc;
-  SWL_CHECK(rows >= 0 && inter > 0 && (size_t)(rows * 2 * inter) * sizeof(uint16_t) <= c->out_size, SWL_ERR_INVALID,
+  SWL_CHECK(bx > 0 && tx > 0 && d > 0 && (size_t)(bx * tx * d) * sizeof(uint16_t) <= c->out_size, SWL_ERR_INVALID,
             "get_outputs_slot: output rows exceed the slot output buffer");
+  void* staged = nullptr;
+  rc = stage_target("get_outputs_slot", c, stage_input, bx, tx, d, &staged);
+  if (rc) return rc;
   rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
   if (rc) return rc;
-  rc = swl::combine_silu_rows_launch(dst, c->out, rows, inter, delta, (hipStream_t)stream);
-  if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+  rc = swl::combine_norm_rows_launch(dst_h, dst_norm, staged, c->out, bx * tx, d, delta, residual, weight, eps,
+                                     (hipStream_t)stream);
+  if (rc) {
+    c->staged = false;
+    return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+  }
+  return SWL_OK;
+}
+
+int swl_w_read_output_silu(int slot_id, void* dst, int64_t bx, int64_t tx, int64_t inter, const void* delta,
+                           int stage_input, void* stream) {
+  SlotCtx* c;
+  int rc = need_data_slot("get_outputs_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(bx > 0 && tx > 0 && inter > 0 && (size_t)(bx * tx * 2 * inter) * sizeof(uint16_t) <= c->out_size,
+            SWL_ERR_INVALID, "get_outputs_slot: output rows exceed the slot output buffer");
+  void* staged = nullptr;
+  rc = stage_target("get_outputs_slot", c, stage_input, bx, tx, inter, &staged);
+  if (rc) return rc;
+  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
+  if (rc) return rc;
+  rc = swl::combine_silu_rows_launch(dst, staged, c->out, bx * tx, inter, delta, (hipStream_t)stream);
+  if (rc) {
+    c->staged = false;
+    return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
+  }
+  return SWL_OK;
+}
+
+int swl_w_submit_staged_input(int slot_id, int64_t bx, int64_t tx, int64_t dx, void* stream) {
+  SlotCtx* c;
+  int rc = need_data_slot("prepare_input_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(c->staged, SWL_ERR_STATE, "prepare_input_slot: no staged input on slot " + std::to_string(slot_id));
+  SWL_CHECK(bx == c->sbx && tx == c->stx && dx == c->sdx, SWL_ERR_INVALID,
+            "prepare_input_slot: input shape differs from the staged rows");
+  c->staged = false;
+  c->bx = bx;
+  c->tx = tx;
+  c->dx = dx;
+  hipStream_t st = (hipStream_t)stream;
+  if (g_w.gpu_ordered) {
+    // the value the aggregator's stream waits for, after the staging read
+    ++c->seq;
+    uint64_t* flag = seq_word(c, swl::kInSeqOffset);
+    return swl::seq_write_launch(1, &flag, &c->seq, st);
+  }
+  // as copy_in: the rows must be complete before this worker signals ready
+  SWL_HIP(hipStreamSynchronize(st));
   return SWL_OK;
 }
 

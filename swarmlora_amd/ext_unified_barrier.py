@@ -37,8 +37,10 @@ _lib.register_signatures({
     "swl_w_slot_sizes": (c_int, [c_int, _P_size, _P_size]),
     "swl_w_copy_output": (c_int, [c_int, c_vp, ctypes.c_size_t, c_vp]),
     "swl_w_read_output": (c_int, [c_int, c_vp, c_i64, c_vp, c_vp, c_vp]),
-    "swl_w_read_output_norm": (c_int, [c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, ctypes.c_float, c_vp]),
-    "swl_w_read_output_silu": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "swl_w_read_output_norm": (c_int, [c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, ctypes.c_float,
+                                       c_int, c_vp]),
+    "swl_w_read_output_silu": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp]),
+    "swl_w_submit_staged_input": (c_int, [c_int, c_i64, c_i64, c_i64, c_vp]),
     "swl_w_prepare_token_ids": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp]),
     "swl_w_prepare_hidden_lm": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, ctypes.c_size_t, c_vp]),
     "swl_w_get_next_token": (c_int, [c_int, _P_i64, c_vp]),
@@ -141,11 +143,12 @@ def _bf16_operand(t, shape, name):
     return t.data_ptr()
 
 
-def read_outputs_norm_slot(slot_id, out_dim, input_template, delta, residual, weight, eps):
+def read_outputs_norm_slot(slot_id, out_dim, input_template, delta, residual, weight, eps, stage=False):
     """An O or Down round's output read with the worker's adds and the next
     LlamaRMSNorm in one launch (an addition): returns (h, norm(h) * weight),
     h = residual + (output + delta), [B, T, out_dim] each; out_dim a
-    multiple of 8."""
+    multiple of 8.  stage: norm(h) is also written into the slot's input
+    buffer as the next round's input (submit_staged_input_slot)."""
     bx, tx, _ = _shape(slot_id)
     d = int(out_dim)
     shape = (bx, tx, d)
@@ -153,22 +156,32 @@ def read_outputs_norm_slot(slot_id, out_dim, input_template, delta, residual, we
     n = torch.empty_like(h)
     if weight.dtype != torch.bfloat16 or weight.numel() != d or not weight.is_contiguous() or weight.data_ptr() % 16:
         raise RuntimeError("read_outputs_norm_slot: weight must be a contiguous, aligned bf16 [out_dim] tensor")
-    _lib.check(_L().swl_w_read_output_norm(int(slot_id), h.data_ptr(), n.data_ptr(), bx * tx, d,
+    _lib.check(_L().swl_w_read_output_norm(int(slot_id), h.data_ptr(), n.data_ptr(), bx, tx, d,
                                            _bf16_operand(delta, shape, "delta"),
                                            _bf16_operand(residual, shape, "residual"), weight.data_ptr(),
-                                           float(eps), _stream()))
+                                           float(eps), 1 if stage else 0, _stream()))
     return h, n
 
 
-def read_outputs_silu_slot(slot_id, inter, input_template, delta=None):
+def read_outputs_silu_slot(slot_id, inter, input_template, delta=None, stage=False):
     """A Gate+Up round's output read (gate | up, plus the fused delta) and
-    F.silu(gate) * up in one launch (an addition): [B, T, inter]."""
+    F.silu(gate) * up in one launch (an addition): [B, T, inter]; stage as
+    read_outputs_norm_slot."""
     bx, tx, _ = _shape(slot_id)
     i = int(inter)
     act = torch.empty(bx, tx, i, dtype=torch.bfloat16, device=input_template.device)
-    _lib.check(_L().swl_w_read_output_silu(int(slot_id), act.data_ptr(), bx * tx, i,
-                                           _bf16_operand(delta, (bx, tx, 2 * i), "delta"), _stream()))
+    _lib.check(_L().swl_w_read_output_silu(int(slot_id), act.data_ptr(), bx, tx, i,
+                                           _bf16_operand(delta, (bx, tx, 2 * i), "delta"), 1 if stage else 0,
+                                           _stream()))
     return act
+
+
+def submit_staged_input_slot(slot_id, input):
+    """prepare_input_slot for an input a fused read already staged in the
+    slot's input buffer (an addition): `input` is that read's result; its
+    shape is checked against the staged rows, nothing is copied."""
+    b, t, d = input.shape
+    _lib.check(_L().swl_w_submit_staged_input(int(slot_id), b, t, d, _stream()))
 
 
 def prepare_token_ids_slot(slot_id, token_ids):

@@ -142,6 +142,9 @@ class BatchedAggregatorOps:
         self._out_host = gpu_ordered == "inputs"
         if gpu_ordered:
             ub.set_gpu_ordered(True, wait_outputs=not self._out_host)
+        # slots whose input buffer already holds the next round's input (a
+        # fused read staged it there): their next submit copies nothing
+        self._staged = set()
         self.dtype_code = dtype_code
         self.dtype = torch.bfloat16 if dtype_code == 15 else torch.float16
         self.hidden_dim = slot_manager.base_client.hidden_dim
@@ -188,7 +191,8 @@ class BatchedAggregatorOps:
         return t is None or (t.dtype == torch.bfloat16 and t.is_contiguous() and t.dim() == 3 and t.shape[-1] == d
                              and t.data_ptr() % 16 == 0)
 
-    def o_proj_get_norm_all(self, slots, layer_idx: int, deltas, out_dim: int, weight, eps: float) -> bool:
+    def o_proj_get_norm_all(self, slots, layer_idx: int, deltas, out_dim: int, weight, eps: float,
+                            stage: bool = False) -> bool:
         """o_proj_get_all and the post-attention norm the caller runs next, in
         one launch (an addition): state.mlp_residual = residual + (o + delta),
         state.hidden = its RMSNorm; False (nothing done) when the operands do
@@ -202,10 +206,13 @@ class BatchedAggregatorOps:
             return False
         with self.timer.stage("scatter"):
             state.mlp_residual, state.hidden = ub.read_outputs_norm_slot(sid, out_dim, state.hidden, d,
-                                                                         state.residual, weight, eps)
+                                                                         state.residual, weight, eps, stage)
+        if stage:
+            self._staged.add(sid)
         return True
 
-    def down_proj_get_norm_all(self, slots, layer_idx: int, deltas, out_dim: int, weight, eps: float) -> bool:
+    def down_proj_get_norm_all(self, slots, layer_idx: int, deltas, out_dim: int, weight, eps: float,
+                               stage: bool = False) -> bool:
         """down_proj_get_all and the next norm (the next layer's input norm or
         the final norm) in one launch (an addition): state.residual =
         mlp_residual + (down + delta), state.hidden = its RMSNorm."""
@@ -218,10 +225,12 @@ class BatchedAggregatorOps:
             return False
         with self.timer.stage("scatter"):
             state.residual, state.hidden = ub.read_outputs_norm_slot(sid, out_dim, state.hidden, d,
-                                                                     state.mlp_residual, weight, eps)
+                                                                     state.mlp_residual, weight, eps, stage)
+        if stage:
+            self._staged.add(sid)
         return True
 
-    def gate_up_get_act_all(self, slots, layer_idx: int, deltas, dims: List[int]):
+    def gate_up_get_act_all(self, slots, layer_idx: int, deltas, dims: List[int], stage: bool = False):
         """gate_up_get_all and the SiLU*up the caller runs next, in one launch
         (an addition): {slot: act [B, T, inter]}, or None when the operands
         do not fit (then the caller takes the separate steps)."""
@@ -239,7 +248,10 @@ class BatchedAggregatorOps:
             if jd is None or not self._fits(jd, 2 * dims[0]):
                 return None
         with self.timer.stage("scatter"):
-            return {sid: ub.read_outputs_silu_slot(sid, dims[0], state.hidden, jd)}
+            act = ub.read_outputs_silu_slot(sid, dims[0], state.hidden, jd, stage)
+        if stage:
+            self._staged.add(sid)
+        return {sid: act}
 
     def _fused_join(self, slots, deltas, dims, n):
         """qkv / gate_up read: the fused output plus its fused delta in one
@@ -263,13 +275,18 @@ class BatchedAggregatorOps:
     def _submit(self, op, layer_idx, slot_id, x):
         b, t, d = x.shape
         with self.timer.stage("gather"):
-            ub.prepare_input_slot(slot_id, op, x)
+            if slot_id in self._staged:
+                self._staged.discard(slot_id)
+                ub.submit_staged_input_slot(slot_id, x)
+            else:
+                ub.prepare_input_slot(slot_id, op, x)
             extq.submit_slot_command(op, layer_idx, slot_id, self.worker_id, b, t, d, self._x_key, 0, 0, 0, 0,
                                      in_seq=self._seq(slot_id), out_host=self._out_host)
             extq.slot_signal_ready(slot_id)
 
     # ---------------------------------------------------------------- embed
     def embed_submit_all(self, slots) -> int:
+        self._staged.clear()  # nothing staged crosses a token boundary
         epoch = extq.get_barrier_done_epoch()
         slot_id, state = next(iter(slots.items()))
         ub.prepare_token_ids_slot(slot_id, state.input_ids)

@@ -200,7 +200,10 @@ class WorkerEngine:
             epoch, deltas = ops.o_proj_submit_all(slots, li, attn, o_mods)
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)
-            if not ops.o_proj_get_norm_all(slots, li, deltas, self.hidden, layer.post_norm, self.eps):
+            # stage=True: the fused read also writes the next round's input
+            # into the slot's input buffer, so that round's submit copies
+            # nothing
+            if not ops.o_proj_get_norm_all(slots, li, deltas, self.hidden, layer.post_norm, self.eps, stage=True):
                 ops.o_proj_get_all(slots, li, deltas, self.hidden)
                 with tm.stage("attn"):
                     for st in slots.values():
@@ -209,7 +212,7 @@ class WorkerEngine:
             epoch, deltas = ops.gate_up_submit_all(slots, li, gu_mods)
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)
-            mlp = ops.gate_up_get_act_all(slots, li, deltas, layer.fused_gate_up.dims)
+            mlp = ops.gate_up_get_act_all(slots, li, deltas, layer.fused_gate_up.dims, stage=True)
             if mlp is None:
                 gu = ops.gate_up_get_all(slots, li, deltas, layer.fused_gate_up.dims)
                 with tm.stage("attn"):
@@ -218,7 +221,8 @@ class WorkerEngine:
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)
             nxt = self.layers[li + 1].input_norm if li + 1 < len(self.layers) else self.final_norm
-            normed = ops.down_proj_get_norm_all(slots, li, deltas, self.hidden, nxt, self.eps)
+            normed = ops.down_proj_get_norm_all(slots, li, deltas, self.hidden, nxt, self.eps,
+                                                stage=li + 1 < len(self.layers))
             if not normed:
                 ops.down_proj_get_all(slots, li, deltas, self.hidden)
         sids = list(slots)

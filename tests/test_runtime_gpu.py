@@ -371,8 +371,21 @@ def _read_proc(claim, out):
             a = ub.read_outputs_silu_slot(sid, I, x, d)
             torch.cuda.synchronize()
             results.append(same(a, ref_a))
+        # staging: the normalised rows also land in the slot's input buffer,
+        # and the staged submit checks the shape (the parent reads the buffer)
+        x = torch.zeros(1, 2, 64, dtype=torch.bfloat16, device=dev)
+        ub.prepare_input_slot(sid, ub.OP_O_PROJ, x)
+        r = torch.randn(1, 2, H, generator=g, device=dev).to(torch.bfloat16)
+        h, n = ub.read_outputs_norm_slot(sid, H, x, None, r, w, 1e-5, stage=True)
+        try:
+            ub.submit_staged_input_slot(sid, torch.empty(1, 2, H + 8, dtype=torch.bfloat16, device=dev))
+            results.append(False)
+        except RuntimeError as e:
+            results.append("differs from the staged rows" in str(e))
+        ub.submit_staged_input_slot(sid, n)
+        staged_rows = n.reshape(-1).view(torch.int16).cpu().numpy().tobytes()  # plain bytes through the queue
         ub.close_slot(sid)
-        out.put((results, None))
+        out.put(((results, staged_rows), None))
     except Exception:
         import traceback
         out.put((None, traceback.format_exc()))
@@ -385,7 +398,9 @@ def test_read_outputs_matches_copy_and_adds(pool):
     not, 1-3 token rows, fused multi-block outputs, and an element count that
     is not a multiple of 8 with operands off 16-byte alignment (the scalar
     path); and the reads fused with the next RMSNorm and with SiLU*up are bit
-    for bit the read, the adds and ops.rms_norm / ops.silu_mul.  The slot
+    for bit the read, the adds and ops.rms_norm / ops.silu_mul.  A staged
+    read leaves the normalised rows in the slot's input buffer, and the
+    staged submit refuses a shape other than the staged one.  The slot
     output holds random bf16 values written by this process (the aggregator
     side)."""
     agg = _agg()
@@ -399,14 +414,19 @@ def test_read_outputs_matches_copy_and_adds(pool):
     p = ctx.Process(target=_read_proc, args=(claim, out))
     try:
         p.start()
-        results, err = out.get(timeout=180)
+        got, err = out.get(timeout=180)
+        assert err is None, err
+        results, staged_bytes = got
+        staged_rows = torch.frombuffer(bytearray(staged_bytes), dtype=torch.int16)
+        sin, _ = agg.slot_tensors(claim["slot_id"])
+        torch.cuda.synchronize()
+        results.append(bool(torch.equal(sin[:staged_rows.numel()].view(torch.int16).cpu(), staged_rows)))
     finally:
         p.join(timeout=30)
         if p.is_alive():
             p.kill()
         agg.release_slot(claim["slot_id"], 6)
-    assert err is None, err
-    assert results == [True] * 10, results
+    assert results == [True] * 12, results
 
 
 def _timeout_proc(claim, out):
