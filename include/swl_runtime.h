@@ -235,6 +235,12 @@ int swl_w_read_output_silu(int slot_id, void* dst, int64_t bx, int64_t tx, int64
  * one, records it, and completes as prepare_input_slot does (host sync, or
  * the input sequence word in GPU-ordered mode). */
 int swl_w_submit_staged_input(int slot_id, int64_t bx, int64_t tx, int64_t dx, void* stream);
+/* The slot's input buffer for the caller to write the next round's
+ * [bx, tx, dx] bf16 rows into directly (the worker's attention output, the
+ * O round's input), recorded as staged: swl_w_submit_staged_input then
+ * completes that round's prepare_input_slot without a copy.  The caller's
+ * writes must be on the stream it later passes to the submit. */
+int swl_w_stage_input(int slot_id, int64_t bx, int64_t tx, int64_t dx, void** input_buffer);
 /* prepare_token_ids_slot (ext_unified_barrier.cpp:350-393): int64 ids. */
 int swl_w_prepare_token_ids(int slot_id, const void* src, int64_t bx, int64_t tx, void* stream);
 /* prepare_hidden_for_lm_head_slot (ext_unified_barrier.cpp:443-486). */

@@ -127,6 +127,21 @@ int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream
   return SWL_OK;
 }
 
+// Checks and records a fused read's staging of the next round's input
+// ([bx, tx, d] bf16 rows into the slot's input buffer); null when not asked.
+int stage_target(const char* fn, SlotCtx* c, int stage_input, int64_t bx, int64_t tx, int64_t d, void** dst) {
+  *dst = nullptr;
+  if (!stage_input) return SWL_OK;
+  SWL_CHECK((size_t)(bx * tx * d) * sizeof(uint16_t) <= c->in_size, SWL_ERR_INVALID,
+            std::string(fn) + ": staged input exceeds the slot input buffer");
+  *dst = c->in;
+  c->staged = true;
+  c->sbx = bx;
+  c->stx = tx;
+  c->sdx = d;
+  return SWL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -258,6 +273,18 @@ int swl_w_slot_sizes(int slot_id, size_t* input_buffer_size, size_t* output_buff
   return SWL_OK;
 }
 
+int swl_w_stage_input(int slot_id, int64_t bx, int64_t tx, int64_t dx, void** input_buffer) {
+  SlotCtx* c;
+  int rc = need_data_slot("prepare_input_slot", slot_id, &c);
+  if (rc) return rc;
+  SWL_CHECK(input_buffer != nullptr && bx > 0 && tx > 0 && dx > 0, SWL_ERR_INVALID, "stage_input: bad arguments");
+  void* dst = nullptr;
+  rc = stage_target("prepare_input_slot", c, 1, bx, tx, dx, &dst);
+  if (rc) return rc;
+  *input_buffer = dst;
+  return SWL_OK;
+}
+
 int swl_w_copy_output(int slot_id, void* dst, size_t bytes, void* stream) {
   SlotCtx* c;
   int rc = need_data_slot("get_outputs_slot", slot_id, &c);
@@ -291,21 +318,6 @@ int swl_w_read_output(int slot_id, void* dst, int64_t n, const void* delta, cons
   if (rc) return rc;
   rc = swl::combine_rows_launch(dst, c->out, n, delta, residual, (hipStream_t)stream);
   if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
-  return SWL_OK;
-}
-
-// Checks and records a fused read's staging of the next round's input
-// ([bx, tx, d] bf16 rows into the slot's input buffer); null when not asked.
-int stage_target(const char* fn, SlotCtx* c, int stage_input, int64_t bx, int64_t tx, int64_t d, void** dst) {
-  *dst = nullptr;
-  if (!stage_input) return SWL_OK;
-  SWL_CHECK((size_t)(bx * tx * d) * sizeof(uint16_t) <= c->in_size, SWL_ERR_INVALID,
-            std::string(fn) + ": staged input exceeds the slot input buffer");
-  *dst = c->in;
-  c->staged = true;
-  c->sbx = bx;
-  c->stx = tx;
-  c->sdx = d;
   return SWL_OK;
 }
 

@@ -41,6 +41,7 @@ _lib.register_signatures({
                                        c_int, c_vp]),
     "swl_w_read_output_silu": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, c_vp, c_int, c_vp]),
     "swl_w_submit_staged_input": (c_int, [c_int, c_i64, c_i64, c_i64, c_vp]),
+    "swl_w_stage_input": (c_int, [c_int, c_i64, c_i64, c_i64, ctypes.POINTER(c_vp)]),
     "swl_w_prepare_token_ids": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp]),
     "swl_w_prepare_hidden_lm": (c_int, [c_int, c_vp, c_i64, c_i64, c_i64, ctypes.c_size_t, c_vp]),
     "swl_w_get_next_token": (c_int, [c_int, _P_i64, c_vp]),
@@ -182,6 +183,26 @@ def submit_staged_input_slot(slot_id, input):
     shape is checked against the staged rows, nothing is copied."""
     b, t, d = input.shape
     _lib.check(_L().swl_w_submit_staged_input(int(slot_id), b, t, d, _stream()))
+
+
+class _DeviceArray:
+    """__cuda_array_interface__ view of the slot's mapped input buffer."""
+
+    def __init__(self, ptr, shape):
+        self.__cuda_array_interface__ = {"data": (ptr, False), "shape": tuple(shape), "typestr": "<i2",
+                                         "version": 3, "strides": None}
+
+
+def stage_input_view(slot_id, b, t, d):
+    """A bf16 [b, t, d] view of the slot's input buffer for a producer to
+    write the next round's input into directly (an addition); the next
+    submit then takes submit_staged_input_slot.  The view is valid until
+    the slot's next prepare_* or staged submit."""
+    ptr = c_vp()
+    _lib.check(_L().swl_w_stage_input(int(slot_id), int(b), int(t), int(d), ctypes.byref(ptr)))
+    raw = torch.as_tensor(_DeviceArray(ptr.value, (int(b), int(t), int(d))),
+                          device=torch.device("cuda", _state["device"]))
+    return raw.view(torch.bfloat16)
 
 
 def prepare_token_ids_slot(slot_id, token_ids):

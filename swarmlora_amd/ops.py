@@ -506,6 +506,10 @@ def paged_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_cache: 
         max_pos = cos_sin.shape[0]
     if out is None:
         out = torch.empty(nseq, L, hq * d, dtype=BF16, device=q.device)
+    else:
+        _need(out, "out")
+        if out.numel() != nseq * L * hq * d or not out.is_contiguous():
+            raise ValueError("out must be contiguous [nseq, L, hq * d]")
     _lib.check(_lib.load().swl_paged_attention_bf16(
         _ptr(q), _ptr(k), _ptr(v), qs, ks, vs, nseq, L, hq, hkv, d, _ptr(k_cache), _ptr(v_cache), nb, bs,
         _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens), _ptr(positions if rope else None),

@@ -103,10 +103,13 @@ class WorkerBatchedOps:
     @staticmethod
     def batch_flash_attention(slot_ids: list, qkv_results: dict, paged_kv, cos_sin_cache: torch.Tensor,
                               layer_idx: int, num_heads: int, num_kv_heads: int, head_dim: int,
-                              attn_meta: dict = None) -> Dict[int, torch.Tensor]:
+                              attn_meta: dict = None, out: Optional[Dict[int, torch.Tensor]] = None
+                              ) -> Dict[int, torch.Tensor]:
         """RoPE at attn_meta['positions'], append k/v at cache_seqlens, causal
         GQA attention over the pages; returns {slot: [1, q_len, hidden]}.
-        q/k/v may be views of the fused QKV output (read in place)."""
+        q/k/v may be views of the fused QKV output (read in place).  out (an
+        addition): {slot: [1, q_len, hidden] bf16} to write a lone slot's
+        result into (a staged slot input buffer)."""
         q_len = attn_meta["bufs_q"].shape[1]
         n = len(slot_ids)
 
@@ -117,9 +120,10 @@ class WorkerBatchedOps:
         q = gather(0, num_heads)
         k = gather(1, num_kv_heads)
         v = gather(2, num_kv_heads)
+        dst = out.get(slot_ids[0]) if out is not None and n == 1 else None
         out = ops.paged_attention(q, k, v, paged_kv.key_caches[layer_idx], paged_kv.value_caches[layer_idx],
                                   attn_meta["block_tables"], attn_meta["cache_seqlens"], attn_meta["positions"],
-                                  cos_sin_cache, 1.0 / (head_dim ** 0.5))
+                                  cos_sin_cache, 1.0 / (head_dim ** 0.5), out=dst)
         return {sid: out[i:i + 1] for i, sid in enumerate(slot_ids)}
 
 
@@ -252,6 +256,22 @@ class BatchedAggregatorOps:
         if stage:
             self._staged.add(sid)
         return {sid: act}
+
+    def stage_attn_outputs(self, slots, q_len: int, width: int):
+        """{slot: [1, q_len, width] view of the slot's input buffer} for the
+        attention to write the O round's input into (an addition), so that
+        round's submit copies nothing; None when the slot's rows are not
+        bf16 or do not fit the buffer."""
+        one = self._one_bf16_slot(slots)
+        if one is None or width % 8:
+            return None
+        sid, state = one
+        try:
+            view = ub.stage_input_view(sid, 1, q_len, width)
+        except RuntimeError:
+            return None
+        self._staged.add(sid)
+        return {sid: view}
 
     def _fused_join(self, slots, deltas, dims, n):
         """qkv / gate_up read: the fused output plus its fused delta in one

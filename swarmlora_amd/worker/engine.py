@@ -193,10 +193,14 @@ class WorkerEngine:
             qkv = ops.qkv_get_all(slots, li, deltas, layer.fused_qkv.dims)
             with tm.stage("attn"):
                 attn = {}
+                # a lone slot's attention writes straight into its input
+                # buffer: the O round's submit then copies nothing
+                staged = (ops.stage_attn_outputs(slots, next(iter(groups)), self.num_heads * self.head_dim)
+                          if len(groups) == 1 else None)
                 for q_len, sids in groups.items():
                     attn.update(WorkerBatchedOps.batch_flash_attention(sids, qkv, self.kv, self.cos_sin, li,
                                                                        self.num_heads, self.num_kv_heads,
-                                                                       self.head_dim, metas[q_len]))
+                                                                       self.head_dim, metas[q_len], out=staged))
             epoch, deltas = ops.o_proj_submit_all(slots, li, attn, o_mods)
             with tm.stage("gemm"):
                 ops.barrier_sync(epoch)

@@ -383,7 +383,20 @@ def _read_proc(claim, out):
         except RuntimeError as e:
             results.append("differs from the staged rows" in str(e))
         ub.submit_staged_input_slot(sid, n)
-        staged_rows = n.reshape(-1).view(torch.int16).cpu().numpy().tobytes()  # plain bytes through the queue
+        # the input buffer seen through stage_input_view holds those rows;
+        # rows a producer writes into such a view are what the parent reads
+        seen = ub.stage_input_view(sid, 1, 2, H)
+        torch.cuda.synchronize()
+        results.append(same(seen, n))
+        try:
+            ub.stage_input_view(sid, 1, claim["input_buffer_size"] // (2 * H) + 1, H)
+            results.append(False)
+        except RuntimeError as e:
+            results.append("exceeds the slot input buffer" in str(e))
+        rows = torch.randn(1, 3, H, generator=g, device=dev).to(torch.bfloat16)
+        ub.stage_input_view(sid, 1, 3, H).copy_(rows)
+        ub.submit_staged_input_slot(sid, rows)
+        staged_rows = rows.reshape(-1).view(torch.int16).cpu().numpy().tobytes()  # plain bytes through the queue
         ub.close_slot(sid)
         out.put(((results, staged_rows), None))
     except Exception:
@@ -399,8 +412,10 @@ def test_read_outputs_matches_copy_and_adds(pool):
     is not a multiple of 8 with operands off 16-byte alignment (the scalar
     path); and the reads fused with the next RMSNorm and with SiLU*up are bit
     for bit the read, the adds and ops.rms_norm / ops.silu_mul.  A staged
-    read leaves the normalised rows in the slot's input buffer, and the
-    staged submit refuses a shape other than the staged one.  The slot
+    read leaves the normalised rows in the slot's input buffer, the staged
+    submit refuses a shape other than the staged one, stage_input_view
+    refuses rows beyond the buffer, and rows written into its view are what
+    the aggregator side reads.  The slot
     output holds random bf16 values written by this process (the aggregator
     side)."""
     agg = _agg()
@@ -426,7 +441,7 @@ def test_read_outputs_matches_copy_and_adds(pool):
         if p.is_alive():
             p.kill()
         agg.release_slot(claim["slot_id"], 6)
-    assert results == [True] * 12, results
+    assert results == [True] * 14, results
 
 
 def _timeout_proc(claim, out):
