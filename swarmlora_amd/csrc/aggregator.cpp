@@ -16,6 +16,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -828,6 +829,13 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
   auto seq_word = [](int sid, size_t off) {
     return reinterpret_cast<uint64_t*>(static_cast<char*>(g_pool.slots[sid].out) + g_pool.out_size + off);
   };
+  // SWL_AGG_TIMING=1: per-round host phases (wait for every slot's ready,
+  // drain, launch, stream sync) summed and printed when the loop exits
+  const bool timing = std::getenv("SWL_AGG_TIMING") && std::atoi(std::getenv("SWL_AGG_TIMING")) != 0;
+  using tclk = std::chrono::steady_clock;
+  double t_ready = 0, t_drain = 0, t_launch = 0, t_sync = 0;
+  long t_rounds = 0;
+  auto us_since = [](tclk::time_point a) { return std::chrono::duration<double, std::micro>(tclk::now() - a).count(); };
   while (c->quit.load(std::memory_order_acquire) == 0) {
     int N = 0;
     rc = swl_agg_token_boundary(&active.w[0], &active.w[1], &N);
@@ -839,8 +847,13 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
     const int ops_per_token = 1 + 4 * g_num_layers + 1;
     for (int op_idx = 0; op_idx < ops_per_token; ++op_idx) {
       int cnt = 0;
+      auto tp = tclk::now();
       rc = swl_agg_wait_for_slots(&active.w[0], &active.w[1], &cnt);
       if (rc) return rc;
+      if (timing) {
+        t_ready += us_since(tp);
+        tp = tclk::now();
+      }
       if (cnt < 0) {
         swl_agg_signal_done();
         break;
@@ -854,6 +867,10 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
       int got = 0;
       rc = drain_impl(active.w[0], active.w[1], N, sids, wids, ops, layers, toks, keys, seqs, outh, &got);
       if (rc) return rc;
+      if (timing) {
+        t_drain += us_since(tp);
+        tp = tclk::now();
+      }
       if (got == 0 || c->quit.load(std::memory_order_acquire) != 0) {
         if (c->quit.load(std::memory_order_acquire) != 0) swl_agg_signal_done();
         continue;
@@ -923,7 +940,15 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
         // on both sides (its worker waits for the outputs on its stream)
         bool sync = nord < m;
         for (int i = 0; i < m; ++i) sync = sync || outh[i] != 0;
+        if (timing) {
+          t_launch += us_since(tp);
+          tp = tclk::now();
+        }
         if (sync) SWL_HIP(hipStreamSynchronize(st));
+        if (timing) {
+          t_sync += us_since(tp);
+          ++t_rounds;
+        }
         int32_t late[SWL_MAX_SLOTS];
         const int nlate = swl_agg_take_seq_timeouts(late, SWL_MAX_SLOTS);
         for (int i = 0; i < nlate && i < SWL_MAX_SLOTS; ++i) {
@@ -942,6 +967,10 @@ extern "C" int swl_agg_main_loop(int num_slots, int dtype_code) {
     }
     ++tokens_done;
   }
+  if (timing && t_rounds)
+    std::printf("[Aggregator] host phases per round (us, %ld rounds): ready wait %.1f, drain %.1f, launch %.1f, "
+                "stream sync %.1f\n", t_rounds, t_ready / t_rounds, t_drain / t_rounds, t_launch / t_rounds,
+                t_sync / t_rounds);
   std::printf("[Aggregator] Slot-based loop exited after %ld tokens (%ld ops)\n", tokens_done, ops_done);
   std::fflush(stdout);
   return SWL_OK;

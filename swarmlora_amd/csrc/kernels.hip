@@ -4344,6 +4344,47 @@ __global__ __launch_bounds__(1024) void copy_signal_kernel(u32x4* __restrict__ d
   if (threadIdx.x == 0) __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// A worker read's GPU-ordered slot words, handled inside its own launch.
+struct SeqSyncDev {
+  const uint64_t* wait_flag;  // or null: no wait
+  uint64_t want;
+  uint32_t* timed_out;
+  int32_t tag;
+  uint32_t limit_ticks;       // s_memrealtime runs at 100 MHz
+  uint64_t* signal_flag;      // or null: no signal (single-workgroup launches only)
+  uint64_t value;
+};
+
+// Every workgroup: lane 0 polls the flag (system-scope loads and a sleep,
+// bounded like seq_wait_kernel; a wait that runs out reports its tag and the
+// read still runs), then after the barrier every thread takes an agent-scope
+// fence (the XCD's caches drop lines older than the producer's writes).
+__device__ __forceinline__ void seq_sync_wait(const SeqSyncDev& s) {
+  if (!s.wait_flag) return;
+  if (threadIdx.x == 0) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(s.wait_flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < s.want) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > s.limit_ticks) {
+        __hip_atomic_store(s.timed_out + s.tag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(32);
+    }
+  }
+  __syncthreads();
+  __threadfence();
+}
+
+// The launch's only workgroup, after all of its stores: every thread
+// releases its stores at agent scope (written back from the XCD's L2), and
+// after the barrier one lane stores the flag with system-scope release.
+__device__ __forceinline__ void seq_sync_signal(const SeqSyncDev& s) {
+  if (!s.signal_flag) return;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(s.signal_flag, s.value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 struct CombineArgs {
   bf16* dst;
   const bf16* src;
@@ -4351,12 +4392,14 @@ struct CombineArgs {
   const bf16* res;    // or null
   int64_t n;
   int32_t vec;        // every pointer 16-byte aligned
+  SeqSyncDev sync;    // wait only
 };
 
 // A worker's read of its round output: out (+ its LoRA delta) (+ the
 // residual), each add rounded to bf16 as torch's bf16 adds are; 8 elements
 // a thread.
 __global__ __launch_bounds__(256) void combine_rows_kernel(CombineArgs a) {
+  seq_sync_wait(a.sync);
   const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (i0 >= a.n) return;
   auto one = [&](float s, float d, float r) {
@@ -4380,8 +4423,9 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(CombineArgs a) {
     a.dst[i] = one(bf2f(a.src[i]), a.delta ? bf2f(a.delta[i]) : 0.f, a.res ? bf2f(a.res[i]) : 0.f);
 }
 
-// The read of an O or Down round's output followed by the next norm, one
-// workgroup of 256 threads per token row: h = bf16(res + bf16(out + delta))
+// The read of an O or Down round's output followed by the next norm, a
+// workgroup of 256 threads per token row (rows blockIdx.x, + gridDim.x, ...):
+// h = bf16(res + bf16(out + delta))
 // is written to dst_h, then LlamaRMSNorm of h to dst_n with the same
 // per-thread sums and reduction as rmsnorm_rows_kernel, so both match the
 // separate read and norm bit for bit.  d a multiple of 8, every pointer
@@ -4395,13 +4439,17 @@ struct CombineNormArgs {
   const bf16* res;    // or null
   const bf16* w;
   int64_t d;
+  int64_t rows;
   float eps;
+  SeqSyncDev sync;
 };
 
 __global__ __launch_bounds__(256) void combine_norm_rows_kernel(CombineNormArgs a) {
   __shared__ float sh[4];
-  const int64_t off = (int64_t)blockIdx.x * a.d;
+  seq_sync_wait(a.sync);
   const int64_t nv = a.d >> 3;
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+  const int64_t off = row * a.d;
   float ss = 0.f;
   for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
     float s[8], dl[8], r[8];
@@ -4434,25 +4482,31 @@ __global__ __launch_bounds__(256) void combine_norm_rows_kernel(CombineNormArgs 
     *reinterpret_cast<u32x4*>(a.dst_n + off + 8 * i) = __builtin_bit_cast(u32x4, o);
     if (a.dst_n2) *reinterpret_cast<u32x4*>(a.dst_n2 + off + 8 * i) = __builtin_bit_cast(u32x4, o);
   }
+  }
+  seq_sync_signal(a.sync);
 }
 
 // The read of a Gate+Up round's output followed by SiLU*up: g = bf16(gate +
 // dgate), u = bf16(up + dup), act = bf16(bf16(silu(g)) * u) as
 // silu_mul_rows_kernel computes it; rows of 2 inter (gate | up) in, inter
-// out.  inter a multiple of 8, pointers 16-byte aligned.
+// out.  inter a multiple of 8, pointers 16-byte aligned.  Rows blockIdx.y,
+// + gridDim.y, ...; 8-element groups of a row by a grid stride over x.
 struct CombineSiluArgs {
   bf16* dst;
   bf16* dst2;         // a second copy, or null
   const bf16* src;
   const bf16* delta;  // [rows][2 inter] or null
   int64_t inter;
+  int64_t rows;
+  SeqSyncDev sync;
 };
 
-__global__ __launch_bounds__(256) void combine_silu_rows_kernel(CombineSiluArgs a) {
-  const int t = blockIdx.y;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (a.inter >> 3)) return;
-  const int64_t ri = (int64_t)t * 2 * a.inter + 8 * i;
+__global__ __launch_bounds__(1024) void combine_silu_rows_kernel(CombineSiluArgs a) {
+  seq_sync_wait(a.sync);
+  const int64_t nv = a.inter >> 3;
+  for (int64_t t = blockIdx.y; t < a.rows; t += gridDim.y)
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += (int64_t)gridDim.x * blockDim.x) {
+  const int64_t ri = t * 2 * a.inter + 8 * i;
   float g[8], u[8];
   unpack8(ld16(a.src + ri), g);
   unpack8(ld16(a.src + ri + a.inter), u);
@@ -4472,8 +4526,10 @@ __global__ __launch_bounds__(256) void combine_silu_rows_kernel(CombineSiluArgs 
     const float sg = bf2f(f2bf(g[j] / (1.0f + __expf(-g[j]))));
     o[j] = f2bf(sg * u[j]);
   }
-  *reinterpret_cast<u32x4*>(a.dst + (int64_t)t * a.inter + 8 * i) = __builtin_bit_cast(u32x4, o);
-  if (a.dst2) *reinterpret_cast<u32x4*>(a.dst2 + (int64_t)t * a.inter + 8 * i) = __builtin_bit_cast(u32x4, o);
+  *reinterpret_cast<u32x4*>(a.dst + t * a.inter + 8 * i) = __builtin_bit_cast(u32x4, o);
+  if (a.dst2) *reinterpret_cast<u32x4*>(a.dst2 + t * a.inter + 8 * i) = __builtin_bit_cast(u32x4, o);
+  }
+  seq_sync_signal(a.sync);
 }
 
 struct WaitCopyArgs {
@@ -4542,10 +4598,40 @@ int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag,
   return SWL_OK;
 }
 
+namespace {
+// Host SeqSync -> kernel form; a signal only where the launch has one
+// workgroup (single_wg).
+int seq_sync_dev(const SeqSync* s, bool single_wg, const char* fn, SeqSyncDev* d) {
+  *d = SeqSyncDev{};
+  if (!s) return SWL_OK;
+  if (s->wait_flag) {
+    SWL_CHECK(s->timed_out != nullptr && s->tag >= 0 && s->tag < SWL_MAX_SLOTS, SWL_ERR_INVALID,
+              std::string(fn) + ": bad wait time-out word");
+    d->wait_flag = s->wait_flag;
+    d->want = s->want;
+    d->timed_out = s->timed_out;
+    d->tag = s->tag;
+    d->limit_ticks = (uint32_t)std::min<uint64_t>((uint64_t)s->limit_us * 100, 0xFFFFFFFFull);
+  }
+  if (s->signal_flag) {
+    SWL_CHECK(single_wg, SWL_ERR_INVALID, std::string(fn) + ": a fused signal needs at most " +
+                                              std::to_string(kFusedSignalRows) + " rows");
+    d->signal_flag = s->signal_flag;
+    d->value = s->value;
+  }
+  return SWL_OK;
+}
+}  // namespace
+
 int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta, const void* res,
-                        hipStream_t stream) {
+                        hipStream_t stream, const SeqSync* sync) {
   SWL_CHECK(dst && src && n >= 0, SWL_ERR_INVALID, "combine_rows: bad arguments");
-  if (n == 0) return SWL_OK;
+  SWL_CHECK(!sync || !sync->signal_flag, SWL_ERR_INVALID, "combine_rows: no fused signal");
+  if (n == 0) {  // nothing to read: the wait alone
+    if (!sync || !sync->wait_flag) return SWL_OK;
+    const uint64_t* f = sync->wait_flag;
+    return seq_wait_launch(1, &f, &sync->want, &sync->tag, sync->timed_out, sync->limit_us, stream);
+  }
   CombineArgs a{};
   a.dst = reinterpret_cast<bf16*>(dst);
   a.src = reinterpret_cast<const bf16*>(src);
@@ -4554,6 +4640,8 @@ int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta
   a.n = n;
   auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
   a.vec = (al(dst) && al(src) && al(delta) && al(res)) ? 1 : 0;
+  int rc = seq_sync_dev(sync, false, "combine_rows", &a.sync);
+  if (rc) return rc;
   const int64_t threads = (n + 7) / 8;
   hipLaunchKernelGGL(combine_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);
   SWL_LAUNCH_CHECK("combine_rows_kernel launch");
@@ -4561,13 +4649,17 @@ int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta
 }
 
 int combine_norm_rows_launch(void* dst_h, void* dst_n, void* dst_n2, const void* src, int64_t rows, int64_t d,
-                             const void* delta, const void* res, const void* w, float eps, hipStream_t stream) {
+                             const void* delta, const void* res, const void* w, float eps, hipStream_t stream,
+                             const SeqSync* sync) {
   auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
   SWL_CHECK(dst_h && dst_n && src && w && rows >= 0 && d > 0 && d % 8 == 0, SWL_ERR_INVALID,
             "combine_norm_rows: bad arguments (d must be a multiple of 8)");
   SWL_CHECK(al(dst_h) && al(dst_n) && al(dst_n2) && al(src) && al(delta) && al(res) && al(w), SWL_ERR_INVALID,
             "combine_norm_rows: pointers must be 16-byte aligned");
-  if (rows == 0) return SWL_OK;
+  if (rows == 0 && !sync) return SWL_OK;
+  SWL_CHECK(rows > 0, SWL_ERR_INVALID, "combine_norm_rows: no rows to wait or signal for");
+  const bool one = sync && sync->signal_flag;  // the signal's one workgroup loops over the rows
+  SWL_CHECK(!one || rows <= kFusedSignalRows, SWL_ERR_INVALID, "combine_norm_rows: too many rows for a fused signal");
   CombineNormArgs a{};
   a.dst_h = reinterpret_cast<bf16*>(dst_h);
   a.dst_n = reinterpret_cast<bf16*>(dst_n);
@@ -4577,29 +4669,38 @@ int combine_norm_rows_launch(void* dst_h, void* dst_n, void* dst_n2, const void*
   a.res = reinterpret_cast<const bf16*>(res);
   a.w = reinterpret_cast<const bf16*>(w);
   a.d = d;
+  a.rows = rows;
   a.eps = eps;
-  hipLaunchKernelGGL(combine_norm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, stream, a);
+  int rc = seq_sync_dev(sync, one, "combine_norm_rows", &a.sync);
+  if (rc) return rc;
+  hipLaunchKernelGGL(combine_norm_rows_kernel, dim3(one ? 1u : (unsigned)rows), dim3(256), 0, stream, a);
   SWL_LAUNCH_CHECK("combine_norm_rows_kernel launch");
   return SWL_OK;
 }
 
 int combine_silu_rows_launch(void* dst, void* dst2, const void* src, int64_t rows, int64_t inter, const void* delta,
-                             hipStream_t stream) {
+                             hipStream_t stream, const SeqSync* sync) {
   auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p % 16) == 0; };
   SWL_CHECK(dst && src && rows >= 0 && inter > 0 && inter % 8 == 0, SWL_ERR_INVALID,
             "combine_silu_rows: bad arguments (inter must be a multiple of 8)");
   SWL_CHECK(rows <= 65535, SWL_ERR_INVALID, "combine_silu_rows: at most 65535 rows");
   SWL_CHECK(al(dst) && al(dst2) && al(src) && al(delta), SWL_ERR_INVALID,
             "combine_silu_rows: pointers must be 16-byte aligned");
-  if (rows == 0) return SWL_OK;
+  if (rows == 0 && !sync) return SWL_OK;
+  SWL_CHECK(rows > 0, SWL_ERR_INVALID, "combine_silu_rows: no rows to wait or signal for");
+  const bool one = sync && sync->signal_flag;  // one 1024-thread workgroup loops over everything
+  SWL_CHECK(!one || rows <= kFusedSignalRows, SWL_ERR_INVALID, "combine_silu_rows: too many rows for a fused signal");
   CombineSiluArgs a{};
   a.dst = reinterpret_cast<bf16*>(dst);
   a.dst2 = reinterpret_cast<bf16*>(dst2);
   a.src = reinterpret_cast<const bf16*>(src);
   a.delta = reinterpret_cast<const bf16*>(delta);
   a.inter = inter;
-  const dim3 grid((unsigned)(((inter >> 3) + 255) / 256), (unsigned)rows);
-  hipLaunchKernelGGL(combine_silu_rows_kernel, grid, dim3(256), 0, stream, a);
+  a.rows = rows;
+  int rc = seq_sync_dev(sync, one, "combine_silu_rows", &a.sync);
+  if (rc) return rc;
+  const dim3 grid(one ? 1u : (unsigned)(((inter >> 3) + 255) / 256), one ? 1u : (unsigned)rows);
+  hipLaunchKernelGGL(combine_silu_rows_kernel, grid, dim3(one ? 1024 : 256), 0, stream, a);
   SWL_LAUNCH_CHECK("combine_silu_rows_kernel launch");
   return SWL_OK;
 }

@@ -49,29 +49,47 @@ int seq_write_launch(int n, uint64_t* const* flag, const uint64_t* value, hipStr
 constexpr size_t kCopySignalMax = 256 * 1024;
 int copy_signal_launch(void* dst, const void* src, size_t bytes, uint64_t* flag, uint64_t value, hipStream_t stream);
 
-// The converse: waits on `stream` until *flag >= want (as seq_wait_launch,
-// with its time-out report into timed_out[tag]), then copies `bytes` from
-// src to dst, in one launch of one workgroup for copies up to
-// kCopySignalMax bytes with 16-byte aligned pointers; otherwise
-// seq_wait_launch + hipMemcpyAsync.
+// GPU-ordered slot words handled inside a worker read's own launch (null
+// flags: none): before reading, every workgroup waits until *wait_flag >=
+// want (as seq_wait_launch, with its time-out report into timed_out[tag]);
+// after its stores, the launch writes *signal_flag = value (system-scope
+// release after the stores are written back), which needs the launch to be
+// one workgroup: reads of at most kFusedSignalRows rows.
+struct SeqSync {
+  const uint64_t* wait_flag = nullptr;
+  uint64_t want = 0;
+  uint32_t* timed_out = nullptr;
+  int32_t tag = 0;
+  uint32_t limit_us = 0;
+  uint64_t* signal_flag = nullptr;
+  uint64_t value = 0;
+};
+constexpr int64_t kFusedSignalRows = 8;
+
 // dst[i] = bf16(res[i] + bf16(src[i] + delta[i])) for i < n bf16 elements
 // (delta and res optional: the same bf16 roundings as the two separate adds
-// out + delta and residual + that), one launch.
+// out + delta and residual + that), one launch; sync: a wait only.
 int combine_rows_launch(void* dst, const void* src, int64_t n, const void* delta, const void* res,
-                        hipStream_t stream);
+                        hipStream_t stream, const SeqSync* sync = nullptr);
 
 // The same read followed by LlamaRMSNorm of every row (rows x d): dst_h =
 // h, dst_n (and dst_n2 when not null) = bf16(bf16(h * rsqrt(mean(h^2) +
 // eps)) * w), bit for bit the separate read and rmsnorm_rows_kernel.
 // d % 8 == 0, 16-byte aligned.
 int combine_norm_rows_launch(void* dst_h, void* dst_n, void* dst_n2, const void* src, int64_t rows, int64_t d,
-                             const void* delta, const void* res, const void* w, float eps, hipStream_t stream);
+                             const void* delta, const void* res, const void* w, float eps, hipStream_t stream,
+                             const SeqSync* sync = nullptr);
 // A Gate+Up read (rows of 2 inter, optional delta) followed by SiLU*up into
 // rows of inter (dst, and dst2 when not null), bit for bit the separate read
 // and silu_mul_rows_kernel.
 int combine_silu_rows_launch(void* dst, void* dst2, const void* src, int64_t rows, int64_t inter, const void* delta,
-                             hipStream_t stream);
+                             hipStream_t stream, const SeqSync* sync = nullptr);
 
+// The converse of copy_signal_launch: waits on `stream` until *flag >= want
+// (as seq_wait_launch, with its time-out report into timed_out[tag]), then
+// copies `bytes` from src to dst, in one launch of one workgroup for copies
+// up to kCopySignalMax bytes with 16-byte aligned pointers; otherwise
+// seq_wait_launch + hipMemcpyAsync.
 int wait_copy_launch(const uint64_t* flag, uint64_t want, int32_t tag, uint32_t* timed_out, uint32_t limit_us,
                      void* dst, const void* src, size_t bytes, hipStream_t stream);
 

@@ -29,6 +29,9 @@ struct SlotCtx {
   // [sbx, stx, sdx], waiting for swl_w_submit_staged_input
   bool staged = false;
   int64_t sbx = 0, stx = 0, sdx = 0;
+  // GPU-ordered mode: the staging read also wrote the input sequence word
+  // (value seq), so the staged submit launches nothing
+  bool signaled = false;
 };
 
 // Limit of this worker's stream wait for a round's outputs (the aggregator's
@@ -127,6 +130,33 @@ int copy_in(const char* fn, SlotCtx* c, const void* src, size_t bytes, hipStream
   return SWL_OK;
 }
 
+// The GPU-ordered words a fused read handles in its own launch: the wait
+// for the last round's output word (wait_outputs' condition), and, when it
+// stages the next input of at most kFusedSignalRows rows, the signal of that
+// input's word (value seq + 1, taken by commit_read_sync once the launch is
+// queued).
+swl::SeqSync read_sync(SlotCtx* c, bool staging, int64_t rows) {
+  swl::SeqSync s;
+  if (g_w.gpu_ordered == 1 && c->seq != 0) {
+    s.wait_flag = seq_word(c, swl::kOutSeqOffset);
+    s.want = c->seq;
+    s.timed_out = g_w.out_timeout;
+    s.tag = c->slot_id;
+    s.limit_us = out_wait_limit_us();
+  }
+  if (staging && g_w.gpu_ordered && rows <= swl::kFusedSignalRows) {
+    s.signal_flag = seq_word(c, swl::kInSeqOffset);
+    s.value = c->seq + 1;
+  }
+  return s;
+}
+
+void commit_read_sync(SlotCtx* c, const swl::SeqSync& s) {
+  if (!s.signal_flag) return;
+  c->seq = s.value;
+  c->signaled = true;
+}
+
 // Checks and records a fused read's staging of the next round's input
 // ([bx, tx, d] bf16 rows into the slot's input buffer); null when not asked.
 int stage_target(const char* fn, SlotCtx* c, int stage_input, int64_t bx, int64_t tx, int64_t d, void** dst) {
@@ -136,6 +166,7 @@ int stage_target(const char* fn, SlotCtx* c, int stage_input, int64_t bx, int64_
             std::string(fn) + ": staged input exceeds the slot input buffer");
   *dst = c->in;
   c->staged = true;
+  c->signaled = false;
   c->sbx = bx;
   c->stx = tx;
   c->sdx = d;
@@ -246,6 +277,7 @@ int swl_w_prepare_input(int slot_id, const void* src, int64_t bx, int64_t tx, in
   if (rc) return rc;
   SWL_CHECK(src && bx > 0 && tx > 0 && dx > 0 && elem_size > 0, SWL_ERR_INVALID, "Input must be 3D [B, T, D]");
   c->staged = false;
+  c->signaled = false;
   rc = copy_in("prepare_input_slot", c, src, (size_t)bx * tx * dx * elem_size, (hipStream_t)stream);
   if (rc) return rc;
   c->bx = bx;
@@ -314,9 +346,8 @@ int swl_w_read_output(int slot_id, void* dst, int64_t n, const void* delta, cons
   SWL_CHECK((size_t)n * sizeof(uint16_t) <= c->out_size, SWL_ERR_INVALID,
             "get_outputs_slot: output (" + std::to_string(n * 2) + " bytes) exceeds slot output buffer (" +
                 std::to_string(c->out_size) + " bytes)");
-  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
-  if (rc) return rc;
-  rc = swl::combine_rows_launch(dst, c->out, n, delta, residual, (hipStream_t)stream);
+  const swl::SeqSync sync = read_sync(c, false, 0);  // the output wait inside the read's launch
+  rc = swl::combine_rows_launch(dst, c->out, n, delta, residual, (hipStream_t)stream, &sync);
   if (rc) return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
   return SWL_OK;
 }
@@ -332,14 +363,14 @@ int swl_w_read_output_norm(int slot_id, void* dst_h, void* dst_norm, int64_t bx,
   void* staged = nullptr;
   rc = stage_target("get_outputs_slot", c, stage_input, bx, tx, d, &staged);
   if (rc) return rc;
-  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
-  if (rc) return rc;
+  const swl::SeqSync sync = read_sync(c, staged != nullptr, bx * tx);
   rc = swl::combine_norm_rows_launch(dst_h, dst_norm, staged, c->out, bx * tx, d, delta, residual, weight, eps,
-                                     (hipStream_t)stream);
+                                     (hipStream_t)stream, &sync);
   if (rc) {
     c->staged = false;
     return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
   }
+  commit_read_sync(c, sync);
   return SWL_OK;
 }
 
@@ -353,13 +384,13 @@ int swl_w_read_output_silu(int slot_id, void* dst, int64_t bx, int64_t tx, int64
   void* staged = nullptr;
   rc = stage_target("get_outputs_slot", c, stage_input, bx, tx, inter, &staged);
   if (rc) return rc;
-  rc = wait_outputs("get_outputs_slot", c, (hipStream_t)stream);
-  if (rc) return rc;
-  rc = swl::combine_silu_rows_launch(dst, staged, c->out, bx * tx, inter, delta, (hipStream_t)stream);
+  const swl::SeqSync sync = read_sync(c, staged != nullptr, bx * tx);
+  rc = swl::combine_silu_rows_launch(dst, staged, c->out, bx * tx, inter, delta, (hipStream_t)stream, &sync);
   if (rc) {
     c->staged = false;
     return swl::fail(rc, std::string("get_outputs_slot: ") + swl::last_error());
   }
+  commit_read_sync(c, sync);
   return SWL_OK;
 }
 
@@ -375,6 +406,10 @@ int swl_w_submit_staged_input(int slot_id, int64_t bx, int64_t tx, int64_t dx, v
   c->tx = tx;
   c->dx = dx;
   hipStream_t st = (hipStream_t)stream;
+  if (g_w.gpu_ordered && c->signaled) {
+    c->signaled = false;  // the staging read wrote the word (value seq)
+    return SWL_OK;
+  }
   if (g_w.gpu_ordered) {
     // the value the aggregator's stream waits for, after the staging read
     ++c->seq;
