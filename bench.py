@@ -29,12 +29,15 @@ the roofline and the floor; configs 1 and 2 also on the host's CPU cores.
 
 `config.drop_in` is the drop-in (multi-process) path: a spawned aggregator
 process and --ipc-workers worker processes over the shared-memory ring and
-IPC slot buffers, 32 layers (130 rounds per token), host-synchronised rounds
-with the reference's worker-side LoRA and with adapters pooled in the
-aggregator's rounds; tokens/s and µs per round of the median of 3 windows
-timed once every slot is active, and the mean [LAYER_PROFILE] stage split
-(gather / round wait / scatter / LoRA / norms and attention) of
-stage-synchronised tokens.
+IPC slot buffers, 32 layers (130 rounds per token), in four modes: the
+reference's host-synchronised protocol with the worker-side LoRA, the same
+with the worker's input copies and then also its output reads ordered on
+the GPU, and host-synchronised with adapters pooled in the aggregator's
+rounds.  The modes run in turn, twice (a run's level varies more between
+runs than within one); per mode tokens/s and µs per round of the median of
+its 6 windows (3 per run, timed once every slot is active), each pass's
+median, and the mean [LAYER_PROFILE] stage split (gather / round wait /
+scatter / LoRA / norms and attention) of stage-synchronised tokens.
 """
 
 import argparse
@@ -86,7 +89,9 @@ def parse():
                     help="decode: skip the per-config figures (BASELINE configs 1, 2, 3 and 5)")
     ap.add_argument("--ipc-layers", type=int, default=32, help="drop-in leg: 8B-shaped layers")
     ap.add_argument("--ipc-tokens", type=int, default=6, help="drop-in leg: decode tokens per timed window")
-    ap.add_argument("--ipc-reps", type=int, default=3, help="drop-in leg: timed windows (the median is reported)")
+    ap.add_argument("--ipc-reps", type=int, default=3, help="drop-in leg: timed windows per run")
+    ap.add_argument("--ipc-passes", type=int, default=2,
+                    help="drop-in leg: passes over the modes in turn (the median window of all is reported)")
     ap.add_argument("--ipc-modes", default="host_sync,gpu_ordered_inputs,gpu_ordered,host_sync_pooled",
                     help="drop-in leg: comma list of " + ", ".join(IPC_MODES) + " (the decode line's default: the "
                          "reference's protocol with the worker's own LoRA, host-synchronised, then with its input "
@@ -591,15 +596,16 @@ IPC_MODES = {  # name: (GPU-ordered rounds, adapters pooled in the aggregator)
 }
 
 
-def ipc_measure(W, L, n_tok, modes, reps=3):
+def ipc_measure(W, L, n_tok, modes, reps=3, passes=1):
     """The multi-process serving path: this process is the aggregator (native
     main loop on a thread, 8B-shaped weights for L layers, embed and LM
     head), W worker processes decode one token per step each through the
-    shared-memory ring and IPC-mapped slots, once per mode of IPC_MODES.
-    Per mode: tokens/s, step time and µs per round from `reps` timed windows
-    of n_tok tokens (per window the slowest worker; the median window), then
-    the mean [LAYER_PROFILE] stage split of two stage-timed tokens per
-    worker."""
+    shared-memory ring and IPC-mapped slots, once per mode of IPC_MODES in
+    each of `passes` passes over the modes (fresh worker processes per run).
+    Per mode: tokens/s, step time and µs per round from the median of all
+    its timed windows (`reps` windows of n_tok tokens per run, per window the
+    slowest worker), each pass's median, then the mean [LAYER_PROFILE] stage
+    split of two stage-timed tokens per worker and run."""
     import multiprocessing as mp
     import threading
     import torch
@@ -609,8 +615,8 @@ def ipc_measure(W, L, n_tok, modes, reps=3):
     dev = torch.device("cuda:0")
     s = DecodeShape(layers=L)
     wts = synthetic_weights(s, dev, seed=0)
-    res = {}
-    for mode in modes:
+    runs = {m: [] for m in modes}
+    for mode in [m for _ in range(passes) for m in modes]:
         gpu_ordered, pooled = IPC_MODES[mode]
         q = extq.create_queue(1024, 1024)
         extq.init_batch_control(W)
@@ -669,37 +675,44 @@ def ipc_measure(W, L, n_tok, modes, reps=3):
             agg.clear_adapters()
             agg.cleanup_slot_pool()
             extq.close_queue()
-        rounds = 2 + 4 * L
         per_win = [max(w[i] for w in wins) / n_tok for i in range(reps)]  # slowest worker per window
-        step_s = statistics.median(per_win)
+        runs[mode].append((per_win, profs, max(pre), load0))
+    rounds = 2 + 4 * L
+    res = {}
+    for mode, rr in runs.items():
+        wins_all = [x for r in rr for x in r[0]]
+        profs = [p for r in rr for p in r[1]]
+        step_s = statistics.median(wins_all)
         split = {k: round(statistics.fmean(r[k] for r in profs), 1)
                  for k in ("gather_us", "gemm_us", "scatter_us", "lora_us", "attn_us", "compute_us", "wall_us")}
         split["ipc_pct"] = round(100.0 * (split["gather_us"] + split["scatter_us"]) / split["wall_us"], 1)
         split["round_wait_us"] = round(split["gemm_us"] / rounds, 1)
         res[mode] = {"tok_s": round(W / step_s, 1), "ms_per_step": round(step_s * 1e3, 3),
                      "us_per_round": round(step_s * 1e6 / rounds, 1),
-                     "us_per_round_windows": [round(x * 1e6 / rounds, 1) for x in per_win],
-                     "untimed_tokens_before_all_active": max(pre), "host_load_1min": round(load0, 2),
+                     "us_per_round_passes": [round(statistics.median(r[0]) * 1e6 / rounds, 1) for r in rr],
+                     "us_per_round_windows": [round(x * 1e6 / rounds, 1) for x in wins_all],
+                     "untimed_tokens_before_all_active": max(r[2] for r in rr),
+                     "host_load_1min": [round(r[3], 2) for r in rr],
                      "layer_profile": split}
     return res
 
 
-def _drop_in_child(W, L, n_tok, modes, reps, out):
+def _drop_in_child(W, L, n_tok, modes, reps, passes, out):
     """ipc_measure in a process of its own (a fresh aggregator: nothing of the
     parent's GPU state, threads or memory carries over)."""
     try:
-        out.put((ipc_measure(W, L, n_tok, modes, reps), None))
+        out.put((ipc_measure(W, L, n_tok, modes, reps, passes), None))
     except Exception:
         import traceback
         out.put((None, traceback.format_exc()))
 
 
-def drop_in_leg(W, L, n_tok, modes, reps=3):
+def drop_in_leg(W, L, n_tok, modes, reps=3, passes=1):
     """ipc_measure run by a freshly spawned aggregator process."""
     import multiprocessing as mp
     ctx = mp.get_context("spawn")
     out = ctx.Queue()
-    p = ctx.Process(target=_drop_in_child, args=(W, L, n_tok, modes, reps, out))
+    p = ctx.Process(target=_drop_in_child, args=(W, L, n_tok, modes, reps, passes, out))
     p.start()
     try:
         res, err = out.get(timeout=900)
@@ -718,14 +731,14 @@ def ipc(args):
     W = min(args.workers, 8)
     L = args.ipc_layers
     modes = [m for m in args.ipc_modes.split(",") if m]
-    res = drop_in_leg(W, L, args.ipc_tokens, modes, args.ipc_reps)
+    res = drop_in_leg(W, L, args.ipc_tokens, modes, args.ipc_reps, args.ipc_passes)
     first = res[modes[0]]
     line = {
         "metric": f"multi-process decode tok/s (drop-in path, {modes[0]})",
         "value": first["tok_s"],
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.ipc_tokens * args.ipc_reps,
+        "steps": args.ipc_tokens * args.ipc_reps * args.ipc_passes,
         "warmup": IPC_WARM,
         "ms_per_step": first["ms_per_step"],
         "higher_is_better": True,
@@ -850,15 +863,16 @@ def main():
         W_ipc = max(1, min(args.ipc_workers, 8))
         modes = [m for m in args.ipc_modes.split(",") if m]
         try:
-            res = drop_in_leg(W_ipc, args.ipc_layers, args.ipc_tokens, modes, args.ipc_reps)
+            res = drop_in_leg(W_ipc, args.ipc_layers, args.ipc_tokens, modes, args.ipc_reps, args.ipc_passes)
             drop_in = {
                 "workload": f"{W_ipc} worker processes + a spawned aggregator process, {args.ipc_layers} 8B-shaped "
                             f"layers ({2 + 4 * args.ipc_layers} rounds per token), rank-16 adapter per worker; "
                             "host_sync: adapter applied on the worker, host-synchronised rounds (the reference's "
                             "protocol); gpu_ordered_inputs: the same with the input copies ordered on the GPU; "
                             "gpu_ordered: input copies and output reads ordered on the GPU; host_sync_pooled: "
-                            f"adapters pooled in the aggregator's rounds; {args.ipc_reps} windows of "
-                            f"{args.ipc_tokens} tokens once every slot is active, median window",
+                            f"adapters pooled in the aggregator's rounds; {args.ipc_passes} passes over the "
+                            f"modes in turn, {args.ipc_reps} windows of {args.ipc_tokens} tokens per run once "
+                            "every slot is active, median window of all passes",
                 "workers": W_ipc, "layers": args.ipc_layers, "rounds_per_token": 2 + 4 * args.ipc_layers, **res}
         except Exception as e:  # the headline line is still printed
             drop_in = {"error": f"{type(e).__name__}: {e}"[:2000]}
