@@ -344,7 +344,7 @@ struct EpiArgs {
 // fragment tiles).
 template <int SS>
 __device__ __forceinline__ u32x4 ld_w_step(const bf16* wp, int s, int n) {
-  return ldg16(wp + SS * (s < n ? s : n - 1));
+  return ldg16_nt(wp + SS * (s < n ? s : n - 1));
 }
 
 template <int SS, int D>
@@ -1095,7 +1095,7 @@ __global__ __launch_bounds__(kFkWaves * 64, 1) void fullk_kernel(FullKArgs args)
     const bf16* p = a->w + ((int64_t)tile * a->total_steps + s0) * 512 + 8 * lane;
 #pragma unroll
     for (int s = 0; s < kFkMaxSteps; ++s) {
-      wf[s] = ldg16(p);
+      wf[s] = ldg16_nt(p);
       if (s + 1 < nsw) p += 512;
     }
   };
@@ -2567,11 +2567,11 @@ __global__ __launch_bounds__(64 * W) void attn_tile_kernel(AttnArgs a, float* pa
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_global_load_lds((gbl_ptr)(a.kc + base + koff + (i & 1) * 8 * krow + (i >> 1) * 64),
-                                       (lds_ptr)(dst + i * kTileKBlk), 16, 0, 0);
+                                       (lds_ptr)(dst + i * kTileKBlk), 16, 0, kLoadNT);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_global_load_lds((gbl_ptr)(a.vc + base + voff + 4 * i * krow),
-                                       (lds_ptr)(dst + kTileKBytes + i * 1024), 16, 0, 0);
+                                       (lds_ptr)(dst + kTileKBytes + i * 1024), 16, 0, kLoadNT);
   };
 
   // q of the G query heads as the MFMA B operand: lane l holds column l % 16
