@@ -750,8 +750,8 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
       blk[c] = find_blk(a.L, nc);
       brow[c] = reinterpret_cast<const bf16*>(ep->b[blk[c]]) + (nc - blk_start_of(a.L, blk[c])) * r;
       if (live && r <= 16 && (r & 7) == 0) {
-        bq[c][0] = ld16(brow[c]);
-        if (r == 16) bq[c][1] = ld16(brow[c] + 8);
+        bq[c][0] = ldg16_nt(brow[c]);
+        if (r == 16) bq[c][1] = ldg16_nt(brow[c] + 8);
       }
     }
   }
@@ -765,8 +765,8 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     const int64_t qc = nq + c * a.inter;
     if (nq < ncols && ks < a.n_ks) {
       const float* pk = a.part + (int64_t)tok * a.N + qc + ks * kstride;
-      if (vec) {
-        q = *reinterpret_cast<const f32x4*>(pk);
+      if (vec) {  // read once: non-temporal
+        q = __builtin_nontemporal_load((const __attribute__((address_space(1))) f32x4*)(const void*)pk);
       } else {
         for (int e = 0; e < 4; ++e)
           if (nq + e < ncols) q[e] = pk[e];
