@@ -480,7 +480,7 @@ def per_config_measure(args):
                                                 "torch-CPU bf16, median of >= 5"}
     del cpu_rounds
     # config 3: the prefill rounds (MFMA bound)
-    pf = prefill_measure(steps=5)
+    pf = prefill_measure(steps=20)  # 5 calls per round under-measure: the first after a sync starts slow
     res["config3"] = {"unit": "layer (4 rounds)", "us": round(pf["ms"] * 1e3, 1), "TFLOPs": pf["tflops"],
                       "frac_mfma": round(pf["tflops"] / 2500.0, 4), "token_rows": pf["T"],
                       "floor_us": round(pf["flops"] / 2.5e15 * 1e6, 1),
