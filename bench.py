@@ -347,13 +347,21 @@ def _cpu_us(fn, budget_s=3.0, min_reps=20):
     return statistics.median(ts) * 1e6
 
 
+def _copies_for(nbytes, total=512 << 20):
+    """Copies of a weight of nbytes that together pass `total` bytes."""
+    return max(1, -(-total // nbytes))
+
+
 def _decode_layer_case(dev, n_slots, adapter_of_slot, n_pool, seed):
     """One 8B-shaped layer's four projection rounds (fused QKV, O, Gate+Up,
     Down) over n_slots one-token slots, every weight and adapter bf16
     ~N(0, 0.02), activations ~N(0, 1); n_pool rank-16 adapters (scale 2.0)
     on all seven projections, slot i using adapter adapter_of_slot[i].
     Weights and stacked lora_A in fragment tiles (the decode step's layout).
-    Returns the round closures and their algorithmic bytes."""
+    Each round keeps enough copies of its weight (at least 512 MB, twice the
+    last-level cache) and every call takes the next one, so replays stream
+    the weight from HBM as the decode step's layers do instead of finding it
+    in the cache.  Returns the round closures and their algorithmic bytes."""
     import torch
     from swarmlora_amd import ops
     H, KV, I, r = 4096, 1024, 14336, 16
@@ -367,7 +375,9 @@ def _decode_layer_case(dev, n_slots, adapter_of_slot, n_pool, seed):
     out = []
     for nm, k, dims in rounds:
         n = sum(dims)
-        w = ops.pack_weight(rn(n, k))
+        w_rm = rn(n, k)
+        ws = [ops.pack_weight(w_rm) for _ in range(_copies_for(2 * n * k))]
+        del w_rm
         table = ops.LoraTable(dev)
         for _ in range(n_pool):
             table.add(ops.pack_weight(rn(r * len(dims), k)), [rn(d, r) for d in dims], r, 2.0)
@@ -376,7 +386,9 @@ def _decode_layer_case(dev, n_slots, adapter_of_slot, n_pool, seed):
         ids = list(adapter_of_slot)
         fz = ops.round_fusion(w_layout=1, a_layout=1)
 
-        def run(xs=xs, ys=ys, w=w, table=table, ids=ids, dims=dims, fz=fz):
+        def run(xs=xs, ys=ys, ws=ws, table=table, ids=ids, dims=dims, fz=fz, turn=[0]):
+            w = ws[turn[0] % len(ws)]
+            turn[0] += 1
             ops.round_ex(xs, ys, [1] * len(xs), w, None, seg_lora=ids, table=table, blk_cols=dims, fusion=fz)
 
         nbytes = 2 * (n * k + n_slots * (k + n) + len(used) * r * len(dims) * k + len(used) * r * n)
@@ -406,13 +418,19 @@ def per_config_measure(args):
     w1 = rn(QKV, H)
     xs1 = [rn(1, H, std=1.0) for _ in range(4)]
     ad1 = [(rn(r, H), rn(QKV, r)) for _ in range(4)]
-    wp1 = ops.pack_weight(w1)
+    wp1 = [ops.pack_weight(w1) for _ in range(_copies_for(2 * QKV * H))]  # streamed from HBM (see above)
     tab1 = ops.LoraTable(dev)
     ids1 = [tab1.add(ops.pack_weight(a), [b], r, 2.0) for a, b in ad1]
     ys1 = [torch.empty(1, QKV, dtype=torch.bfloat16, device=dev) for _ in range(4)]
     fz1 = ops.round_fusion(w_layout=1, a_layout=1)
-    us1 = _graph_us(lambda: ops.round_ex(xs1, ys1, [1] * 4, wp1, None, seg_lora=ids1, table=tab1, blk_cols=[QKV],
-                                         fusion=fz1), iters=50)
+    turn1 = [0]
+
+    def run1():
+        w = wp1[turn1[0] % len(wp1)]
+        turn1[0] += 1
+        ops.round_ex(xs1, ys1, [1] * 4, w, None, seg_lora=ids1, table=tab1, blk_cols=[QKV], fusion=fz1)
+
+    us1 = _graph_us(run1, iters=50)
     b1 = 2 * (QKV * H + 4 * (H + QKV) + 4 * r * (H + QKV))
     # the CPU torch path on the same shapes (gather, x @ W.T, (x @ A.T) @ B.T * s, add, scatter)
     from oracle import reference_path as ref
