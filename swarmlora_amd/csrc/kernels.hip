@@ -4850,6 +4850,28 @@ int round_launch_ws(int n_seg, const int64_t* rows, const void* const* seg_in, v
 
   // ------------------------------------------------------ prefill regime
   SWL_CHECK(K % TK == 0, SWL_ERR_INVALID, "round: K must be a multiple of 64 for > 64 tokens");
+  // Segments by rows, most first (stable): the small ones (one-row slots)
+  // share the last, partly empty row tile, whose skipped MFMA blocks leave
+  // time for their LoRA k-steps, instead of adding a step run per segment
+  // to a full tile (the slowest tile ends the launch).  A row's result does
+  // not depend on its position in the batch.
+  int ord[kMaxSeg];
+  for (int i = 0; i < n_seg; ++i) ord[i] = i;
+  std::stable_sort(ord, ord + n_seg, [&](int x, int y) { return rows[x] > rows[y]; });
+  int64_t rows_by[kMaxSeg];
+  const void* in_by[kMaxSeg];
+  void* out_by[kMaxSeg];
+  int32_t lora_by[kMaxSeg];
+  for (int i = 0; i < n_seg; ++i) {
+    rows_by[i] = rows[ord[i]];
+    in_by[i] = seg_in[ord[i]];
+    out_by[i] = seg_out[ord[i]];
+    lora_by[i] = seg_lora ? seg_lora[ord[i]] : -1;
+  }
+  rows = rows_by;
+  seg_in = in_by;
+  seg_out = out_by;
+  if (seg_lora) seg_lora = lora_by;
   // the 256 x 256 GEMM and the shrink read the token rows in place from the
   // slot buffers (16-byte aligned: checked above); only the 128 x 128
   // kernel takes a packed copy
