@@ -691,20 +691,26 @@ __global__ __launch_bounds__(WAVES * 64, (TT <= 2 && WAVES < 16) ? 6 : 4) void s
   }
 }
 
-// One workgroup per (64 column quads, token); the four lane groups of a wave
-// (lanes l, l^16, l^32, l^48) share 16 quads.  Each lane group sums every
-// fourth K-slice partial of the quads (all its loads issued at once), the
-// groups fold with shuffles and lane group g keeps column g of each quad.
-// The token's LoRA shrink row is reduced over the K-slices by the whole
-// workgroup into LDS, the lane's row of lora_B having been requested before
-// the reductions; bias and the expand are added and the result is rounded
-// once to bf16.  MODE (swl_round_fusion.out_mode) then decides what is
-// stored: 0 the row (the scatter), 1 the residual update and its sum of
-// squares, 2 SiLU(gate) * up (each lane owns a gate and an up column), 3 the
-// row with RoPE on q and k, k and v also appended to their KV pages.
-template <int MODE>
-__global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
-  constexpr int C = MODE == 2 ? 2 : 1;  // column sets per lane (gate, up)
+// One workgroup per (64 Q column quads, token); the four lane groups of a
+// wave (lanes l, l^16, l^32, l^48) share 16 quads, Q times over (quad slot q
+// of the lane at column offset q x 256 gridDim.x, so each slot of the grid
+// is one contiguous run of columns).  Each lane group sums every fourth
+// K-slice partial of the quads (all its loads issued at once), the groups
+// fold with shuffles and lane group g keeps column g of each quad.  The
+// token's LoRA shrink row is reduced over the K-slices by the whole
+// workgroup into LDS, the lane's rows of lora_B having been requested
+// before the reductions; bias and the expand are added and the result is
+// rounded once to bf16.  MODE (swl_round_fusion.out_mode) then decides what
+// is stored: 0 the row (the scatter), 1 the residual update and its sum of
+// squares, 2 SiLU(gate) * up (each lane owns a gate and an up column of
+// each quad slot), 3 the row with RoPE on q and k, k and v also appended to
+// their KV pages.  Q > 1 (modes 0 and 2) takes the same columns in fewer
+// workgroups, for rounds whose grid would not be resident at once.
+template <int MODE, int Q = 1>
+__global__ __launch_bounds__(256, (MODE == 2 ? 2 : 1) * Q >= 4 ? 4 : 1) void epilogue_kernel(EpiArgs a) {
+  static_assert(Q == 1 || MODE == 0 || MODE == 2, "modes 1 and 3 reduce or exchange over one quad slot");
+  constexpr int C = MODE == 2 ? 2 : 1;  // column sets per quad slot (gate, up)
+  constexpr int CQ = C * Q;             // column sets per lane: set c = slot c / C, gate/up c % C
   __shared__ float us[kMaxURow];
   __shared__ float ured[256];
   __shared__ float xch[256];
@@ -712,11 +718,15 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int kg = lane >> 4;
   const int64_t ncols = MODE == 2 ? a.inter : a.N;  // output columns
+  const int64_t qoff = (int64_t)gridDim.x * 256;    // columns between quad slots
   const int64_t nq = (((int64_t)blockIdx.x * 4 + wv) * 16 + (lane & 15)) * 4;  // first column of the quad
   const int64_t n = nq + kg;                                                   // this lane's column
   const bool live = n < ncols;
   const int lora = a.has_lora ? a.lora[tok] : -1;
   const bool vec = (a.N & 3) == 0 && (MODE != 2 || (a.inter & 3) == 0);
+  // output column of set c (within the ncols) and whether it exists
+  auto col_of = [&](int c) { return n + (c / C) * qoff; };
+  auto live_of = [&](int c) { return col_of(c) < ncols; };
 
   // values the output fusions need after the reduction, requested first:
   // the residual element (1); the position and the cache length (3)
@@ -733,11 +743,11 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
 
   // lora_B rows of this lane's column(s) (rank <= 16, multiple of 8: registers)
   const swl_lora_entry* ep = lora >= 0 ? a.L.table + lora : nullptr;
-  int r = 0, blk[C];
-  const bf16* brow[C];
-  u32x4 bq[C][2];
+  int r = 0, blk[CQ];
+  const bf16* brow[CQ];
+  u32x4 bq[CQ][2];
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
+  for (int c = 0; c < CQ; ++c) {
     blk[c] = 0;
     brow[c] = nullptr;
     bq[c][0] = bq[c][1] = u32x4{0u, 0u, 0u, 0u};
@@ -745,11 +755,12 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   if (ep) {
     r = ep->rank;
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const int64_t nc = (live ? n : 0) + c * a.inter;
+    for (int c = 0; c < CQ; ++c) {
+      const bool lc = live_of(c);
+      const int64_t nc = (lc ? col_of(c) : 0) + (c % C) * a.inter;
       blk[c] = find_blk(a.L, nc);
       brow[c] = reinterpret_cast<const bf16*>(ep->b[blk[c]]) + (nc - blk_start_of(a.L, blk[c])) * r;
-      if (live && r <= 16 && (r & 7) == 0) {
+      if (lc && r <= 16 && (r & 7) == 0) {
         bq[c][0] = ldg16_nt(brow[c]);
         if (r == 16) bq[c][1] = ldg16_nt(brow[c] + 8);
       }
@@ -762,22 +773,25 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   const int64_t kstride = (int64_t)a.ntok * a.N;
   auto ld_part = [&](int c, int ks) {
     f32x4 q = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int64_t qc = nq + c * a.inter;
-    if (nq < ncols && ks < a.n_ks) {
+    const int64_t nqc = nq + (c / C) * qoff;  // first column of the set's quad
+    const int64_t qc = nqc + (c % C) * a.inter;
+    if (nqc < ncols && ks < a.n_ks) {
       const float* pk = a.part + (int64_t)tok * a.N + qc + ks * kstride;
       if (vec) {  // read once: non-temporal
         q = __builtin_nontemporal_load((const __attribute__((address_space(1))) f32x4*)(const void*)pk);
       } else {
         for (int e = 0; e < 4; ++e)
-          if (nq + e < ncols) q[e] = pk[e];
+          if (nqc + e < ncols) q[e] = pk[e];
       }
     }
     return q;
   };
-  constexpr int B0 = C == 2 ? 2 : 8;  // first batch per lane group (two column sets: 8 K-slices)
-  f32x4 q0[C][B0];
+  // first batch per lane group and set: 8 K-slices with one set, 2 with
+  // two, 1 with four (registers for four waves per SIMD)
+  constexpr int B0 = CQ >= 4 ? 1 : CQ >= 2 ? 2 : 8;
+  f32x4 q0[CQ][B0];
 #pragma unroll
-  for (int c = 0; c < C; ++c)
+  for (int c = 0; c < CQ; ++c)
 #pragma unroll
     for (int j = 0; j < B0; ++j) q0[c][j] = ld_part(c, kg + 4 * j);
 
@@ -818,18 +832,19 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     }
   }
 
-  f32x4 s[C];
+  f32x4 s[CQ];
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
+  for (int c = 0; c < CQ; ++c) {
     s[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < B0; ++j) s[c] += q0[c][j];
-    for (int ks0 = kg + 4 * B0; ks0 < a.n_ks; ks0 += 32) {
-      f32x4 q[8];
+    constexpr int NB = CQ >= 4 ? 4 : 8;  // later batches
+    for (int ks0 = kg + 4 * B0; ks0 < a.n_ks; ks0 += 4 * NB) {
+      f32x4 q[NB];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) q[j] = ld_part(c, ks0 + 4 * j);
+      for (int j = 0; j < NB; ++j) q[j] = ld_part(c, ks0 + 4 * j);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s[c] += q[j];
+      for (int j = 0; j < NB; ++j) s[c] += q[j];
     }
   }
 
@@ -850,17 +865,17 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
 
   // fold the four lane groups; lane group kg keeps component kg; then bias
   // and the LoRA expand
-  float v[C];
+  float v[CQ];
 #pragma unroll
-  for (int c = 0; c < C; ++c) {
+  for (int c = 0; c < CQ; ++c) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       s[c][e] += __shfl_xor(s[c][e], 16, 64);
       s[c][e] += __shfl_xor(s[c][e], 32, 64);
     }
     v[c] = kg == 0 ? s[c][0] : kg == 1 ? s[c][1] : kg == 2 ? s[c][2] : s[c][3];
-    if (!live) continue;
-    const int64_t nc = n + c * a.inter;
+    if (!live_of(c)) continue;
+    const int64_t nc = col_of(c) + (c % C) * a.inter;
     if (a.bias) v[c] += bf2f(a.bias[nc]);
     if (ep) {
       const float* ub = us + blk[c] * r;
@@ -889,7 +904,9 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
   }
 
   if constexpr (MODE == 0) {
-    if (live) yrow[n] = f2bf(v[0]);
+#pragma unroll
+    for (int c = 0; c < CQ; ++c)
+      if (live_of(c)) yrow[col_of(c)] = f2bf(v[c]);
   } else if constexpr (MODE == 1) {
     // h = bf16(h + out); the workgroup's sum of squares of the new h
     float sq = 0.f;
@@ -905,9 +922,11 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpiArgs a) {
     if (threadIdx.x == 0)
       a.ss_out[(int64_t)tok * a.ss_stride + blockIdx.x] = (ured[0] + ured[1]) + (ured[2] + ured[3]);
   } else if constexpr (MODE == 2) {
-    if (live) {
-      const float g = bf2f(f2bf(v[0])), u = bf2f(f2bf(v[1]));
-      yrow[n] = f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      if (!live_of(2 * q)) continue;
+      const float g = bf2f(f2bf(v[2 * q])), u = bf2f(f2bf(v[2 * q + 1]));
+      yrow[col_of(2 * q)] = f2bf(bf2f(f2bf(g / (1.0f + __expf(-g)))) * u);
     }
   } else {
     // columns of this workgroup: 2 heads of 128; RoPE pairs (d, d + 64)
@@ -3347,6 +3366,18 @@ int launch_fullk(const bf16* w, const bf16* bias, int64_t N, int64_t K, int ntok
   return SWL_OK;
 }
 
+// Epilogue workgroups resident per CU (registers bound it; cached)
+template <int MODE, int Q>
+int epi_occupancy() {
+  static const int occ = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, epilogue_kernel<MODE, Q>, 256, 0) != hipSuccess || n <= 0)
+      n = 1;
+    return n;
+  }();
+  return occ;
+}
+
 // Decode-shaped projection of ntok (<= 64) token rows: y[i] = x[i] . W^T
 // (+ bias) (+ LoRA delta of entry tok_lora[i]).  xrows[i] / yrows[i] are the
 // token's input / output rows (slot buffers).
@@ -3579,13 +3610,35 @@ int launch_skinny(const bf16* w, const bf16* bias, int64_t N, int64_t K, int nto
     e.hkv = fz->hkv;
     e.bs = fz->block_size;
   }
+  // quad slots per lane (modes 0 and 2): the fewest with which the grid
+  // runs in the fewest waves of resident workgroups (Gate+Up's SiLU
+  // epilogue at 28 rows: 1568 workgroups of one slot, 784 of two)
   const int64_t quads = (epi_cols + 3) / 4;
-  const dim3 egrid((unsigned)((quads + 63) / 64), (unsigned)ntok);
+  int q = 1;
+  if (mode == 0 || mode == 2) {
+    const int64_t cus = cu_count();
+    auto waves_of = [&](int qq, int occ) {
+      const int64_t wgs = (quads + 64 * qq - 1) / (64 * qq) * ntok;
+      return (wgs + occ * cus - 1) / (occ * cus);
+    };
+    const int occ1 = mode == 2 ? epi_occupancy<2, 1>() : epi_occupancy<0, 1>();
+    const int occ2 = mode == 2 ? epi_occupancy<2, 2>() : epi_occupancy<0, 2>();
+    int64_t best = waves_of(1, occ1);
+    if (waves_of(2, occ2) < best) {
+      best = waves_of(2, occ2);
+      q = 2;
+    }
+    if (mode == 0 && waves_of(4, epi_occupancy<0, 4>()) < best) q = 4;
+  }
+  const dim3 egrid((unsigned)((quads + 64 * q - 1) / (64 * q)), (unsigned)ntok);
   hipEvent_t te0 = timer_event(tslot, 2), te1 = timer_event(tslot, 3);
-  switch (mode) {
-    case 1: launch_maybe_timed(epilogue_kernel<1>, egrid, dim3(256), 0, st, te0, te1, e); break;
-    case 2: launch_maybe_timed(epilogue_kernel<2>, egrid, dim3(256), 0, st, te0, te1, e); break;
-    case 3: launch_maybe_timed(epilogue_kernel<3>, egrid, dim3(256), 0, st, te0, te1, e); break;
+  switch (mode * 8 + q) {
+    case 8 + 1: launch_maybe_timed(epilogue_kernel<1>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    case 16 + 1: launch_maybe_timed(epilogue_kernel<2>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    case 16 + 2: launch_maybe_timed(epilogue_kernel<2, 2>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    case 24 + 1: launch_maybe_timed(epilogue_kernel<3>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    case 2: launch_maybe_timed(epilogue_kernel<0, 2>, egrid, dim3(256), 0, st, te0, te1, e); break;
+    case 4: launch_maybe_timed(epilogue_kernel<0, 4>, egrid, dim3(256), 0, st, te0, te1, e); break;
     default: launch_maybe_timed(epilogue_kernel<0>, egrid, dim3(256), 0, st, te0, te1, e); break;
   }
   SWL_LAUNCH_CHECK("epilogue_kernel launch");
