@@ -29,11 +29,11 @@ the roofline and the floor; configs 1 and 2 also on the host's CPU cores.
 
 `config.drop_in` is the drop-in (multi-process) path: a spawned aggregator
 process and --ipc-workers worker processes over the shared-memory ring and
-IPC slot buffers, 32 layers (130 rounds per token), in four modes: the
-reference's host-synchronised protocol with the worker-side LoRA, the same
-with the worker's input copies and then also its output reads ordered on
-the GPU, and host-synchronised with adapters pooled in the aggregator's
-rounds.  The modes run in turn, twice (a run's level varies more between
+IPC slot buffers, 32 layers (130 rounds per token), in three modes by
+default: the reference's host-synchronised protocol with the worker-side
+LoRA, the same with the worker's input copies ordered on the GPU, and
+host-synchronised with adapters pooled in the aggregator's rounds
+(--ipc-modes adds the others).  The modes run in turn, twice (a run's level varies more between
 runs than within one); per mode tokens/s and µs per round of the median of
 its 6 windows (3 per run, timed once every slot is active), each pass's
 median, and the mean [LAYER_PROFILE] stage split (gather / round wait /
